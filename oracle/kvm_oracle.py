@@ -1,0 +1,519 @@
+"""CPU oracle for the KVM (Key-Value Means) forward path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (``kvm-paper_amd/``) may
+import, call or link this module.  It is used by ``tests/``, by
+``__graft_entry__.smoke()`` and by the ``cpu_baseline`` leg of ``bench.py``,
+always as the checker or as the timed CPU baseline, never as a fallback.
+
+This is a restatement, in plain PyTorch on the CPU, of the eager reference
+``model/kvm_mixer.py`` (the paper's "historical golden") with the FP32 merge
+routing of ``model/kvm_fp32_routing_reference.py``.  It works at the post-QKV
+boundary: inputs are q ``[B,Hq,T,D]``, k ``[B,Hkv,T,D]``, v ``[B,Hkv,T,Dv]``
+and the merge gate ``[B,Hkv,T,1]``; outputs are the per-head attention
+outputs before ``c_proj`` and the carried state dict in the reference's keys.
+
+Every function cites the reference lines it follows.  The same torch CPU ops
+as the reference are used at every rounding point, so on the same torch build
+the oracle reproduces the reference bit for bit (pinned by the golden fixtures
+under ``tests/golden/``).
+
+Parity pinning (see tests/test_oracle_*.py):
+  * schedule/budget functions: closed-form tables and the golden fixtures;
+  * ``prep_k`` / LayerNorm: textbook formula in fp64;
+  * ``attend``: brute-force fp64 softmax attention;
+  * ``route_merge``: brute-force fp64 argmax on small inputs;
+  * ``prefill`` / ``decode_step`` trajectories: golden fixtures written by
+    ``tests/golden/make_golden.py`` from the reference itself, plus
+    invariants (sink never merged, counts sum to coverage, decode after a
+    prefill of T tokens equals the last row of a prefill of T+1 tokens).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+# Carried-state keys (model/kvm_mixer.py:518-525).
+S_K = "kvm_s_k"
+S_V = "kvm_s_v"
+S_VLEN = "kvm_s_vlen"
+COVERAGE = "kvm_state_coverage_len"
+BSWA_BEGIN = "kvm_bswa_begin"
+BSWA_K = "kvm_bswa_k"
+BSWA_V = "kvm_bswa_v"
+BSWA_GATE = "kvm_bswa_merge_gate"
+
+
+@dataclass
+class OracleConfig:
+    """The mixer attributes the forward path reads (kvm_mixer.py:79-118)."""
+
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    value_dim: int
+    chunk_len: int = 256
+    n_bswa_chunks: int = 2
+    n_max_d_chunks: int = 1
+    sink_len: int = 1
+    rope_partial_dim: int = 64  # effective value (<=0 already mapped to D)
+    state_budget_mode: str = "fixed"
+    state_growth_factor: float = 1.0
+    state_growth_exponent: float = 0.5
+    state_round_down: int = 1
+    state_min_len: int = -1
+    state_saturation_n: int | None = None
+    gate_keys: bool = True
+    gate_values: bool = True
+    gate_appends: bool = False
+    gate_initial: bool = False
+    use_head_temps: bool = True
+    use_vlens: bool = True
+    fp32_routing: bool = True  # kvm_fp32_routing_reference.py:24-49
+
+    @property
+    def max_state_len(self) -> int:
+        return self.chunk_len * self.n_max_d_chunks  # kvm_mixer.py:99
+
+    @property
+    def group(self) -> int:
+        return self.q_heads // self.kv_heads
+
+
+@dataclass
+class OracleParams:
+    """Learned tensors used after the QKV boundary."""
+
+    ln_weight: torch.Tensor  # ln_s_k.weight [D]
+    ln_bias: torch.Tensor  # ln_s_k.bias [D]
+    front_temp: torch.Tensor | None  # [Hq] (kvm_mixer.py:113-115)
+    state_temp: torch.Tensor | None  # [Hq] (kvm_mixer.py:116-118)
+    ln_eps: float = 1e-5
+
+
+@dataclass
+class UpdateRecord:
+    """What one block-boundary update decided (for parity tests)."""
+
+    ctx_len: int
+    available: int
+    state_len_before: int
+    n_append: int
+    append_idx: torch.Tensor | None  # [B,Hkv,n_append] token offsets in chunk
+    merge_idx: torch.Tensor  # [B,Hkv,n_merge] token offsets in chunk
+    route: torch.Tensor | None  # [B,Hkv,n_merge] slot per merged token
+    s_k_before: torch.Tensor | None = None
+    s_v_before: torch.Tensor | None = None
+    s_vlen_before: torch.Tensor | None = None
+
+
+@dataclass
+class Recorder:
+    keep_states: bool = False
+    updates: list[UpdateRecord] = field(default_factory=list)
+
+
+# ---------------------------------------------------------------------------
+# Schedule (kvm_mixer.py:25-28, 131-172; kvm_triton_training_kernels.py:27-171)
+# ---------------------------------------------------------------------------
+
+
+def round_down_to_multiple(x: int, multiple: int) -> int:
+    """kvm_mixer.py:25-28."""
+    x = max(int(x), 0)
+    m = max(int(multiple), 1)
+    return x - x % m
+
+
+def bswa_begin_for_total_len(total_len: int, chunk_len: int, n_bswa: int) -> int:
+    """Window start for a sequence of ``total_len`` tokens (kvm_mixer.py:167-172)."""
+    end = round_down_to_multiple(int(total_len) + chunk_len - 1, chunk_len)
+    return max(0, end - n_bswa * chunk_len)
+
+
+def desired_state_len(cfg: OracleConfig, ctx_len: int, available: int, current: int) -> int:
+    """State budget after an update (kvm_mixer.py:131-165)."""
+    t = max(int(ctx_len), 0)
+    avail = max(int(available), 0)
+    cur = max(int(current), 0)
+    mode = cfg.state_budget_mode
+    if mode == "fixed":
+        target = cfg.state_min_len
+    elif mode == "power_law":
+        target = int(math.floor(cfg.state_growth_factor * (float(t) ** cfg.state_growth_exponent)))
+        target = max(round_down_to_multiple(target, cfg.state_round_down), cfg.state_min_len)
+    elif mode == "kvm_saturation":
+        n_sat = float(cfg.state_saturation_n)
+        target = int(math.floor((n_sat * float(t)) / (n_sat + float(t))))
+        target = max(round_down_to_multiple(target, cfg.state_round_down), cfg.state_min_len)
+    else:
+        raise ValueError(f"Unsupported state_budget_mode={mode!r}")
+    target = min(target, avail, cfg.max_state_len)
+    return max(target, cur)
+
+
+def prefill_schedule(cfg: OracleConfig, T: int) -> dict[str, Any]:
+    """Per-chunk schedule of a prefill of T tokens, as host integers.
+
+    Follows the eager loop (kvm_mixer.py:450-488) and the Triton schedule
+    (kvm_triton_training_kernels.py:85-171): for every query chunk m (m >= n)
+    the attention state length, and for every overflow chunk the state length
+    before/after and the number of appended slots.
+    """
+    C, n = cfg.chunk_len, cfg.n_bswa_chunks
+    front = min(T, n * C)
+    current = min(T, C)
+    coverage = current
+    updates = []  # (overflow_chunk, ctx_len, available, before, after, n_append)
+    attn_state = {}
+    for qb in range(front, T, C):
+        qe = min(T, qb + C)
+        begin = bswa_begin_for_total_len(qe, C, n)
+        if begin != coverage:
+            raise AssertionError("schedule coverage drifted")
+        attn_state[qb // C] = current
+        nxt = bswa_begin_for_total_len(min(T, qe + C), C, n)
+        if nxt <= begin:
+            continue
+        want = desired_state_len(cfg, qe, nxt, current)
+        n_app = min(max(want - current, 0), nxt - begin)
+        updates.append((begin // C, qe, nxt, current, current + n_app, n_app))
+        current += n_app
+        coverage = nxt
+    return {
+        "front_len": front,
+        "initial_state_len": min(T, C),
+        "attention_state_len": attn_state,
+        "updates": updates,
+        "final_state_len": current,
+        "final_coverage": coverage,
+    }
+
+
+# ---------------------------------------------------------------------------
+# Building blocks
+# ---------------------------------------------------------------------------
+
+
+def _ln(x: torch.Tensor, p: OracleParams) -> torch.Tensor:
+    return F.layer_norm(x, (x.size(-1),), p.ln_weight, p.ln_bias, p.ln_eps)
+
+
+def prep_k(k: torch.Tensor, p: OracleParams, rope_partial_dim: int) -> torch.Tensor:
+    """LN_s of the key with its first ``rope_partial_dim`` dims zeroed (kvm_mixer.py:120-129)."""
+    zeroed = torch.cat([torch.zeros_like(k[..., :rope_partial_dim]), k[..., rope_partial_dim:]], dim=-1)
+    return _ln(zeroed, p)
+
+
+def repeat_kv(x: torch.Tensor, group: int) -> torch.Tensor:
+    """GQA head expansion (value_residual_mixin.py:278-281)."""
+    return x if group == 1 else x.repeat_interleave(group, dim=1)
+
+
+def _temps(p: OracleParams, cfg: OracleConfig):
+    if cfg.use_head_temps:
+        return (
+            p.state_temp.view(1, cfg.q_heads, 1, 1),
+            p.front_temp.view(1, cfg.q_heads, 1, 1),
+        )
+    return 1.0, 1.0
+
+
+def state_values_for_attention(s_v, s_vlen, cfg: OracleConfig):
+    """Value rows the state contributes (kvm_mixer.py:205-208)."""
+    if cfg.use_vlens:
+        return (F.normalize(s_v.float(), dim=-1) * s_vlen).bfloat16()
+    return s_v / s_vlen
+
+
+def attend(q, bswa_k, bswa_v, s_k, s_v, s_vlen, p: OracleParams, cfg: OracleConfig):
+    """Softmax over [state slots ; window keys] with a lower-right causal mask.
+
+    kvm_mixer.py:194-229 (mask: :16-22).
+    """
+    g = cfg.group
+    s_k_norm = repeat_kv(_ln(s_k, p), g)
+    bk = repeat_kv(bswa_k, g)
+    s_v_att = repeat_kv(state_values_for_attention(s_v, s_vlen, cfg), g)
+    bv = repeat_kv(bswa_v, g)
+    st, ft = _temps(p, cfg)
+    k_star = torch.cat([s_k_norm * st, bk * ft], dim=2)
+    v_star = torch.cat([s_v_att, bv], dim=2)
+    q_len, kv_len = int(q.size(2)), int(k_star.size(2))
+    qi = torch.arange(q_len).unsqueeze(1)
+    ki = torch.arange(kv_len).unsqueeze(0)
+    mask = ki <= qi + (kv_len - q_len)
+    return F.scaled_dot_product_attention(q, k_star, v_star, attn_mask=mask, is_causal=False)
+
+
+def front_attention(q, k, v, p: OracleParams, cfg: OracleConfig):
+    """Causal attention over the first min(T, nC) tokens (kvm_mixer.py:419-432, 174-192)."""
+    _, ft = _temps(p, cfg)
+    g = cfg.group
+    return F.scaled_dot_product_attention(
+        q, repeat_kv(k, g) * ft, repeat_kv(v, g), is_causal=True
+    )
+
+
+def split_append_merge(k_block, n_append, k_ref):
+    """Pick the n_append least-similar tokens for appending (kvm_mixer.py:44-75)."""
+    B, H, L = int(k_block.size(0)), int(k_block.size(1)), int(k_block.size(2))
+    n_append = min(max(int(n_append), 0), L)
+    n_merge = L - n_append
+    all_idx = torch.arange(L, dtype=torch.long).view(1, 1, L).expand(B, H, L)
+    empty = all_idx[:, :, :0]
+    if L == 0:
+        return empty, empty
+    if n_append == 0:
+        return empty, all_idx
+    if n_merge == 0:
+        return all_idx, empty
+    if int(k_ref.size(2)) == 0:
+        return all_idx[:, :, n_merge:], all_idx[:, :, :n_merge]
+    scores = torch.matmul(k_block, k_ref.transpose(-1, -2)).float().max(dim=-1).values
+    order = torch.argsort(scores, dim=-1, descending=False)
+    app = torch.sort(order[..., :n_append], dim=-1).values
+    mrg = torch.sort(order[..., n_append:], dim=-1).values
+    return app, mrg
+
+
+def _gather(x, idx):
+    return x.gather(2, idx.unsqueeze(-1).expand(-1, -1, -1, int(x.size(-1))))
+
+
+def append_rows(s_k, s_v, s_vlen, k_new, v_new, cfg: OracleConfig):
+    """Append new slots (kvm_mixer.py:231-248)."""
+    if int(k_new.size(2)) == 0:
+        return s_k, s_v, s_vlen
+    if cfg.use_vlens:
+        vlen_new = torch.norm(v_new.float(), dim=-1, keepdim=True)
+    else:
+        vlen_new = torch.ones_like(v_new[..., :1])
+    return (
+        torch.cat([s_k, k_new], dim=2),
+        torch.cat([s_v, v_new], dim=2),
+        torch.cat([s_vlen, vlen_new], dim=2),
+    )
+
+
+def route_merge(k_merge, s_k_norm, protected: int, fp32_routing: bool):
+    """Slot index per merged token: first argmax over non-sink slots.
+
+    FP32 logits from the key-dtype operands (kvm_fp32_routing_reference.py:30-34);
+    the historical golden scores in the key dtype (kvm_mixer.py:326-328).
+    """
+    if fp32_routing:
+        logits = torch.matmul(k_merge.float(), s_k_norm.float().transpose(-1, -2))
+    else:
+        logits = torch.matmul(k_merge, s_k_norm.transpose(-1, -2))
+    logits[..., :protected] = float("-inf")
+    return logits.max(dim=-1, keepdim=True).indices
+
+
+def merge_into_state(k_merge, v_merge, s_k, s_v, s_vlen, protected, p, cfg: OracleConfig):
+    """Add each merged token into its routed slot (kvm_mixer.py:321-340; fp32 routing variant)."""
+    best = route_merge(k_merge, _ln(s_k, p), protected, cfg.fp32_routing)
+    onehot = torch.zeros(
+        (*k_merge.shape[:-1], int(s_k.size(2))), dtype=k_merge.dtype
+    ).scatter_(-1, best, torch.ones((), dtype=k_merge.dtype).expand_as(best))
+    s_k = s_k + onehot.mT @ k_merge
+    s_v = s_v + onehot.mT @ v_merge
+    if not cfg.use_vlens:
+        # Restated as written at kvm_mixer.py:337-338: the sum runs over the
+        # slot axis of the [.., n_merge, S] one-hot, i.e. one per merged token,
+        # and broadcasts onto [.., S, 1] (every slot gains 1 when n_merge == S;
+        # a shape error otherwise).  This is the reference's behaviour, not a
+        # per-slot count.
+        s_vlen = s_vlen + onehot.sum(-1, keepdim=True)
+    return s_k, s_v, s_vlen, best.squeeze(-1)
+
+
+def overflow_streams(overflow_k, overflow_v, gate, p: OracleParams, cfg: OracleConfig):
+    """Routing/merge/append streams of an overflow chunk (kvm_mixer.py:264-281)."""
+    k_plain = prep_k(overflow_k, p, cfg.rope_partial_dim)
+    v_plain = overflow_v
+    k_gated = k_plain * gate if cfg.gate_keys else k_plain
+    v_gated = v_plain * gate if cfg.gate_values else v_plain
+    if cfg.gate_appends:
+        k_app, v_app = k_gated, v_gated
+    else:
+        k_app, v_app = k_plain, v_plain
+    return k_plain, k_gated, v_gated, k_app, v_app
+
+
+def update_from_overflow(
+    s_k, s_v, s_vlen, overflow_k, overflow_v, gate, ctx_len, available,
+    p: OracleParams, cfg: OracleConfig, rec: Recorder | None = None,
+):
+    """One block-boundary memory update (kvm_mixer.py:250-319)."""
+    if int(overflow_k.size(2)) == 0:
+        return s_k, s_v, s_vlen
+    k_plain, k_gated, v_gated, k_app, v_app = overflow_streams(overflow_k, overflow_v, gate, p, cfg)
+    cur = int(s_k.size(2))
+    want = desired_state_len(cfg, ctx_len, available, cur)
+    L = int(k_plain.size(2))
+    n_app = min(max(want - cur, 0), L)
+    record = None
+    if rec is not None:
+        record = UpdateRecord(ctx_len, available, cur, n_app, None, None, None)
+        if rec.keep_states:
+            record.s_k_before, record.s_v_before, record.s_vlen_before = s_k, s_v, s_vlen
+        rec.updates.append(record)
+    if n_app > 0:
+        app_idx, mrg_idx = split_append_merge(k_plain, n_app, _ln(s_k, p))
+        k_merge, v_merge = _gather(k_gated, mrg_idx), _gather(v_gated, mrg_idx)
+        s_k, s_v, s_vlen = append_rows(
+            s_k, s_v, s_vlen, _gather(k_app, app_idx), _gather(v_app, app_idx), cfg
+        )
+    else:
+        B, H = int(k_plain.size(0)), int(k_plain.size(1))
+        app_idx = torch.zeros(B, H, 0, dtype=torch.long)
+        mrg_idx = torch.arange(L).view(1, 1, L).expand(B, H, L)
+        k_merge, v_merge = k_gated, v_gated
+    if record is not None:
+        record.append_idx, record.merge_idx = app_idx, mrg_idx
+    if int(k_merge.size(2)) == 0:
+        return s_k, s_v, s_vlen
+    cur = int(s_k.size(2))
+    protected = min(cfg.sink_len, cur)
+    if cur <= protected:
+        raise AssertionError("KVM state update requires at least one non-sink slot before merging.")
+    s_k, s_v, s_vlen, route = merge_into_state(k_merge, v_merge, s_k, s_v, s_vlen, protected, p, cfg)
+    if record is not None:
+        record.route = route
+    return s_k, s_v, s_vlen
+
+
+# ---------------------------------------------------------------------------
+# Prefill and decode
+# ---------------------------------------------------------------------------
+
+
+def initial_state(k, v, gate, L0, p: OracleParams, cfg: OracleConfig):
+    """State from the first chunk (kvm_mixer.py:434-447)."""
+    s_k = prep_k(k[..., :L0, :], p, cfg.rope_partial_dim)
+    s_v = v[..., :L0, :]
+    if cfg.gate_initial:
+        s_k = s_k * gate[..., :L0, :]
+        s_v = s_v * gate[..., :L0, :]
+    if cfg.use_vlens:
+        s_vlen = torch.norm(v[..., :L0, :].float(), dim=-1, keepdim=True)
+    else:
+        s_vlen = torch.ones_like(v[..., :L0, :1])
+    return s_k, s_v, s_vlen
+
+
+def prefill(q, k, v, gate, p: OracleParams, cfg: OracleConfig, rec: Recorder | None = None):
+    """Prefill at the post-QKV boundary (kvm_mixer.py:403-516).
+
+    Returns (y [B,Hq,T,Dv] before c_proj, carried-state dict).
+    """
+    T = int(q.size(2))
+    C, n = cfg.chunk_len, cfg.n_bswa_chunks
+    front = min(T, n * C)
+    outs = [front_attention(q[:, :, :front], k[:, :, :front], v[:, :, :front], p, cfg)]
+    L0 = min(T, C)
+    s_k, s_v, s_vlen = initial_state(k, v, gate, L0, p, cfg)
+    coverage = L0
+    for qb in range(front, T, C):
+        qe = min(T, qb + C)
+        begin = bswa_begin_for_total_len(qe, C, n)
+        if begin != coverage:
+            raise AssertionError("KVM prefill state coverage drifted from the active BSWA window.")
+        outs.append(attend(q[:, :, qb:qe], k[:, :, begin:qe], v[:, :, begin:qe], s_k, s_v, s_vlen, p, cfg))
+        nxt = bswa_begin_for_total_len(min(T, qe + C), C, n)
+        if nxt > begin:
+            s_k, s_v, s_vlen = update_from_overflow(
+                s_k, s_v, s_vlen, k[:, :, begin:nxt], v[:, :, begin:nxt], gate[:, :, begin:nxt],
+                qe, nxt, p, cfg, rec,
+            )
+            coverage = nxt
+    y = torch.cat(outs, dim=-2)
+    begin = bswa_begin_for_total_len(T, C, n)
+    if coverage != max(L0, begin):
+        raise AssertionError("KVM prefill state progression drifted from the decode-state bookkeeping.")
+    state = {
+        S_K: s_k, S_V: s_v, S_VLEN: s_vlen, COVERAGE: coverage, BSWA_BEGIN: begin,
+        BSWA_K: k[:, :, begin:], BSWA_V: v[:, :, begin:], BSWA_GATE: gate[:, :, begin:],
+    }
+    return y, state
+
+
+def decode_step(state, total_len, q, k, v, gate, p: OracleParams, cfg: OracleConfig, rec: Recorder | None = None):
+    """One cached single-token decode step (kvm_mixer.py:572-713).
+
+    ``total_len`` is the number of tokens already seen.  Returns
+    (y [B,Hq,1,Dv] before c_proj, new state dict).
+    """
+    if int(q.size(2)) != 1:
+        raise AssertionError("KVM cached decode expects single-token inputs.")
+    C, n = cfg.chunk_len, cfg.n_bswa_chunks
+    s_k, s_v, s_vlen = state[S_K], state[S_V], state[S_VLEN]
+    old_begin = int(state[BSWA_BEGIN])
+    coverage = int(state[COVERAGE])
+    full_k = torch.cat([state[BSWA_K], k], dim=2)
+    full_v = torch.cat([state[BSWA_V], v], dim=2)
+    full_g = torch.cat([state[BSWA_GATE], gate], dim=2)
+    new_total = total_len + 1
+    direct_target = min(new_total, C)
+    new_begin = bswa_begin_for_total_len(new_total, C, n)
+    new_coverage = max(direct_target, new_begin)
+    if coverage < direct_target:
+        lo, hi = max(coverage - old_begin, 0), max(direct_target - old_begin, 0)
+        s_k, s_v, s_vlen = append_rows(
+            s_k, s_v, s_vlen, prep_k(full_k[:, :, lo:hi], p, cfg.rope_partial_dim), full_v[:, :, lo:hi], cfg
+        )
+        coverage = direct_target
+    if coverage > new_coverage:
+        raise AssertionError("KVM cache state coverage cannot shrink during decoding.")
+    if coverage < new_coverage:
+        lo, hi = max(coverage - old_begin, 0), max(new_coverage - old_begin, 0)
+        if hi - lo != C:
+            raise AssertionError("KVM decode can only materialize one overflow BSWA chunk per step.")
+        s_k, s_v, s_vlen = update_from_overflow(
+            s_k, s_v, s_vlen, full_k[:, :, lo:hi], full_v[:, :, lo:hi], full_g[:, :, lo:hi],
+            n * C + coverage, coverage + C, p, cfg, rec,
+        )
+        coverage = new_coverage
+    lo, hi = max(new_begin - old_begin, 0), max(new_total - old_begin, 0)
+    bk, bv, bg = full_k[:, :, lo:hi], full_v[:, :, lo:hi], full_g[:, :, lo:hi]
+    active = int(s_k.size(2)) if new_begin > 0 else 0
+    out = attend(q, bk, bv, s_k[:, :, :active], s_v[:, :, :active], s_vlen[:, :, :active], p, cfg)
+    new_state = {
+        S_K: s_k, S_V: s_v, S_VLEN: s_vlen, COVERAGE: coverage, BSWA_BEGIN: new_begin,
+        BSWA_K: bk, BSWA_V: bv, BSWA_GATE: bg,
+    }
+    return out, new_state
+
+
+# ---------------------------------------------------------------------------
+# Exact (fp64) helpers for near-tie classification and brute-force checks
+# ---------------------------------------------------------------------------
+
+
+def exact_logits(k_merge: torch.Tensor, s_k_norm: torch.Tensor) -> torch.Tensor:
+    """fp64 logits of bf16/fp32 operands (exact for bf16 x bf16 with D <= 2^20)."""
+    return torch.matmul(k_merge.double(), s_k_norm.double().transpose(-1, -2))
+
+
+def fp32_dot_error_bound(k_merge: torch.Tensor, s_k_norm: torch.Tensor) -> torch.Tensor:
+    """Worst-case |fl32(a.b) - a.b| for a recursive fp32 sum, per (token, slot).
+
+    gamma_D * sum_d |a_d b_d| with gamma_D = D u / (1 - D u), u = 2^-24.
+    """
+    D = int(k_merge.size(-1))
+    u = 2.0 ** -24
+    gamma = D * u / (1.0 - D * u)
+    return gamma * torch.matmul(k_merge.double().abs(), s_k_norm.double().abs().transpose(-1, -2))
+
+
+def brute_force_attention(q, keys, values, mask):
+    """fp64 softmax attention, scale 1/sqrt(D)."""
+    qd, kd, vd = q.double(), keys.double(), values.double()
+    s = torch.matmul(qd, kd.transpose(-1, -2)) / math.sqrt(int(q.size(-1)))
+    s = s.masked_fill(~mask, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vd)
