@@ -1,0 +1,286 @@
+"""Benchmark of the MI355X KVM forward path (one GPU).
+
+Workloads:
+  prefill  config 2: one KVM layer, B1 Hq=Hkv=32 D128, T=32768, chunk 512,
+           n_bswa 2, fixed memory (state_min_len 256; the first chunk fills
+           the state, so 512 slots are live), q/k/v ~ N(0,1)/sqrt(128),
+           gate 1+elu(N(0,1)), bf16, fp32 routing/accumulation.
+           A step = one prefill at the post-QKV boundary (q/k/v/gate
+           resident in HBM -> [B, T, Hq*D] output + final state).
+  decode   config 4: B64 Hq=Hkv=32 D128, chunk 256, n_bswa 2 (512-token
+           window), 1024 memory slots at total length 131072; a step =
+           one token for all 64 sequences (ring write, the state update when
+           a chunk boundary is crossed, split-K attention).  The timed
+           region is `--decode-steps` consecutive tokens from a fresh
+           snapshot, so the one update per 256 tokens is included.
+
+Prints ONE JSON line: value = prefill tokens/s; the decode figures are in
+the "decode" object.  roofline: achieved algorithmic FLOP/s (prefill
+attention kernel, bf16 MFMA) and bytes/s (decode attention), both timed with
+HIP events on the launch stream.  cpu_baseline: the CPU oracle (an eager
+restatement of the reference, pinned to it by golden fixtures) on a bounded
+sample of the prefill workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+from types import SimpleNamespace
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "kvm-paper_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_BF16_FLOPS = 2.5e15   # MI355X dense bf16 MFMA
+PEAK_HBM_BYTES = 8.0e12    # MI355X HBM3E
+
+
+def _config(Hq, Hkv, D, C, n_bswa, min_len, n_max):
+    return SimpleNamespace(
+        num_attention_heads=Hq, num_key_value_heads=Hkv, hidden_size=Hq * D, d_qk_head=D, d_v_head=D,
+        d_head=None, num_hidden_layers=1, mup_base_dim=Hq * D, use_tokenshift_att=0, use_value_residual=0,
+        kvm_value_residual_mode="rwkv", kvm_token_shift_mode="rwkv", rope_partial_dim=64, sink_len=1,
+        chunk_len=C, n_max_d_chunks=n_max, n_bswa_chunks=n_bswa, state_budget_mode="fixed",
+        state_growth_factor=1.0, state_growth_exponent=0.5, state_round_down=1, state_min_len=min_len,
+        state_saturation_n=None, kvm_use_merge_gate_keys=1, kvm_use_merge_gate_values=1,
+        kvm_apply_merge_gate_to_appends=0, kvm_apply_merge_gate_to_initial_state=0, kvm_use_head_temps=1,
+        kvm_use_vlens=1, kvm_aotriton_forward_attention=0,
+    )
+
+
+def attention_pairs(plan, n_bswa):
+    """Sum over queries of visible keys (state slots + window, causal)."""
+    C, T = plan.chunk_len, plan.seq_len
+    total = 0
+    for m in range(plan.n_chunks):
+        qb, qe = m * C, min(T, (m + 1) * C)
+        S = plan.chunk_state_len[m]
+        wb = max(0, (m - n_bswa + 1) * C)
+        L = qe - qb
+        # query t sees S + (t - wb + 1) keys
+        total += L * S + sum(t - wb + 1 for t in (qb, qe - 1)) * L // 2
+    return total
+
+
+def routing_pairs(plan):
+    return sum(plan.chunk_len * (b + a) for b, a in zip(plan.upd_state_before, plan.upd_n_append))
+
+
+def bench_prefill(args, torch, kvm_amd):
+    B, H, D, T, C = 1, 32, 128, 32768, 512
+    cfg = _config(H, H, D, C, 2, 256, 1)
+    dev = torch.device("cuda:0")
+    mixer = kvm_amd.SequenceMixer(cfg, 0).to(dev, torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, H, T, D, generator=gen, device=dev, dtype=torch.float32).div_(math.sqrt(D)).bfloat16()
+    k = torch.randn(B, H, T, D, generator=gen, device=dev, dtype=torch.float32).div_(math.sqrt(D)).bfloat16()
+    v = torch.randn(B, H, T, D, generator=gen, device=dev, dtype=torch.float32).div_(math.sqrt(D)).bfloat16()
+    g = (1 + torch.nn.functional.elu(torch.randn(B, H, T, 1, generator=gen, device=dev))).bfloat16()
+    plan = mixer.make_plan(T)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            mixer.prefill_raw(q, k, v, g, plan=plan)
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+        for e in evs:
+            for x in e:
+                x.record()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(args.steps):
+            mixer.prefill_raw(q, k, v, g, plan=plan, events=evs[i])
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    attn_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+    chain_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    attn_flop = 4 * D * H * B * attention_pairs(plan, 2)
+    route_flop = 2 * D * H * B * routing_pairs(plan)
+    return dict(
+        ms=ms, wall_ms=wall * 1e3 / args.steps, tok_s=B * T / (ms * 1e-3), attn_ms=attn_ms, chain_ms=chain_ms,
+        attn_flop=attn_flop, route_flop=route_flop, plan=plan, inputs=(q, k, v, g), mixer=mixer,
+    )
+
+
+def bench_decode(args, torch, kvm_amd):
+    B, H, D, C, n = 64, 32, 128, 256, 2
+    S, total = 1024, 131072
+    W = n * C
+    cfg = _config(H, H, D, C, n, S, 4)
+    dev = torch.device("cuda:0")
+    mixer = kvm_amd.SequenceMixer(cfg, 0).to(dev, torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    cnt = torch.randint(1, 4097, (B, H, S, 1), generator=gen, device=dev).float()
+    mean_k = torch.randn(B, H, S, D, generator=gen, device=dev) * math.sqrt(0.5)
+    mean_v = torch.randn(B, H, S, D, generator=gen, device=dev) * math.sqrt(0.5)
+    begin = max(0, (total + C - 1) // C * C - W)
+    R = total - begin
+    snap = kvm_amd.DecodeCacheSnapshot(
+        state_k=(mean_k * cnt).bfloat16(), state_v=(mean_v * cnt).bfloat16(),
+        state_vlen=mean_v.norm(dim=-1, keepdim=True),
+        recent_k=(torch.randn(B, H, R, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16(),
+        recent_v=(torch.randn(B, H, R, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16(),
+        recent_gate=(1 + torch.nn.functional.elu(torch.randn(B, H, R, 1, generator=gen, device=dev))).bfloat16(),
+        total_len=total, state_coverage_len=max(min(total, C), begin), recent_begin=begin,
+    )
+    steps = args.decode_steps
+    qs = (torch.randn(steps, B, H, 1, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16()
+    ks = (torch.randn(steps, B, H, 1, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16()
+    vs = (torch.randn(steps, B, H, 1, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16()
+    gs = (1 + torch.nn.functional.elu(torch.randn(steps, B, H, 1, 1, generator=gen, device=dev))).bfloat16()
+    cache = mixer.make_decode_cache(snap, state_capacity=S)
+
+    def run(timed):
+        cache.reset_(snap)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        ea = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i in range(steps):
+            ev[i][0].record()
+            mixer._decode_advance(ks[i], vs[i], gs[i], cache)
+            ea[i][0].record()
+            mixer._decode_attention(qs[i], cache)
+            ea[i][1].record()
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        return ev, ea
+
+    with torch.no_grad():
+        for _ in range(max(1, args.warmup)):
+            run(False)
+        ev, ea = run(True)
+    step_ms = [a.elapsed_time(b) for a, b in ev]
+    attn_ms = [a.elapsed_time(b) for a, b in ea]
+    total_ms = sum(step_ms)
+    rows = B * H
+    # Algorithmic bytes per attention launch: each key and value row read once.
+    active = S
+    bytes_per = []
+    for i in range(steps):
+        t = total + 1 + i
+        rb = max(0, (t + C - 1) // C * C - W)
+        bytes_per.append(rows * (active + (t - rb)) * (2 * D) * 2 + 2 * rows * D * 2)
+    return dict(
+        ms_per_step=total_ms / steps, tok_s=B * steps / (total_ms * 1e-3), attn_ms=sum(attn_ms) / steps,
+        bytes=sum(bytes_per) / steps, update_step_ms=step_ms[0], other_step_ms=sum(step_ms[1:]) / max(steps - 1, 1),
+        steps=steps,
+    )
+
+
+def cpu_baseline(torch, sample_T):
+    """The CPU oracle (eager restatement of model/kvm_mixer.py with fp32
+    routing) on the first sample_T tokens of the prefill workload."""
+    from oracle import kvm_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, int(os.environ.get("KVM_CPU_THREADS", "16")))
+    torch.set_num_threads(threads)
+    B, H, D, C = 1, 32, 128, 512
+    gen = torch.Generator().manual_seed(0)
+    q = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
+    k = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
+    v = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
+    g = (1 + torch.nn.functional.elu(torch.randn(B, H, sample_T, 1, generator=gen))).bfloat16()
+    cfg = O.OracleConfig(q_heads=H, kv_heads=H, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=2,
+                         sink_len=1, rope_partial_dim=64, state_min_len=256)
+    p = O.OracleParams(ln_weight=torch.ones(D).bfloat16(), ln_bias=torch.zeros(D).bfloat16(),
+                       front_temp=torch.ones(H).bfloat16(), state_temp=torch.ones(H).bfloat16())
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        O.prefill(q, k, v, g, p, cfg)
+        times.append(time.perf_counter() - t0)
+    sec = min(times)
+    return dict(value=B * sample_T / sec, unit="tokens/s", cores=threads, kind="port",
+                sample=f"oracle prefill of the first {sample_T} tokens of the config-2 layer "
+                       f"(B1 H32 D128 C512, 512 slots), best of 2 runs, {sec:.2f} s each")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--cpu-sample", type=int, default=4096)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import kvm_amd
+
+    kvm_amd.load_library()
+    print("bench: prefill config 2 ...", file=sys.stderr, flush=True)
+    pf = bench_prefill(args, torch, kvm_amd)
+    print(f"bench: prefill {pf['ms']:.3f} ms/step (attention {pf['attn_ms']:.3f} ms, updates {pf['chain_ms']:.3f} ms)",
+          file=sys.stderr, flush=True)
+    dec = None
+    if not args.skip_decode:
+        print("bench: decode config 4 ...", file=sys.stderr, flush=True)
+        dec = bench_decode(args, torch, kvm_amd)
+        print(f"bench: decode {dec['ms_per_step']:.3f} ms/token-step (attention {dec['attn_ms']:.3f} ms)",
+              file=sys.stderr, flush=True)
+    cpu = None
+    if not args.skip_cpu:
+        print("bench: cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, args.cpu_sample)
+    attn_achieved = pf["attn_flop"] / (pf["attn_ms"] * 1e-3)
+    line = {
+        "metric": "KVM prefill tokens/s @32K and decode tokens/s @128K; % MFMA/HBM roofline",
+        "value": round(pf["tok_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pf["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian q/k/v, 1+elu gates; random-init layer parameters)",
+        "config": {"workload": "config 2: KVM layer prefill B1 H32 D128 T32768 C512 fixed memory (512 live slots)",
+                   "global_batch": 1, "seq_len": 32768, "parallelism": "none (1 GPU)"},
+        "prefill": {
+            "ms_per_step": round(pf["ms"], 4), "attention_ms": round(pf["attn_ms"], 4),
+            "update_chain_ms": round(pf["chain_ms"], 4), "algorithmic_flop": pf["attn_flop"] + pf["route_flop"],
+            "attention_flop": pf["attn_flop"], "routing_flop": pf["route_flop"],
+            "whole_path_frac_of_mfma_peak": round((pf["attn_flop"] + pf["route_flop"]) / (pf["ms"] * 1e-3) / PEAK_BF16_FLOPS, 4),
+        },
+        "roofline": {
+            "bound": "mfma", "kernel": "k_attn_prefill", "achieved": round(attn_achieved / 1e12, 2),
+            "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s", "frac": round(attn_achieved / PEAK_BF16_FLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if dec is not None:
+        bw = dec["bytes"] / (dec["attn_ms"] * 1e-3)
+        line["decode"] = {
+            "workload": "config 4: B64 H32 D128, 1024 slots + 512-token window at 128K context, "
+                        f"{dec['steps']} tokens from a fresh snapshot (one state update included)",
+            "value": round(dec["tok_s"], 1), "unit": "tokens/s", "ms_per_step": round(dec["ms_per_step"], 4),
+            "attention_ms": round(dec["attn_ms"], 4), "update_step_ms": round(dec["update_step_ms"], 4),
+            "other_step_ms": round(dec["other_step_ms"], 4),
+            "roofline": {"bound": "hbm", "kernel": "k_decode_partial+k_decode_combine",
+                         "achieved": round(bw / 1e9, 1), "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s",
+                         "frac": round(bw / PEAK_HBM_BYTES, 4), "traffic": None},
+        }
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

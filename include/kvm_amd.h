@@ -1,0 +1,225 @@
+/*
+ * kvm_amd.h - C ABI of the MI355X (gfx950) Key-Value Means forward path.
+ *
+ * The library (libkvm_amd.so, built from kvm-paper_amd/csrc) implements the
+ * forward path of the KVM token mixer at the post-QKV boundary: prefill
+ * (block-sliding-window attention plus attention over compressed memory
+ * slots), the block-boundary memory update (routing, append, merge) and
+ * single-token decode.  Every entry point takes plain device pointers,
+ * element strides and sizes; nothing here names a torch type.  All work is
+ * enqueued on the caller's HIP stream (`stream`, a hipStream_t; NULL is the
+ * legacy default stream) and no entry point synchronises the device or
+ * allocates device memory: scratch space is passed in as `workspace`, sized
+ * by the matching *_workspace_bytes() query.
+ *
+ * Tensors
+ *   bf16 tensors are stored as raw 16-bit bfloat16; the last (feature) axis
+ *   is always contiguous and every other axis is described by an element
+ *   stride.  "rows" are (batch, kv_head) pairs, row = b * kv_heads + h.
+ *   State tensors are dense [rows, capacity, dim] (bf16) and
+ *   [rows, capacity] (fp32 vlen), the layout of the reference decode cache
+ *   (model/kvm_triton_decode.py:73-105).
+ *
+ * Errors
+ *   Entry points return KVM_OK (0) or a negative code; kvm_last_error()
+ *   returns a thread-local message describing the last failure.
+ *   KVM_EINVAL marks an argument the reference would reject with ValueError
+ *   or AssertionError, KVM_EHIP a HIP runtime failure, KVM_ESPACE a
+ *   workspace or capacity that is too small (RuntimeError in the reference,
+ *   model/kvm_triton_decode.py:207-211).
+ *
+ * Numeric contract (the reference's Triton path, model/kvm_triton_mixer.py:199-211,
+ * evaluated against the eager golden model/kvm_mixer.py with the FP32
+ * routing of model/kvm_fp32_routing_reference.py:24-49):
+ *   - routing keys  prep(k) = LayerNorm_s(k with dims < rope_partial_dim
+ *     zeroed), rounded to bf16; gated streams bf16(prep(k) * g), bf16(v * g);
+ *   - append novelty scores bf16-rounded dot products, lowest first, ties to
+ *     the lower token index;
+ *   - merge routing fp32 dot products of bf16 operands, first maximum wins,
+ *     the first sink_len slots never receive merges;
+ *   - merge sums accumulated in fp32 in token order (deterministic), then
+ *     state = bf16(state + bf16(sum)) as the eager bf16 arithmetic does;
+ *   - attention keys bf16(key * temperature), fp32 scores and softmax,
+ *     probabilities rounded to bf16 for the PV product, fp32 accumulation.
+ */
+#ifndef KVM_AMD_H
+#define KVM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVM_ABI_VERSION 1
+
+#define KVM_OK 0
+#define KVM_EINVAL (-1)
+#define KVM_EHIP (-2)
+#define KVM_ESPACE (-3)
+
+/* Static description of one KVM layer (the mixer attributes the forward
+ * path reads: model/kvm_mixer.py:79-118, model/rwkv7_backbone.py:319-373).
+ * All fields are 8 bytes wide so the struct has no padding. */
+typedef struct kvm_layer {
+  int64_t batch;
+  int64_t q_heads;          /* num_attention_heads */
+  int64_t kv_heads;         /* num_key_value_heads (q_heads % kv_heads == 0) */
+  int64_t head_dim;         /* d_qk_head: 64 or 128 */
+  int64_t value_dim;        /* d_v_head: must equal head_dim */
+  int64_t chunk_len;        /* C: 1..4096 */
+  int64_t n_bswa_chunks;    /* n: window = n * C tokens */
+  int64_t sink_len;         /* slots never merged into */
+  int64_t rope_partial_dim; /* dims zeroed before LayerNorm_s (already mapped from <=0 to head_dim) */
+  int64_t gate_keys;        /* kvm_use_merge_gate_keys */
+  int64_t gate_values;      /* kvm_use_merge_gate_values */
+  int64_t gate_appends;     /* kvm_apply_merge_gate_to_appends */
+  int64_t gate_initial;     /* kvm_apply_merge_gate_to_initial_state */
+  double ln_eps;            /* ln_s_k.eps */
+  const void *ln_weight;    /* fp32 [head_dim] (ln_s_k.weight) */
+  const void *ln_bias;      /* fp32 [head_dim] (ln_s_k.bias) */
+  const void *state_temp;   /* fp32 [q_heads] (state_head_temp, ones when disabled) */
+  const void *front_temp;   /* fp32 [q_heads] (front_head_temp, ones when disabled) */
+} kvm_layer;
+
+/* A token source: keys, values and merge gates of every (batch, kv_head).
+ * Element (b, h, t, :) of k lives at k + b*k_sb + h*k_sh + t*k_st.  When
+ * ring > 0 the token index is taken modulo ring (the decode window ring). */
+typedef struct kvm_seq {
+  const void *k;            /* bf16 [B, Hkv, *, head_dim] */
+  const void *v;            /* bf16 [B, Hkv, *, value_dim] */
+  const void *gate;         /* bf16 [B, Hkv, *, 1] */
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t g_sb, g_sh, g_st;
+  int64_t ring;
+} kvm_seq;
+
+/* Carried memory state (model/kvm_triton_decode.py:73-105):
+ * s_k, s_v         bf16 [rows, capacity, dim] running key / value sums
+ * s_vlen           fp32 [rows, capacity]      value norms (kvm_use_vlens=1)
+ * s_k_attn         bf16 [rows, capacity, dim] LayerNorm_s(s_k)
+ * s_v_attn         bf16 [rows, capacity, dim] bf16(normalize(s_v) * s_vlen) */
+typedef struct kvm_state {
+  void *s_k;
+  void *s_v;
+  void *s_vlen;
+  void *s_k_attn;
+  void *s_v_attn;
+  int64_t capacity;
+} kvm_state;
+
+/* One prefill (model/kvm_triton_mixer.py:560-666 forward_prefill, eager
+ * semantics model/kvm_mixer.py:403-516).  The schedule arrays are HOST
+ * int32 arrays computed by the caller from the state budget
+ * (model/kernels/kvm_triton_training_kernels.py:85-171). */
+typedef struct kvm_prefill_desc {
+  kvm_layer layer;
+  const void *q;                 /* bf16 [B, Hq, T, head_dim] */
+  int64_t q_sb, q_sh, q_st;
+  kvm_seq kv;                    /* k, v, gate of the prompt (ring = 0) */
+  int64_t seq_len;               /* T */
+  void *out;                     /* bf16 out[b, t, hq, :] at out + b*o_sb + t*o_st + hq*o_sh */
+  int64_t o_sb, o_st, o_sh;
+  kvm_state state;               /* receives the final state; capacity >= final length */
+  int64_t n_chunks;              /* ceil(T / C) */
+  const int32_t *chunk_state_len;/* host [n_chunks]: memory slots visible to query chunk m */
+  const int32_t *chunk_snapshot; /* host [n_chunks]: updates applied before chunk m */
+  int64_t n_updates;
+  const int32_t *upd_token_begin;/* host [n_updates]: first token of the overflow chunk */
+  const int32_t *upd_state_before;/* host [n_updates] */
+  const int32_t *upd_n_append;   /* host [n_updates] */
+  int64_t max_state_len;         /* largest state length reached (snapshot row count) */
+  int64_t snapshot_ring;         /* snapshots kept in the workspace (>= 2) */
+  void *workspace;
+  int64_t workspace_bytes;
+  int32_t *route_log;            /* optional device int32 [n_updates, rows, C]: slot per overflow token */
+  int32_t *append_log;           /* optional device int32 [n_updates, rows, C]: 1 if appended */
+  void *const *events;           /* optional hipEvent_t[4] recorded on `stream`: before the first
+                                    and after the last memory update, before the first and
+                                    after the last attention launch (for timing) */
+} kvm_prefill_desc;
+
+/* ABI self-description, checked by the host binding at load time. */
+int kvm_abi_version(void);
+int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc */
+const char *kvm_last_error(void);
+
+/* Workspace of kvm_prefill for the given descriptor (snapshot_ring and
+ * max_state_len set). */
+int64_t kvm_prefill_workspace_bytes(const kvm_prefill_desc *d);
+
+/* Whole prefill: initial state from the first chunk, every block-boundary
+ * update of the schedule, and the attention of every query chunk.
+ * Replaces build_prefill_forward (model/kernels/kvm_triton_training_kernels.py:3386-3619)
+ * as called from model/kvm_triton_mixer.py:470-536. */
+int kvm_prefill(const kvm_prefill_desc *d, void *stream);
+
+/* Write prep(k) (gated when layer->gate_initial), v (gated likewise) and
+ * |v| of tokens [tok_begin, tok_begin + n_tok) of src into memory slots
+ * [slot_begin, slot_begin + n_tok), with their attention rows.  The initial
+ * state of a prefill (model/kvm_mixer.py:434-447) and the decode-time
+ * direct-state append (model/kvm_triton_mixer.py:866-900). */
+int kvm_state_append_direct(const kvm_layer *layer, const kvm_seq *src,
+                            int64_t tok_begin, int64_t n_tok,
+                            const kvm_state *st, int64_t slot_begin,
+                            void *stream);
+
+/* Recompute s_k_attn / s_v_attn of slots [slot_begin, slot_begin + n_slots)
+ * from s_k, s_v, s_vlen (model/kvm_triton_decode.py:264-291 reset_). */
+int kvm_state_refresh(const kvm_layer *layer, const kvm_state *st,
+                      int64_t slot_begin, int64_t n_slots, void *stream);
+
+/* Scratch of one kvm_state_update over n_tok overflow tokens.  Its first
+ * three arrays hold, after the call, the streams of the overflow tokens
+ * (bf16 [rows, n_tok, head_dim] each, at byte offsets 0, A and 2A with
+ * A = rows * n_tok * head_dim * 2 rounded up to a multiple of 256):
+ * prep(k), the merge key and the merge value. */
+int64_t kvm_update_workspace_bytes(const kvm_layer *layer, int64_t n_tok);
+
+/* One block-boundary memory update from overflow tokens
+ * [tok_begin, tok_begin + n_tok) of src: append the n_append least novel
+ * tokens, route the rest to their most similar non-sink slot and add them
+ * in.  state_before is the current state length.  The attention rows of the
+ * updated state are written to (attn_k_out, attn_v_out), which may alias
+ * st->s_k_attn / st->s_v_attn; routing reads st->s_k_attn.
+ * route_out / append_out (optional, device int32 [rows, n_tok]) receive the
+ * slot of every token and whether it was appended.
+ * Replaces run_forward_state_update (model/kernels/kvm_triton_training_kernels.py:1530-1800);
+ * eager model/kvm_mixer.py:250-340 with model/kvm_fp32_routing_reference.py:24-49. */
+int kvm_state_update(const kvm_layer *layer, const kvm_seq *src,
+                     int64_t tok_begin, int64_t n_tok, int64_t state_before,
+                     int64_t n_append, const kvm_state *st, void *attn_k_out,
+                     void *attn_v_out, void *workspace, int64_t workspace_bytes,
+                     int32_t *route_out, int32_t *append_out, void *stream);
+
+/* Write one token (src token 0) into slot `pos` of the window ring
+ * ring_k/ring_v [rows, ring_cap, dim], ring_gate [rows, ring_cap].
+ * Replaces write_recent_ring (model/kernels/kvm_triton_decode.py:18-70, 287-322). */
+int kvm_ring_write(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
+                   void *ring_v, void *ring_gate, int64_t ring_cap,
+                   int64_t pos, void *stream);
+
+/* Scratch of kvm_decode_attention for a window of up to max_rows
+ * (state + ring) key rows. */
+int64_t kvm_decode_workspace_bytes(const kvm_layer *layer, int64_t max_rows);
+
+/* Single-token attention over active_state_len memory slots and recent_len
+ * window rows stored in the ring from ring_start (modulo ring_cap).
+ * q: bf16 [B, Hq, 1, head_dim] at q + b*q_sb + h*q_sh;
+ * out: bf16 [B, Hq, value_dim] at out + b*o_sb + h*o_sh.
+ * Split over key rows, combined deterministically.
+ * Replaces kvm_decode_attention (model/kernels/kvm_triton_decode.py:175-284, 409-467). */
+int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
+                         int64_t q_sh, const kvm_state *st,
+                         int64_t active_state_len, const void *ring_k,
+                         const void *ring_v, int64_t ring_cap,
+                         int64_t ring_start, int64_t recent_len, void *out,
+                         int64_t o_sb, int64_t o_sh, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVM_AMD_H */

@@ -1,0 +1,449 @@
+// extern "C" entry points of libkvm_amd.so (declared in include/kvm_amd.h):
+// argument validation, workspace layout and the prefill launch schedule.
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <string>
+
+#include "kvm_internal.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(KVM_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define KVM_HIP(expr, what)                     \
+  do {                                          \
+    hipError_t e_ = (expr);                     \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+int check_layer(const kvm_layer *L) {
+  if (!L) return fail(KVM_EINVAL, "layer descriptor is NULL");
+  if (L->batch < 1 || L->q_heads < 1 || L->kv_heads < 1)
+    return fail(KVM_EINVAL, "batch and head counts must be positive");
+  if (L->q_heads % L->kv_heads)
+    return fail(KVM_EINVAL, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
+                (long long)L->q_heads, (long long)L->kv_heads);
+  if (L->head_dim != 64 && L->head_dim != 128)
+    return fail(KVM_EINVAL, "head_dim must be 64 or 128, got %lld",
+                (long long)L->head_dim);
+  if (L->value_dim != L->head_dim)
+    return fail(KVM_EINVAL, "value_dim must equal head_dim");
+  if (L->chunk_len < 1 || L->chunk_len > 4096)
+    return fail(KVM_EINVAL, "chunk_len must be in [1, 4096], got %lld",
+                (long long)L->chunk_len);
+  if (L->n_bswa_chunks < 1) return fail(KVM_EINVAL, "n_bswa_chunks must be >= 1");
+  if (L->sink_len < 0) return fail(KVM_EINVAL, "sink_len must be >= 0");
+  if (L->rope_partial_dim < 0 || L->rope_partial_dim > L->head_dim)
+    return fail(KVM_EINVAL, "rope_partial_dim must be in [0, head_dim]");
+  if (!L->ln_weight || !L->ln_bias || !L->state_temp || !L->front_temp)
+    return fail(KVM_EINVAL, "layer parameter pointers must be set");
+  if (!(L->ln_eps > 0.0)) return fail(KVM_EINVAL, "ln_eps must be positive");
+  return KVM_OK;
+}
+
+int check_seq(const kvm_seq *s, const char *what) {
+  if (!s || !s->k || !s->v || !s->gate)
+    return fail(KVM_EINVAL, "%s: k, v and gate pointers must be set", what);
+  if (!aligned16(s->k) || !aligned16(s->v))
+    return fail(KVM_EINVAL, "%s: k and v must be 16-byte aligned", what);
+  const int64_t st[6] = {s->k_sb, s->k_sh, s->k_st, s->v_sb, s->v_sh, s->v_st};
+  for (int i = 0; i < 6; ++i)
+    if (st[i] % 8)
+      return fail(KVM_EINVAL, "%s: k/v strides must be multiples of 8 elements", what);
+  if (s->ring < 0) return fail(KVM_EINVAL, "%s: ring must be >= 0", what);
+  return KVM_OK;
+}
+
+int check_state(const kvm_state *st, bool need_attn) {
+  if (!st || !st->s_k || !st->s_v || !st->s_vlen)
+    return fail(KVM_EINVAL, "state: s_k, s_v and s_vlen must be set");
+  if (need_attn && (!st->s_k_attn || !st->s_v_attn))
+    return fail(KVM_EINVAL, "state: s_k_attn and s_v_attn must be set");
+  if (!aligned16(st->s_k) || !aligned16(st->s_v) ||
+      (st->s_k_attn && !aligned16(st->s_k_attn)) ||
+      (st->s_v_attn && !aligned16(st->s_v_attn)))
+    return fail(KVM_EINVAL, "state tensors must be 16-byte aligned");
+  if (st->capacity < 1) return fail(KVM_EINVAL, "state capacity must be positive");
+  return KVM_OK;
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct PrefillLayout {
+  size_t update_bytes;
+  size_t snap_elems;  // elements of one snapshot array (keys or values)
+  size_t total;
+};
+
+PrefillLayout prefill_layout(const kvm_prefill_desc *d) {
+  PrefillLayout p;
+  const kvm_layer &L = d->layer;
+  p.update_bytes = align256(size_t(kvm::update_scratch_bytes(L, L.chunk_len)));
+  p.snap_elems = size_t(L.batch * L.kv_heads) * size_t(d->max_state_len) *
+                 size_t(L.head_dim);
+  p.total = p.update_bytes +
+            2 * size_t(d->snapshot_ring) * align256(p.snap_elems * 2);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvm_abi_version(void) { return KVM_ABI_VERSION; }
+
+int64_t kvm_struct_size(int which) {
+  switch (which) {
+    case 0: return sizeof(kvm_layer);
+    case 1: return sizeof(kvm_seq);
+    case 2: return sizeof(kvm_state);
+    case 3: return sizeof(kvm_prefill_desc);
+    default: return -1;
+  }
+}
+
+const char *kvm_last_error(void) { return g_error.c_str(); }
+
+int64_t kvm_update_workspace_bytes(const kvm_layer *layer, int64_t n_tok) {
+  if (check_layer(layer) != KVM_OK || n_tok < 1) return -1;
+  return kvm::update_scratch_bytes(*layer, n_tok);
+}
+
+int64_t kvm_decode_workspace_bytes(const kvm_layer *layer, int64_t max_rows) {
+  if (check_layer(layer) != KVM_OK) return -1;
+  return kvm::decode_workspace_bytes(*layer, max_rows);
+}
+
+int64_t kvm_prefill_workspace_bytes(const kvm_prefill_desc *d) {
+  if (!d || check_layer(&d->layer) != KVM_OK) return -1;
+  if (d->max_state_len < 1 || d->snapshot_ring < 2) return -1;
+  return int64_t(prefill_layout(d).total);
+}
+
+int kvm_state_append_direct(const kvm_layer *layer, const kvm_seq *src,
+                            int64_t tok_begin, int64_t n_tok,
+                            const kvm_state *st, int64_t slot_begin,
+                            void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_seq(src, "src")) ||
+      (rc = check_state(st, true)))
+    return rc;
+  if (n_tok < 0 || tok_begin < 0 || slot_begin < 0 ||
+      slot_begin + n_tok > st->capacity)
+    return fail(KVM_ESPACE, "direct append of %lld tokens at slot %lld exceeds capacity %lld",
+                (long long)n_tok, (long long)slot_begin, (long long)st->capacity);
+  kvm::AttnRows attn{static_cast<uint16_t *>(st->s_k_attn),
+                     static_cast<uint16_t *>(st->s_v_attn), st->capacity};
+  KVM_HIP(kvm::launch_append_direct(*layer, *src, tok_begin, n_tok, *st,
+                                    slot_begin, attn, layer->gate_initial != 0,
+                                    as_stream(stream)),
+          "kvm_state_append_direct");
+  return KVM_OK;
+}
+
+int kvm_state_refresh(const kvm_layer *layer, const kvm_state *st,
+                      int64_t slot_begin, int64_t n_slots, void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_state(st, true))) return rc;
+  if (slot_begin < 0 || n_slots < 0 || slot_begin + n_slots > st->capacity)
+    return fail(KVM_EINVAL, "refresh range exceeds the state capacity");
+  kvm::AttnRows attn{static_cast<uint16_t *>(st->s_k_attn),
+                     static_cast<uint16_t *>(st->s_v_attn), st->capacity};
+  KVM_HIP(kvm::launch_refresh(*layer, *st, slot_begin, n_slots, attn,
+                              as_stream(stream)),
+          "kvm_state_refresh");
+  return KVM_OK;
+}
+
+int kvm_state_update(const kvm_layer *layer, const kvm_seq *src,
+                     int64_t tok_begin, int64_t n_tok, int64_t state_before,
+                     int64_t n_append, const kvm_state *st, void *attn_k_out,
+                     void *attn_v_out, void *workspace, int64_t workspace_bytes,
+                     int32_t *route_out, int32_t *append_out, void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_seq(src, "src")) ||
+      (rc = check_state(st, true)))
+    return rc;
+  if (n_tok < 1 || n_tok > 4096)
+    return fail(KVM_EINVAL, "update token count must be in [1, 4096]");
+  if (n_append < 0 || n_append > n_tok)
+    return fail(KVM_EINVAL, "n_append must be in [0, n_tok]");
+  if (state_before < 1)
+    return fail(KVM_EINVAL, "a state update needs a non-empty state");
+  const int64_t after = state_before + n_append;
+  if (after > st->capacity)
+    return fail(KVM_ESPACE, "state of %lld slots exceeds capacity %lld",
+                (long long)after, (long long)st->capacity);
+  if (n_append < n_tok && after <= std::min(layer->sink_len, after))
+    return fail(KVM_EINVAL,
+                "KVM state update requires at least one non-sink slot before merging.");
+  if (!attn_k_out || !attn_v_out || !aligned16(attn_k_out) || !aligned16(attn_v_out))
+    return fail(KVM_EINVAL, "attention output rows must be set and 16-byte aligned");
+  const int64_t need = kvm::update_scratch_bytes(*layer, n_tok);
+  if (!workspace || workspace_bytes < need)
+    return fail(KVM_ESPACE, "update workspace of %lld bytes is smaller than %lld",
+                (long long)workspace_bytes, (long long)need);
+  kvm::UpdateScratch sc = kvm::carve_update_scratch(workspace, *layer, n_tok);
+  kvm::AttnRows in{static_cast<uint16_t *>(st->s_k_attn),
+                   static_cast<uint16_t *>(st->s_v_attn), st->capacity};
+  kvm::AttnRows out{static_cast<uint16_t *>(attn_k_out),
+                    static_cast<uint16_t *>(attn_v_out), st->capacity};
+  hipStream_t s = as_stream(stream);
+  KVM_HIP(kvm::launch_update(*layer, *src, tok_begin, n_tok, state_before,
+                             n_append, *st, in, out, sc, s),
+          "kvm_state_update");
+  const size_t bytes = size_t(layer->batch * layer->kv_heads) * size_t(n_tok) * 4;
+  if (route_out)
+    KVM_HIP(hipMemcpyAsync(route_out, sc.route, bytes, hipMemcpyDeviceToDevice, s),
+            "route copy");
+  if (append_out)
+    KVM_HIP(hipMemcpyAsync(append_out, sc.is_append, bytes, hipMemcpyDeviceToDevice, s),
+            "append flag copy");
+  return KVM_OK;
+}
+
+int kvm_ring_write(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
+                   void *ring_v, void *ring_gate, int64_t ring_cap, int64_t pos,
+                   void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_seq(src, "src"))) return rc;
+  if (!ring_k || !ring_v || !ring_gate || !aligned16(ring_k) || !aligned16(ring_v))
+    return fail(KVM_EINVAL, "ring buffers must be set and 16-byte aligned");
+  if (ring_cap < 1 || pos < 0 || pos >= ring_cap)
+    return fail(KVM_EINVAL, "ring position %lld outside [0, %lld)", (long long)pos,
+                (long long)ring_cap);
+  KVM_HIP(kvm::launch_ring_write(*layer, *src, ring_k, ring_v, ring_gate, ring_cap,
+                                 pos, as_stream(stream)),
+          "kvm_ring_write");
+  return KVM_OK;
+}
+
+int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
+                         int64_t q_sh, const kvm_state *st,
+                         int64_t active_state_len, const void *ring_k,
+                         const void *ring_v, int64_t ring_cap,
+                         int64_t ring_start, int64_t recent_len, void *out,
+                         int64_t o_sb, int64_t o_sh, void *workspace,
+                         int64_t workspace_bytes, void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_state(st, true))) return rc;
+  if (!q || !aligned16(q) || q_sb % 8 || q_sh % 8)
+    return fail(KVM_EINVAL, "q must be 16-byte aligned with strides multiple of 8");
+  if (!out) return fail(KVM_EINVAL, "out must be set");
+  if (!ring_k || !ring_v || !aligned16(ring_k) || !aligned16(ring_v) || ring_cap < 1)
+    return fail(KVM_EINVAL, "ring buffers must be set and 16-byte aligned");
+  if (active_state_len < 0 || active_state_len > st->capacity)
+    return fail(KVM_EINVAL, "active state length outside the state capacity");
+  if (recent_len < 0 || recent_len > ring_cap || ring_start < 0 || ring_start >= ring_cap)
+    return fail(KVM_EINVAL, "recent window outside the ring");
+  if (active_state_len + recent_len < 1)
+    return fail(KVM_EINVAL, "decode attention needs at least one key row");
+  const int64_t need = kvm::decode_workspace_bytes(*layer, active_state_len + recent_len);
+  if (!workspace || workspace_bytes < need)
+    return fail(KVM_ESPACE, "decode workspace of %lld bytes is smaller than %lld",
+                (long long)workspace_bytes, (long long)need);
+  KVM_HIP(kvm::launch_decode(*layer, q, q_sb, q_sh, *st, active_state_len, ring_k,
+                             ring_v, ring_cap, ring_start, recent_len, out, o_sb,
+                             o_sh, workspace, as_stream(stream)),
+          "kvm_decode_attention");
+  return KVM_OK;
+}
+
+int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
+  if (!d) return fail(KVM_EINVAL, "prefill descriptor is NULL");
+  int rc;
+  const kvm_layer &L = d->layer;
+  if ((rc = check_layer(&L)) || (rc = check_seq(&d->kv, "kv")) ||
+      (rc = check_state(&d->state, false)))
+    return rc;
+  if (d->kv.ring != 0) return fail(KVM_EINVAL, "prefill tokens cannot come from a ring");
+  if (!d->q || !aligned16(d->q) || d->q_sb % 8 || d->q_sh % 8 || d->q_st % 8)
+    return fail(KVM_EINVAL, "q must be 16-byte aligned with strides multiple of 8");
+  if (!d->out || !aligned16(d->out) || d->o_sb % 4 || d->o_st % 4 || d->o_sh % 4)
+    return fail(KVM_EINVAL, "out must be 16-byte aligned with strides multiple of 4");
+  const int64_t T = d->seq_len, C = L.chunk_len, n = L.n_bswa_chunks;
+  if (T < 1) return fail(KVM_EINVAL, "seq_len must be positive");
+  const int64_t n_chunks = (T + C - 1) / C;
+  if (d->n_chunks != n_chunks)
+    return fail(KVM_EINVAL, "n_chunks %lld != ceil(T / C) = %lld",
+                (long long)d->n_chunks, (long long)n_chunks);
+  if (!d->chunk_state_len || !d->chunk_snapshot)
+    return fail(KVM_EINVAL, "chunk schedule arrays must be set");
+  if (d->n_updates < 0 || (d->n_updates > 0 && (!d->upd_token_begin ||
+                                                !d->upd_state_before ||
+                                                !d->upd_n_append)))
+    return fail(KVM_EINVAL, "update schedule arrays must be set");
+  if (d->snapshot_ring < 2) return fail(KVM_EINVAL, "snapshot_ring must be >= 2");
+  const int64_t L0 = std::min(T, C);
+  if (d->max_state_len < L0 || d->max_state_len > d->state.capacity)
+    return fail(KVM_ESPACE, "max_state_len %lld must be in [%lld, capacity %lld]",
+                (long long)d->max_state_len, (long long)L0,
+                (long long)d->state.capacity);
+  // Schedule sanity: chunk m >= n sees the snapshot after m - n updates.
+  for (int64_t m = 0; m < n_chunks; ++m) {
+    const int32_t s = d->chunk_state_len[m], snap = d->chunk_snapshot[m];
+    if (m < n) {
+      if (s != 0) return fail(KVM_EINVAL, "front chunk %lld must see no memory slots", (long long)m);
+      continue;
+    }
+    if (snap < 0 || snap > d->n_updates || s < 1 || s > d->max_state_len)
+      return fail(KVM_EINVAL, "chunk %lld schedule (state %d, snapshot %d) is invalid",
+                  (long long)m, s, snap);
+    if (m > n && snap < d->chunk_snapshot[m - 1])
+      return fail(KVM_EINVAL, "chunk snapshots must be nondecreasing");
+  }
+  int64_t cur = L0;
+  for (int64_t u = 0; u < d->n_updates; ++u) {
+    const int64_t tb = d->upd_token_begin[u];
+    if (d->upd_state_before[u] != cur)
+      return fail(KVM_EINVAL, "update %lld starts from %d slots, schedule has %lld",
+                  (long long)u, d->upd_state_before[u], (long long)cur);
+    if (tb < 0 || tb % C || tb + C > T)
+      return fail(KVM_EINVAL, "update %lld overflow chunk at token %lld is invalid",
+                  (long long)u, (long long)tb);
+    const int64_t na = d->upd_n_append[u];
+    if (na < 0 || na > C) return fail(KVM_EINVAL, "update %lld append count invalid", (long long)u);
+    if (na < C && cur + na <= std::min(L.sink_len, cur + na))
+      return fail(KVM_EINVAL,
+                  "KVM state update requires at least one non-sink slot before merging.");
+    cur += na;
+    if (cur > d->max_state_len)
+      return fail(KVM_ESPACE, "state grows past max_state_len");
+  }
+  const PrefillLayout lay = prefill_layout(d);
+  if (!d->workspace || d->workspace_bytes < int64_t(lay.total))
+    return fail(KVM_ESPACE, "prefill workspace of %lld bytes is smaller than %lld",
+                (long long)d->workspace_bytes, (long long)lay.total);
+
+  hipStream_t s = as_stream(stream);
+  auto mark = [&](int i) -> int {
+    if (d->events && d->events[i])
+      KVM_HIP(hipEventRecord(static_cast<hipEvent_t>(d->events[i]), s), "event record");
+    return KVM_OK;
+  };
+  unsigned char *ws = static_cast<unsigned char *>(d->workspace);
+  kvm::UpdateScratch sc = kvm::carve_update_scratch(ws, L, C);
+  uint16_t *snap_k = reinterpret_cast<uint16_t *>(ws + lay.update_bytes);
+  const size_t snap_bytes = align256(lay.snap_elems * 2);
+  uint16_t *snap_v = reinterpret_cast<uint16_t *>(
+      ws + lay.update_bytes + size_t(d->snapshot_ring) * snap_bytes);
+  const int64_t snap_stride = int64_t(snap_bytes / 2);
+  const int64_t R = d->snapshot_ring;
+  auto snap_rows = [&](int64_t idx) {
+    return kvm::AttnRows{snap_k + (idx % R) * snap_stride,
+                         snap_v + (idx % R) * snap_stride, d->max_state_len};
+  };
+
+  // Initial state: the first min(T, C) tokens (model/kvm_mixer.py:434-447).
+  if ((rc = mark(0)) != KVM_OK) return rc;
+  KVM_HIP(kvm::launch_append_direct(L, d->kv, 0, L0, d->state, 0, snap_rows(0),
+                                    L.gate_initial != 0, s),
+          "initial state");
+
+  kvm::PrefillAttnArgs a;
+  a.q = d->q;
+  a.q_sb = d->q_sb; a.q_sh = d->q_sh; a.q_st = d->q_st;
+  a.kv = d->kv;
+  a.T = T;
+  a.out = d->out;
+  a.o_sb = d->o_sb; a.o_st = d->o_st; a.o_sh = d->o_sh;
+  a.snap_k = snap_k;
+  a.snap_v = snap_v;
+  a.snap_stride = snap_stride;
+  a.snap_cap = d->max_state_len;
+
+  int64_t next_chunk = 0;
+  bool attn_marked = false;
+  // Launch attention for every chunk whose snapshot index is < ready.
+  auto flush = [&](int64_t ready) -> int {
+    if (!attn_marked && next_chunk < n_chunks) {
+      int r = mark(2);
+      if (r != KVM_OK) return r;
+      attn_marked = true;
+    }
+    while (next_chunk < n_chunks &&
+           (next_chunk < n || d->chunk_snapshot[next_chunk] < ready)) {
+      kvm::ChunkTable table;
+      int64_t cnt = 0;
+      while (next_chunk + cnt < n_chunks && cnt < kvm::kMaxChunksPerLaunch) {
+        const int64_t m = next_chunk + cnt;
+        if (m >= n && d->chunk_snapshot[m] >= ready) break;
+        table.state_len[cnt] = m >= n ? d->chunk_state_len[m] : 0;
+        table.snap_slot[cnt] = m >= n ? int32_t(d->chunk_snapshot[m] % R) : 0;
+        ++cnt;
+      }
+      KVM_HIP(kvm::launch_prefill_attention(L, a, next_chunk, cnt, table, s),
+              "prefill attention");
+      next_chunk += cnt;
+    }
+    return KVM_OK;
+  };
+
+  const size_t log_stride = size_t(L.batch * L.kv_heads) * size_t(C);
+  for (int64_t u = 0; u < d->n_updates; ++u) {
+    // Snapshot u + 1 overwrites ring slot (u + 1) % R: every chunk reading
+    // snapshot u + 1 - R must have been launched (stream order does the rest).
+    if (u + 1 - R >= 0) {
+      if ((rc = flush(u + 1)) != KVM_OK) return rc;
+      if (next_chunk < n_chunks && next_chunk >= n &&
+          d->chunk_snapshot[next_chunk] <= u + 1 - R)
+        return fail(KVM_EINVAL, "snapshot ring too small for the schedule");
+    }
+    KVM_HIP(kvm::launch_update(L, d->kv, d->upd_token_begin[u], C,
+                               d->upd_state_before[u], d->upd_n_append[u],
+                               d->state, snap_rows(u), snap_rows(u + 1), sc, s),
+            "state update");
+    if (d->route_log)
+      KVM_HIP(hipMemcpyAsync(d->route_log + u * log_stride, sc.route, log_stride * 4,
+                             hipMemcpyDeviceToDevice, s),
+              "route log copy");
+    if (d->append_log)
+      KVM_HIP(hipMemcpyAsync(d->append_log + u * log_stride, sc.is_append,
+                             log_stride * 4, hipMemcpyDeviceToDevice, s),
+              "append log copy");
+  }
+  if ((rc = mark(1)) != KVM_OK) return rc;
+  if ((rc = flush(d->n_updates + 1)) != KVM_OK) return rc;
+  if ((rc = mark(3)) != KVM_OK) return rc;
+
+  // Final attention rows into the caller's state.
+  if (d->state.s_k_attn && d->state.s_v_attn) {
+    const kvm::AttnRows last = snap_rows(d->n_updates);
+    const size_t row_bytes = size_t(cur) * size_t(L.head_dim) * 2;
+    const size_t dpitch = size_t(d->state.capacity) * size_t(L.head_dim) * 2;
+    const size_t spitch = size_t(d->max_state_len) * size_t(L.head_dim) * 2;
+    const size_t rows = size_t(L.batch * L.kv_heads);
+    KVM_HIP(hipMemcpy2DAsync(d->state.s_k_attn, dpitch, last.k, spitch, row_bytes,
+                             rows, hipMemcpyDeviceToDevice, s),
+            "final key rows");
+    KVM_HIP(hipMemcpy2DAsync(d->state.s_v_attn, dpitch, last.v, spitch, row_bytes,
+                             rows, hipMemcpyDeviceToDevice, s),
+            "final value rows");
+  }
+  return KVM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,280 @@
+// Single-token KVM decode attention on gfx950.
+//
+// Reference semantics: model/kvm_mixer.py:572-713 (forward_single, attention
+// through _attend_with_state_and_bswa :194-229 with q_len = 1) and the
+// Triton kernel it replaces, model/kernels/kvm_triton_decode.py:175-284
+// (one program per (batch, q_head), serial scan).
+//
+// Here the key rows [memory slots ; window ring rows] of every
+// (batch, kv_head) are split into segments of 256 rows.  A workgroup (4
+// waves) owns one segment of one kv row and serves every query head of that
+// kv head it is launched for (the GQA group shares each K/V read).  A wave
+// reads 64 rows with D/8 lanes per row, i.e. 4 (D=128) or 8 (D=64) whole
+// rows per 16-byte-per-lane load: each load instruction covers 1 KiB of
+// contiguous HBM.  Scores, the wave softmax and the PV accumulation are in
+// fp32; the 4 waves merge (max, sum, acc) through LDS, and a second kernel
+// merges the segments in a fixed order (deterministic split-K).
+
+#include "kvm_device.hpp"
+#include "kvm_internal.hpp"
+
+namespace kvm {
+namespace {
+
+constexpr int kRowsPerWave = 64;
+constexpr int kWaves = 4;
+constexpr int kSegRows = kRowsPerWave * kWaves;
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int D, int GQ>
+__global__ __launch_bounds__(256) void k_decode_partial(
+    kvm_layer L, const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
+    const uint16_t *__restrict__ sk, const uint16_t *__restrict__ sv,
+    int64_t cap, int active, const uint16_t *__restrict__ rk,
+    const uint16_t *__restrict__ rv, int64_t ring_cap, int64_t ring_start,
+    int recent_len, int nseg, float *__restrict__ part_acc,
+    float *__restrict__ part_ml) {
+  constexpr int G = D / 8;             // lanes per key row
+  constexpr int RPS = 64 / G;          // rows per wave step
+  constexpr int STEPS = kRowsPerWave / RPS;
+  __shared__ float sm_m[kWaves][GQ], sm_l[kWaves][GQ];
+  __shared__ float sm_acc[kWaves][GQ][D];
+
+  const int seg = blockIdx.x;
+  const int row = blockIdx.y;
+  const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
+  const int group = Hq / Hkv;
+  const int b = row / Hkv, hk = row % Hkv;
+  const int hq0 = hk * group + blockIdx.z * GQ;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / G, part = lane % G;
+  const int total = active + recent_len;
+  const float scale = kLog2e / sqrtf(float(D));
+
+  float qv[GQ][8], ts[GQ], tf[GQ];
+#pragma unroll
+  for (int j = 0; j < GQ; ++j) {
+    load8(q + b * q_sb + (hq0 + j) * q_sh + part * 8, qv[j]);
+    ts[j] = static_cast<const float *>(L.state_temp)[hq0 + j];
+    tf[j] = static_cast<const float *>(L.front_temp)[hq0 + j];
+  }
+
+  const int r0 = seg * kSegRows + wave * kRowsPerWave;
+  const uint16_t *skrow = sk + int64_t(row) * cap * D;
+  const uint16_t *svrow = sv + int64_t(row) * cap * D;
+  const uint16_t *rkrow = rk + int64_t(row) * ring_cap * D;
+  const uint16_t *rvrow = rv + int64_t(row) * ring_cap * D;
+
+  // Issue every K and V load of the wave first (2 x STEPS x 16 B per lane).
+  uint4 kraw[STEPS], vraw[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int r = r0 + s * RPS + sub;
+    kraw[s] = make_uint4(0, 0, 0, 0);
+    vraw[s] = make_uint4(0, 0, 0, 0);
+    if (r < total) {
+      int64_t o;
+      const uint16_t *kb, *vb;
+      if (r < active) {
+        o = int64_t(r) * D;
+        kb = skrow;
+        vb = svrow;
+      } else {
+        o = ((ring_start + (r - active)) % ring_cap) * D;
+        kb = rkrow;
+        vb = rvrow;
+      }
+      kraw[s] = *reinterpret_cast<const uint4 *>(kb + o + part * 8);
+      vraw[s] = *reinterpret_cast<const uint4 *>(vb + o + part * 8);
+    }
+  }
+
+  // Scores: bf16(key * temperature) . q (model/kernels/kvm_triton_decode.py:225-228).
+  float sc[GQ][STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int r = r0 + s * RPS + sub;
+    float kx[8];
+    unpack8(kraw[s], kx);
+#pragma unroll
+    for (int j = 0; j < GQ; ++j) {
+      const float tau = r < active ? ts[j] : tf[j];
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d += rbf(kx[i] * tau) * qv[j][i];
+      d = group_sum<G>(d);
+      sc[j][s] = r < total ? d * scale : -INFINITY;
+    }
+  }
+
+  float m[GQ], l[GQ], acc[GQ][8];
+#pragma unroll
+  for (int j = 0; j < GQ; ++j) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) mx = fmaxf(mx, sc[j][s]);
+#pragma unroll
+    for (int o = G; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    m[j] = mx;
+    l[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[j][i] = 0.f;
+  }
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    float vx[8];
+    unpack8(vraw[s], vx);
+#pragma unroll
+    for (int j = 0; j < GQ; ++j) {
+      const float p = (m[j] == -INFINITY) ? 0.f : exp2f(sc[j][s] - m[j]);
+      l[j] += p;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[j][i] += p * vx[i];
+    }
+  }
+  // Reduce over the RPS rows a step holds (lanes with equal `part`).
+#pragma unroll
+  for (int j = 0; j < GQ; ++j) {
+#pragma unroll
+    for (int o = G; o < 64; o <<= 1) {
+      l[j] += __shfl_xor(l[j], o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[j][i] += __shfl_xor(acc[j][i], o);
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int j = 0; j < GQ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm_acc[wave][j][part * 8 + i] = acc[j][i];
+      if (part == 0) {
+        sm_m[wave][j] = m[j];
+        sm_l[wave][j] = l[j];
+      }
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < GQ * D; e += 256) {
+    const int j = e / D, d = e % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][j]);
+    float a = 0.f, s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = (sm_m[w][j] == -INFINITY) ? 0.f : exp2f(sm_m[w][j] - M);
+      a += sm_acc[w][j][d] * f;
+      s += sm_l[w][j] * f;
+    }
+    const int64_t pid = int64_t(b) * Hq + hq0 + j;
+    part_acc[(pid * nseg + seg) * D + d] = a;
+    if (d == 0) {
+      part_ml[(pid * nseg + seg) * 2 + 0] = M;
+      part_ml[(pid * nseg + seg) * 2 + 1] = s;
+    }
+  }
+}
+
+// Merge the segments of one (batch, q_head) in segment order.
+template <int D>
+__global__ __launch_bounds__(D) void k_decode_combine(
+    int Hq, int nseg, const float *__restrict__ part_acc,
+    const float *__restrict__ part_ml, uint16_t *__restrict__ out,
+    int64_t o_sb, int64_t o_sh) {
+  const int pid = blockIdx.x;
+  const int b = pid / Hq, h = pid % Hq;
+  const int d = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < nseg; ++s)
+    M = fmaxf(M, part_ml[(int64_t(pid) * nseg + s) * 2]);
+  float a = 0.f, l = 0.f;
+  for (int s = 0; s < nseg; ++s) {
+    const float ms = part_ml[(int64_t(pid) * nseg + s) * 2];
+    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    a += part_acc[(int64_t(pid) * nseg + s) * D + d] * f;
+    l += part_ml[(int64_t(pid) * nseg + s) * 2 + 1] * f;
+  }
+  out[b * o_sb + h * o_sh + d] = uint16_t(f2bf(a / l));
+}
+
+template <int D, int GQ>
+hipError_t launch_partial(const kvm_layer &L, const void *q, int64_t q_sb,
+                          int64_t q_sh, const kvm_state &st, int64_t active,
+                          const void *ring_k, const void *ring_v,
+                          int64_t ring_cap, int64_t ring_start,
+                          int64_t recent_len, int nseg, float *pacc,
+                          float *pml, hipStream_t stream) {
+  const int group = int(L.q_heads / L.kv_heads);
+  dim3 grid(unsigned(nseg), unsigned(L.batch * L.kv_heads),
+            unsigned(group / GQ));
+  hipLaunchKernelGGL((k_decode_partial<D, GQ>), grid, dim3(256), 0, stream, L,
+                     static_cast<const uint16_t *>(q), q_sb, q_sh,
+                     static_cast<const uint16_t *>(st.s_k_attn),
+                     static_cast<const uint16_t *>(st.s_v_attn), st.capacity,
+                     int(active), static_cast<const uint16_t *>(ring_k),
+                     static_cast<const uint16_t *>(ring_v), ring_cap,
+                     ring_start, int(recent_len), nseg, pacc, pml);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_partial_d(const kvm_layer &L, const void *q, int64_t q_sb,
+                            int64_t q_sh, const kvm_state &st, int64_t active,
+                            const void *ring_k, const void *ring_v,
+                            int64_t ring_cap, int64_t ring_start,
+                            int64_t recent_len, int nseg, float *pacc,
+                            float *pml, hipStream_t stream) {
+  const int64_t group = L.q_heads / L.kv_heads;
+#define KVM_PARTIAL(GQ)                                                      \
+  launch_partial<D, GQ>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,       \
+                        ring_cap, ring_start, recent_len, nseg, pacc, pml, \
+                        stream)
+  if (group % 4 == 0) return KVM_PARTIAL(4);
+  if (group % 2 == 0) return KVM_PARTIAL(2);
+  return KVM_PARTIAL(1);
+#undef KVM_PARTIAL
+}
+
+}  // namespace
+
+int64_t decode_segments(int64_t rows_total) {
+  return (rows_total + kSegRows - 1) / kSegRows;
+}
+
+int64_t decode_workspace_bytes(const kvm_layer &L, int64_t max_rows) {
+  const int64_t nseg = decode_segments(max_rows < 1 ? 1 : max_rows);
+  return L.batch * L.q_heads * nseg * (L.head_dim + 2) * 4;
+}
+
+hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
+                         int64_t q_sh, const kvm_state &st, int64_t active,
+                         const void *ring_k, const void *ring_v,
+                         int64_t ring_cap, int64_t ring_start,
+                         int64_t recent_len, void *out, int64_t o_sb,
+                         int64_t o_sh, void *workspace, hipStream_t stream) {
+  const int nseg = int(decode_segments(active + recent_len));
+  const int64_t npid = L.batch * L.q_heads;
+  float *pacc = static_cast<float *>(workspace);
+  float *pml = pacc + npid * nseg * L.head_dim;
+  hipError_t e;
+  if (L.head_dim == 128)
+    e = launch_partial_d<128>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
+                              ring_cap, ring_start, recent_len, nseg, pacc,
+                              pml, stream);
+  else
+    e = launch_partial_d<64>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
+                             ring_cap, ring_start, recent_len, nseg, pacc, pml,
+                             stream);
+  if (e != hipSuccess) return e;
+  if (L.head_dim == 128)
+    hipLaunchKernelGGL(k_decode_combine<128>, dim3(unsigned(npid)), dim3(128),
+                       0, stream, int(L.q_heads), nseg, pacc, pml,
+                       static_cast<uint16_t *>(out), o_sb, o_sh);
+  else
+    hipLaunchKernelGGL(k_decode_combine<64>, dim3(unsigned(npid)), dim3(64), 0,
+                       stream, int(L.q_heads), nseg, pacc, pml,
+                       static_cast<uint16_t *>(out), o_sb, o_sh);
+  return hipGetLastError();
+}
+
+}  // namespace kvm

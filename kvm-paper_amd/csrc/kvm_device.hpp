@@ -1,0 +1,122 @@
+// Device-side helpers shared by the KVM kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// bfloat16 <-> float.  Rounding is round-to-nearest-even, the rounding torch
+// uses for every float -> bfloat16 conversion (c10/util/BFloat16.h).
+__device__ __forceinline__ float bf2f(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+// Round a float to the nearest bfloat16 value, kept as float.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// 8 consecutive bf16 <-> 8 floats (one 16-byte access).
+__device__ __forceinline__ void unpack8(const uint4 u, float (&x)[8]) {
+  x[0] = __uint_as_float(u.x << 16);
+  x[1] = __uint_as_float(u.x & 0xffff0000u);
+  x[2] = __uint_as_float(u.y << 16);
+  x[3] = __uint_as_float(u.y & 0xffff0000u);
+  x[4] = __uint_as_float(u.z << 16);
+  x[5] = __uint_as_float(u.z & 0xffff0000u);
+  x[6] = __uint_as_float(u.w << 16);
+  x[7] = __uint_as_float(u.w & 0xffff0000u);
+}
+__device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+  uint4 u;
+  u.x = f2bf(x[0]) | (f2bf(x[1]) << 16);
+  u.y = f2bf(x[2]) | (f2bf(x[3]) << 16);
+  u.z = f2bf(x[4]) | (f2bf(x[5]) << 16);
+  u.w = f2bf(x[6]) | (f2bf(x[7]) << 16);
+  return u;
+}
+__device__ __forceinline__ void load8(const uint16_t *p, float (&x)[8]) {
+  unpack8(*reinterpret_cast<const uint4 *>(p), x);
+}
+__device__ __forceinline__ void store8(uint16_t *p, const float (&x)[8]) {
+  *reinterpret_cast<uint4 *>(p) = pack8(x);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4 u) {
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// LayerNorm of one D-wide row held as 8 floats in each of D/8 consecutive
+// lanes (lane part p holds dims 8p..8p+7).  Two-pass mean / biased
+// variance in fp32, y = (x - mean) * (1 / sqrt(var + eps)) * w + b, the
+// formula of torch.nn.functional.layer_norm.
+template <int D>
+__device__ __forceinline__ void layer_norm8(float (&x)[8], int part,
+                                            const float *__restrict__ w,
+                                            const float *__restrict__ b,
+                                            float eps) {
+  constexpr int G = D / 8;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i];
+  s = group_sum<G>(s);
+  const float mean = s / float(D);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float c = x[i] - mean;
+    q += c * c;
+  }
+  q = group_sum<G>(q);
+  const float rstd = 1.0f / sqrtf(q / float(D) + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = part * 8 + i;
+    x[i] = (x[i] - mean) * rstd * w[d] + b[d];
+  }
+}
+
+// Euclidean norm of a D-wide row held as 8 floats per lane in D/8 lanes.
+template <int D>
+__device__ __forceinline__ float row_norm8(const float (&x)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i] * x[i];
+  return sqrtf(group_sum<D / 8>(s));
+}
+
+// Value row as the state contributes it to attention:
+// bf16(normalize(v) * vlen), normalize(v) = v / max(|v|, 1e-12)
+// (torch.nn.functional.normalize; model/kvm_mixer.py:205-206).
+template <int D>
+__device__ __forceinline__ void attn_value8(float (&v)[8], float vlen) {
+  const float n = fmaxf(row_norm8<D>(v), 1e-12f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = rbf((v[i] / n) * vlen);
+}
+
+}  // namespace kvm

@@ -1,0 +1,90 @@
+// Internal launcher interface shared by the KVM translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kvm_amd.h"
+
+namespace kvm {
+
+// Scratch of one block-boundary update over n_tok overflow tokens
+// (all arrays [rows, n_tok, ...], row-major).
+struct UpdateScratch {
+  uint16_t *pk;       // prep(k)                      bf16 [rows, n_tok, D]
+  uint16_t *gk;       // merge key  (gated or not)    bf16 [rows, n_tok, D]
+  uint16_t *gv;       // merge value (gated or not)   bf16 [rows, n_tok, D]
+  float *novelty;     // bf16-rounded max similarity  fp32 [rows, n_tok]
+  int32_t *route;     // destination slot             int32 [rows, n_tok]
+  int32_t *is_append; // 1 if appended                int32 [rows, n_tok]
+};
+
+int64_t update_scratch_bytes(const kvm_layer &L, int64_t n_tok);
+UpdateScratch carve_update_scratch(void *ws, const kvm_layer &L, int64_t n_tok);
+
+// Attention-row arrays of a state: bf16 [rows, cap, D] each.
+struct AttnRows {
+  uint16_t *k;
+  uint16_t *v;
+  int64_t cap;
+};
+
+hipError_t launch_append_direct(const kvm_layer &L, const kvm_seq &src,
+                                int64_t tok_begin, int64_t n_tok,
+                                const kvm_state &st, int64_t slot_begin,
+                                AttnRows attn, bool apply_gate,
+                                hipStream_t stream);
+
+hipError_t launch_refresh(const kvm_layer &L, const kvm_state &st,
+                          int64_t slot_begin, int64_t n_slots, AttnRows attn,
+                          hipStream_t stream);
+
+// One update.  Routing reads attn_in (the attention rows of the state before
+// the update; appended rows are added to it), the refreshed rows of every
+// slot < state_before + n_append are written to attn_out.
+hipError_t launch_update(const kvm_layer &L, const kvm_seq &src,
+                         int64_t tok_begin, int64_t n_tok, int64_t state_before,
+                         int64_t n_append, const kvm_state &st, AttnRows attn_in,
+                         AttnRows attn_out, const UpdateScratch &sc,
+                         hipStream_t stream);
+
+hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
+                             void *ring_k, void *ring_v, void *ring_gate,
+                             int64_t ring_cap, int64_t pos, hipStream_t stream);
+
+int64_t decode_segments(int64_t rows_total);
+int64_t decode_workspace_bytes(const kvm_layer &L, int64_t max_rows);
+hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
+                         int64_t q_sh, const kvm_state &st, int64_t active,
+                         const void *ring_k, const void *ring_v,
+                         int64_t ring_cap, int64_t ring_start,
+                         int64_t recent_len, void *out, int64_t o_sb,
+                         int64_t o_sh, void *workspace, hipStream_t stream);
+
+// Per-launch table of the query chunks an attention launch covers.
+constexpr int kMaxChunksPerLaunch = 256;
+struct ChunkTable {
+  int32_t state_len[kMaxChunksPerLaunch];  // memory slots visible to the chunk
+  int32_t snap_slot[kMaxChunksPerLaunch];  // ring slot of its snapshot
+};
+
+struct PrefillAttnArgs {
+  const void *q;
+  int64_t q_sb, q_sh, q_st;
+  kvm_seq kv;
+  int64_t T;
+  void *out;
+  int64_t o_sb, o_st, o_sh;
+  const uint16_t *snap_k;  // snapshot ring base (keys)
+  const uint16_t *snap_v;  // snapshot ring base (values)
+  int64_t snap_stride;     // elements between consecutive snapshots
+  int64_t snap_cap;        // slots per row in a snapshot
+};
+
+hipError_t launch_prefill_attention(const kvm_layer &L,
+                                    const PrefillAttnArgs &a,
+                                    int64_t chunk_begin, int64_t n_chunks,
+                                    const ChunkTable &table,
+                                    hipStream_t stream);
+
+}  // namespace kvm

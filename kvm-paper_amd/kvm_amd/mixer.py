@@ -1,0 +1,544 @@
+"""Drop-in KVM ``SequenceMixer`` running the forward path on MI355X HIP kernels.
+
+Selection: ``model.token_mixer_class_path: kvm_amd.mixer.SequenceMixer``
+(with ``kvm-paper_amd/`` on ``sys.path``) in place of
+``model.kvm_triton_mixer.SequenceMixer`` (configs/prolong/kvm_triton.yaml:4).
+The constructor ``SequenceMixer(config, layer_idx)``, the parameter names and
+labels, the ``forward`` / ``forward_inference`` / ``forward_prefix`` /
+``forward_prefill`` / ``forward_single`` / ``_decode_one_token`` signatures
+and the carried-state cache entry follow the reference:
+  * model/value_residual_mixin.py:14-295   heads, projections, value residual
+  * model/kvm_mixer.py:78-118, 342-401     KVM parameters, forward_prefix
+  * model/kvm_triton_mixer.py:198-757      prefill / decode at the QKV boundary
+
+Everything after the post-QKV boundary (window + memory attention, the
+block-boundary memory update, decode) runs in libkvm_amd.so through its C ABI
+(include/kvm_amd.h).  The projections before the boundary are plain torch
+modules, as in the reference.  Autograd (training) is not provided: a
+prefill that needs gradients raises ValueError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import _lib
+from .decode_cache import DecodeCacheSnapshot, KVMDecodeCache
+from .schedule import (
+    PrefillPlan,
+    StateBudget,
+    bswa_begin_for_total_len,
+    prefill_plan,
+    state_length_after_cycle,
+)
+
+# Snapshot memory budget of one prefill (bytes); the snapshot ring is sized to
+# hold every snapshot when they fit, otherwise attention launches are batched.
+_SNAPSHOT_BUDGET = int(os.environ.get("KVM_AMD_SNAPSHOT_BYTES", str(8 << 30)))
+
+
+def set_label(label, module, mup_d_in_ratio=None):
+    """Optimizer label of parameters (utils/opt.py:4-10)."""
+    if isinstance(module, torch.Tensor):
+        module.label = label
+        module.mup_d_in_ratio = mup_d_in_ratio
+    else:
+        for p in module.parameters():
+            set_label(label, p, mup_d_in_ratio)
+    return module
+
+
+def apply_rotary_embeddings(x_BTHD, position_embeddings):
+    """Interleaved-pair RoPE (model/rwkv7_backbone.py:76-88)."""
+    cos, sin = position_embeddings
+    assert cos.size(1) == x_BTHD.size(1), f"{cos.size()} {x_BTHD.size()}"
+    x_flip = x_BTHD.view(*x_BTHD.shape[:-1], x_BTHD.shape[-1] // 2, 2).flip(-1).view(x_BTHD.shape)
+    return cos * x_BTHD + sin * x_flip
+
+
+def _token_shift(x, scale, prev=None):
+    """RWKV token shift (model/tokenshift.py:11-37, fallback "first")."""
+    if prev is None:
+        prev = x[:, :1]
+    elif prev.dtype != x.dtype or prev.device != x.device:
+        prev = prev.to(device=x.device, dtype=x.dtype)
+    return x + scale * (torch.cat([prev, x[:, :-1]], dim=1) - x)
+
+
+class _LayerHandle:
+    """A KvmLayer struct plus the fp32 parameter copies it points to."""
+
+    def __init__(self, struct: _lib.KvmLayer, keep):
+        self.struct = struct
+        self.keep = keep
+
+    def ref(self):
+        return ctypes.byref(self.struct)
+
+
+class SequenceMixer(nn.Module):
+    """KVM token mixer (post-QKV path on HIP kernels)."""
+
+    _CACHE_S_K = "kvm_s_k"
+    _CACHE_S_V = "kvm_s_v"
+    _CACHE_S_VLEN = "kvm_s_vlen"
+    _CACHE_STATE_COVERAGE_LEN = "kvm_state_coverage_len"
+    _CACHE_BSWA_BEGIN = "kvm_bswa_begin"
+    _CACHE_BSWA_K = "kvm_bswa_k"
+    _CACHE_BSWA_V = "kvm_bswa_v"
+    _CACHE_BSWA_MERGE_GATE = "kvm_bswa_merge_gate"
+    # Same cache key as the reference mixer (model/kvm_triton_mixer.py:214).
+    _CACHE_TRITON_DECODE = "kvm_triton_decode_cache"
+    _CACHE_Q_FINAL = "att_q_final_token"
+    _CACHE_K_FINAL = "att_k_final_token"
+    _CACHE_V_FINAL = "att_v_final_token"
+    _CACHE_X_FINAL = "att_x_final_token"
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        # --- heads and projections (model/value_residual_mixin.py:15-166) ---
+        self.layer_idx = layer_idx
+        self.config = config
+        self.num_attention_heads = config.num_attention_heads
+        self.num_key_value_heads = (
+            config.num_key_value_heads if config.num_key_value_heads is not None else config.num_attention_heads
+        )
+        if self.num_key_value_heads <= 0:
+            raise ValueError("num_key_value_heads must be positive")
+        if self.num_attention_heads % self.num_key_value_heads:
+            raise ValueError("num_attention_heads must be divisible by num_key_value_heads")
+        self.kv_group_size = self.num_attention_heads // self.num_key_value_heads
+        self.hidden_size = config.hidden_size
+        self.d_qk_head = config.d_qk_head or config.d_head or (config.hidden_size // config.num_attention_heads)
+        self.d_v_head = config.d_v_head or config.d_head or (config.hidden_size // config.num_attention_heads)
+        d_q = self.num_attention_heads * self.d_qk_head
+        d_k = self.num_key_value_heads * self.d_qk_head
+        d_v = self.num_key_value_heads * self.d_v_head
+        d_out = self.num_attention_heads * self.d_v_head
+        self.q_projection_size, self.k_projection_size = d_q, d_k
+        self.value_projection_size, self.attention_output_size = d_v, d_out
+        self.rwkv_tokenshift_fallback = "first"
+        self.tokenshift_mode = config.kvm_token_shift_mode if config.use_tokenshift_att else "none"
+        if self.tokenshift_mode == "rwkv":
+            ratio = 1.0 - (layer_idx / config.num_hidden_layers)
+            ddd_q = torch.arange(d_q, dtype=torch.float32) / d_q
+            ddd_k = torch.arange(d_k, dtype=torch.float32) / d_k
+            ddd_v = torch.arange(d_v, dtype=torch.float32) / d_v
+            self.x_q = set_label("scalars", nn.Parameter(1.0 - torch.pow(ddd_q, 0.2 * ratio)))
+            self.x_k = set_label("scalars", nn.Parameter(1.0 - torch.pow(ddd_k, 0.7 * ratio)))
+            self.x_v = set_label("scalars", nn.Parameter(1.0 - torch.pow(ddd_v, 0.7 * ratio)))
+        self.c_q = set_label("matrix_params", nn.Linear(self.hidden_size, d_q, bias=False))
+        self.c_k = set_label("matrix_params", nn.Linear(self.hidden_size, d_k, bias=False))
+        self.c_v = set_label("matrix_params", nn.Linear(self.hidden_size, d_v, bias=False))
+        self.ln_q = set_label("scalars", nn.LayerNorm(self.d_qk_head))
+        self.ln_k = set_label("scalars", nn.LayerNorm(self.d_qk_head))
+        self.c_proj = set_label("matrix_params", nn.Linear(d_out, self.hidden_size, bias=False))
+        with torch.no_grad():
+            self.c_proj.weight.zero_()
+        self.lamb = None
+        self.value_residual_mode = "none"
+        if config.use_value_residual:
+            mode = config.kvm_value_residual_mode
+            if mode not in ("linear", "rwkv", "rwkv_post_tokenshift"):
+                raise AssertionError(f"Unsupported value residual mode: {mode!r}")
+            self.value_residual_mode = mode
+            if mode == "linear":
+                self.lamb = set_label("scalars", nn.Parameter(torch.tensor(0.5)))
+            else:
+                if not hasattr(self, "x_v"):
+                    self.x_v = set_label("scalars", nn.Parameter(torch.zeros(d_v)))
+
+                def lora_dim(c, mult, power):
+                    return max(32, int(round((mult * (c ** power)) / 32) * 32))
+
+                r = lora_dim(self.hidden_size, 1.3, 0.5)
+                r_base = lora_dim(config.mup_base_dim, 1.3, 0.5)
+                self.v_gate1 = set_label("matrix_params", nn.Linear(self.hidden_size, r, bias=False))
+                self.v_gate2 = set_label("matrix_params", nn.Linear(r, d_v, bias=False), mup_d_in_ratio=r / r_base)
+                with torch.no_grad():
+                    self.v_gate1.weight.zero_()
+                    w = torch.empty(r, d_v)
+                    nn.init.orthogonal_(w, gain=0.1)
+                    self.v_gate2.weight.copy_(w.T)
+                linear = torch.arange(d_v, dtype=torch.float32) / (d_v - 1) - 0.5
+                self.v_gate0 = set_label("scalars", nn.Parameter(torch.zeros(1, 1, d_v) + 0.73 - linear.view(1, 1, d_v) * 0.4))
+                if mode == "rwkv_post_tokenshift" and d_v != self.hidden_size:
+                    self.x_v_hidden = set_label("scalars", nn.Parameter(torch.zeros(self.hidden_size)))
+
+        # --- KVM attributes (model/kvm_mixer.py:79-118) ---
+        self.rope_partial_dim = config.rope_partial_dim if config.rope_partial_dim > 0 else self.d_qk_head
+        self.ln_s_k = set_label("scalars", nn.LayerNorm(self.d_qk_head))
+        self.sink_len = config.sink_len
+        self.chunk_len = config.chunk_len
+        self.n_max_d_chunks = config.n_max_d_chunks
+        self.n_bswa_chunks = config.n_bswa_chunks
+        self.max_state_len = self.chunk_len * self.n_max_d_chunks
+        self.state_budget_mode = config.state_budget_mode
+        self.state_growth_factor = config.state_growth_factor
+        self.state_growth_exponent = config.state_growth_exponent
+        self.state_round_down = config.state_round_down
+        self.state_min_len = config.state_min_len
+        self.state_saturation_n = config.state_saturation_n
+        if config.kvm_use_merge_gate_keys or config.kvm_use_merge_gate_values:
+            self.key_weighting = set_label(
+                "matrix_params", nn.Linear(config.hidden_size, self.num_key_value_heads, bias=False))
+        if config.kvm_use_head_temps:
+            self.front_head_temp = set_label("scalars", nn.Parameter(torch.ones(config.num_attention_heads)))
+            self.state_head_temp = set_label("scalars", nn.Parameter(torch.ones(config.num_attention_heads)))
+        # --- constraints of the HIP path (model/kvm_triton_mixer.py:216-219) ---
+        if not config.kvm_use_vlens:
+            raise ValueError("the HIP KVM mixer requires kvm_use_vlens=1")
+        if self.d_qk_head != self.d_v_head or self.d_qk_head not in (64, 128):
+            raise ValueError("the HIP KVM mixer supports d_qk_head == d_v_head in {64, 128}")
+        if not 1 <= self.chunk_len <= 4096:
+            raise ValueError("the HIP KVM mixer needs chunk_len in [1, 4096]")
+
+    # ------------------------------------------------------------------ helpers
+    @property
+    def state_budget(self) -> StateBudget:
+        return StateBudget(
+            mode=self.state_budget_mode, growth_factor=float(self.state_growth_factor),
+            growth_exponent=float(self.state_growth_exponent), round_down=int(self.state_round_down),
+            min_len=int(self.state_min_len),
+            saturation_n=None if self.state_saturation_n is None else int(self.state_saturation_n),
+            max_state_len=int(self.max_state_len),
+        )
+
+    def _bswa_begin_for_total_len(self, total_len: int) -> int:
+        return bswa_begin_for_total_len(total_len, self.chunk_len, self.n_bswa_chunks)
+
+    def _desired_state_len(self, ctx_len: int, available_context: int, current_state_len: int) -> int:
+        return self.state_budget.desired(ctx_len, available_context, current_state_len)
+
+    def make_plan(self, q_len: int) -> PrefillPlan:
+        """Host schedule of a prefill (model/kvm_triton_mixer.py:257-343 make_schedule)."""
+        return prefill_plan(q_len, self.chunk_len, self.n_bswa_chunks, self.state_budget)
+
+    def _head_temperatures(self, device):
+        if self.config.kvm_use_head_temps:
+            return self.state_head_temp.detach().float().contiguous(), self.front_head_temp.detach().float().contiguous()
+        ones = torch.ones(self.num_attention_heads, device=device, dtype=torch.float32)
+        return ones, ones
+
+    def _layer_struct(self, batch: int, device, gate_initial: bool | None = None) -> _LayerHandle:
+        w = self.ln_s_k.weight.detach().float().contiguous()
+        b = self.ln_s_k.bias.detach().float().contiguous()
+        ts, tf = self._head_temperatures(device)
+        cfg = self.config
+        gi = bool(cfg.kvm_apply_merge_gate_to_initial_state) if gate_initial is None else bool(gate_initial)
+        s = _lib.KvmLayer(
+            batch=int(batch), q_heads=self.num_attention_heads, kv_heads=self.num_key_value_heads,
+            head_dim=self.d_qk_head, value_dim=self.d_v_head, chunk_len=self.chunk_len,
+            n_bswa_chunks=self.n_bswa_chunks, sink_len=self.sink_len,
+            rope_partial_dim=self.rope_partial_dim,
+            gate_keys=int(bool(cfg.kvm_use_merge_gate_keys)), gate_values=int(bool(cfg.kvm_use_merge_gate_values)),
+            gate_appends=int(bool(cfg.kvm_apply_merge_gate_to_appends)), gate_initial=int(gi),
+            ln_eps=float(self.ln_s_k.eps),
+            ln_weight=w.data_ptr(), ln_bias=b.data_ptr(), state_temp=ts.data_ptr(), front_temp=tf.data_ptr(),
+        )
+        return _LayerHandle(s, (w, b, ts, tf))
+
+    def _repeat_kv_for_query_heads(self, x: torch.Tensor) -> torch.Tensor:
+        return x if self.kv_group_size == 1 else x.repeat_interleave(self.kv_group_size, dim=1)
+
+    # -------------------------------------------------------- pre-boundary part
+    def get_first_layer_kwargs(self, x0, x, x_prior_token=None, **kwargs):
+        """model/value_residual_mixin.py:239-246."""
+        if self.value_residual_mode == "none":
+            return {"v_first": None}
+        return {"v_first": self.c_v(x)}
+
+    def _value_gate(self, x):
+        return torch.sigmoid(self.v_gate0 + self.v_gate2(self.v_gate1(x)))
+
+    def calc_qkv(self, x, v_first, past_key_values):
+        """Projections, value residual, token shift, ln_q/ln_k (model/value_residual_mixin.py:173-237)."""
+        B, T, _ = x.size()
+        states = past_key_values.get_states(self.layer_idx) if past_key_values is not None else {}
+        past = past_key_values.get_seq_length(self.layer_idx) if past_key_values is not None else 0
+        if past > 0 and T != 1:
+            raise AssertionError("cached decode expects single-token inputs.")
+        q, k, v = self.c_q(x), self.c_k(x), self.c_v(x)
+        if self.value_residual_mode == "linear":
+            v = (1 - self.lamb) * v + self.lamb * v_first.view_as(v)
+        elif self.value_residual_mode == "rwkv":
+            g = self._value_gate(x)
+            v = v + (v_first.to(v.dtype) - v) * g.to(v.dtype)
+        qp = kp = vp = xp = None
+        if past_key_values is not None:
+            qp, kp = states.get(self._CACHE_Q_FINAL), states.get(self._CACHE_K_FINAL)
+            vp, xp = states.get(self._CACHE_V_FINAL), states.get(self._CACHE_X_FINAL)
+            past_key_values.update(self.layer_idx, offset=0, states_dict={
+                self._CACHE_Q_FINAL: q[:, -1:].detach(), self._CACHE_K_FINAL: k[:, -1:].detach(),
+                self._CACHE_V_FINAL: v[:, -1:].detach(), self._CACHE_X_FINAL: x[:, -1:].detach(),
+            })
+        if self.tokenshift_mode == "rwkv":
+            q = _token_shift(q, self.x_q, qp)
+            k = _token_shift(k, self.x_k, kp)
+            v = _token_shift(v, self.x_v, vp)
+        if self.value_residual_mode == "rwkv_post_tokenshift":
+            shift = self.x_v if self.value_projection_size == self.hidden_size else self.x_v_hidden
+            xv = _token_shift(x, shift.view(1, 1, self.hidden_size), xp)
+            g = self._value_gate(xv)
+            v = v + (v_first.to(v.dtype) - v) * g.to(v.dtype)
+        q = self.ln_q(q.reshape(B, T, self.num_attention_heads, -1))
+        k = self.ln_k(k.reshape(B, T, self.num_key_value_heads, -1))
+        v = v.reshape(B, T, self.num_key_value_heads, -1)
+        return q, k, v
+
+    def forward_prefix(self, x, v_first, position_embeddings, attention_mask, past_key_values=None, **kwargs):
+        """q/k/v/merge gate at the post-QKV boundary (model/kvm_mixer.py:367-401)."""
+        B, T, _ = x.size()
+        q, k, v = self.calc_qkv(x, v_first, past_key_values)
+        q = apply_rotary_embeddings(q, position_embeddings)
+        k = apply_rotary_embeddings(k, position_embeddings)
+        if self.config.kvm_use_merge_gate_keys or self.config.kvm_use_merge_gate_values:
+            merge_gate = 1.0 + F.elu(self.key_weighting(x).view(B, T, self.num_key_value_heads, 1)).transpose(1, 2)
+        else:
+            merge_gate = torch.ones((B, self.num_key_value_heads, T, 1), device=x.device, dtype=torch.float)
+        return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), merge_gate
+
+    # ------------------------------------------------------------ entry points
+    def forward(self, x, v_first, position_embeddings, attention_mask, past_key_values=None, **kwargs):
+        q, k, v, g = self.forward_prefix(x, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
+        return self.forward_prefill(q, k, v, g, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
+
+    def forward_inference(self, x, v_first, position_embeddings, attention_mask, past_key_values=None, **kwargs):
+        """Prefill on an empty cache, single-token decode otherwise (model/kvm_mixer.py:527-570)."""
+        past = past_key_values.get_seq_length(self.layer_idx) if past_key_values is not None else 0
+        q, k, v, g = self.forward_prefix(x, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
+        if past == 0:
+            return self.forward_prefill(q, k, v, g, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
+        return self.forward_single(q, k, v, g, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
+
+    def _check_no_grad(self, *tensors):
+        needs_grad = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (*tensors, self.ln_s_k.weight, self.ln_s_k.bias,
+                                      getattr(self, "state_head_temp", tensors[0]),
+                                      getattr(self, "front_head_temp", tensors[0])))
+        if needs_grad:
+            raise ValueError("the HIP KVM mixer implements the forward path only; run it under torch.no_grad()")
+
+    def prefill_raw(self, q, k, v, merge_gate, *, plan: PrefillPlan | None = None, state_capacity: int | None = None,
+                    route_log: bool = False, snapshot_budget: int | None = None,
+                    events=None) -> dict:
+        """Post-QKV prefill on the HIP library; returns the raw outputs.
+
+        q [B,Hq,T,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] bf16 (any strides with a
+        contiguous last axis), merge_gate [B,Hkv,T,1].  Returns a dict with
+        ``out`` [B,T,Hq,Dv], the final state tensors ``state_k``, ``state_v``,
+        ``state_vlen``, ``state_k_attn``, ``state_v_attn`` ([B*Hkv, cap, D]),
+        ``plan`` and, when requested, ``route_log`` / ``append_log``
+        [n_updates, B*Hkv, C] int32.  ``events``: optional four recorded
+        torch.cuda.Event objects bracketing the update chain and the
+        attention launches (timing).
+        """
+        if q.dtype != torch.bfloat16:
+            raise ValueError("the HIP KVM mixer computes in bfloat16; got " + str(q.dtype))
+        B, Hq, T, D = q.shape
+        if Hq != self.num_attention_heads:
+            raise AssertionError("KVM query head count mismatch.")
+        if int(k.size(1)) != self.num_key_value_heads:
+            raise AssertionError("KVM key/value head count mismatch.")
+        dev = q.device
+        if plan is None:
+            plan = self.make_plan(int(T))
+        cap = max(plan.final_state_len, int(state_capacity or 0))
+        rows = B * self.num_key_value_heads
+        bf = dict(device=dev, dtype=torch.bfloat16)
+        out = torch.empty(B, T, Hq, self.d_v_head, **bf)
+        st = {
+            "state_k": torch.empty(rows, cap, D, **bf), "state_v": torch.empty(rows, cap, D, **bf),
+            "state_vlen": torch.empty(rows, cap, device=dev, dtype=torch.float32),
+            "state_k_attn": torch.empty(rows, cap, D, **bf), "state_v_attn": torch.empty(rows, cap, D, **bf),
+        }
+        qv = _lib._bf16_view(q, "q")
+        seq, keep = _lib.seq4(k, v, merge_gate)
+        layer = self._layer_struct(B, dev)
+        lib = _lib.load()
+        n_snaps = plan.n_updates + 1
+        per_snap = 2 * rows * plan.max_state_len * D * 2
+        budget = _SNAPSHOT_BUDGET if snapshot_budget is None else int(snapshot_budget)
+        ring = max(2, min(n_snaps, budget // max(per_snap, 1)))
+        arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin,
+                                               plan.upd_state_before, plan.upd_n_append)]
+        d = _lib.KvmPrefillDesc()
+        d.layer = layer.struct
+        d.q, d.q_sb, d.q_sh, d.q_st = qv.data_ptr(), qv.stride(0), qv.stride(1), qv.stride(2)
+        d.kv = seq
+        d.seq_len = int(T)
+        d.out, d.o_sb, d.o_st, d.o_sh = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
+        d.state = _lib.state_struct(st["state_k"], st["state_v"], st["state_vlen"], st["state_k_attn"],
+                                    st["state_v_attn"], cap)
+        d.n_chunks = plan.n_chunks
+        d.chunk_state_len, d.chunk_snapshot = arrs[0], arrs[1]
+        d.n_updates = plan.n_updates
+        d.upd_token_begin, d.upd_state_before, d.upd_n_append = arrs[2], arrs[3], arrs[4]
+        d.max_state_len = plan.max_state_len
+        d.snapshot_ring = ring
+        nbytes = int(lib.kvm_prefill_workspace_bytes(ctypes.byref(d)))
+        if nbytes < 0:
+            raise ValueError("invalid prefill descriptor: " + lib.kvm_last_error().decode())
+        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
+        logs = {}
+        if route_log:
+            n = max(plan.n_updates, 1)
+            logs["route_log"] = torch.full((n, rows, self.chunk_len), -1, device=dev, dtype=torch.int32)
+            logs["append_log"] = torch.zeros((n, rows, self.chunk_len), device=dev, dtype=torch.int32)
+            d.route_log, d.append_log = logs["route_log"].data_ptr(), logs["append_log"].data_ptr()
+        ev_arr = None
+        if events is not None:
+            ev_arr = (ctypes.c_void_p * 4)(*[e.cuda_event if e is not None else None for e in events])
+            d.events = ctypes.cast(ev_arr, ctypes.c_void_p)
+        _lib.check(lib.kvm_prefill(ctypes.byref(d), _lib.stream_handle(dev)), "kvm_prefill")
+        del keep, ws
+        res = {"out": out, "plan": plan, "capacity": cap, **st, **logs}
+        return res
+
+    def forward_prefill(self, q, k, v, merge_gate, v_first, position_embeddings, attention_mask,
+                        past_key_values=None, **kwargs):
+        """Prefill at the post-QKV boundary (model/kvm_triton_mixer.py:560-666)."""
+        if attention_mask is not None:
+            raise ValueError("the HIP KVM mixer does not support attention_mask")
+        self._check_no_grad(q, k, v, merge_gate)
+        B, _, T, _ = q.size()
+        plan = self.make_plan(int(T))
+        cap = None
+        if past_key_values is not None:
+            cap = max(plan.final_state_len, min(self.chunk_len, self.max_state_len),
+                      state_length_after_cycle(self.state_budget, self.chunk_len, self.n_bswa_chunks,
+                                               int(T), plan.final_state_len, self.n_bswa_chunks * self.chunk_len))
+        res = self.prefill_raw(q, k, v, merge_gate, plan=plan, state_capacity=cap)
+        y = self.c_proj(res["out"].view(B, T, -1))
+        if past_key_values is not None:
+            begin = self._bswa_begin_for_total_len(int(T))
+            if plan.final_coverage != max(plan.initial_state_len, begin):
+                raise AssertionError("KVM prefill state progression drifted from cache bookkeeping.")
+            cache = self._cache_from_prefill(res, k, v, merge_gate, int(T), begin)
+            past_key_values.update(self.layer_idx, offset=int(T), states_dict={self._CACHE_TRITON_DECODE: cache})
+        return y
+
+    def _cache_from_prefill(self, res, k, v, gate, T, begin) -> KVMDecodeCache:
+        """Decode cache adopting the prefill's state buffers (no copy, no refresh)."""
+        B = int(k.size(0))
+        cache = KVMDecodeCache(self, None, state_capacity=res["capacity"], _device=k.device, _batch=B)
+        cache.state_k, cache.state_v, cache.state_vlen = res["state_k"], res["state_v"], res["state_vlen"]
+        cache.state_k_attn, cache.state_v_attn = res["state_k_attn"], res["state_v_attn"]
+        R = T - begin
+        rows = cache.kv_rows
+        cache.recent_k[:, :R].copy_(k[:, :, begin:].reshape(rows, R, self.d_qk_head))
+        cache.recent_v[:, :R].copy_(v[:, :, begin:].reshape(rows, R, self.d_v_head))
+        cache.recent_gate[:, :R].copy_(gate[:, :, begin:].reshape(rows, R))
+        cache.total_len = T
+        cache.state_len = res["plan"].final_state_len
+        cache.state_coverage_len = res["plan"].final_coverage
+        cache.recent_begin = begin
+        cache.recent_start = 0
+        cache.recent_len = R
+        return cache
+
+    def forward_single(self, q, k, v, merge_gate, v_first, position_embeddings, attention_mask,
+                       past_key_values=None, **kwargs):
+        """Decode one token through the cache (model/kvm_triton_mixer.py:668-715)."""
+        if attention_mask is not None:
+            raise ValueError("the HIP KVM mixer does not support attention_mask")
+        if past_key_values is None:
+            raise ValueError("HIP KVM cached decode requires past_key_values")
+        if int(q.size(2)) != 1:
+            raise AssertionError("HIP KVM cached decode expects a single-token input")
+        cache = past_key_values.get_states(self.layer_idx).get(self._CACHE_TRITON_DECODE)
+        if not isinstance(cache, KVMDecodeCache):
+            raise RuntimeError("HIP KVM cache is missing its decode state; run a prefill with this cache first")
+        if cache.mixer is not self:
+            raise RuntimeError("HIP KVM decode cache belongs to another mixer")
+        past = past_key_values.get_seq_length(self.layer_idx)
+        if cache.total_len != past:
+            raise AssertionError(f"HIP KVM decode cache length disagrees with the layer cache: {cache.total_len} != {past}")
+        out = self._decode_one_token(q, k, v, merge_gate, cache)
+        past_key_values.update(self.layer_idx, offset=1, states_dict={self._CACHE_TRITON_DECODE: cache})
+        return self.c_proj(out.transpose(1, 2).contiguous().view(int(q.size(0)), 1, -1))
+
+    def _decode_one_token(self, q, k, v, merge_gate, decode_cache: KVMDecodeCache) -> torch.Tensor:
+        """Advance ``decode_cache`` by one post-QKV token and attend (model/kvm_triton_mixer.py:717-757)."""
+        self._decode_advance(k, v, merge_gate, decode_cache)
+        return self._decode_attention(q, decode_cache)
+
+    def _decode_advance(self, k, v, merge_gate, decode_cache: KVMDecodeCache) -> None:
+        """Cache bookkeeping of one decode token: direct-state append while the
+        prompt is shorter than a chunk, the state update when the window
+        crosses a chunk boundary, and the ring write."""
+        if int(k.size(2)) != 1:
+            raise ValueError("HIP KVM decode cache update accepts one token")
+        c = decode_cache
+        new_total = c.total_len + 1
+        new_begin = self._bswa_begin_for_total_len(new_total)
+        direct_target = min(new_total, c.chunk_len)
+        new_cov = max(direct_target, new_begin)
+        if new_cov < c.state_coverage_len:
+            raise AssertionError("KVM decode state coverage cannot shrink")
+        lib = _lib.load()
+        stream = _lib.stream_handle(c.device)
+        if direct_target > c.state_coverage_len:
+            if direct_target - c.state_coverage_len != 1:
+                raise AssertionError("decode crossed more than one direct-state token")
+            c._reserve_state_capacity(c.state_len + 1)
+            seq, keep = _lib.seq4(k, v, merge_gate)
+            # Eager decode appends the ungated prepared key (model/kvm_mixer.py:627-642).
+            _lib.check(lib.kvm_state_append_direct(c.direct_layer.ref(), seq, 0, 1, c.state_struct(),
+                                                   c.state_len, stream), "kvm_state_append_direct")
+            del keep
+            c.state_len += 1
+            c.state_coverage_len = direct_target
+        if new_cov > c.state_coverage_len:
+            if new_cov - c.state_coverage_len != self.chunk_len:
+                raise AssertionError("decode crossed more than one state boundary")
+            self._run_decode_state_update(c)
+            c.state_coverage_len = new_cov
+        c.append_recent_(k, v, merge_gate, total_len=new_total, recent_begin=new_begin)
+
+    def _run_decode_state_update(self, c: KVMDecodeCache) -> None:
+        """Fold the oldest window chunk into the state (model/kvm_triton_mixer.py:759-864;
+        eager model/kvm_mixer.py:646-669)."""
+        cur = c.state_len
+        want = self._desired_state_len(self.n_bswa_chunks * c.chunk_len + c.state_coverage_len,
+                                       c.state_coverage_len + c.chunk_len, cur)
+        n_app = min(max(want - cur, 0), c.chunk_len)
+        c._reserve_state_capacity(cur + n_app)
+        seq, keep = _lib.seq_rows(c.recent_k, c.recent_v, c.recent_gate, c.kv_heads, ring=c.ring_capacity)
+        lib = _lib.load()
+        _lib.check(lib.kvm_state_update(
+            c.layer.ref(), seq, c.recent_start, c.chunk_len, cur, n_app, c.state_struct(),
+            c.state_k_attn.data_ptr(), c.state_v_attn.data_ptr(), c.update_workspace.data_ptr(),
+            c.update_workspace.numel(), c.route_by_token.data_ptr(), c.append_by_token.data_ptr(),
+            _lib.stream_handle(c.device)), "kvm_state_update")
+        del keep
+        c.state_len = cur + n_app
+        c.update_count += 1
+
+    def _decode_attention(self, q: torch.Tensor, c: KVMDecodeCache) -> torch.Tensor:
+        """Attention of one query over the state and the window ring (model/kvm_triton_mixer.py:902-929)."""
+        active = c.state_len if c.total_len > c.ring_capacity else 0
+        qv = _lib._bf16_view(q, "q")
+        lib = _lib.load()
+        _lib.check(lib.kvm_decode_attention(
+            c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), active,
+            c.recent_k.data_ptr(), c.recent_v.data_ptr(), c.ring_capacity, c.recent_start, c.recent_len,
+            c.out.data_ptr(), c.out.stride(0), c.out.stride(1), c.decode_workspace.data_ptr(),
+            c.decode_workspace.numel(), _lib.stream_handle(c.device)), "kvm_decode_attention")
+        return c.out
+
+    def make_decode_cache(self, snapshot: DecodeCacheSnapshot, state_capacity: int | None = None) -> KVMDecodeCache:
+        """Decode cache from a carried-state snapshot (model/kvm_triton_decode.py:47-186)."""
+        S = int(snapshot.state_k.size(2))
+        cap = max(S, int(state_capacity or 0))
+        return KVMDecodeCache(self, snapshot, state_capacity=cap)
+
+
+__all__ = ["SequenceMixer", "apply_rotary_embeddings", "set_label"]

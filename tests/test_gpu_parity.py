@@ -1,0 +1,360 @@
+"""GPU parity of the HIP KVM path against the CPU oracle and the reference's
+golden fixtures (tests/golden/*.npz, written from the reference's eager
+mixer with FP32 routing).
+
+Bars (north star):
+  * routing: the slot of every overflow token equals the reference's, except
+    (a) near-ties whose fp32 similarity margin is below the fp32 summation
+    error bound (reported), and (b) tokens whose bf16 LayerNorm operand
+    differs from the CPU's by rounding (reported);
+  * outputs and carried state: bf16, max |err| <= 2e-2 and mean <= 2e-3
+    (errors in fp32).
+Every call goes through the C ABI of libkvm_amd.so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+import golden_io
+import kvm_testlib as T
+from oracle import kvm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+BF16_FIXTURES = [n for n in golden_io.names() if golden_io.load(n)["meta"]["dtype"] == "bf16"]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd import _lib
+
+    return _lib.load()
+
+
+def _rows(x):
+    """[B, H, S, D] -> [B*H, S, D]."""
+    return x.reshape(-1, x.size(-2), x.size(-1))
+
+
+def _align256(n):
+    return (n + 255) // 256 * 256
+
+
+def _fixture_mixer(fx):
+    cfg = T.fixture_config(fx["meta"])
+    m = T.make_mixer(cfg, fx["in_ln_w"], fx["in_ln_b"], fx["in_front_temp"], fx["in_state_temp"])
+    return cfg, m
+
+
+@pytest.mark.parametrize("name", BF16_FIXTURES)
+def test_update_routing_matches_oracle(lib, name):
+    """One kvm_state_update per recorded update, from the oracle's state."""
+    from kvm_amd import _lib
+
+    fx = golden_io.load(name)
+    meta = fx["meta"]
+    T.log(f"[update-parity] {name}")
+    ocfg, p = golden_io.oracle_setup(fx)
+    Tn = meta["T"]
+    q, k, v, g = (fx["in_" + x][:, :, :Tn] for x in ("q", "k", "v", "gate"))
+    rec = O.Recorder(keep_states=True)
+    _, st_final = O.prefill(q, k, v, g, p, ocfg, rec)
+    plan_tb = O.prefill_schedule(ocfg, Tn)["updates"]
+    _, mixer = _fixture_mixer(fx)
+    layer = mixer._layer_struct(meta["B"], torch.device(DEV))
+    kd, vd, gd = k.to(DEV), v.to(DEV), g.to(DEV)
+    seq, keep = _lib.seq4(kd, vd, gd)
+    C, D = meta["C"], meta["D"]
+    rows = meta["B"] * meta["Hkv"]
+    n_mis = n_tie = n_operand = n_total = 0
+    for i, u in enumerate(rec.updates):
+        before = u.state_len_before
+        after = before + u.n_append
+        cap = after
+        s_k = torch.zeros(rows, cap, D, dtype=torch.bfloat16)
+        s_v = torch.zeros_like(s_k)
+        vlen = torch.zeros(rows, cap)
+        s_k[:, :before] = _rows(u.s_k_before)
+        s_v[:, :before] = _rows(u.s_v_before)
+        vlen[:, :before] = u.s_vlen_before.reshape(rows, before)
+        ka = torch.zeros_like(s_k)
+        va = torch.zeros_like(s_k)
+        ka[:, :before] = _rows(O._ln(u.s_k_before, p))
+        va[:, :before] = _rows(O.state_values_for_attention(u.s_v_before, u.s_vlen_before, ocfg))
+        dev = [t.to(DEV).contiguous() for t in (s_k, s_v, vlen, ka, va)]
+        out_k, out_v = torch.empty_like(dev[3]), torch.empty_like(dev[4])
+        state = _lib.state_struct(*dev, cap)
+        nws = int(lib.kvm_update_workspace_bytes(layer.ref(), C))
+        ws = torch.zeros(nws, dtype=torch.uint8, device=DEV)
+        route = torch.full((rows, C), -7, dtype=torch.int32, device=DEV)
+        app = torch.full((rows, C), -7, dtype=torch.int32, device=DEV)
+        tb = plan_tb[i][0] * C
+        _lib.check(lib.kvm_state_update(layer.ref(), seq, tb, C, before, u.n_append, state,
+                                        out_k.data_ptr(), out_v.data_ptr(), ws.data_ptr(), nws,
+                                        route.data_ptr(), app.data_ptr(), 0), "update")
+        torch.cuda.synchronize()
+        route, app = route.cpu(), app.cpu()
+        # Oracle routes per token.
+        o_app = torch.zeros(rows, C, dtype=torch.int32)
+        o_route = torch.full((rows, C), -1, dtype=torch.int32)
+        B, H = meta["B"], meta["Hkv"]
+        ai = u.append_idx.reshape(rows, -1)
+        mi = u.merge_idx.reshape(rows, -1)
+        rt = u.route.reshape(rows, -1)
+        for r in range(rows):
+            for j, t in enumerate(ai[r].tolist()):
+                o_app[r, t] = 1
+                o_route[r, t] = before + j
+            o_route[r, mi[r]] = rt[r].to(torch.int32)
+        # GPU streams of the overflow tokens (workspace layout of include/kvm_amd.h).
+        A = _align256(rows * C * D * 2)
+        wsc = ws.cpu()
+        g_pk = wsc[:A][: rows * C * D * 2].view(torch.bfloat16).view(rows, C, D)
+        g_gk = wsc[A:2 * A][: rows * C * D * 2].view(torch.bfloat16).view(rows, C, D)
+        o_pk = _rows(O.prep_k(k[:, :, tb:tb + C], p, ocfg.rope_partial_dim))
+        o_gk = o_pk * _rows(g[:, :, tb:tb + C]) if ocfg.gate_keys else o_pk
+        pk_diff_tok = (g_pk != o_pk).any(-1) | (g_gk != o_gk).any(-1)
+        # Append sets: equal, or differing only inside a tie at the cut.
+        if u.n_append > 0:
+            nov = torch.matmul(o_pk.unsqueeze(0), _rows(O._ln(u.s_k_before, p)).transpose(-1, -2).unsqueeze(0))
+            nov = nov.squeeze(0).float().max(-1).values  # bf16 scores as the reference ranks them
+            for r in range(rows):
+                diff = (app[r] != o_app[r]).nonzero().flatten()
+                if len(diff):
+                    cut = torch.sort(nov[r]).values[u.n_append - 1]
+                    for t in diff.tolist():
+                        assert nov[r, t] == cut or bool(pk_diff_tok[r, t]), f"update {i} row {r}: append set differs at token {t} (no tie)"
+        # Merge routes.
+        s_attn_gpu = dev[3].cpu()  # appended rows written by the GPU
+        for r in range(rows):
+            for t in range(C):
+                if app[r, t] or o_app[r, t]:
+                    continue
+                n_total += 1
+                if route[r, t] == o_route[r, t]:
+                    continue
+                n_mis += 1
+                gb, ob = int(route[r, t]), int(o_route[r, t])
+                if bool(pk_diff_tok[r, t]):
+                    n_operand += 1
+                    continue
+                # Near-tie under the oracle's operands.
+                a = o_gk[r, t].double()
+                kattn = s_attn_gpu[r].double()
+                la, lb = float(a @ kattn[ob]), float(a @ kattn[gb])
+                bound = float(O.fp32_dot_error_bound(o_gk[r, t:t + 1], s_attn_gpu[r, [ob, gb]]).max())
+                assert abs(la - lb) <= 2 * bound + 1e-6 * max(abs(la), 1.0), (
+                    f"update {i} row {r} token {t}: GPU slot {gb} vs reference {ob}, margin {la - lb:.3e} > bound {bound:.3e}")
+                n_tie += 1
+        # State after the update (when the routes agree the sums must too).
+        if n_mis == 0:
+            nxt = rec.updates[i + 1] if i + 1 < len(rec.updates) else None
+            ref_k = _rows(nxt.s_k_before) if nxt is not None else _rows(st_final[O.S_K])
+            ref_v = _rows(nxt.s_v_before) if nxt is not None else _rows(st_final[O.S_V])
+            gk_ = dev[0].cpu()[:, :after]
+            gv_ = dev[1].cpu()[:, :after]
+            T.assert_close_bf16(gk_, ref_k[:, :after], f"update {i} s_k", max_abs=6e-2, mean_abs=1e-4)
+            T.assert_close_bf16(gv_, ref_v[:, :after], f"update {i} s_v", max_abs=6e-2, mean_abs=1e-4)
+    T.log(f"[update-parity] {name}: {n_total} merged tokens, {n_mis} route mismatches "
+          f"({n_tie} fp32 near-ties, {n_operand} bf16 LayerNorm operand roundings)")
+    assert n_mis <= max(2, n_total // 500)
+
+
+def _prefill_gpu(fx, route_log=True):
+    meta = fx["meta"]
+    cfg, mixer = _fixture_mixer(fx)
+    Tn = meta["T"]
+    q, k, v, g = (fx["in_" + x][:, :, :Tn].to(DEV) for x in ("q", "k", "v", "gate"))
+    with torch.no_grad():
+        res = mixer.prefill_raw(q, k, v, g, route_log=route_log)
+    torch.cuda.synchronize()
+    return mixer, res
+
+
+@pytest.mark.parametrize("name", BF16_FIXTURES)
+def test_prefill_matches_golden(lib, name):
+    fx = golden_io.load(name)
+    meta = fx["meta"]
+    T.log(f"[prefill-golden] {name} B{meta['B']} Hq{meta['Hq']} Hkv{meta['Hkv']} T{meta['T']} C{meta['C']}")
+    mixer, res = _prefill_gpu(fx)
+    out = res["out"].cpu().transpose(1, 2)  # [B, Hq, T, D]
+    mx, mean = T.assert_close_bf16(out, fx["y_prefill"], f"{name} prefill output")
+    # Routes of every update against the reference's recorded routes.
+    plan = res["plan"]
+    n_pre = meta["n_prefill_updates"]
+    assert plan.n_updates == n_pre
+    rows = meta["B"] * meta["Hkv"]
+    agree = total = 0
+    for i in range(n_pre):
+        gr = res["route_log"][i].cpu()
+        ga = res["append_log"][i].cpu()
+        ref_route = fx[f"upd{i}_route"].reshape(rows, -1)
+        if f"upd{i}_merge_idx" in fx:
+            mi = fx[f"upd{i}_merge_idx"].reshape(rows, -1).long()
+            g_sel = torch.stack([gr[r, mi[r]] for r in range(rows)])
+        else:
+            g_sel = gr
+        agree += int((g_sel == ref_route).sum())
+        total += ref_route.numel()
+    T.log(f"[prefill-golden] {name}: out max {mx:.2e} mean {mean:.2e}; routes {agree}/{total} agree")
+    assert agree >= total - max(2, total // 200)
+
+
+@pytest.mark.parametrize("name", [n for n in BF16_FIXTURES if n.startswith("decode")])
+def test_decode_matches_golden(lib, name):
+    fx = golden_io.load(name)
+    meta = fx["meta"]
+    T.log(f"[decode-golden] {name} T{meta['T']} steps {meta['decode_steps']}")
+    cfg, mixer = _fixture_mixer(fx)
+    Tn, steps = meta["T"], meta["decode_steps"]
+    q, k, v, g = (fx["in_" + x].to(DEV) for x in ("q", "k", "v", "gate"))
+    cache = T.LayerStatesCache()
+    with torch.no_grad():
+        mixer.forward_prefill(q[:, :, :Tn], k[:, :, :Tn], v[:, :, :Tn], g[:, :, :Tn], None, None, None, cache)
+        outs = []
+        for s in range(steps):
+            t = Tn + s
+            y = mixer.forward_single(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], g[:, :, t:t + 1],
+                                     None, None, None, cache)
+            outs.append(y.float().cpu())
+    torch.cuda.synchronize()
+    y = torch.cat(outs, dim=1).view(meta["B"], steps, meta["Hq"], meta["D"]).transpose(1, 2)
+    mx, mean = T.assert_close_bf16(y, fx["y_decode"], f"{name} decode outputs")
+    dc = cache.get_states(0)[mixer._CACHE_TRITON_DECODE]
+    sd = dc.logical_state_dict()
+    for key in (O.S_K, O.S_V, O.S_VLEN, O.BSWA_K, O.BSWA_V, O.BSWA_GATE):
+        ref = fx["final_" + key]
+        got = sd[key].cpu()
+        assert got.shape == ref.shape, f"{key}: {tuple(got.shape)} vs {tuple(ref.shape)}"
+        if key == O.S_VLEN:
+            assert torch.allclose(got.float(), ref.float(), rtol=1e-5, atol=1e-5), key
+        else:
+            T.assert_close_bf16(got, ref, f"{name} final {key}", max_abs=6e-2)
+    assert sd[O.COVERAGE] == int(fx["final_kvm_state_coverage_len"])
+    assert sd[O.BSWA_BEGIN] == int(fx["final_kvm_bswa_begin"])
+    T.log(f"[decode-golden] {name}: out max {mx:.2e} mean {mean:.2e}; {dc.update_count} decode updates")
+
+
+# ---------------------------------------------------------------------------
+# Attention numerics against fp64 on the GPU's own state.
+
+def _fp64_attention(q, keys, values, visible):
+    s = (q.double() @ keys.double().transpose(-1, -2)) / math.sqrt(q.size(-1))
+    s = s.masked_fill(~visible, float("-inf"))
+    return torch.softmax(s, dim=-1) @ values.double()
+
+
+def _random_inputs(B, Hq, Hkv, Tn, D, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, Hq, Tn, D, generator=gen) / math.sqrt(D)).bfloat16()
+    k = (torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16()
+    v = (torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16()
+    g = (1.0 + torch.nn.functional.elu(torch.randn(B, Hkv, Tn, 1, generator=gen))).bfloat16()
+    return q, k, v, g
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Tn,D,C,mode", [
+    (1, 4, 2, 1000, 128, 128, "fixed"),
+    (2, 2, 2, 777, 64, 64, "power_law"),
+])
+def test_last_chunk_attention_exact(lib, B, Hq, Hkv, Tn, D, C, mode):
+    """The last query chunk attends to the final state: compare with fp64."""
+    T.log(f"[attn-exact] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode=mode, min_len=C, n_max=3, factor=6.0)
+    gen = torch.Generator().manual_seed(7)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 11)
+    with torch.no_grad():
+        res = m.prefill_raw(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV))
+    torch.cuda.synchronize()
+    plan = res["plan"]
+    S = plan.final_state_len
+    mlast = plan.n_chunks - 1
+    assert plan.chunk_state_len[mlast] == S
+    qb, qe = mlast * C, Tn
+    wb = max(0, (mlast - cfg.n_bswa_chunks + 1) * C)
+    grp = Hq // Hkv
+    ka = res["state_k_attn"].cpu()[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1)
+    va = res["state_v_attn"].cpu()[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1)
+    kw = k[:, :, wb:qe].repeat_interleave(grp, 1)
+    vw = v[:, :, wb:qe].repeat_interleave(grp, 1)
+    keys = torch.cat([(ka.float() * stt.float().view(1, Hq, 1, 1)).bfloat16(),
+                      (kw.float() * ft.float().view(1, Hq, 1, 1)).bfloat16()], 2)
+    vals = torch.cat([va, vw], 2)
+    qpos = torch.arange(qb, qe).view(-1, 1)
+    kpos = torch.cat([torch.full((S,), -1), torch.arange(wb, qe)]).view(1, -1)
+    ref = _fp64_attention(q[:, :, qb:qe], keys, vals, kpos <= qpos)
+    got = res["out"].cpu()[:, qb:qe].transpose(1, 2)
+    mx, mean = T.assert_close_bf16(got, ref, "last-chunk attention", max_abs=8e-3, mean_abs=6e-4)
+    T.log(f"[attn-exact] max {mx:.2e} mean {mean:.2e}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,R,W,start", [
+    (4, 8, 8, 128, 1000, 300, 512, 400),
+    (2, 8, 2, 64, 37, 129, 128, 100),
+    (3, 4, 4, 128, 0, 60, 64, 10),
+])
+def test_decode_attention_exact(lib, B, Hq, Hkv, D, S, R, W, start):
+    """kvm_decode_attention against fp64, including a wrapped window ring."""
+    from kvm_amd import _lib
+
+    T.log(f"[decode-exact] B{B} Hq{Hq} Hkv{Hkv} D{D} S{S} R{R} W{W} start{start}")
+    gen = torch.Generator().manual_seed(3)
+    rows = B * Hkv
+    cap = max(S, 1) + 5
+    ka = torch.randn(rows, cap, D, generator=gen).bfloat16()
+    va = (0.5 * torch.randn(rows, cap, D, generator=gen)).bfloat16()
+    rk = torch.randn(rows, W, D, generator=gen).bfloat16()
+    rv = torch.randn(rows, W, D, generator=gen).bfloat16()
+    q = (torch.randn(B, Hq, 1, D, generator=gen) / math.sqrt(D)).bfloat16()
+    ts = (1 + 0.2 * torch.randn(Hq, generator=gen)).float()
+    tf = (1 + 0.2 * torch.randn(Hq, generator=gen)).float()
+    cfg = T.mixer_config(Hq, Hkv, D, 64)
+    m = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), tf, ts)
+    layer = m._layer_struct(B, torch.device(DEV))
+    dev = {n: t.to(DEV) for n, t in dict(ka=ka, va=va, rk=rk, rv=rv, q=q).items()}
+    st = _lib.state_struct(dev["ka"], dev["va"], dev["va"][:, :, :1].contiguous(), dev["ka"], dev["va"], cap)
+    nws = int(lib.kvm_decode_workspace_bytes(layer.ref(), S + R))
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib.kvm_decode_attention(layer.ref(), dev["q"].data_ptr(), dev["q"].stride(0), dev["q"].stride(1),
+                                        st, S, dev["rk"].data_ptr(), dev["rv"].data_ptr(), W, start, R,
+                                        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), nws, 0), "decode")
+    torch.cuda.synchronize()
+    grp = Hq // Hkv
+    idx = (start + torch.arange(R)) % W
+    ts_b, tf_b = m.state_head_temp.float().cpu(), m.front_head_temp.float().cpu()
+    keys = torch.cat([(ka[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1).float() * ts_b.view(1, Hq, 1, 1)).bfloat16(),
+                      (rk[:, idx].view(B, Hkv, R, D).repeat_interleave(grp, 1).float() * tf_b.view(1, Hq, 1, 1)).bfloat16()], 2)
+    vals = torch.cat([va[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1), rv[:, idx].view(B, Hkv, R, D).repeat_interleave(grp, 1)], 2)
+    ref = _fp64_attention(q, keys, vals, torch.ones(1, S + R, dtype=torch.bool)).squeeze(2)
+    mx, mean = T.assert_close_bf16(out.cpu(), ref, "decode attention", max_abs=1e-2, mean_abs=1e-3)
+    T.log(f"[decode-exact] max {mx:.2e} mean {mean:.2e}")
+
+
+def test_prefill_deterministic(lib):
+    """Two prefills of the same input are bit-identical (no atomics anywhere)."""
+    B, Hq, Hkv, Tn, D, C = 1, 8, 8, 4096, 128, 256
+    T.log(f"[determinism] B{B} H{Hq} T{Tn} C{C}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, min_len=C)
+    m = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = (t.to(DEV) for t in _random_inputs(B, Hq, Hkv, Tn, D, 5))
+    with torch.no_grad():
+        a = m.prefill_raw(q, k, v, g, route_log=True)
+        b = m.prefill_raw(q, k, v, g, route_log=True)
+    torch.cuda.synchronize()
+    for key in ("out", "state_k", "state_v", "state_k_attn", "state_v_attn", "route_log"):
+        assert torch.equal(a[key], b[key]), key
+    assert bool(torch.isfinite(a["out"].float()).all())
