@@ -22,6 +22,16 @@
 // operand (the key order inside a 32-key step is permuted identically in the
 // A operand, which leaves the sum unchanged).  Online softmax in fp32
 // registers with exp2; P rounded to bf16 for the PV product.
+//
+// VALU budget (the limiter next to MFMA on CDNA): bf16 packing uses the
+// hardware v_cvt_pk_bf16_f32, exp2 the raw v_exp_f32, the softmax scale is
+// folded into one fma per score, masks are applied only on tail / diagonal
+// blocks, the O rescale is skipped when no row maximum of the wave moved,
+// and a wave skips blocks that lie entirely above its causal diagonal.  The
+// next K/V block is fetched into registers while the current one is
+// consumed.  Workgroups are renumbered so that each XCD (dispatch is
+// round-robin over the 8 XCDs) runs a contiguous range of (head, chunk)
+// tiles: the window keys shared by neighbouring chunks stay in that XCD's L2.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -32,6 +42,15 @@ namespace {
 constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kXcds = 8;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
 
 template <int D>
 struct AttnSmem {
@@ -41,65 +60,106 @@ struct AttnSmem {
   uint16_t vt[D * VSTR];
 };
 
+// Register staging of one K/V block: each thread owns KPT 16-byte pieces of
+// K (key p / (D/8), dims 8 * (p % (D/8))) and one 4-key x 8-dim piece of V.
 template <int D>
-struct AttnState {
-  f32x4 o[2][D / 16];  // O^T tiles [row tile][dv tile]
-  float m[2];          // running max (log2 domain) of row rt*16 + lane%16
-  float l[2];          // lane-partial running sum
+struct Stage {
+  static constexpr int KPT = BN * (D / 8) / 256;  // K pieces per thread
+  static constexpr int VUNITS = (BN / 4) * (D / 8);
+  uint4 k[KPT];
+  uint4 v[4];
 };
 
-// One block of up to BN keys: stage K (x tau, bf16) and V^T in LDS, then
-// update the online softmax of the wave's 32 query rows.
-// kpos0: absolute position of key 0 (window keys) or -1 (memory slots,
-// never masked causally).  qpos0: position of the wave's first query row.
 template <int D>
-__device__ __forceinline__ void attend_block(
-    AttnSmem<D> &sm, AttnState<D> &as, const bf16x8 (&qf)[2][D / 32],
-    const uint16_t *__restrict__ kp, int64_t kstride,
-    const uint16_t *__restrict__ vp, int64_t vstride, int nvalid, float tau,
-    int64_t kpos0, int64_t qpos0, float scale) {
-  constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
-  const int tid = threadIdx.x, lane = tid & 63;
-  __syncthreads();
-  for (int p = tid; p < BN * (D / 8); p += 256) {
+__device__ __forceinline__ void stage_load(Stage<D> &sg,
+                                           const uint16_t *__restrict__ kp,
+                                           int64_t kstride,
+                                           const uint16_t *__restrict__ vp,
+                                           int64_t vstride, int nvalid) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < Stage<D>::KPT; ++i) {
+    const int p = tid + i * 256;
     const int key = p / (D / 8), part = p % (D / 8);
-    float x[8];
-    if (key < nvalid) {
-      load8(kp + key * kstride + part * 8, x);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = rbf(x[i] * tau);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = 0.f;
-    }
-    store8(&sm.k[key * KSTR + part * 8], x);
+    sg.k[i] = key < nvalid
+                  ? *reinterpret_cast<const uint4 *>(kp + key * kstride + part * 8)
+                  : make_uint4(0, 0, 0, 0);
   }
-  for (int p = tid; p < (BN / 4) * (D / 8); p += 256) {
-    const int kg = p % (BN / 4), dg = p / (BN / 4);
-    uint16_t e[4][8];
+  if (tid < Stage<D>::VUNITS) {
+    const int kg = tid % (BN / 4), dg = tid / (BN / 4);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int key = kg * 4 + r;
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if (key < nvalid)
-        u = *reinterpret_cast<const uint4 *>(vp + key * vstride + dg * 8);
-      e[r][0] = u.x & 0xffff; e[r][1] = u.x >> 16;
-      e[r][2] = u.y & 0xffff; e[r][3] = u.y >> 16;
-      e[r][4] = u.z & 0xffff; e[r][5] = u.z >> 16;
-      e[r][6] = u.w & 0xffff; e[r][7] = u.w >> 16;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint2 w;
-      w.x = uint32_t(e[0][i]) | (uint32_t(e[1][i]) << 16);
-      w.y = uint32_t(e[2][i]) | (uint32_t(e[3][i]) << 16);
-      *reinterpret_cast<uint2 *>(&sm.vt[(dg * 8 + i) * VSTR + kg * 4]) = w;
+      sg.v[r] = key < nvalid ? *reinterpret_cast<const uint4 *>(
+                                   vp + key * vstride + dg * 8)
+                             : make_uint4(0, 0, 0, 0);
     }
   }
-  __syncthreads();
+}
 
-  // S^T = K Q^T: s[kt][rt][i] = score(key kt*16 + 4*(lane/16) + i,
-  //                                   row  rt*16 + lane%16)
+// bf16 pair (lo half of a, lo half of b) -> one word, etc.
+__device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(AttnSmem<D> &sm,
+                                            const Stage<D> &sg, float tau) {
+  constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < Stage<D>::KPT; ++i) {
+    const int p = tid + i * 256;
+    const int key = p / (D / 8), part = p % (D / 8);
+    float x[8];
+    unpack8(sg.k[i], x);
+    uint4 w;
+    w.x = pack_bf16x2(x[0] * tau, x[1] * tau);
+    w.y = pack_bf16x2(x[2] * tau, x[3] * tau);
+    w.z = pack_bf16x2(x[4] * tau, x[5] * tau);
+    w.w = pack_bf16x2(x[6] * tau, x[7] * tau);
+    *reinterpret_cast<uint4 *>(&sm.k[key * KSTR + part * 8]) = w;
+  }
+  if (tid < Stage<D>::VUNITS) {
+    const int kg = tid % (BN / 4), dg = tid / (BN / 4);
+    const uint32_t a[4][4] = {{sg.v[0].x, sg.v[0].y, sg.v[0].z, sg.v[0].w},
+                              {sg.v[1].x, sg.v[1].y, sg.v[1].z, sg.v[1].w},
+                              {sg.v[2].x, sg.v[2].y, sg.v[2].z, sg.v[2].w},
+                              {sg.v[3].x, sg.v[3].y, sg.v[3].z, sg.v[3].w}};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // dims 2j (low halves) and 2j+1 (high halves) of keys kg*4 .. kg*4+3
+      uint2 lo, hi;
+      lo.x = lo_lo(a[0][j], a[1][j]);
+      lo.y = lo_lo(a[2][j], a[3][j]);
+      hi.x = hi_hi(a[0][j], a[1][j]);
+      hi.y = hi_hi(a[2][j], a[3][j]);
+      *reinterpret_cast<uint2 *>(&sm.vt[(dg * 8 + 2 * j) * VSTR + kg * 4]) = lo;
+      *reinterpret_cast<uint2 *>(&sm.vt[(dg * 8 + 2 * j + 1) * VSTR + kg * 4]) = hi;
+    }
+  }
+}
+
+template <int D>
+struct AttnState {
+  f32x4 o[2][D / 16];  // O^T tiles [row tile][dv tile]
+  float m[2];          // running max of scaled scores (log2 domain)
+  float l[2];          // lane-partial running sum
+};
+
+// Online-softmax update with the block staged in LDS.  `mask` selects the
+// masked path (tail keys >= nvalid, or causal keys kpos0 + key > row).
+template <int D, bool MASK>
+__device__ __forceinline__ void consume_block(const AttnSmem<D> &sm,
+                                              AttnState<D> &as,
+                                              const bf16x8 (&qf)[2][D / 32],
+                                              int nvalid, int64_t kpos0,
+                                              int64_t qpos0, float scale) {
+  constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
+  const int lane = threadIdx.x & 63;
   f32x4 s[4][2];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
@@ -115,26 +175,32 @@ __device__ __forceinline__ void attend_block(
   }
 
   bf16x8 pb[2][BN / 32];
+  bool moved = false;
+  float alpha[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const int64_t qpos = qpos0 + rt * 16 + (lane & 15);
+    if constexpr (MASK) {
+      const int64_t qpos = qpos0 + rt * 16 + (lane & 15);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kt * 16 + (lane >> 4) * 4 + i;
+          if (key >= nvalid || (kpos0 >= 0 && kpos0 + key > qpos))
+            s[kt][rt][i] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt * 16 + (lane >> 4) * 4 + i;
-        float x = s[kt][rt][i] * scale;
-        if (key >= nvalid || (kpos0 >= 0 && kpos0 + key > qpos)) x = -INFINITY;
-        s[kt][rt][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    }
+    for (int kt = 0; kt < 4; ++kt)
+      mx = fmaxf(fmaxf(mx, fmaxf(s[kt][rt][0], s[kt][rt][1])),
+                 fmaxf(s[kt][rt][2], s[kt][rt][3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(as.m[rt], mx);
+    const float m_new = fmaxf(as.m[rt], mx * scale);
+    moved |= m_new != as.m[rt];
     const float base = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = (as.m[rt] == -INFINITY) ? 0.f : exp2f(as.m[rt] - base);
+    alpha[rt] = (as.m[rt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(as.m[rt] - base);
     float psum = 0.f;
     uint32_t pk[4][2];
 #pragma unroll
@@ -142,20 +208,25 @@ __device__ __forceinline__ void attend_block(
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = exp2f(s[kt][rt][i] - base);
+        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][i], scale, -base));
         psum += p[i];
       }
-      pk[kt][0] = f2bf(p[0]) | (f2bf(p[1]) << 16);
-      pk[kt][1] = f2bf(p[2]) | (f2bf(p[3]) << 16);
+      pk[kt][0] = pack_bf16x2(p[0], p[1]);
+      pk[kt][1] = pack_bf16x2(p[2], p[3]);
     }
 #pragma unroll
     for (int ks = 0; ks < BN / 32; ++ks)
       pb[rt][ks] = as_bf16x8(make_uint4(pk[2 * ks][0], pk[2 * ks][1],
                                         pk[2 * ks + 1][0], pk[2 * ks + 1][1]));
-    as.l[rt] = as.l[rt] * alpha + psum;
+    as.l[rt] = as.l[rt] * alpha[rt] + psum;
     as.m[rt] = m_new;
+  }
+  // Rescale O only when some row maximum of the wave moved.
+  if (__ballot(moved)) {
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha;
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha[rt];
   }
 
   // O^T += V^T P^T
@@ -173,18 +244,56 @@ __device__ __forceinline__ void attend_block(
   }
 }
 
+// Stream `nkeys` keys starting at (kp, vp) through LDS.  kpos0 >= 0 gives the
+// position of the first key (window keys, causal); -1 marks memory slots.
 template <int D>
-__global__ __launch_bounds__(256) void k_attn_prefill(
-    kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
-    ChunkTable table) {
+__device__ __forceinline__ void attend_range(
+    AttnSmem<D> &sm, AttnState<D> &as, const bf16x8 (&qf)[2][D / 32],
+    const uint16_t *__restrict__ kp, int64_t kstride,
+    const uint16_t *__restrict__ vp, int64_t vstride, int nkeys, float tau,
+    int64_t kpos0, int64_t qpos0, float scale) {
+  if (nkeys <= 0) return;
+  Stage<D> sg;
+  stage_load<D>(sg, kp, kstride, vp, vstride, min(BN, nkeys));
+  for (int j0 = 0; j0 < nkeys; j0 += BN) {
+    const int nvalid = min(BN, nkeys - j0);
+    __syncthreads();  // the previous block is consumed
+    stage_store<D>(sm, sg, tau);
+    __syncthreads();
+    const int jn = j0 + BN;
+    if (jn < nkeys)
+      stage_load<D>(sg, kp + int64_t(jn) * kstride, kstride, vp + int64_t(jn) * vstride,
+                    vstride, min(BN, nkeys - jn));
+    const int64_t kb = kpos0 >= 0 ? kpos0 + j0 : -1;
+    // Wave-uniform block classification.
+    if (kb >= 0 && kb > qpos0 + 31) continue;  // above the wave's diagonal
+    const bool diag = kb >= 0 && kb + BN - 1 > qpos0;
+    if (nvalid < BN || diag)
+      consume_block<D, true>(sm, as, qf, nvalid, kb, qpos0, scale);
+    else
+      consume_block<D, false>(sm, as, qf, nvalid, kb, qpos0, scale);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256)
+void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
+                    int qtiles, int n_chunks, ChunkTable table) {
   __shared__ __attribute__((aligned(16))) AttnSmem<D> sm;
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
-  const int qrow = blockIdx.y;
+  // XCD-contiguous renumbering of the 1-D grid: logical order (q row, chunk, q tile).
+  const int N = gridDim.x;
+  const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int q8 = N / kXcds, r8 = N % kXcds;
+  const int logical = x * q8 + min(x, r8) + j;
+  const int per_row = n_chunks * qtiles;
+  const int qrow = logical / per_row;
+  const int rem = logical % per_row;
+  const int c_local = rem / qtiles, qt = rem % qtiles;
   const int b = qrow / Hq, hq = qrow % Hq;
   const int hk = hq / (Hq / Hkv);
   const int kvrow = b * Hkv + hk;
-  const int c_local = blockIdx.x / qtiles, qt = blockIdx.x % qtiles;
   const int m = chunk_begin + c_local;
   const int64_t T = A.T;
   const int64_t q0 = int64_t(m) * C + int64_t(qt) * BM;
@@ -225,20 +334,15 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
   if (m >= n && S > 0) {
     const int64_t soff = int64_t(table.snap_slot[c_local]) * A.snap_stride +
                          int64_t(kvrow) * A.snap_cap * D;
-    const uint16_t *sk = A.snap_k + soff;
-    const uint16_t *sv = A.snap_v + soff;
-    for (int j0 = 0; j0 < S; j0 += BN)
-      attend_block<D>(sm, as, qf, sk + int64_t(j0) * D, D, sv + int64_t(j0) * D, D,
-                      min(BN, S - j0), tau_s, -1, qpos0, scale);
+    attend_range<D>(sm, as, qf, A.snap_k + soff, D, A.snap_v + soff, D, S, tau_s,
+                    -1, qpos0, scale);
   }
   // Window tokens [wb, q_hi), causal.
   const int64_t wb = max(int64_t(0), int64_t(m - n + 1) * C);
   const uint16_t *kb = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
   const uint16_t *vb = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
-  for (int64_t k0 = wb; k0 < q_hi; k0 += BN)
-    attend_block<D>(sm, as, qf, kb + k0 * A.kv.k_st, A.kv.k_st, vb + k0 * A.kv.v_st,
-                    A.kv.v_st, int(min(int64_t(BN), q_hi - k0)), tau_f, k0, qpos0,
-                    scale);
+  attend_range<D>(sm, as, qf, kb + wb * A.kv.k_st, A.kv.k_st, vb + wb * A.kv.v_st,
+                  A.kv.v_st, int(q_hi - wb), tau_f, wb, qpos0, scale);
 
   // Normalise and store: lane holds dv = dt*16 + 4*(lane/16) + i of row lane%16.
   uint16_t *obase = static_cast<uint16_t *>(A.out) + b * A.o_sb + hq * A.o_sh;
@@ -253,8 +357,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
         uint2 w;
-        w.x = f2bf(as.o[rt][dt][0] * inv) | (f2bf(as.o[rt][dt][1] * inv) << 16);
-        w.y = f2bf(as.o[rt][dt][2] * inv) | (f2bf(as.o[rt][dt][3] * inv) << 16);
+        w.x = pack_bf16x2(as.o[rt][dt][0] * inv, as.o[rt][dt][1] * inv);
+        w.y = pack_bf16x2(as.o[rt][dt][2] * inv, as.o[rt][dt][3] * inv);
         *reinterpret_cast<uint2 *>(obase + t * A.o_st + dt * 16 + (lane >> 4) * 4) = w;
       }
     }
@@ -270,13 +374,14 @@ hipError_t launch_prefill_attention(const kvm_layer &L,
                                     hipStream_t stream) {
   if (n_chunks <= 0) return hipSuccess;
   const int qtiles = int((L.chunk_len + BM - 1) / BM);
-  dim3 grid(unsigned(n_chunks * qtiles), unsigned(L.batch * L.q_heads));
+  const int64_t n_wg = n_chunks * qtiles * L.batch * L.q_heads;
+  const dim3 grid{unsigned(n_wg), 1u, 1u};
   if (L.head_dim == 128)
     hipLaunchKernelGGL(k_attn_prefill<128>, grid, dim3(256), 0, stream, L, a,
-                       int(chunk_begin), qtiles, table);
+                       int(chunk_begin), qtiles, int(n_chunks), table);
   else
     hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), 0, stream, L, a,
-                       int(chunk_begin), qtiles, table);
+                       int(chunk_begin), qtiles, int(n_chunks), table);
   return hipGetLastError();
 }
 

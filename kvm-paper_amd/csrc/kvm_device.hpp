@@ -7,21 +7,24 @@
 namespace kvm {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// bfloat16 <-> float.  Rounding is round-to-nearest-even, the rounding torch
-// uses for every float -> bfloat16 conversion (c10/util/BFloat16.h).
+// bfloat16 <-> float.  float -> bfloat16 rounds to nearest even (the
+// rounding torch uses for every float -> bfloat16 conversion), done by the
+// gfx950 instruction v_cvt_pk_bf16_f32.
 __device__ __forceinline__ float bf2f(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return pack2bf(f, 0.f) & 0xffffu;
 }
 // Round a float to the nearest bfloat16 value, kept as float.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
@@ -39,10 +42,10 @@ __device__ __forceinline__ void unpack8(const uint4 u, float (&x)[8]) {
 }
 __device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
   uint4 u;
-  u.x = f2bf(x[0]) | (f2bf(x[1]) << 16);
-  u.y = f2bf(x[2]) | (f2bf(x[3]) << 16);
-  u.z = f2bf(x[4]) | (f2bf(x[5]) << 16);
-  u.w = f2bf(x[6]) | (f2bf(x[7]) << 16);
+  u.x = pack2bf(x[0], x[1]);
+  u.y = pack2bf(x[2], x[3]);
+  u.z = pack2bf(x[4], x[5]);
+  u.w = pack2bf(x[6], x[7]);
   return u;
 }
 __device__ __forceinline__ void load8(const uint16_t *p, float (&x)[8]) {

@@ -74,6 +74,13 @@ class OracleConfig:
     use_head_temps: bool = True
     use_vlens: bool = True
     fp32_routing: bool = True  # kvm_fp32_routing_reference.py:24-49
+    # Order of tokens whose append novelty ties at the cut.  "reference":
+    # torch.argsort(stable=False) exactly as kvm_mixer.py:69 calls it (the
+    # order of equal keys is whatever the CPU sort kernel produces; with
+    # AVX-512 it is not index order).  "lower_index": ties go to the lower
+    # token index, the rule of the reference's Triton kernel
+    # (kvm_triton_training_kernels.py:509-513) and of the HIP kernels.
+    append_tie_break: str = "reference"
 
     @property
     def max_state_len(self) -> int:
@@ -259,7 +266,7 @@ def front_attention(q, k, v, p: OracleParams, cfg: OracleConfig):
     )
 
 
-def split_append_merge(k_block, n_append, k_ref):
+def split_append_merge(k_block, n_append, k_ref, stable: bool = False):
     """Pick the n_append least-similar tokens for appending (kvm_mixer.py:44-75)."""
     B, H, L = int(k_block.size(0)), int(k_block.size(1)), int(k_block.size(2))
     n_append = min(max(int(n_append), 0), L)
@@ -275,7 +282,7 @@ def split_append_merge(k_block, n_append, k_ref):
     if int(k_ref.size(2)) == 0:
         return all_idx[:, :, n_merge:], all_idx[:, :, :n_merge]
     scores = torch.matmul(k_block, k_ref.transpose(-1, -2)).float().max(dim=-1).values
-    order = torch.argsort(scores, dim=-1, descending=False)
+    order = torch.argsort(scores, dim=-1, descending=False, stable=stable)
     app = torch.sort(order[..., :n_append], dim=-1).values
     mrg = torch.sort(order[..., n_append:], dim=-1).values
     return app, mrg
@@ -364,7 +371,9 @@ def update_from_overflow(
             record.s_k_before, record.s_v_before, record.s_vlen_before = s_k, s_v, s_vlen
         rec.updates.append(record)
     if n_app > 0:
-        app_idx, mrg_idx = split_append_merge(k_plain, n_app, _ln(s_k, p))
+        app_idx, mrg_idx = split_append_merge(
+            k_plain, n_app, _ln(s_k, p), stable=cfg.append_tie_break == "lower_index"
+        )
         k_merge, v_merge = _gather(k_gated, mrg_idx), _gather(v_gated, mrg_idx)
         s_k, s_v, s_vlen = append_rows(
             s_k, s_v, s_vlen, _gather(k_app, app_idx), _gather(v_app, app_idx), cfg

@@ -79,7 +79,7 @@ class LayerStatesCache:
 
 
 def err_stats(a: torch.Tensor, b: torch.Tensor):
-    d = (a.float().cpu() - b.float().cpu()).abs()
+    d = (a.detach().float().cpu() - b.detach().float().cpu()).abs()
     return float(d.max()), float(d.mean())
 
 
