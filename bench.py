@@ -202,8 +202,9 @@ def cpu_baseline(torch, sample_T):
         times.append(time.perf_counter() - t0)
     sec = min(times)
     return dict(value=B * sample_T / sec, unit="tokens/s", cores=threads, kind="port",
-                sample=f"oracle prefill of the first {sample_T} tokens of the config-2 layer "
-                       f"(B1 H32 D128 C512, 512 slots), best of 2 runs, {sec:.2f} s each")
+                sample=f"CPU oracle (eager restatement of model/kvm_mixer.py, fp32 routing) prefill of "
+                       f"{sample_T} tokens of the config-2 layer (B1 H32 D128 C512, 512 slots), "
+                       f"best of 2 runs: {sec:.2f} s")
 
 
 def main():
@@ -212,7 +213,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=256)
-    ap.add_argument("--cpu-sample", type=int, default=4096)
+    ap.add_argument("--cpu-sample", type=int, default=32768,
+                    help="tokens of the prefill workload the CPU baseline runs (default: all)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
     args = ap.parse_args()

@@ -16,69 +16,19 @@
 //   k_route<PREP=0, ROUTE>    (growable only) merge routing against the
 //       post-append state;
 //   k_merge_refresh           16 slots per workgroup: each slot gathers the
-//       tokens routed to it in token order (fp32 sum, deterministic, no
-//       atomics), writes bf16(state + bf16(sum)) and its LayerNorm /
-//       normalized-value attention rows.
+//       tokens routed to it in token order (an LDS list built by a ballot
+//       scan; fp32 sum, deterministic, no atomics), writes
+//       bf16(state + bf16(sum)) and its LayerNorm / normalized-value
+//       attention rows.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
+#include "kvm_seq.hpp"
 
 namespace kvm {
 namespace {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ int64_t seq_tok(const kvm_seq &s, int64_t t) {
-  return s.ring > 0 ? (t % s.ring) : t;
-}
-__device__ __forceinline__ const uint16_t *seq_k(const kvm_seq &s, int b,
-                                                 int h, int64_t t) {
-  return static_cast<const uint16_t *>(s.k) + b * s.k_sb + h * s.k_sh +
-         seq_tok(s, t) * s.k_st;
-}
-__device__ __forceinline__ const uint16_t *seq_v(const kvm_seq &s, int b,
-                                                 int h, int64_t t) {
-  return static_cast<const uint16_t *>(s.v) + b * s.v_sb + h * s.v_sh +
-         seq_tok(s, t) * s.v_st;
-}
-__device__ __forceinline__ float seq_g(const kvm_seq &s, int b, int h,
-                                       int64_t t) {
-  const uint16_t *g = static_cast<const uint16_t *>(s.gate) + b * s.g_sb +
-                      h * s.g_sh + seq_tok(s, t) * s.g_st;
-  return bf2f(*g);
-}
-
-// prep(k) = LayerNorm_s(k with dims < r zeroed), rounded to bf16
-// (model/kvm_mixer.py:120-129).
-template <int D>
-__device__ __forceinline__ void prep_key(float (&k)[8], int part,
-                                         const kvm_layer &L) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (part * 8 + i < L.rope_partial_dim) k[i] = 0.f;
-  layer_norm8<D>(k, part, static_cast<const float *>(L.ln_weight),
-                 static_cast<const float *>(L.ln_bias), float(L.ln_eps));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) k[i] = rbf(k[i]);
-}
-
-// Attention rows of one slot from its (bf16) key / value sums and vlen.
-template <int D>
-__device__ __forceinline__ void attn_rows(const float (&sk)[8],
-                                          const float (&sv)[8], float vlen,
-                                          int part, const kvm_layer &L,
-                                          float (&ka)[8], float (&va)[8]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ka[i] = sk[i];
-    va[i] = sv[i];
-  }
-  layer_norm8<D>(ka, part, static_cast<const float *>(L.ln_weight),
-                 static_cast<const float *>(L.ln_bias), float(L.ln_eps));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ka[i] = rbf(ka[i]);
-  attn_value8<D>(va, vlen);
-}
 
 // ---------------------------------------------------------------------------
 // Direct append: tokens [tok_begin, +n_tok) -> slots [slot_begin, +n_tok).
@@ -153,11 +103,15 @@ __global__ __launch_bounds__(kThreads) void k_refresh(kvm_layer L,
 // ---------------------------------------------------------------------------
 // Token x slot similarity on MFMA 16x16x32 bf16.
 //
-// Workgroup: 64 overflow tokens of one row, 4 waves of 16 tokens.  The
-// similarity is computed transposed, D^T[slot][token] = S_attn . X^T, so the
-// accumulator lane layout (lane l holds slots 4*(l/16)+i of token l%16)
-// reduces over slots within a lane and then across the 4 lane groups.
-// Slot rows stream through LDS in blocks of 64.
+// Workgroup: 64 overflow tokens of one row.  The similarity is computed
+// transposed, D^T[slot][token] = S_attn . X^T, so the accumulator lane layout
+// (lane l holds slots 4*(l/16)+i of token l%16) reduces over slots within a
+// lane, then across the 4 lane groups.  Each of the 4 waves takes a
+// contiguous quarter of the slots for all 64 tokens (the 4 token tiles stay
+// in registers as B operands); slot rows are read straight from global
+// memory into A-operand registers, the next 16-slot tile being fetched while
+// the current one is multiplied.  The per-wave results are combined in slot
+// order, so the first maximum wins as in torch.max.
 //
 // PREP: compute prep(k), gated streams from the raw tokens (written to
 //       scratch); otherwise read the routing operand from scratch.
@@ -173,25 +127,42 @@ __global__ __launch_bounds__(kThreads) void k_route(
   constexpr int STR = D + 8;  // LDS row stride (elements), 16 B pad
   constexpr int KS = D / 32;
   __shared__ __attribute__((aligned(16))) uint16_t tok_lds[64 * STR];
-  __shared__ __attribute__((aligned(16))) uint16_t slot_lds[64 * STR];
+  __shared__ float best_lds[4][64];
+  __shared__ int idx_lds[4][64];
 
   const int row = blockIdx.x;
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int tok0 = blockIdx.y * 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // (1) routing operand of the 64 tokens -> LDS (zeros past n_tok).
-  for (int p = tid; p < 64 * G; p += kThreads) {
+  // (1) routing operand of the 64 tokens -> LDS (zeros past n_tok).  All
+  //     token loads are issued before any is consumed.
+  constexpr int IT = 64 * G / kThreads;
+  uint4 kr[IT], vr[IT];
+  float gr[IT];
+  if constexpr (PREP) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int p = tid + it * kThreads;
+      const int i_tok = tok0 + p / G;
+      const int64_t t = tok_begin + (i_tok < n_tok ? i_tok : 0);
+      kr[it] = *reinterpret_cast<const uint4 *>(seq_k(src, b, h, t) + (p % G) * 8);
+      vr[it] = *reinterpret_cast<const uint4 *>(seq_v(src, b, h, t) + (p % G) * 8);
+      gr[it] = seq_g(src, b, h, t);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int p = tid + it * kThreads;
     const int lt = p / G, part = p % G;
     const int i_tok = tok0 + lt;
     const bool valid = i_tok < n_tok;
     float x[8];
     if constexpr (PREP) {
-      const int64_t t = tok_begin + (valid ? i_tok : 0);
       float k[8], v[8];
-      load8(seq_k(src, b, h, t) + part * 8, k);
-      load8(seq_v(src, b, h, t) + part * 8, v);
-      const float g = seq_g(src, b, h, t);
+      unpack8(kr[it], k);
+      unpack8(vr[it], v);
+      const float g = gr[it];
       prep_key<D>(k, part, L);
       float gk[8], gv[8];
 #pragma unroll
@@ -220,79 +191,122 @@ __global__ __launch_bounds__(kThreads) void k_route(
   }
   __syncthreads();
 
-  // (2) B operand (X^T): token wave*16 + lane%16, dims ks*32 + 8*(lane/16).
-  bf16x8 bx[KS];
+  // (2) B operands (X^T) of the 4 token tiles: token tt*16 + lane%16,
+  //     dims ks*32 + 8*(lane/16).
+  bf16x8 bx[4][KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    bx[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
-        &tok_lds[(wave * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      bx[tt][ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
+          &tok_lds[(tt * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
 
-  float best = -INFINITY;
-  int bidx = -1;
+  float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int bidx[4] = {-1, -1, -1, -1};
   const uint16_t *sbase = sref.k + int64_t(row) * sref.cap * D;
 
-  // (3) slot blocks of 64 rows.
-  for (int j0 = 0; j0 < s_lim; j0 += 64) {
-    __syncthreads();
-    for (int p = tid; p < 64 * G; p += kThreads) {
-      const int ls = p / G, part = p % G;
-      const int j = j0 + ls;
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if (j < s_lim)
-        u = *reinterpret_cast<const uint4 *>(sbase + int64_t(j) * D + part * 8);
-      *reinterpret_cast<uint4 *>(&slot_lds[ls * STR + part * 8]) = u;
+  // (3) this wave's 16-slot tiles [t_lo, t_hi), fetched NB tiles at a time
+  //     with the next batch in flight while the current one is multiplied.
+  constexpr int NB = 4;
+  const int ntiles = (s_lim + 15) / 16;
+  const int tw = (ntiles + 3) / 4;
+  const int t_lo = min(wave * tw, ntiles), t_hi = min(t_lo + tw, ntiles);
+  auto fetch = [&](int tile0, uint4 (&a)[NB][KS]) {
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt) {
+      const int j = (tile0 + bt) * 16 + (lane & 15);
+      const bool ok = tile0 + bt < t_hi && j < s_lim;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        a[bt][ks] = ok ? *reinterpret_cast<const uint4 *>(sbase + int64_t(j) * D + ks * 32 +
+                                                          (lane >> 4) * 8)
+                       : make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+  };
+  uint4 a_cur[NB][KS], a_nxt[NB][KS];
+  if (t_lo < t_hi) fetch(t_lo, a_cur);
+  for (int tile0 = t_lo; tile0 < t_hi; tile0 += NB) {
+    if (tile0 + NB < t_hi) fetch(tile0 + NB, a_nxt);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int bt = 0; bt < NB; ++bt) {
+      const int tile = tile0 + bt;
+      if (tile >= t_hi) break;
+      f32x4 acc[4];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(
-            &slot_lds[(st * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx[ks], acc, 0, 0, 0);
+      for (int tt = 0; tt < 4; ++tt) {
+        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a_cur[bt][ks]), bx[tt][ks],
+                                                            acc[tt], 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = j0 + st * 16 + (lane >> 4) * 4 + i;
-        if constexpr (NOVELTY) {
-          if (j < s_lim) best = fmaxf(best, rbf(acc[i]));
-        } else {
-          if (j >= protect && j < s_lim && acc[i] > best) {
-            best = acc[i];
-            bidx = j;
+        const int j = tile * 16 + (lane >> 4) * 4 + i;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          if constexpr (NOVELTY) {
+            if (j < s_lim) best[tt] = fmaxf(best[tt], rbf(acc[tt][i]));
+          } else {
+            if (j >= protect && j < s_lim && acc[tt][i] > best[tt]) {
+              best[tt] = acc[tt][i];
+              bidx[tt] = j;
+            }
           }
         }
       }
     }
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) a_cur[bt][ks] = a_nxt[bt][ks];
   }
 
-  // (4) combine the 4 lane groups holding the same token.
+  // (4) combine the 4 lane groups holding the same token, then the waves.
 #pragma unroll
-  for (int o = 16; o <= 32; o <<= 1) {
-    const float ob = __shfl_xor(best, o);
-    const int oi = __shfl_xor(bidx, o);
-    if constexpr (NOVELTY) {
-      best = fmaxf(best, ob);
-    } else {
-      if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) {
-        best = ob;
-        bidx = oi;
+  for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+      const float ob = __shfl_xor(best[tt], o);
+      const int oi = __shfl_xor(bidx[tt], o);
+      if constexpr (NOVELTY) {
+        best[tt] = fmaxf(best[tt], ob);
+      } else if (oi >= 0 && (bidx[tt] < 0 || ob > best[tt] || (ob == best[tt] && oi < bidx[tt]))) {
+        best[tt] = ob;
+        bidx[tt] = oi;
       }
     }
+    if (lane < 16) {
+      best_lds[wave][tt * 16 + lane] = best[tt];
+      idx_lds[wave][tt * 16 + lane] = bidx[tt];
+    }
   }
-  if (lane < 16) {
-    const int i_tok = tok0 + wave * 16 + lane;
+  __syncthreads();
+  if (tid < 64) {
+    const int i_tok = tok0 + tid;
+    float bv = best_lds[0][tid];
+    int bi = idx_lds[0][tid];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float ov = best_lds[w][tid];
+      const int oi = idx_lds[w][tid];
+      if constexpr (NOVELTY) {
+        bv = fmaxf(bv, ov);
+      } else if (oi >= 0 && (bi < 0 || ov > bv)) {  // waves hold increasing slots
+        bv = ov;
+        bi = oi;
+      }
+    }
     if (i_tok < n_tok) {
       const int64_t o = int64_t(row) * n_tok + i_tok;
       if constexpr (NOVELTY) {
-        sc.novelty[o] = best;
+        sc.novelty[o] = bv;
       } else if constexpr (PREP) {
         // No appends in this update: every token merges.
         sc.is_append[o] = 0;
-        sc.route[o] = bidx;
+        sc.route[o] = bi;
       } else {
-        if (sc.is_append[o] == 0) sc.route[o] = bidx;
+        if (sc.is_append[o] == 0) sc.route[o] = bi;
       }
     }
   }
@@ -377,54 +391,97 @@ __global__ __launch_bounds__(512) void k_rank_append(
 // Merge + refresh (model/kvm_mixer.py:329-335): slot j gains
 // bf16(sum of merge keys / values routed to it), summed in fp32 in token
 // order; every slot < s_after gets fresh attention rows in attn_out.
-// Workgroup: 4 waves x (64 / (D/8)) slots, D/8 lanes per slot.
+// Workgroup: 4 waves x (64 / (D/8)) slots, D/8 lanes per slot.  The tokens
+// routed to the workgroup's slots are first listed in LDS in token order
+// (a ballot scan, no global traffic), then each slot gathers its list four
+// rows at a time so the loads overlap.
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_merge_refresh(
     kvm_layer L, int n_tok, int s_after, kvm_state st, AttnRows attn_out,
     UpdateScratch sc) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  int *rt = reinterpret_cast<int *>(smem);
   constexpr int G = D / 8;
   constexpr int SPW = 64 / G;  // slots per wave
+  constexpr int SPB = 4 * SPW; // slots per workgroup
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  int *rt = reinterpret_cast<int *>(smem);  // [n_tok] slot of each token (-1: appended)
+  int *list = rt + n_tok;                   // [n_tok] tokens grouped by slot
+  __shared__ int counts[SPB];
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t base = int64_t(row) * n_tok;
+  const int part = lane % G;
+  const int grp = lane / G;
+  const int local = wave * SPW + grp;
+  const int j = blockIdx.y * SPB + local;
+  const bool valid = j < s_after;
+  const int jj = valid ? j : 0;
+
+  // The slot's current sums and vlen (in flight during the scans).
+  const int64_t so = (int64_t(row) * st.capacity + jj) * D + part * 8;
+  const uint4 k_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_k) + so);
+  const uint4 v_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_v) + so);
+  const float vlen = static_cast<const float *>(st.s_vlen)[int64_t(row) * st.capacity + jj];
+
   for (int t = tid; t < n_tok; t += kThreads)
     rt[t] = sc.is_append[base + t] ? -1 : sc.route[base + t];
   __syncthreads();
 
-  const int part = lane % G;
-  const int grp = lane / G;
-  const int j = blockIdx.y * (4 * SPW) + wave * SPW + grp;
-  const bool valid = j < s_after;
-  float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int cnt = 0;
   const uint64_t gmask = (G == 64) ? ~0ull : ((1ull << G) - 1ull);
+  int cnt = 0;
   for (int g0 = 0; g0 < n_tok; g0 += G) {
     const int t = g0 + part;
     const bool hit = valid && t < n_tok && rt[t] == j;
-    uint64_t m = (__ballot(hit) >> (grp * G)) & gmask;
-    while (m) {
-      const int p = __ffsll((unsigned long long)m) - 1;
-      m &= m - 1;
-      const int64_t off = (base + g0 + p) * D + part * 8;
-      float xk[8], xv[8];
-      load8(sc.gk + off, xk);
-      load8(sc.gv + off, xv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        sk[i] += xk[i];
-        sv[i] += xv[i];
+    cnt += __popcll((__ballot(hit) >> (grp * G)) & gmask);
+  }
+  if (part == 0) counts[local] = cnt;
+  __syncthreads();
+  int off = 0;
+  for (int i = 0; i < local; ++i) off += counts[i];
+  if (cnt > 0) {
+    int w = off;
+    for (int g0 = 0; g0 < n_tok; g0 += G) {
+      const int t = g0 + part;
+      const bool hit = valid && t < n_tok && rt[t] == j;
+      uint64_t m = (__ballot(hit) >> (grp * G)) & gmask;
+      while (m) {
+        const int p = __ffsll((unsigned long long)m) - 1;
+        m &= m - 1;
+        if (part == 0) list[w] = g0 + p;
+        ++w;
       }
-      ++cnt;
     }
   }
-  const int jj = valid ? j : 0;
-  const int64_t so = (int64_t(row) * st.capacity + jj) * D + part * 8;
+  __syncthreads();
+
+  float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < cnt; i0 += 4) {
+    uint4 xk[4], xv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i0 + u < cnt) {
+        const int64_t o = (base + list[off + i0 + u]) * D + part * 8;
+        xk[u] = *reinterpret_cast<const uint4 *>(sc.gk + o);
+        xv[u] = *reinterpret_cast<const uint4 *>(sc.gv + o);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i0 + u < cnt) {
+        float fk[8], fv[8];
+        unpack8(xk[u], fk);
+        unpack8(xv[u], fv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          sk[i] += fk[i];
+          sv[i] += fv[i];
+        }
+      }
+    }
+  }
   float k[8], v[8];
-  load8(static_cast<const uint16_t *>(st.s_k) + so, k);
-  load8(static_cast<const uint16_t *>(st.s_v) + so, v);
+  unpack8(k_raw, k);
+  unpack8(v_raw, v);
   if (cnt > 0) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -436,8 +493,6 @@ __global__ __launch_bounds__(kThreads) void k_merge_refresh(
       store8(static_cast<uint16_t *>(st.s_v) + so, v);
     }
   }
-  const float vlen =
-      static_cast<const float *>(st.s_vlen)[int64_t(row) * st.capacity + jj];
   float ka[8], va[8];
   attn_rows<D>(k, v, vlen, part, L, ka, va);
   if (valid) {
@@ -573,7 +628,7 @@ static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
   constexpr int spb = 4 * (64 / (D / 8));
   dim3 mgrid(rows, unsigned((s_after + spb - 1) / spb));
   hipLaunchKernelGGL(k_merge_refresh<D>, mgrid, dim3(kThreads),
-                     size_t(n_tok) * 4, stream, L, int(n_tok), s_after, st,
+                     size_t(n_tok) * 8, stream, L, int(n_tok), s_after, st,
                      attn_out, sc);
   return hipGetLastError();
 }
