@@ -27,11 +27,14 @@
 // hardware v_cvt_pk_bf16_f32, exp2 the raw v_exp_f32, the softmax scale is
 // folded into one fma per score, masks are applied only on tail / diagonal
 // blocks, the O rescale is skipped when no row maximum of the wave moved,
-// and a wave skips blocks that lie entirely above its causal diagonal.  The
-// next K/V block is fetched into registers while the current one is
-// consumed.  Workgroups are renumbered so that each XCD (dispatch is
-// round-robin over the 8 XCDs) runs a contiguous range of (head, chunk)
-// tiles: the window keys shared by neighbouring chunks stay in that XCD's L2.
+// and a wave skips 32-key halves that lie entirely above its causal
+// diagonal.  Latency: two LDS buffers (one barrier per block; the next
+// block is fetched while the current one is multiplied) and a single
+// inlined copy of the pipeline for both key ranges keep the kernel under
+// 256 VGPRs, so two workgroups share a CU and cover each other's waits.
+// Workgroups are renumbered so that each XCD (dispatch is round-robin over
+// the 8 XCDs) runs a contiguous range of (head, chunk) tiles: the window
+// keys shared by neighbouring chunks stay in that XCD's L2.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -150,51 +153,48 @@ struct AttnState {
   float l[2];          // lane-partial running sum
 };
 
-// Online-softmax update with the block staged in LDS.  `mask` selects the
-// masked path (tail keys >= nvalid, or causal keys kpos0 + key > row).
-template <int D, bool MASK>
-__device__ __forceinline__ void consume_block(const AttnSmem<D> &sm,
-                                              AttnState<D> &as,
-                                              const bf16x8 (&qf)[2][D / 32],
-                                              int nvalid, int64_t kpos0,
-                                              int64_t qpos0, float scale) {
+// Online-softmax update with 32 keys (half of a staged block, key offset
+// k0 in the block).  Masked path: keys >= nvalid, or causal keys
+// kpos0 + key > row (kpos0 < 0: memory slots, never causal).
+template <int D>
+__device__ __forceinline__ void consume_half(const AttnSmem<D> &sm, int k0,
+                                             AttnState<D> &as,
+                                             const bf16x8 (&qf)[2][D / 32],
+                                             bool masked, int nvalid,
+                                             int64_t kpos0, int64_t qpos0,
+                                             float scale) {
   constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
   const int lane = threadIdx.x & 63;
-  f32x4 s[4][2];
+  f32x4 s[2][2];
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
+  for (int kt = 0; kt < 2; ++kt) {
     s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
       const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(
-          &sm.k[(kt * 16 + (lane & 15)) * KSTR + ks * 32 + (lane >> 4) * 8]));
+          &sm.k[(k0 + kt * 16 + (lane & 15)) * KSTR + ks * 32 + (lane >> 4) * 8]));
       s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], s[kt][0], 0, 0, 0);
       s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], s[kt][1], 0, 0, 0);
     }
   }
-
-  bf16x8 pb[2][BN / 32];
+  bf16x8 pb[2];
   bool moved = false;
   float alpha[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    if constexpr (MASK) {
+    if (masked) {
       const int64_t qpos = qpos0 + rt * 16 + (lane & 15);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kt * 16 + (lane >> 4) * 4 + i;
-          if (key >= nvalid || (kpos0 >= 0 && kpos0 + key > qpos))
-            s[kt][rt][i] = -INFINITY;
+          const int key = k0 + kt * 16 + (lane >> 4) * 4 + i;
+          if (key >= nvalid || (kpos0 >= 0 && kpos0 + key > qpos)) s[kt][rt][i] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-      mx = fmaxf(fmaxf(mx, fmaxf(s[kt][rt][0], s[kt][rt][1])),
-                 fmaxf(s[kt][rt][2], s[kt][rt][3]));
+    float mx = fmaxf(fmaxf(fmaxf(s[0][rt][0], s[0][rt][1]), fmaxf(s[0][rt][2], s[0][rt][3])),
+                     fmaxf(fmaxf(s[1][rt][0], s[1][rt][1]), fmaxf(s[1][rt][2], s[1][rt][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(as.m[rt], mx * scale);
@@ -202,9 +202,9 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm,
     const float base = (m_new == -INFINITY) ? 0.f : m_new;
     alpha[rt] = (as.m[rt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(as.m[rt] - base);
     float psum = 0.f;
-    uint32_t pk[4][2];
+    uint32_t pk[2][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -214,10 +214,7 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm,
       pk[kt][0] = pack_bf16x2(p[0], p[1]);
       pk[kt][1] = pack_bf16x2(p[2], p[3]);
     }
-#pragma unroll
-    for (int ks = 0; ks < BN / 32; ++ks)
-      pb[rt][ks] = as_bf16x8(make_uint4(pk[2 * ks][0], pk[2 * ks][1],
-                                        pk[2 * ks + 1][0], pk[2 * ks + 1][1]));
+    pb[rt] = as_bf16x8(make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]));
     as.l[rt] = as.l[rt] * alpha[rt] + psum;
     as.m[rt] = m_new;
   }
@@ -228,58 +225,23 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm,
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha[rt];
   }
-
-  // O^T += V^T P^T
+  // O^T += V^T P^T over these 32 keys.
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) {
-#pragma unroll
-    for (int ks = 0; ks < BN / 32; ++ks) {
-      const uint16_t *vrow = &sm.vt[(dt * 16 + (lane & 15)) * VSTR + ks * 32 + (lane >> 4) * 4];
-      const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
-      const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
-      const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-      as.o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks], as.o[0][dt], 0, 0, 0);
-      as.o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks], as.o[1][dt], 0, 0, 0);
-    }
-  }
-}
-
-// Stream `nkeys` keys starting at (kp, vp) through LDS.  kpos0 >= 0 gives the
-// position of the first key (window keys, causal); -1 marks memory slots.
-template <int D>
-__device__ __forceinline__ void attend_range(
-    AttnSmem<D> &sm, AttnState<D> &as, const bf16x8 (&qf)[2][D / 32],
-    const uint16_t *__restrict__ kp, int64_t kstride,
-    const uint16_t *__restrict__ vp, int64_t vstride, int nkeys, float tau,
-    int64_t kpos0, int64_t qpos0, float scale) {
-  if (nkeys <= 0) return;
-  Stage<D> sg;
-  stage_load<D>(sg, kp, kstride, vp, vstride, min(BN, nkeys));
-  for (int j0 = 0; j0 < nkeys; j0 += BN) {
-    const int nvalid = min(BN, nkeys - j0);
-    __syncthreads();  // the previous block is consumed
-    stage_store<D>(sm, sg, tau);
-    __syncthreads();
-    const int jn = j0 + BN;
-    if (jn < nkeys)
-      stage_load<D>(sg, kp + int64_t(jn) * kstride, kstride, vp + int64_t(jn) * vstride,
-                    vstride, min(BN, nkeys - jn));
-    const int64_t kb = kpos0 >= 0 ? kpos0 + j0 : -1;
-    // Wave-uniform block classification.
-    if (kb >= 0 && kb > qpos0 + 31) continue;  // above the wave's diagonal
-    const bool diag = kb >= 0 && kb + BN - 1 > qpos0;
-    if (nvalid < BN || diag)
-      consume_block<D, true>(sm, as, qf, nvalid, kb, qpos0, scale);
-    else
-      consume_block<D, false>(sm, as, qf, nvalid, kb, qpos0, scale);
+    const uint16_t *vrow = &sm.vt[(dt * 16 + (lane & 15)) * VSTR + k0 + (lane >> 4) * 4];
+    const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
+    const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
+    const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+    as.o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0], as.o[0][dt], 0, 0, 0);
+    as.o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1], as.o[1][dt], 0, 0, 0);
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(256)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
                     int qtiles, int n_chunks, ChunkTable table) {
-  __shared__ __attribute__((aligned(16))) AttnSmem<D> sm;
+  __shared__ __attribute__((aligned(16))) AttnSmem<D> sm[2];
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
   // XCD-contiguous renumbering of the 1-D grid: logical order (q row, chunk, q tile).
@@ -329,20 +291,57 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
   const float tau_s = static_cast<const float *>(L.state_temp)[hq];
   const float tau_f = static_cast<const float *>(L.front_temp)[hq];
 
-  // Memory slots.
+  // Key ranges: the memory slots (state temperature, never causal), then
+  // the window tokens [wb, q_hi) (front temperature, causal).  One copy of
+  // the pipeline serves both.
   const int S = table.state_len[c_local];
-  if (m >= n && S > 0) {
-    const int64_t soff = int64_t(table.snap_slot[c_local]) * A.snap_stride +
-                         int64_t(kvrow) * A.snap_cap * D;
-    attend_range<D>(sm, as, qf, A.snap_k + soff, D, A.snap_v + soff, D, S, tau_s,
-                    -1, qpos0, scale);
-  }
-  // Window tokens [wb, q_hi), causal.
   const int64_t wb = max(int64_t(0), int64_t(m - n + 1) * C);
-  const uint16_t *kb = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
-  const uint16_t *vb = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
-  attend_range<D>(sm, as, qf, kb + wb * A.kv.k_st, A.kv.k_st, vb + wb * A.kv.v_st,
-                  A.kv.v_st, int(q_hi - wb), tau_f, wb, qpos0, scale);
+  const int64_t soff = int64_t(table.snap_slot[c_local]) * A.snap_stride +
+                       int64_t(kvrow) * A.snap_cap * D;
+  const uint16_t *kwin = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
+  const uint16_t *vwin = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
+#pragma unroll 1
+  for (int seg = 0; seg < 2; ++seg) {
+    const bool st = seg == 0;
+    const int nkeys = st ? ((m >= n) ? S : 0) : int(q_hi - wb);
+    if (nkeys <= 0) continue;
+    const uint16_t *kp = st ? A.snap_k + soff : kwin + wb * A.kv.k_st;
+    const uint16_t *vp = st ? A.snap_v + soff : vwin + wb * A.kv.v_st;
+    const int64_t kstride = st ? D : A.kv.k_st;
+    const int64_t vstride = st ? D : A.kv.v_st;
+    const float tau = st ? tau_s : tau_f;
+    const int64_t kpos0 = st ? -1 : wb;
+    const int nb = (nkeys + BN - 1) / BN;
+    __syncthreads();  // both buffers are free
+    {
+      Stage<D> sg;
+      stage_load<D>(sg, kp, kstride, vp, vstride, min(BN, nkeys));
+      stage_store<D>(sm[0], sg, tau);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int j = 0; j < nb; ++j) {
+      const int j0 = j * BN;
+      const int nvalid = min(BN, nkeys - j0);
+      const int64_t kb = kpos0 >= 0 ? kpos0 + j0 : -1;
+      const bool more = j + 1 < nb;
+      Stage<D> sg;
+      if (more) {
+        const int jn = (j + 1) * BN;
+        stage_load<D>(sg, kp + int64_t(jn) * kstride, kstride, vp + int64_t(jn) * vstride,
+                      vstride, min(BN, nkeys - jn));
+      }
+      const bool masked = nvalid < BN || (kb >= 0 && kb + BN - 1 > qpos0);
+#pragma unroll 1
+      for (int h = 0; h < 2; ++h) {
+        // wave-uniform: skip halves above the wave's causal diagonal / past the tail
+        const bool live = h * 32 < nvalid && !(kb >= 0 && kb + h * 32 > qpos0 + 31);
+        if (live) consume_half<D>(sm[j & 1], h * 32, as, qf, masked, nvalid, kb, qpos0, scale);
+      }
+      if (more) stage_store<D>(sm[(j + 1) & 1], sg, tau);
+      __syncthreads();
+    }
+  }
 
   // Normalise and store: lane holds dv = dt*16 + 4*(lane/16) + i of row lane%16.
   uint16_t *obase = static_cast<uint16_t *>(A.out) + b * A.o_sb + hq * A.o_sh;
