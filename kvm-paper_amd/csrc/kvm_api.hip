@@ -93,6 +93,8 @@ hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct PrefillLayout {
+  size_t slices;       // per-update scratch slices (one prep batch)
+  size_t slice_bytes;
   size_t update_bytes;
   size_t snap_elems;  // elements of one snapshot array (keys or values)
   size_t total;
@@ -101,7 +103,10 @@ struct PrefillLayout {
 PrefillLayout prefill_layout(const kvm_prefill_desc *d) {
   PrefillLayout p;
   const kvm_layer &L = d->layer;
-  p.update_bytes = align256(size_t(kvm::update_scratch_bytes(L, L.chunk_len)));
+  p.slices = size_t(std::max<int64_t>(1, std::min<int64_t>(d->n_updates, kvm::kMaxPrep)));
+  p.slice_bytes = size_t(kvm::update_slice_bytes(L, L.chunk_len));
+  p.update_bytes = align256(p.slices * p.slice_bytes +
+                            size_t(kvm::update_keys_bytes(L, L.chunk_len)));
   p.snap_elems = size_t(L.batch * L.kv_heads) * size_t(d->max_state_len) *
                  size_t(L.head_dim);
   p.total = p.update_bytes +
@@ -206,22 +211,22 @@ int kvm_state_update(const kvm_layer *layer, const kvm_seq *src,
   if (!workspace || workspace_bytes < need)
     return fail(KVM_ESPACE, "update workspace of %lld bytes is smaller than %lld",
                 (long long)workspace_bytes, (long long)need);
-  kvm::UpdateScratch sc = kvm::carve_update_scratch(workspace, *layer, n_tok);
+  kvm::UpdateScratch sc = kvm::carve_update_scratch(
+      workspace, static_cast<unsigned char *>(workspace) + kvm::update_slice_bytes(*layer, n_tok),
+      *layer, n_tok);
   kvm::AttnRows in{static_cast<uint16_t *>(st->s_k_attn),
                    static_cast<uint16_t *>(st->s_v_attn), st->capacity};
   kvm::AttnRows out{static_cast<uint16_t *>(attn_k_out),
                     static_cast<uint16_t *>(attn_v_out), st->capacity};
   hipStream_t s = as_stream(stream);
-  KVM_HIP(kvm::launch_update(*layer, *src, tok_begin, n_tok, state_before,
-                             n_append, *st, in, out, sc, s),
+  kvm::PrepList pl;
+  pl.count = 1;
+  pl.tok_begin[0] = int32_t(tok_begin);
+  KVM_HIP(kvm::launch_prep(*layer, *src, pl, n_tok, sc, 0, s), "kvm_state_update");
+  KVM_HIP(kvm::launch_zero_keys(*layer, n_tok, sc, s), "kvm_state_update");
+  KVM_HIP(kvm::launch_update(*layer, *src, tok_begin, n_tok, state_before, n_append, *st, in,
+                             out, sc, 0, route_out, append_out, s),
           "kvm_state_update");
-  const size_t bytes = size_t(layer->batch * layer->kv_heads) * size_t(n_tok) * 4;
-  if (route_out)
-    KVM_HIP(hipMemcpyAsync(route_out, sc.route, bytes, hipMemcpyDeviceToDevice, s),
-            "route copy");
-  if (append_out)
-    KVM_HIP(hipMemcpyAsync(append_out, sc.is_append, bytes, hipMemcpyDeviceToDevice, s),
-            "append flag copy");
   return KVM_OK;
 }
 
@@ -345,7 +350,7 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
     return KVM_OK;
   };
   unsigned char *ws = static_cast<unsigned char *>(d->workspace);
-  kvm::UpdateScratch sc = kvm::carve_update_scratch(ws, L, C);
+  kvm::UpdateScratch sc = kvm::carve_update_scratch(ws, ws + lay.slices * lay.slice_bytes, L, C);
   uint16_t *snap_k = reinterpret_cast<uint16_t *>(ws + lay.update_bytes);
   const size_t snap_bytes = align256(lay.snap_elems * 2);
   uint16_t *snap_v = reinterpret_cast<uint16_t *>(
@@ -359,6 +364,7 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
 
   // Initial state: the first min(T, C) tokens (model/kvm_mixer.py:434-447).
   if ((rc = mark(0)) != KVM_OK) return rc;
+  KVM_HIP(kvm::launch_zero_keys(L, C, sc, s), "key reset");
   KVM_HIP(kvm::launch_append_direct(L, d->kv, 0, L0, d->state, 0, snap_rows(0),
                                     L.gate_initial != 0, s),
           "initial state");
@@ -412,18 +418,20 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
           d->chunk_snapshot[next_chunk] <= u + 1 - R)
         return fail(KVM_EINVAL, "snapshot ring too small for the schedule");
     }
-    KVM_HIP(kvm::launch_update(L, d->kv, d->upd_token_begin[u], C,
-                               d->upd_state_before[u], d->upd_n_append[u],
-                               d->state, snap_rows(u), snap_rows(u + 1), sc, s),
+    // Overflow-token streams of the next batch of updates, ahead of the chain.
+    if (u % int64_t(lay.slices) == 0) {
+      kvm::PrepList pl;
+      pl.count = int32_t(std::min<int64_t>(int64_t(lay.slices), d->n_updates - u));
+      for (int i = 0; i < pl.count; ++i) pl.tok_begin[i] = d->upd_token_begin[u + i];
+      KVM_HIP(kvm::launch_prep(L, d->kv, pl, C, sc, int64_t(lay.slice_bytes), s), "prep");
+    }
+    const kvm::UpdateScratch su =
+        kvm::scratch_slice(sc, int64_t(lay.slice_bytes), int(u % int64_t(lay.slices)));
+    KVM_HIP(kvm::launch_update(L, d->kv, d->upd_token_begin[u], C, d->upd_state_before[u],
+                               d->upd_n_append[u], d->state, snap_rows(u), snap_rows(u + 1), su,
+                               int(u & 1), d->route_log ? d->route_log + u * log_stride : nullptr,
+                               d->append_log ? d->append_log + u * log_stride : nullptr, s),
             "state update");
-    if (d->route_log)
-      KVM_HIP(hipMemcpyAsync(d->route_log + u * log_stride, sc.route, log_stride * 4,
-                             hipMemcpyDeviceToDevice, s),
-              "route log copy");
-    if (d->append_log)
-      KVM_HIP(hipMemcpyAsync(d->append_log + u * log_stride, sc.is_append,
-                             log_stride * 4, hipMemcpyDeviceToDevice, s),
-              "append log copy");
   }
   if ((rc = mark(1)) != KVM_OK) return rc;
   if ((rc = flush(d->n_updates + 1)) != KVM_OK) return rc;

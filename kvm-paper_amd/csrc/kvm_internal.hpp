@@ -14,13 +14,40 @@ struct UpdateScratch {
   uint16_t *pk;       // prep(k)                      bf16 [rows, n_tok, D]
   uint16_t *gk;       // merge key  (gated or not)    bf16 [rows, n_tok, D]
   uint16_t *gv;       // merge value (gated or not)   bf16 [rows, n_tok, D]
-  float *novelty;     // bf16-rounded max similarity  fp32 [rows, n_tok]
-  int32_t *route;     // destination slot             int32 [rows, n_tok]
+  uint64_t *rkey[2];  // route max-reduction keys, alternating per update [rows, n_tok]
+  uint32_t *nkey;     // novelty max-reduction keys   [rows, n_tok]
+  int32_t *route;     // slot of appended tokens      int32 [rows, n_tok]
   int32_t *is_append; // 1 if appended                int32 [rows, n_tok]
 };
 
-int64_t update_scratch_bytes(const kvm_layer &L, int64_t n_tok);
-UpdateScratch carve_update_scratch(void *ws, const kvm_layer &L, int64_t n_tok);
+// Scratch of updates: a slice per update (pk, gk, gv, route, is_append; the
+// first three at byte offsets 0, A, 2A) and one shared region of reduction
+// keys.
+int64_t update_slice_bytes(const kvm_layer &L, int64_t n_tok);
+int64_t update_keys_bytes(const kvm_layer &L, int64_t n_tok);
+int64_t update_scratch_bytes(const kvm_layer &L, int64_t n_tok);  // one slice + keys
+UpdateScratch carve_update_scratch(void *slice, void *keys, const kvm_layer &L,
+                                   int64_t n_tok);
+// The per-update pointers of slice u (slices are slice_bytes apart).
+__host__ __device__ inline UpdateScratch scratch_slice(UpdateScratch s0, int64_t slice_bytes,
+                                                       int u) {
+  const int64_t o = slice_bytes * u;
+  s0.pk = reinterpret_cast<uint16_t *>(reinterpret_cast<unsigned char *>(s0.pk) + o);
+  s0.gk = reinterpret_cast<uint16_t *>(reinterpret_cast<unsigned char *>(s0.gk) + o);
+  s0.gv = reinterpret_cast<uint16_t *>(reinterpret_cast<unsigned char *>(s0.gv) + o);
+  s0.route = reinterpret_cast<int32_t *>(reinterpret_cast<unsigned char *>(s0.route) + o);
+  s0.is_append = reinterpret_cast<int32_t *>(reinterpret_cast<unsigned char *>(s0.is_append) + o);
+  return s0;
+}
+constexpr int kMaxPrep = 64;
+struct PrepList {
+  int32_t count;
+  int32_t tok_begin[kMaxPrep];  // first overflow token of each update (ring index for rings)
+};
+// Overflow-token streams of P.count updates into slices 0..count-1.
+hipError_t launch_prep(const kvm_layer &L, const kvm_seq &src, const PrepList &P,
+                       int64_t n_tok, const UpdateScratch &s0, int64_t slice_bytes,
+                       hipStream_t stream);
 
 // Attention-row arrays of a state: bf16 [rows, cap, D] each.
 struct AttnRows {
@@ -42,10 +69,16 @@ hipError_t launch_refresh(const kvm_layer &L, const kvm_state &st,
 // One update.  Routing reads attn_in (the attention rows of the state before
 // the update; appended rows are added to it), the refreshed rows of every
 // slot < state_before + n_append are written to attn_out.
+// The key buffers must be zero before the first update on a workspace
+// (launch_zero_keys); each update then clears the buffer of the next one.
+// `parity` alternates between consecutive updates on the same workspace.
+hipError_t launch_zero_keys(const kvm_layer &L, int64_t n_tok,
+                            const UpdateScratch &sc, hipStream_t stream);
 hipError_t launch_update(const kvm_layer &L, const kvm_seq &src,
                          int64_t tok_begin, int64_t n_tok, int64_t state_before,
                          int64_t n_append, const kvm_state &st, AttnRows attn_in,
-                         AttnRows attn_out, const UpdateScratch &sc,
+                         AttnRows attn_out, const UpdateScratch &sc, int parity,
+                         int32_t *route_out, int32_t *append_out,
                          hipStream_t stream);
 
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,

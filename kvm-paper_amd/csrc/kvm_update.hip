@@ -6,20 +6,19 @@
 // model/kvm_triton_mixer.py:199-211 (one rounded state write, cached
 // normalized state rows).
 //
-// One update is up to four launches over rows = batch * kv_heads:
-//   k_route<PREP=1, NOVELTY>  64 tokens per workgroup: LayerNorm_s of the
-//       overflow keys, gated streams to scratch, then the token x slot
-//       similarity on bf16 MFMA (fp32 accumulate) and a per-token reduction
-//       (argmax for merges, bf16-rounded max for append novelty);
-//   k_rank_append             (growable memory only) one workgroup per row
-//       ranks novelty in LDS, appends the least novel tokens as new slots;
-//   k_route<PREP=0, ROUTE>    (growable only) merge routing against the
-//       post-append state;
-//   k_merge_refresh           16 slots per workgroup: each slot gathers the
-//       tokens routed to it in token order (an LDS list built by a ballot
-//       scan; fp32 sum, deterministic, no atomics), writes
-//       bf16(state + bf16(sum)) and its LayerNorm / normalized-value
-//       attention rows.
+// An update is a prep pass (batched ahead over many updates) and then up
+// to four launches over rows = batch * kv_heads:
+//   k_route<NOVELTY>      (growable memory) bf16-rounded max similarity of
+//       every overflow token to the current slots, 64 tokens x 128 slots
+//       per workgroup on MFMA, combined by an order-independent atomicMax;
+//   k_rank_append         (growable) one workgroup per row ranks novelty in
+//       LDS and appends the least novel tokens as new slots;
+//   k_route<ROUTE>        fp32 similarity of the merge keys to the slots,
+//       first argmax (same split and combination);
+//   k_merge_refresh       16 slots per workgroup: each slot sums the tokens
+//       routed to it in token order (fp32, deterministic, no global
+//       atomics), writes bf16(state + bf16(sum)) and its LayerNorm /
+//       normalized-value attention rows.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -101,168 +100,177 @@ __global__ __launch_bounds__(kThreads) void k_refresh(kvm_layer L,
 }
 
 // ---------------------------------------------------------------------------
-// Token x slot similarity on MFMA 16x16x32 bf16.
-//
-// Workgroup: 64 overflow tokens of one row.  The similarity is computed
-// transposed, D^T[slot][token] = S_attn . X^T, so the accumulator lane layout
-// (lane l holds slots 4*(l/16)+i of token l%16) reduces over slots within a
-// lane, then across the 4 lane groups.  Each of the 4 waves takes a
-// contiguous quarter of the slots for all 64 tokens (the 4 token tiles stay
-// in registers as B operands); slot rows are read straight from global
-// memory into A-operand registers, the next 16-slot tile being fetched while
-// the current one is multiplied.  The per-wave results are combined in slot
-// order, so the first maximum wins as in torch.max.
-//
-// PREP: compute prep(k), gated streams from the raw tokens (written to
-//       scratch); otherwise read the routing operand from scratch.
-// NOVELTY: operand prep(k) and value max_j bf16(prep(k).s_attn_j) over all
-//       s_lim slots (model/kvm_mixer.py:66-68); otherwise operand = merge key
-//       and value = first argmax over slots [protect, s_lim) of the fp32 dot
-//       (model/kvm_fp32_routing_reference.py:30-34).
-template <int D, bool PREP, bool NOVELTY>
-__global__ __launch_bounds__(kThreads) void k_route(
-    kvm_layer L, kvm_seq src, int64_t tok_begin, int n_tok, AttnRows sref,
-    int s_lim, int protect, UpdateScratch sc) {
-  constexpr int G = D / 8;
-  constexpr int STR = D + 8;  // LDS row stride (elements), 16 B pad
-  constexpr int KS = D / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t tok_lds[64 * STR];
-  __shared__ float best_lds[4][64];
-  __shared__ int idx_lds[4][64];
+// Reduction keys.  The per-token maximum over slots is combined across
+// workgroups with integer atomicMax on order-preserving encodings, which
+// is exact and independent of arrival order:
+//   novelty  u32  mono(bf16-rounded similarity)
+//   route    u64  mono(fp32 similarity) << 32 | (0xffffffff - slot)
+// so the largest similarity wins and, among equal similarities, the lowest
+// slot (torch.max returns the first maximum).  0 means "no candidate".
+__device__ __forceinline__ uint32_t mono(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unmono(uint32_t m) {
+  return __uint_as_float((m & 0x80000000u) ? (m & 0x7fffffffu) : ~m);
+}
 
+// ---------------------------------------------------------------------------
+// Overflow-token streams of a batch of updates (independent of the state,
+// so computed ahead of the update chain): prep(k) = LayerNorm_s(k with dims
+// < rope_partial_dim zeroed) (model/kvm_mixer.py:120-129), the merge key
+// bf16(prep(k) * g) and value bf16(v * g) when gated (:264-281), and the
+// append flags cleared.  grid (rows, token tiles of 64, updates).
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_prep(kvm_layer L, kvm_seq src, PrepList P,
+                                                   int n_tok, UpdateScratch s0,
+                                                   int64_t slice_bytes) {
+  constexpr int G = D / 8;
+  constexpr int IT = 64 * G / kThreads;
   const int row = blockIdx.x;
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int tok0 = blockIdx.y * 64;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-  // (1) routing operand of the 64 tokens -> LDS (zeros past n_tok).  All
-  //     token loads are issued before any is consumed.
-  constexpr int IT = 64 * G / kThreads;
+  const UpdateScratch sc = scratch_slice(s0, slice_bytes, blockIdx.z);
+  const int64_t tok_begin = P.tok_begin[blockIdx.z];
+  const int tid = threadIdx.x;
+  const int64_t rbase = int64_t(row) * n_tok;
   uint4 kr[IT], vr[IT];
   float gr[IT];
-  if constexpr (PREP) {
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int p = tid + it * kThreads;
-      const int i_tok = tok0 + p / G;
-      const int64_t t = tok_begin + (i_tok < n_tok ? i_tok : 0);
-      kr[it] = *reinterpret_cast<const uint4 *>(seq_k(src, b, h, t) + (p % G) * 8);
-      vr[it] = *reinterpret_cast<const uint4 *>(seq_v(src, b, h, t) + (p % G) * 8);
-      gr[it] = seq_g(src, b, h, t);
-    }
+  for (int it = 0; it < IT; ++it) {
+    const int p = tid + it * kThreads;
+    const int i_tok = tok0 + p / G;
+    const int64_t t = tok_begin + (i_tok < n_tok ? i_tok : 0);
+    kr[it] = *reinterpret_cast<const uint4 *>(seq_k(src, b, h, t) + (p % G) * 8);
+    vr[it] = *reinterpret_cast<const uint4 *>(seq_v(src, b, h, t) + (p % G) * 8);
+    gr[it] = seq_g(src, b, h, t);
   }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int p = tid + it * kThreads;
-    const int lt = p / G, part = p % G;
-    const int i_tok = tok0 + lt;
-    const bool valid = i_tok < n_tok;
-    float x[8];
-    if constexpr (PREP) {
-      float k[8], v[8];
-      unpack8(kr[it], k);
-      unpack8(vr[it], v);
-      const float g = gr[it];
-      prep_key<D>(k, part, L);
-      float gk[8], gv[8];
+    const int i_tok = tok0 + p / G, part = p % G;
+    float k[8], v[8];
+    unpack8(kr[it], k);
+    unpack8(vr[it], v);
+    const float g = gr[it];
+    prep_key<D>(k, part, L);
+    float gk[8], gv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        gk[i] = L.gate_keys ? rbf(k[i] * g) : k[i];
-        gv[i] = L.gate_values ? rbf(v[i] * g) : v[i];
-      }
-      if (valid) {
-        const int64_t off = (int64_t(row) * n_tok + i_tok) * D + part * 8;
-        store8(sc.pk + off, k);
-        store8(sc.gk + off, gk);
-        store8(sc.gv + off, gv);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = valid ? (NOVELTY ? k[i] : gk[i]) : 0.f;
-    } else {
-      if (valid) {
-        const int64_t off = (int64_t(row) * n_tok + i_tok) * D + part * 8;
-        load8((NOVELTY ? sc.pk : sc.gk) + off, x);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = 0.f;
-      }
+    for (int i = 0; i < 8; ++i) {
+      gk[i] = L.gate_keys ? rbf(k[i] * g) : k[i];
+      gv[i] = L.gate_values ? rbf(v[i] * g) : v[i];
     }
-    store8(&tok_lds[lt * STR + part * 8], x);
+    if (i_tok < n_tok) {
+      const int64_t off = (rbase + i_tok) * D + part * 8;
+      store8(sc.pk + off, k);
+      store8(sc.gk + off, gk);
+      store8(sc.gv + off, gv);
+      if (part == 0) sc.is_append[rbase + i_tok] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Token x slot similarity on MFMA 16x16x32 bf16.
+//
+// Workgroup: 64 overflow tokens x one split of at most kSplit slots of one
+// row (grid: rows x token tiles x slot splits).  The similarity is computed
+// transposed, D^T[slot][token] = S_attn . X^T, so the accumulator lane
+// layout (lane l holds slots 4*(l/16)+i of token l%16) reduces over slots
+// within a lane, then across the 4 lane groups and the 4 waves (LDS); one
+// atomicMax per token and workgroup publishes the split's result.  Each wave
+// loads its two 16-slot tiles straight into A-operand registers at kernel
+// start, so the slot rows are in flight while the tokens are prepared.
+//
+// The operand comes from the update's scratch slice (written by k_prep):
+// NOVELTY: prep(k), value max_j bf16(prep(k).s_attn_j) over all s_lim slots
+//       (model/kvm_mixer.py:66-68); otherwise the merge key, value = first
+//       argmax over slots [protect, s_lim) of the fp32 dot
+//       (model/kvm_fp32_routing_reference.py:30-34).
+constexpr int kSplit = 128;  // slots per workgroup
+
+template <int D, bool NOVELTY>
+__global__ __launch_bounds__(kThreads) void k_route(
+    kvm_layer L, int n_tok, AttnRows sref, int s_lim, int protect, UpdateScratch sc,
+    int parity) {
+  constexpr int G = D / 8;
+  constexpr int STR = D + 8;  // LDS row stride (elements), 16 B pad
+  constexpr int KS = D / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t tok_lds[64 * STR];
+  __shared__ uint32_t hi_lds[4][64];
+  __shared__ int idx_lds[4][64];
+
+  const int row = blockIdx.x;
+  const int tok0 = blockIdx.y * 64;
+  const int split = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t rbase = int64_t(row) * n_tok;
+
+  // Slot rows of this wave (two 16-slot tiles) and the 64 token operands,
+  // all issued before any is used.
+  const uint16_t *sbase = sref.k + int64_t(row) * sref.cap * D;
+  const int jw = split * kSplit + wave * 32;
+  uint4 a_reg[2][KS];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int j = jw + st * 16 + (lane & 15);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      a_reg[st][ks] = j < s_lim ? *reinterpret_cast<const uint4 *>(sbase + int64_t(j) * D + ks * 32 +
+                                                                   (lane >> 4) * 8)
+                                : make_uint4(0, 0, 0, 0);
+  }
+  constexpr int IT = 64 * G / kThreads;
+  const uint16_t *opnd = NOVELTY ? sc.pk : sc.gk;
+  uint4 xr[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int p = tid + it * kThreads;
+    const int i_tok = tok0 + p / G;
+    xr[it] = i_tok < n_tok ? *reinterpret_cast<const uint4 *>(opnd + (rbase + i_tok) * D + (p % G) * 8)
+                           : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int p = tid + it * kThreads;
+    *reinterpret_cast<uint4 *>(&tok_lds[(p / G) * STR + (p % G) * 8]) = xr[it];
   }
   __syncthreads();
 
-  // (2) B operands (X^T) of the 4 token tiles: token tt*16 + lane%16,
-  //     dims ks*32 + 8*(lane/16).
-  bf16x8 bx[4][KS];
+  // (2) similarity of the 4 token tiles against the wave's 32 slots.
+  float best[4];
+  int bidx[4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
+  for (int tt = 0; tt < 4; ++tt) {
+    best[tt] = -INFINITY;
+    bidx[tt] = -1;
+    bf16x8 bx[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      bx[tt][ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
+      bx[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
           &tok_lds[(tt * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
-
-  float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  int bidx[4] = {-1, -1, -1, -1};
-  const uint16_t *sbase = sref.k + int64_t(row) * sref.cap * D;
-
-  // (3) this wave's 16-slot tiles [t_lo, t_hi), fetched NB tiles at a time
-  //     with the next batch in flight while the current one is multiplied.
-  constexpr int NB = 4;
-  const int ntiles = (s_lim + 15) / 16;
-  const int tw = (ntiles + 3) / 4;
-  const int t_lo = min(wave * tw, ntiles), t_hi = min(t_lo + tw, ntiles);
-  auto fetch = [&](int tile0, uint4 (&a)[NB][KS]) {
 #pragma unroll
-    for (int bt = 0; bt < NB; ++bt) {
-      const int j = (tile0 + bt) * 16 + (lane & 15);
-      const bool ok = tile0 + bt < t_hi && j < s_lim;
+    for (int st = 0; st < 2; ++st) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        a[bt][ks] = ok ? *reinterpret_cast<const uint4 *>(sbase + int64_t(j) * D + ks * 32 +
-                                                          (lane >> 4) * 8)
-                       : make_uint4(0, 0, 0, 0);
-    }
-  };
-  uint4 a_cur[NB][KS], a_nxt[NB][KS];
-  if (t_lo < t_hi) fetch(t_lo, a_cur);
-  for (int tile0 = t_lo; tile0 < t_hi; tile0 += NB) {
-    if (tile0 + NB < t_hi) fetch(tile0 + NB, a_nxt);
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt) {
-      const int tile = tile0 + bt;
-      if (tile >= t_hi) break;
-      f32x4 acc[4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a_cur[bt][ks]), bx[tt][ks],
-                                                            acc[tt], 0, 0, 0);
-      }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a_reg[st][ks]), bx[ks], acc, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = tile * 16 + (lane >> 4) * 4 + i;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          if constexpr (NOVELTY) {
-            if (j < s_lim) best[tt] = fmaxf(best[tt], rbf(acc[tt][i]));
-          } else {
-            if (j >= protect && j < s_lim && acc[tt][i] > best[tt]) {
-              best[tt] = acc[tt][i];
-              bidx[tt] = j;
-            }
+        const int j = jw + st * 16 + (lane >> 4) * 4 + i;
+        if constexpr (NOVELTY) {
+          if (j < s_lim) best[tt] = fmaxf(best[tt], rbf(acc[i]));
+        } else {
+          if (j >= protect && j < s_lim && acc[i] > best[tt]) {
+            best[tt] = acc[i];
+            bidx[tt] = j;
           }
         }
       }
     }
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) a_cur[bt][ks] = a_nxt[bt][ks];
   }
 
-  // (4) combine the 4 lane groups holding the same token, then the waves.
+  // (3) lane groups, then waves (slot order: lower wave = lower slots).
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
@@ -277,36 +285,34 @@ __global__ __launch_bounds__(kThreads) void k_route(
       }
     }
     if (lane < 16) {
-      best_lds[wave][tt * 16 + lane] = best[tt];
+      hi_lds[wave][tt * 16 + lane] = (NOVELTY || bidx[tt] >= 0) ? mono(best[tt]) : 0u;
       idx_lds[wave][tt * 16 + lane] = bidx[tt];
     }
   }
   __syncthreads();
   if (tid < 64) {
     const int i_tok = tok0 + tid;
-    float bv = best_lds[0][tid];
-    int bi = idx_lds[0][tid];
-#pragma unroll
-    for (int w = 1; w < 4; ++w) {
-      const float ov = best_lds[w][tid];
-      const int oi = idx_lds[w][tid];
-      if constexpr (NOVELTY) {
-        bv = fmaxf(bv, ov);
-      } else if (oi >= 0 && (bi < 0 || ov > bv)) {  // waves hold increasing slots
-        bv = ov;
-        bi = oi;
-      }
-    }
     if (i_tok < n_tok) {
-      const int64_t o = int64_t(row) * n_tok + i_tok;
+      const int64_t o = rbase + i_tok;
       if constexpr (NOVELTY) {
-        sc.novelty[o] = bv;
-      } else if constexpr (PREP) {
-        // No appends in this update: every token merges.
-        sc.is_append[o] = 0;
-        sc.route[o] = bi;
+        uint32_t m = hi_lds[0][tid];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) m = max(m, hi_lds[w][tid]);
+        atomicMax(sc.nkey + o, m);
       } else {
-        if (sc.is_append[o] == 0) sc.route[o] = bi;
+        uint64_t key = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int oi = idx_lds[w][tid];
+          if (oi >= 0) {
+            const uint64_t kk = (uint64_t(hi_lds[w][tid]) << 32) | uint64_t(0xffffffffu - uint32_t(oi));
+            key = kk > key ? kk : key;
+          }
+        }
+        if (key) atomicMax(reinterpret_cast<unsigned long long *>(sc.rkey[parity]) + o,
+                           (unsigned long long)key);
+        // The other key buffer serves the next update: clear it.
+        if (split == 0) sc.rkey[parity ^ 1][o] = 0;
       }
     }
   }
@@ -316,7 +322,8 @@ __global__ __launch_bounds__(kThreads) void k_route(
 // Append ranking (model/kvm_mixer.py:44-75, 231-248): the n_append tokens
 // with the lowest novelty, ties to the lower token index, become slots
 // state_before.. in token order.  One workgroup per row; dynamic LDS holds
-// novelty, flags and positions of the n_tok tokens.
+// novelty, flags and positions of the n_tok tokens.  The novelty keys are
+// cleared after use (this workgroup is their only reader).
 template <int D>
 __global__ __launch_bounds__(512) void k_rank_append(
     kvm_layer L, kvm_seq src, int64_t tok_begin, int n_tok, int n_append,
@@ -330,7 +337,10 @@ __global__ __launch_bounds__(512) void k_rank_append(
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t base = int64_t(row) * n_tok;
 
-  for (int t = tid; t < n_tok; t += nt) nov[t] = sc.novelty[base + t];
+  for (int t = tid; t < n_tok; t += nt) {
+    nov[t] = unmono(sc.nkey[base + t]);
+    sc.nkey[base + t] = 0;
+  }
   __syncthreads();
   for (int t = tid; t < n_tok; t += nt) {
     const float x = nov[t];
@@ -392,82 +402,92 @@ __global__ __launch_bounds__(512) void k_rank_append(
 // bf16(sum of merge keys / values routed to it), summed in fp32 in token
 // order; every slot < s_after gets fresh attention rows in attn_out.
 // Workgroup: 4 waves x (64 / (D/8)) slots, D/8 lanes per slot.  The tokens
-// routed to the workgroup's slots are first listed in LDS in token order
-// (a ballot scan, no global traffic), then each slot gathers its list four
-// rows at a time so the loads overlap.
+// routed to the workgroup's slots are counted and placed with LDS atomics,
+// then each slot's list is sorted by token index (rank sort), so the fp32
+// sums run in token order whatever the arrival order; the gathers are
+// issued four rows at a time.
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_merge_refresh(
     kvm_layer L, int n_tok, int s_after, kvm_state st, AttnRows attn_out,
-    UpdateScratch sc) {
+    UpdateScratch sc, int parity) {
   constexpr int G = D / 8;
-  constexpr int SPW = 64 / G;  // slots per wave
-  constexpr int SPB = 4 * SPW; // slots per workgroup
+  constexpr int SPW = 64 / G;   // slots per wave
+  constexpr int SPB = 4 * SPW;  // slots per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  int *rt = reinterpret_cast<int *>(smem);  // [n_tok] slot of each token (-1: appended)
-  int *list = rt + n_tok;                   // [n_tok] tokens grouped by slot
-  __shared__ int counts[SPB];
+  int *mr = reinterpret_cast<int *>(smem);  // [n_tok] local slot of each token, -1 otherwise
+  int *list = mr + n_tok;                   // [n_tok] placed tokens
+  int *sorted = list + n_tok;               // [n_tok] lists in token order
+  __shared__ int cnt[SPB], off[SPB], fill[SPB];
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t base = int64_t(row) * n_tok;
   const int part = lane % G;
-  const int grp = lane / G;
-  const int local = wave * SPW + grp;
-  const int j = blockIdx.y * SPB + local;
+  const int local = wave * SPW + lane / G;
+  const int j0 = blockIdx.y * SPB;
+  const int j = j0 + local;
   const bool valid = j < s_after;
   const int jj = valid ? j : 0;
 
-  // The slot's current sums and vlen (in flight during the scans).
+  // The slot's current sums and vlen (in flight during the listing).
   const int64_t so = (int64_t(row) * st.capacity + jj) * D + part * 8;
   const uint4 k_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_k) + so);
   const uint4 v_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_v) + so);
   const float vlen = static_cast<const float *>(st.s_vlen)[int64_t(row) * st.capacity + jj];
 
-  for (int t = tid; t < n_tok; t += kThreads)
-    rt[t] = sc.is_append[base + t] ? -1 : sc.route[base + t];
-  __syncthreads();
-
-  const uint64_t gmask = (G == 64) ? ~0ull : ((1ull << G) - 1ull);
-  int cnt = 0;
-  for (int g0 = 0; g0 < n_tok; g0 += G) {
-    const int t = g0 + part;
-    const bool hit = valid && t < n_tok && rt[t] == j;
-    cnt += __popcll((__ballot(hit) >> (grp * G)) & gmask);
+  if (tid < SPB) {
+    cnt[tid] = 0;
+    fill[tid] = 0;
   }
-  if (part == 0) counts[local] = cnt;
   __syncthreads();
-  int off = 0;
-  for (int i = 0; i < local; ++i) off += counts[i];
-  if (cnt > 0) {
-    int w = off;
-    for (int g0 = 0; g0 < n_tok; g0 += G) {
-      const int t = g0 + part;
-      const bool hit = valid && t < n_tok && rt[t] == j;
-      uint64_t m = (__ballot(hit) >> (grp * G)) & gmask;
-      while (m) {
-        const int p = __ffsll((unsigned long long)m) - 1;
-        m &= m - 1;
-        if (part == 0) list[w] = g0 + p;
-        ++w;
-      }
+  for (int t = tid; t < n_tok; t += kThreads) {
+    int r = -1;
+    if (!sc.is_append[base + t]) {
+      const uint64_t key = sc.rkey[parity][base + t];
+      if (key) r = int(0xffffffffu - uint32_t(key & 0xffffffffu));
     }
+    const int lr = (r >= j0 && r < j0 + SPB && r < s_after) ? r - j0 : -1;
+    mr[t] = lr;
+    if (lr >= 0) atomicAdd(&cnt[lr], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int i = 0; i < SPB; ++i) {
+      off[i] = run;
+      run += cnt[i];
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < n_tok; t += kThreads) {
+    const int lr = mr[t];
+    if (lr >= 0) list[off[lr] + atomicAdd(&fill[lr], 1)] = t;
+  }
+  __syncthreads();
+  const int n = valid ? cnt[local] : 0;
+  const int o = off[local];
+  for (int e = part; e < n; e += G) {
+    const int x = list[o + e];
+    int r = 0;
+    for (int f = 0; f < n; ++f) r += list[o + f] < x;
+    sorted[o + r] = x;
   }
   __syncthreads();
 
   float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int i0 = 0; i0 < cnt; i0 += 4) {
+  for (int i0 = 0; i0 < n; i0 += 4) {
     uint4 xk[4], xv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      if (i0 + u < cnt) {
-        const int64_t o = (base + list[off + i0 + u]) * D + part * 8;
-        xk[u] = *reinterpret_cast<const uint4 *>(sc.gk + o);
-        xv[u] = *reinterpret_cast<const uint4 *>(sc.gv + o);
+      if (i0 + u < n) {
+        const int64_t to = (base + sorted[o + i0 + u]) * D + part * 8;
+        xk[u] = *reinterpret_cast<const uint4 *>(sc.gk + to);
+        xv[u] = *reinterpret_cast<const uint4 *>(sc.gv + to);
       }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      if (i0 + u < cnt) {
+      if (i0 + u < n) {
         float fk[8], fv[8];
         unpack8(xk[u], fk);
         unpack8(xv[u], fv);
@@ -482,7 +502,7 @@ __global__ __launch_bounds__(kThreads) void k_merge_refresh(
   float k[8], v[8];
   unpack8(k_raw, k);
   unpack8(v_raw, v);
-  if (cnt > 0) {
+  if (n > 0) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       k[i] = rbf(k[i] + rbf(sk[i]));
@@ -500,6 +520,32 @@ __global__ __launch_bounds__(kThreads) void k_merge_refresh(
     store8(attn_out.k + ao, ka);
     store8(attn_out.v + ao, va);
   }
+}
+
+// Route of every overflow token (appended tokens: their new slot), for logs.
+__global__ __launch_bounds__(256) void k_route_out(int n, UpdateScratch sc, int parity,
+                                                   int32_t *route_out, int32_t *append_out) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int app = sc.is_append[i];
+  int r = -1;
+  if (app) {
+    r = sc.route[i];
+  } else {
+    const uint64_t key = sc.rkey[parity][i];
+    if (key) r = int(0xffffffffu - uint32_t(key & 0xffffffffu));
+  }
+  if (route_out) route_out[i] = r;
+  if (append_out) append_out[i] = app;
+}
+
+// Clear both route-key buffers and the novelty keys of a fresh workspace.
+__global__ __launch_bounds__(256) void k_zero_keys(int64_t n, UpdateScratch sc) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  sc.rkey[0][i] = 0;
+  sc.rkey[1][i] = 0;
+  sc.nkey[i] = 0;
 }
 
 // Window ring write: token 0 of src -> ring slot pos of every row.
@@ -533,26 +579,37 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 }  // namespace
 
-int64_t update_scratch_bytes(const kvm_layer &L, int64_t n_tok) {
-  const size_t rows = size_t(rows_of(L));
-  const size_t tok = rows * size_t(n_tok);
-  return int64_t(3 * align256(tok * size_t(L.head_dim) * 2) +
-                 3 * align256(tok * 4));
+int64_t update_slice_bytes(const kvm_layer &L, int64_t n_tok) {
+  const size_t tok = size_t(rows_of(L)) * size_t(n_tok);
+  return int64_t(3 * align256(tok * size_t(L.head_dim) * 2) + 2 * align256(tok * 4));
 }
 
-UpdateScratch carve_update_scratch(void *ws, const kvm_layer &L,
+int64_t update_keys_bytes(const kvm_layer &L, int64_t n_tok) {
+  const size_t tok = size_t(rows_of(L)) * size_t(n_tok);
+  return int64_t(2 * align256(tok * 8) + align256(tok * 4));
+}
+
+int64_t update_scratch_bytes(const kvm_layer &L, int64_t n_tok) {
+  return update_slice_bytes(L, n_tok) + update_keys_bytes(L, n_tok);
+}
+
+UpdateScratch carve_update_scratch(void *slice, void *keys, const kvm_layer &L,
                                    int64_t n_tok) {
   const size_t tok = size_t(rows_of(L)) * size_t(n_tok);
   const size_t kb = align256(tok * size_t(L.head_dim) * 2);
+  const size_t qb = align256(tok * 8);
   const size_t ib = align256(tok * 4);
-  unsigned char *p = static_cast<unsigned char *>(ws);
+  unsigned char *p = static_cast<unsigned char *>(slice);
+  unsigned char *k = static_cast<unsigned char *>(keys);
   UpdateScratch s;
   s.pk = reinterpret_cast<uint16_t *>(p);
   s.gk = reinterpret_cast<uint16_t *>(p + kb);
   s.gv = reinterpret_cast<uint16_t *>(p + 2 * kb);
-  s.novelty = reinterpret_cast<float *>(p + 3 * kb);
-  s.route = reinterpret_cast<int32_t *>(p + 3 * kb + ib);
-  s.is_append = reinterpret_cast<int32_t *>(p + 3 * kb + 2 * ib);
+  s.route = reinterpret_cast<int32_t *>(p + 3 * kb);
+  s.is_append = reinterpret_cast<int32_t *>(p + 3 * kb + ib);
+  s.rkey[0] = reinterpret_cast<uint64_t *>(k);
+  s.rkey[1] = reinterpret_cast<uint64_t *>(k + qb);
+  s.nkey = reinterpret_cast<uint32_t *>(k + 2 * qb);
   return s;
 }
 
@@ -590,59 +647,79 @@ hipError_t launch_refresh(const kvm_layer &L, const kvm_state &st,
   return hipGetLastError();
 }
 
+hipError_t launch_zero_keys(const kvm_layer &L, int64_t n_tok,
+                            const UpdateScratch &sc, hipStream_t stream) {
+  const int64_t n = rows_of(L) * n_tok;
+  hipLaunchKernelGGL(k_zero_keys, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, n, sc);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep(const kvm_layer &L, const kvm_seq &src, const PrepList &P,
+                       int64_t n_tok, const UpdateScratch &s0, int64_t slice_bytes,
+                       hipStream_t stream) {
+  if (P.count <= 0) return hipSuccess;
+  const dim3 grid{unsigned(rows_of(L)), unsigned((n_tok + 63) / 64), unsigned(P.count)};
+  if (L.head_dim == 128)
+    hipLaunchKernelGGL(k_prep<128>, grid, dim3(kThreads), 0, stream, L, src, P, int(n_tok), s0,
+                       slice_bytes);
+  else
+    hipLaunchKernelGGL(k_prep<64>, grid, dim3(kThreads), 0, stream, L, src, P, int(n_tok), s0,
+                       slice_bytes);
+  return hipGetLastError();
+}
+
 template <int D>
 static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
                                   int64_t tok_begin, int64_t n_tok,
                                   int64_t state_before, int64_t n_append,
                                   const kvm_state &st, AttnRows attn_in,
                                   AttnRows attn_out, const UpdateScratch &sc,
-                                  hipStream_t stream) {
+                                  int parity, int32_t *route_out,
+                                  int32_t *append_out, hipStream_t stream) {
   const unsigned rows = unsigned(rows_of(L));
   const int s_after = int(state_before + n_append);
   const int protect = int(L.sink_len < s_after ? L.sink_len : s_after);
-  dim3 rgrid(rows, unsigned((n_tok + 63) / 64));
+  const unsigned tiles = unsigned((n_tok + 63) / 64);
   hipError_t e;
   if (n_append > 0) {
-    hipLaunchKernelGGL((k_route<D, true, true>), rgrid, dim3(kThreads), 0,
-                       stream, L, src, tok_begin, int(n_tok), attn_in,
-                       int(state_before), 0, sc);
+    const dim3 ngrid{rows, tiles, unsigned((state_before + kSplit - 1) / kSplit)};
+    hipLaunchKernelGGL((k_route<D, true>), ngrid, dim3(kThreads), 0, stream, L, int(n_tok),
+                       attn_in, int(state_before), 0, sc, parity);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t lds = size_t(n_tok) * 12;
     hipLaunchKernelGGL(k_rank_append<D>, dim3(rows), dim3(512), lds, stream, L,
                        src, tok_begin, int(n_tok), int(n_append),
                        int(state_before), st, attn_in, sc);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (n_append < n_tok) {
-      hipLaunchKernelGGL((k_route<D, false, false>), rgrid, dim3(kThreads), 0,
-                         stream, L, src, tok_begin, int(n_tok), attn_in,
-                         s_after, protect, sc);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
-  } else {
-    // No appends: every token merges (the kernel clears the append flags).
-    hipLaunchKernelGGL((k_route<D, true, false>), rgrid, dim3(kThreads), 0,
-                       stream, L, src, tok_begin, int(n_tok), attn_in, s_after,
-                       protect, sc);
+  }
+  const dim3 rgrid{rows, tiles, unsigned((s_after + kSplit - 1) / kSplit)};
+  hipLaunchKernelGGL((k_route<D, false>), rgrid, dim3(kThreads), 0, stream, L, int(n_tok),
+                     attn_in, s_after, protect, sc, parity);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (route_out || append_out) {
+    const int64_t n = int64_t(rows) * n_tok;
+    hipLaunchKernelGGL(k_route_out, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                       int(n), sc, parity, route_out, append_out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   constexpr int spb = 4 * (64 / (D / 8));
-  dim3 mgrid(rows, unsigned((s_after + spb - 1) / spb));
-  hipLaunchKernelGGL(k_merge_refresh<D>, mgrid, dim3(kThreads),
-                     size_t(n_tok) * 8, stream, L, int(n_tok), s_after, st,
-                     attn_out, sc);
+  const dim3 mgrid{rows, unsigned((s_after + spb - 1) / spb), 1u};
+  hipLaunchKernelGGL(k_merge_refresh<D>, mgrid, dim3(kThreads), size_t(n_tok) * 12, stream, L,
+                     int(n_tok), s_after, st, attn_out, sc, parity);
   return hipGetLastError();
 }
 
 hipError_t launch_update(const kvm_layer &L, const kvm_seq &src,
                          int64_t tok_begin, int64_t n_tok, int64_t state_before,
                          int64_t n_append, const kvm_state &st, AttnRows attn_in,
-                         AttnRows attn_out, const UpdateScratch &sc,
+                         AttnRows attn_out, const UpdateScratch &sc, int parity,
+                         int32_t *route_out, int32_t *append_out,
                          hipStream_t stream) {
   if (L.head_dim == 128)
-    return launch_update_d<128>(L, src, tok_begin, n_tok, state_before,
-                                n_append, st, attn_in, attn_out, sc, stream);
-  return launch_update_d<64>(L, src, tok_begin, n_tok, state_before, n_append,
-                             st, attn_in, attn_out, sc, stream);
+    return launch_update_d<128>(L, src, tok_begin, n_tok, state_before, n_append, st, attn_in,
+                                attn_out, sc, parity, route_out, append_out, stream);
+  return launch_update_d<64>(L, src, tok_begin, n_tok, state_before, n_append, st, attn_in,
+                             attn_out, sc, parity, route_out, append_out, stream);
 }
 
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
