@@ -42,6 +42,20 @@ PEAK_BF16_FLOPS = 2.5e15   # MI355X dense bf16 MFMA
 PEAK_HBM_BYTES = 8.0e12    # MI355X HBM3E
 
 
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` as the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE runs measured them (scaled by the
+    plain-copy calibration), or None when no such measurement is recorded."""
+    path = ROOT / "profiles" / "hbm_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if len(f) == 4 and not line.startswith("#") and f[0] == kernel and f[1] == workload:
+            return int(f[2]) + int(f[3])
+    return None
+
+
 def _config(Hq, Hkv, D, C, n_bswa, min_len, n_max):
     return SimpleNamespace(
         num_attention_heads=Hq, num_key_value_heads=Hkv, hidden_size=Hq * D, d_qk_head=D, d_v_head=D,
@@ -217,6 +231,10 @@ def main():
                     help="tokens of the prefill workload the CPU baseline runs (default: all)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+                    help="run one workload (profiling); 'copy' streams a known number of bytes "
+                         "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
+    ap.add_argument("--copy-mib", type=int, default=1024)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -226,8 +244,24 @@ def main():
     import kvm_amd
 
     kvm_amd.load_library()
+    if args.only == "copy":
+        n = args.copy_mib << 19  # bf16 elements
+        src = torch.randn(n, device="cuda:0").bfloat16()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 2 * n, "copy_bytes_written": 2 * n, "launches": 3}))
+        return
+    if args.only == "decode":
+        dec = bench_decode(args, torch, kvm_amd)
+        print(json.dumps({k: v for k, v in dec.items()}))
+        return
     print("bench: prefill config 2 ...", file=sys.stderr, flush=True)
     pf = bench_prefill(args, torch, kvm_amd)
+    if args.only == "prefill":
+        print(json.dumps({"ms": pf["ms"], "attention_ms": pf["attn_ms"], "chain_ms": pf["chain_ms"]}))
+        return
     print(f"bench: prefill {pf['ms']:.3f} ms/step (attention {pf['attn_ms']:.3f} ms, updates {pf['chain_ms']:.3f} ms)",
           file=sys.stderr, flush=True)
     dec = None
@@ -265,7 +299,7 @@ def main():
         "roofline": {
             "bound": "mfma", "kernel": "k_attn_prefill", "achieved": round(attn_achieved / 1e12, 2),
             "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s", "frac": round(attn_achieved / PEAK_BF16_FLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("k_attn_prefill", "config2"),
         },
     }
     if dec is not None:
@@ -278,7 +312,8 @@ def main():
             "other_step_ms": round(dec["other_step_ms"], 4),
             "roofline": {"bound": "hbm", "kernel": "k_decode_partial+k_decode_combine",
                          "achieved": round(bw / 1e9, 1), "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s",
-                         "frac": round(bw / PEAK_HBM_BYTES, 4), "traffic": None},
+                         "frac": round(bw / PEAK_HBM_BYTES, 4),
+                         "traffic": measured_traffic("k_decode_partial", "config4")},
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
