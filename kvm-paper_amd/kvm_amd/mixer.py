@@ -20,6 +20,7 @@ prefill that needs gradients raises ValueError.
 
 from __future__ import annotations
 
+import argparse
 import ctypes
 import math
 import os
@@ -219,6 +220,27 @@ class SequenceMixer(nn.Module):
     def make_plan(self, q_len: int) -> PrefillPlan:
         """Host schedule of a prefill (model/kvm_triton_mixer.py:257-343 make_schedule)."""
         return prefill_plan(q_len, self.chunk_len, self.n_bswa_chunks, self.state_budget)
+
+    def _make_triton_args(self, batch_size: int, q_len: int) -> argparse.Namespace:
+        """Schedule arguments of a prefill, the fields of
+        model/kvm_triton_mixer.py:257-338 that the schedule reads (benchmark
+        harnesses call it, scripts/kvm_benchmark/common.py:153-155)."""
+        b = self.state_budget
+        return argparse.Namespace(
+            batch=int(batch_size), q_heads=self.num_attention_heads, kv_heads=self.num_key_value_heads,
+            q_len=int(math.ceil(q_len / self.chunk_len) * self.chunk_len), logical_q_len=int(q_len),
+            initial_state_len=min(int(q_len), self.chunk_len), state_capacity=self.max_state_len,
+            macro_block=self.chunk_len, bswa_chunks=self.n_bswa_chunks, state_budget_mode=b.mode,
+            schedule_factor=b.growth_factor, schedule_exponent=b.growth_exponent, state_min_len=b.min_len,
+            state_saturation_n=b.saturation_n, state_round_down=b.round_down, dim=self.d_qk_head,
+            value_dim=self.d_v_head, sink_len=self.sink_len, ln_eps=float(self.ln_s_k.eps),
+        )
+
+    def _make_schedule(self, triton_args: argparse.Namespace) -> PrefillPlan:
+        """Host schedule for `_make_triton_args` output
+        (model/kernels/kvm_triton_training_kernels.py:1457-1473); the result
+        carries ``final_state_len`` like the reference's schedule."""
+        return self.make_plan(int(getattr(triton_args, "logical_q_len", triton_args.q_len)))
 
     def _head_temperatures(self, device):
         if self.config.kvm_use_head_temps:

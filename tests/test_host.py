@@ -208,6 +208,26 @@ def test_baseline_config_closed_forms():
     assert p.final_state_len == 1024 and p.max_state_len == 1024
 
 
+def test_benchmark_harness_schedule_helpers():
+    """The helpers the reference's benchmark harness calls on the mixer
+    (scripts/kvm_benchmark/common.py:153-155) give the state length of the
+    schedule, for fixed and growable budgets."""
+    import bench
+    from kvm_amd import SequenceMixer
+
+    cfg = bench._config(32, 32, 128, 512, 2, 256, 1)
+    m = SequenceMixer(cfg, 0)
+    args = m._make_triton_args(8, 32768)
+    assert (args.q_len, args.logical_q_len, args.initial_state_len) == (32768, 32768, 512)
+    assert m._make_schedule(args).final_state_len == 512
+    cfg = bench._config(16, 16, 128, 512, 2, -1, 2)
+    cfg.state_budget_mode, cfg.state_growth_factor = "power_law", 16.0
+    m = SequenceMixer(cfg, 0)
+    # 1000 tokens pad to two chunks; the schedule follows the logical length
+    assert m._make_triton_args(2, 1000).q_len == 1024
+    assert m._make_schedule(m._make_triton_args(2, 65536)).final_state_len == 1024
+
+
 def test_bench_flop_count_matches_brute_force():
     import bench
     from kvm_amd.schedule import StateBudget, prefill_plan
