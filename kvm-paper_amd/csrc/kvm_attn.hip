@@ -13,7 +13,7 @@
 //     keys scaled by the state temperature;
 //   * window tokens [max(0, (m-n+1)C), query] causally, keys scaled by the
 //     front temperature.
-// Workgroup = 4 waves = 128 queries of one (batch, q_head); each wave owns
+// Workgroup = NW waves = 32*NW queries of one (batch, q_head); each wave owns
 // 32 queries (two 16-row MFMA tiles).  Keys stream through LDS in blocks of
 // 64: K row-major (times temperature, rounded to bf16, as the reference
 // does), V transposed.  Scores are computed transposed, S^T = K Q^T, with
@@ -23,18 +23,19 @@
 // A operand, which leaves the sum unchanged).  Online softmax in fp32
 // registers with exp2; P rounded to bf16 for the PV product.
 //
-// VALU budget (the limiter next to MFMA on CDNA): bf16 packing uses the
-// hardware v_cvt_pk_bf16_f32, exp2 the raw v_exp_f32, the softmax scale is
-// folded into one fma per score, masks are applied only on tail / diagonal
-// blocks, the O rescale is skipped when no row maximum of the wave moved,
-// and a wave skips 32-key halves that lie entirely above its causal
-// diagonal.  Latency: two LDS buffers (one barrier per block; the next
-// block is fetched while the current one is multiplied) and a single
-// inlined copy of the pipeline for both key ranges keep the kernel under
-// 256 VGPRs, so two workgroups share a CU and cover each other's waits.
-// Workgroups are renumbered so that each XCD (dispatch is round-robin over
-// the 8 XCDs) runs a contiguous range of (head, chunk) tiles: the window
-// keys shared by neighbouring chunks stay in that XCD's L2.
+// Latency structure: a workgroup of 8 waves (256 queries) shares each staged
+// key block, so a block load feeds twice the MFMA work of a 4-wave tile and
+// each thread stages half as much.  A wave consumes a whole 64-key block per
+// step (8 independent MFMA chains, one max reduction per 64 keys) and keeps
+// a lazily moved reference maximum per row, so the O rescale is rare.  Global loads are buffer loads whose
+// range check zero-fills keys past the end of a range (no per-load
+// branches, 32-bit offsets).  Every 32-key step reads all of its K fragments
+// from LDS before the score MFMAs and all of its V fragments before the
+// softmax arithmetic, so LDS latency overlaps MFMA and VALU work instead of
+// serialising with it.  Two LDS buffers, one barrier per block.  Workgroups
+// are renumbered so that each XCD (dispatch is round-robin over the 8 XCDs)
+// runs a contiguous range of (head, chunk) tiles: the window keys shared by
+// neighbouring chunks stay in that XCD's L2.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -42,13 +43,16 @@
 namespace kvm {
 namespace {
 
-constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;
+// Buffer resource word 3 for raw (unformatted, unswizzled) dword access with
+// range checking: out-of-range loads return zero.
+constexpr int kBufWord3 = 0x00020000;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const f32x2 v = {a, b};
@@ -63,39 +67,54 @@ struct AttnSmem {
   uint16_t vt[D * VSTR];
 };
 
-// Register staging of one K/V block: each thread owns KPT 16-byte pieces of
-// K (key p / (D/8), dims 8 * (p % (D/8))) and one 4-key x 8-dim piece of V.
-template <int D>
+// Register staging of one K/V block over NT threads: K in 16-byte pieces
+// (key p / (D/8), dims 8 * (p % (D/8))), V in units of 2 keys x 8 dims.
+template <int D, int NT>
 struct Stage {
-  static constexpr int KPT = BN * (D / 8) / 256;  // K pieces per thread
-  static constexpr int VUNITS = (BN / 4) * (D / 8);
+  static constexpr int KPIECES = BN * (D / 8);
+  static constexpr int KPT = (KPIECES + NT - 1) / NT;
+  static constexpr int VUNITS = (BN / 2) * (D / 8);
+  static constexpr int VPT = (VUNITS + NT - 1) / NT;
   uint4 k[KPT];
-  uint4 v[4];
+  uint4 v[VPT][2];
 };
 
-template <int D>
-__device__ __forceinline__ void stage_load(Stage<D> &sg,
-                                           const uint16_t *__restrict__ kp,
-                                           int64_t kstride,
-                                           const uint16_t *__restrict__ vp,
-                                           int64_t vstride, int nvalid) {
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
+// Resource over keys [0, nvalid) of a range starting at p with row stride
+// `stride` elements: byte offsets key * stride * 2 + 16 * part of keys past
+// nvalid fall outside it and read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t key_rsrc(const uint16_t *p, int64_t stride,
+                                                          int nvalid) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(p), (short)0,
+                                           int(nvalid * stride * 2), kBufWord3);
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void stage_load(Stage<D, NT> &sg, __amdgpu_buffer_rsrc_t kr,
+                                           uint32_t kstride_b, __amdgpu_buffer_rsrc_t vr,
+                                           uint32_t vstride_b) {
+  using S = Stage<D, NT>;
   const int tid = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < Stage<D>::KPT; ++i) {
-    const int p = tid + i * 256;
-    const int key = p / (D / 8), part = p % (D / 8);
-    sg.k[i] = key < nvalid
-                  ? *reinterpret_cast<const uint4 *>(kp + key * kstride + part * 8)
-                  : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < S::KPT; ++i) {
+    const int p = tid + i * NT;
+    if (S::KPIECES % NT == 0 || p < S::KPIECES) {
+      const int key = p / (D / 8), part = p % (D / 8);
+      sg.k[i] = buf_load16(kr, uint32_t(key) * kstride_b + uint32_t(part) * 16u);
+    }
   }
-  if (tid < Stage<D>::VUNITS) {
-    const int kg = tid % (BN / 4), dg = tid / (BN / 4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kg * 4 + r;
-      sg.v[r] = key < nvalid ? *reinterpret_cast<const uint4 *>(
-                                   vp + key * vstride + dg * 8)
-                             : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < S::VPT; ++i) {
+    const int u = tid + i * NT;
+    if (S::VUNITS % NT == 0 || u < S::VUNITS) {
+      const int kp = u % (BN / 2), dg = u / (BN / 2);
+      const uint32_t off = uint32_t(2 * kp) * vstride_b + uint32_t(dg) * 16u;
+      sg.v[i][0] = buf_load16(vr, off);
+      sg.v[i][1] = buf_load16(vr, off + vstride_b);
     }
   }
 }
@@ -108,40 +127,42 @@ __device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-template <int D>
-__device__ __forceinline__ void stage_store(AttnSmem<D> &sm,
-                                            const Stage<D> &sg, float tau) {
+template <int D, int NT>
+__device__ __forceinline__ void stage_store(AttnSmem<D> &sm, const Stage<D, NT> &sg,
+                                            float tau, bool scale) {
+  using S = Stage<D, NT>;
   constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
   const int tid = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < Stage<D>::KPT; ++i) {
-    const int p = tid + i * 256;
-    const int key = p / (D / 8), part = p % (D / 8);
-    float x[8];
-    unpack8(sg.k[i], x);
-    uint4 w;
-    w.x = pack_bf16x2(x[0] * tau, x[1] * tau);
-    w.y = pack_bf16x2(x[2] * tau, x[3] * tau);
-    w.z = pack_bf16x2(x[4] * tau, x[5] * tau);
-    w.w = pack_bf16x2(x[6] * tau, x[7] * tau);
-    *reinterpret_cast<uint4 *>(&sm.k[key * KSTR + part * 8]) = w;
+  for (int i = 0; i < S::KPT; ++i) {
+    const int p = tid + i * NT;
+    if (S::KPIECES % NT == 0 || p < S::KPIECES) {
+      const int key = p / (D / 8), part = p % (D / 8);
+      uint4 w = sg.k[i];
+      if (scale) {
+        float x[8];
+        unpack8(w, x);
+        w.x = pack_bf16x2(x[0] * tau, x[1] * tau);
+        w.y = pack_bf16x2(x[2] * tau, x[3] * tau);
+        w.z = pack_bf16x2(x[4] * tau, x[5] * tau);
+        w.w = pack_bf16x2(x[6] * tau, x[7] * tau);
+      }
+      *reinterpret_cast<uint4 *>(&sm.k[key * KSTR + part * 8]) = w;
+    }
   }
-  if (tid < Stage<D>::VUNITS) {
-    const int kg = tid % (BN / 4), dg = tid / (BN / 4);
-    const uint32_t a[4][4] = {{sg.v[0].x, sg.v[0].y, sg.v[0].z, sg.v[0].w},
-                              {sg.v[1].x, sg.v[1].y, sg.v[1].z, sg.v[1].w},
-                              {sg.v[2].x, sg.v[2].y, sg.v[2].z, sg.v[2].w},
-                              {sg.v[3].x, sg.v[3].y, sg.v[3].z, sg.v[3].w}};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // dims 2j (low halves) and 2j+1 (high halves) of keys kg*4 .. kg*4+3
-      uint2 lo, hi;
-      lo.x = lo_lo(a[0][j], a[1][j]);
-      lo.y = lo_lo(a[2][j], a[3][j]);
-      hi.x = hi_hi(a[0][j], a[1][j]);
-      hi.y = hi_hi(a[2][j], a[3][j]);
-      *reinterpret_cast<uint2 *>(&sm.vt[(dg * 8 + 2 * j) * VSTR + kg * 4]) = lo;
-      *reinterpret_cast<uint2 *>(&sm.vt[(dg * 8 + 2 * j + 1) * VSTR + kg * 4]) = hi;
+  for (int i = 0; i < S::VPT; ++i) {
+    const int u = tid + i * NT;
+    if (S::VUNITS % NT == 0 || u < S::VUNITS) {
+      const int kp = u % (BN / 2), dg = u / (BN / 2);
+      const uint32_t a0[4] = {sg.v[i][0].x, sg.v[i][0].y, sg.v[i][0].z, sg.v[i][0].w};
+      const uint32_t a1[4] = {sg.v[i][1].x, sg.v[i][1].y, sg.v[i][1].z, sg.v[i][1].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // dims 2j (low halves) and 2j+1 (high halves) of keys 2kp, 2kp+1
+        *reinterpret_cast<uint32_t *>(&sm.vt[(dg * 8 + 2 * j) * VSTR + 2 * kp]) = lo_lo(a0[j], a1[j]);
+        *reinterpret_cast<uint32_t *>(&sm.vt[(dg * 8 + 2 * j + 1) * VSTR + 2 * kp]) = hi_hi(a0[j], a1[j]);
+      }
     }
   }
 }
@@ -149,62 +170,93 @@ __device__ __forceinline__ void stage_store(AttnSmem<D> &sm,
 template <int D>
 struct AttnState {
   f32x4 o[2][D / 16];  // O^T tiles [row tile][dv tile]
-  float m[2];          // running max of scaled scores (log2 domain)
+  float m[2];          // reference maximum of each row (log2 domain), -inf before any key
   float l[2];          // lane-partial running sum
 };
 
-// Online-softmax update with 32 keys (half of a staged block, key offset
-// k0 in the block).  Masked path: keys >= nvalid, or causal keys
-// kpos0 + key > row (kpos0 < 0: memory slots, never causal).
+// A row's reference maximum moves only when a block's maximum exceeds it by
+// more than this (log2 units): probabilities stay <= 2^8, exactly
+// representable range for fp32 sums and bf16 P, and the O rescale (64
+// multiplies per lane) is skipped in almost every block.
+constexpr float kRescaleSlack = 8.0f;
+
+// Online-softmax update with the 64 keys of a staged block.  Masked path:
+// keys >= nvalid, or (causal ranges) keys past the query: key > qrel + row,
+// where qrel is the wave's first query minus the position of the block's
+// first key.
 template <int D>
-__device__ __forceinline__ void consume_half(const AttnSmem<D> &sm, int k0,
-                                             AttnState<D> &as,
-                                             const bf16x8 (&qf)[2][D / 32],
-                                             bool masked, int nvalid,
-                                             int64_t kpos0, int64_t qpos0,
-                                             float scale) {
+__device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D> &as,
+                                              const bf16x8 (&qf)[2][D / 32], bool masked,
+                                              int nvalid, bool causal, int qrel, float scale) {
   constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
   const int lane = threadIdx.x & 63;
-  f32x4 s[2][2];
+  // S^T tiles for 64 keys: s[kt][rt], kt = 16-key tile, rt = 16-query tile.
+  f32x4 s[4][2];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
+  for (int kt = 0; kt < 4; ++kt) {
+    bf16x8 kf[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+      kf[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
+          &sm.k[(kt * 16 + (lane & 15)) * KSTR + ks * 32 + (lane >> 4) * 8]));
     s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
-      const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(
-          &sm.k[(k0 + kt * 16 + (lane & 15)) * KSTR + ks * 32 + (lane >> 4) * 8]));
-      s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], s[kt][0], 0, 0, 0);
-      s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], s[kt][1], 0, 0, 0);
+      s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[0][ks], s[kt][0], 0, 0, 0);
+      s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[1][ks], s[kt][1], 0, 0, 0);
     }
   }
-  bf16x8 pb[2];
-  bool moved = false;
-  float alpha[2];
+  if (masked) {
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    if (masked) {
-      const int64_t qpos = qpos0 + rt * 16 + (lane & 15);
+    for (int rt = 0; rt < 2; ++rt) {
+      const int lim = qrel + rt * 16 + (lane & 15);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = k0 + kt * 16 + (lane >> 4) * 4 + i;
-          if (key >= nvalid || (kpos0 >= 0 && kpos0 + key > qpos)) s[kt][rt][i] = -INFINITY;
+          const int key = kt * 16 + (lane >> 4) * 4 + i;
+          if (key >= nvalid || (causal && key > lim)) s[kt][rt][i] = -INFINITY;
         }
     }
-    float mx = fmaxf(fmaxf(fmaxf(s[0][rt][0], s[0][rt][1]), fmaxf(s[0][rt][2], s[0][rt][3])),
-                     fmaxf(fmaxf(s[1][rt][0], s[1][rt][1]), fmaxf(s[1][rt][2], s[1][rt][3])));
+  }
+  bool need = false;
+  float m_new[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float mx = fmaxf(fmaxf(s[0][rt][0], s[0][rt][1]), s[0][rt][2]);
+    mx = fmaxf(fmaxf(mx, s[0][rt][3]), s[1][rt][0]);
+    mx = fmaxf(fmaxf(mx, s[1][rt][1]), s[1][rt][2]);
+    mx = fmaxf(fmaxf(mx, s[1][rt][3]), s[2][rt][0]);
+    mx = fmaxf(fmaxf(mx, s[2][rt][1]), s[2][rt][2]);
+    mx = fmaxf(fmaxf(mx, s[2][rt][3]), s[3][rt][0]);
+    mx = fmaxf(fmaxf(mx, s[3][rt][1]), s[3][rt][2]);
+    mx = fmaxf(mx, s[3][rt][3]);
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(as.m[rt], mx * scale);
-    moved |= m_new != as.m[rt];
-    const float base = (m_new == -INFINITY) ? 0.f : m_new;
-    alpha[rt] = (as.m[rt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(as.m[rt] - base);
-    float psum = 0.f;
-    uint32_t pk[2][2];
+    m_new[rt] = mx * scale;
+    need |= m_new[rt] > as.m[rt] + kRescaleSlack;
+  }
+  if (__ballot(need)) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int rt = 0; rt < 2; ++rt) {
+      const bool mv = m_new[rt] > as.m[rt] + kRescaleSlack;
+      const float alpha = mv ? (as.m[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(as.m[rt] - m_new[rt])) : 1.f;
+      if (mv) as.m[rt] = m_new[rt];
+      as.l[rt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha;
+    }
+  }
+  // P^T in the B-operand layout: two 32-key steps, each lane 8 keys (4 per kt).
+  bf16x8 pb[2][2];  // [32-key step][rt]
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float base = as.m[rt] == -INFINITY ? 0.f : as.m[rt];
+    float psum = 0.f;
+    uint32_t pk[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -214,33 +266,30 @@ __device__ __forceinline__ void consume_half(const AttnSmem<D> &sm, int k0,
       pk[kt][0] = pack_bf16x2(p[0], p[1]);
       pk[kt][1] = pack_bf16x2(p[2], p[3]);
     }
-    pb[rt] = as_bf16x8(make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]));
-    as.l[rt] = as.l[rt] * alpha[rt] + psum;
-    as.m[rt] = m_new;
+    pb[0][rt] = as_bf16x8(make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]));
+    pb[1][rt] = as_bf16x8(make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]));
+    as.l[rt] += psum;
   }
-  // Rescale O only when some row maximum of the wave moved.
-  if (__ballot(moved)) {
+  // O^T += V^T P^T over the 64 keys (two 32-key steps).
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+  for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha[rt];
-  }
-  // O^T += V^T P^T over these 32 keys.
-#pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) {
-    const uint16_t *vrow = &sm.vt[(dt * 16 + (lane & 15)) * VSTR + k0 + (lane >> 4) * 4];
-    const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
-    const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
-    const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-    as.o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0], as.o[0][dt], 0, 0, 0);
-    as.o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1], as.o[1][dt], 0, 0, 0);
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const uint16_t *vrow = &sm.vt[(dt * 16 + (lane & 15)) * VSTR + h * 32 + (lane >> 4) * 4];
+      const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
+      const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
+      const bf16x8 vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+      as.o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[h][0], as.o[0][dt], 0, 0, 0);
+      as.o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[h][1], as.o[1][dt], 0, 0, 0);
+    }
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
-                    int qtiles, int n_chunks, ChunkTable table) {
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles, int n_chunks,
+                    ChunkTable table) {
+  constexpr int NT = NW * 64, BM = NW * 32;
   __shared__ __attribute__((aligned(16))) AttnSmem<D> sm[2];
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
@@ -261,7 +310,8 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
   const int64_t q0 = int64_t(m) * C + int64_t(qt) * BM;
   if (q0 >= T) return;
   const int64_t q_hi = min(min(q0 + BM, int64_t(m + 1) * C), T);  // exclusive
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t qpos0 = q0 + wave * 32;
 
   // Q fragments (B operand of S^T): row rt*16 + lane%16, dims ks*32 + 8*(lane/16).
@@ -309,36 +359,39 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
     const uint16_t *vp = st ? A.snap_v + soff : vwin + wb * A.kv.v_st;
     const int64_t kstride = st ? D : A.kv.k_st;
     const int64_t vstride = st ? D : A.kv.v_st;
+    const uint32_t kstride_b = uint32_t(kstride * 2), vstride_b = uint32_t(vstride * 2);
     const float tau = st ? tau_s : tau_f;
-    const int64_t kpos0 = st ? -1 : wb;
+    const bool do_scale = tau != 1.0f;
+    const bool causal = !st;
     const int nb = (nkeys + BN - 1) / BN;
     __syncthreads();  // both buffers are free
     {
-      Stage<D> sg;
-      stage_load<D>(sg, kp, kstride, vp, vstride, min(BN, nkeys));
-      stage_store<D>(sm[0], sg, tau);
+      Stage<D, NT> sg;
+      const int nv = min(BN, nkeys);
+      stage_load<D, NT>(sg, key_rsrc(kp, kstride, nv), kstride_b, key_rsrc(vp, vstride, nv), vstride_b);
+      stage_store<D, NT>(sm[0], sg, tau, do_scale);
     }
     __syncthreads();
 #pragma unroll 1
     for (int j = 0; j < nb; ++j) {
       const int j0 = j * BN;
       const int nvalid = min(BN, nkeys - j0);
-      const int64_t kb = kpos0 >= 0 ? kpos0 + j0 : -1;
       const bool more = j + 1 < nb;
-      Stage<D> sg;
+      Stage<D, NT> sg;
       if (more) {
         const int jn = (j + 1) * BN;
-        stage_load<D>(sg, kp + int64_t(jn) * kstride, kstride, vp + int64_t(jn) * vstride,
-                      vstride, min(BN, nkeys - jn));
+        const int nv = min(BN, nkeys - jn);
+        stage_load<D, NT>(sg, key_rsrc(kp + int64_t(jn) * kstride, kstride, nv), kstride_b,
+                          key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), vstride_b);
       }
-      const bool masked = nvalid < BN || (kb >= 0 && kb + BN - 1 > qpos0);
-#pragma unroll 1
-      for (int h = 0; h < 2; ++h) {
-        // wave-uniform: skip halves above the wave's causal diagonal / past the tail
-        const bool live = h * 32 < nvalid && !(kb >= 0 && kb + h * 32 > qpos0 + 31);
-        if (live) consume_half<D>(sm[j & 1], h * 32, as, qf, masked, nvalid, kb, qpos0, scale);
-      }
-      if (more) stage_store<D>(sm[(j + 1) & 1], sg, tau);
+      // Causal ranges: position of the block's first key is wb + j0.
+      const int64_t qrel64 = causal ? qpos0 - (wb + j0) : int64_t(BN);
+      const int qrel = int(min(max(qrel64, int64_t(-64)), int64_t(BN)));
+      const bool masked = nvalid < BN || qrel < BN - 1;
+      // wave-uniform: skip blocks entirely above the wave's causal diagonal
+      if (qrel + 31 >= 0)
+        consume_block<D>(sm[j & 1], as, qf, masked, nvalid, causal, qrel, scale);
+      if (more) stage_store<D, NT>(sm[(j + 1) & 1], sg, tau, do_scale);
       __syncthreads();
     }
   }
@@ -364,24 +417,29 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin,
   }
 }
 
-}  // namespace
-
-hipError_t launch_prefill_attention(const kvm_layer &L,
-                                    const PrefillAttnArgs &a,
-                                    int64_t chunk_begin, int64_t n_chunks,
-                                    const ChunkTable &table,
-                                    hipStream_t stream) {
-  if (n_chunks <= 0) return hipSuccess;
-  const int qtiles = int((L.chunk_len + BM - 1) / BM);
+template <int D, int NW>
+hipError_t launch_nw(const kvm_layer &L, const PrefillAttnArgs &a, int64_t chunk_begin,
+                     int64_t n_chunks, const ChunkTable &table, hipStream_t stream) {
+  const int qtiles = int((L.chunk_len + NW * 32 - 1) / (NW * 32));
   const int64_t n_wg = n_chunks * qtiles * L.batch * L.q_heads;
   const dim3 grid{unsigned(n_wg), 1u, 1u};
-  if (L.head_dim == 128)
-    hipLaunchKernelGGL(k_attn_prefill<128>, grid, dim3(256), 0, stream, L, a,
-                       int(chunk_begin), qtiles, int(n_chunks), table);
-  else
-    hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), 0, stream, L, a,
-                       int(chunk_begin), qtiles, int(n_chunks), table);
+  hipLaunchKernelGGL((k_attn_prefill<D, NW>), grid, dim3(NW * 64), 0, stream, L, a,
+                     int(chunk_begin), qtiles, int(n_chunks), table);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prefill_attention(const kvm_layer &L, const PrefillAttnArgs &a,
+                                    int64_t chunk_begin, int64_t n_chunks,
+                                    const ChunkTable &table, hipStream_t stream) {
+  if (n_chunks <= 0) return hipSuccess;
+  const bool wide = L.chunk_len >= 256;
+  if (L.head_dim == 128)
+    return wide ? launch_nw<128, 8>(L, a, chunk_begin, n_chunks, table, stream)
+                : launch_nw<128, 4>(L, a, chunk_begin, n_chunks, table, stream);
+  return wide ? launch_nw<64, 8>(L, a, chunk_begin, n_chunks, table, stream)
+              : launch_nw<64, 4>(L, a, chunk_begin, n_chunks, table, stream);
 }
 
 }  // namespace kvm

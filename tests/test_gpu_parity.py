@@ -293,6 +293,8 @@ def _random_inputs(B, Hq, Hkv, Tn, D, seed):
 @pytest.mark.parametrize("B,Hq,Hkv,Tn,D,C,mode", [
     (1, 4, 2, 1000, 128, 128, "fixed"),
     (2, 2, 2, 777, 64, 64, "power_law"),
+    (1, 4, 2, 1300, 128, 256, "fixed"),
+    (1, 2, 2, 1700, 64, 512, "power_law"),
 ])
 def test_last_chunk_attention_exact(lib, B, Hq, Hkv, Tn, D, C, mode):
     """The last query chunk attends to the final state: compare with fp64."""
@@ -387,3 +389,41 @@ def test_prefill_deterministic(lib):
     for key in ("out", "state_k", "state_v", "state_k_attn", "state_v_attn", "route_log"):
         assert torch.equal(a[key], b[key]), key
     assert bool(torch.isfinite(a["out"].float()).all())
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Tn,D,C,mode", [
+    (1, 4, 2, 1300, 128, 256, "fixed"),
+    (1, 2, 1, 1700, 64, 512, "power_law"),
+])
+def test_prefill_wide_chunks_match_oracle(lib, B, Hq, Hkv, Tn, D, C, mode):
+    """Whole prefill (every query chunk, every update) at chunk lengths that
+    use the 8-wave attention tiles, against the CPU oracle."""
+    T.log(f"[prefill-wide] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode=mode, min_len=C, n_max=2, factor=6.0)
+    gen = torch.Generator().manual_seed(5)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 13)
+    with torch.no_grad():
+        res = m.prefill_raw(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV))
+    torch.cuda.synchronize()
+    ocfg = O.OracleConfig(
+        q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=cfg.n_bswa_chunks,
+        n_max_d_chunks=cfg.n_max_d_chunks, sink_len=cfg.sink_len, rope_partial_dim=cfg.rope_partial_dim,
+        state_budget_mode=mode, state_growth_factor=cfg.state_growth_factor,
+        state_growth_exponent=cfg.state_growth_exponent, state_round_down=1, state_min_len=C,
+        append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
+    y_ref, st = O.prefill(q, k, v, g, p, ocfg)
+    got = res["out"].cpu().transpose(1, 2)
+    mx, mean = T.assert_close_bf16(got, y_ref, "wide-chunk prefill output")
+    S = res["plan"].final_state_len
+    sk = res["state_k"].cpu()[:, :S].view(B, Hkv, S, D)
+    # state sums: bf16 values of magnitude up to ~C; relative bound of a few bf16 ulps
+    scale = float(st[O.S_K].float().abs().max())
+    smx, smean = T.err_stats(sk, st[O.S_K])
+    assert smx <= 2e-2 * scale and smean <= 2e-3 * scale, f"final s_k: max {smx:.3e}, mean {smean:.3e}, scale {scale:.3e}"
+    T.log(f"[prefill-wide] out max {mx:.2e} mean {mean:.2e}; S={S}; s_k max {smx:.2e} mean {smean:.2e} (scale {scale:.2e})")
