@@ -59,11 +59,34 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 u) {
   return __builtin_bit_cast(bf16x8, u);
 }
 
-// Sum over aligned groups of G consecutive lanes (G a power of two <= 64).
+// DPP lane moves within rows of 16 lanes (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;      // rotate right by 4 within 16 lanes
+constexpr int kDppRowRor8 = 0x128;      // rotate right by 8 within 16 lanes
+constexpr int kDppRowHalfMirror = 0x141;  // lane i -> 7 - i within 8 lanes
+
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64);
+// every lane of a group gets the same value.  Groups of 8 and 16 use DPP.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G == 16) {
+    v += dpp<kDppRowRor8>(v);
+    v += dpp<kDppRowRor4>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppQuadXor1>(v);
+  } else if constexpr (G == 8) {
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppQuadXor1>(v);
+  } else {
 #pragma unroll
-  for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  }
   return v;
 }
 template <int G>
