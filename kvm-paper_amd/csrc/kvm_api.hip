@@ -3,6 +3,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <string>
@@ -105,8 +106,11 @@ PrefillLayout prefill_layout(const kvm_prefill_desc *d) {
   const kvm_layer &L = d->layer;
   p.slices = size_t(std::max<int64_t>(1, std::min<int64_t>(d->n_updates, kvm::kMaxPrep)));
   p.slice_bytes = size_t(kvm::update_slice_bytes(L, L.chunk_len));
-  p.update_bytes = align256(p.slices * p.slice_bytes +
-                            size_t(kvm::update_keys_bytes(L, L.chunk_len)));
+  // The per-update scratch (prep slices + reduction keys) and the chain's
+  // scratch share one region: a prefill uses one or the other.
+  p.update_bytes = align256(std::max(p.slices * p.slice_bytes +
+                                         size_t(kvm::update_keys_bytes(L, L.chunk_len)),
+                                     size_t(kvm::chain_scratch_bytes(L, L.chunk_len))));
   p.snap_elems = size_t(L.batch * L.kv_heads) * size_t(d->max_state_len) *
                  size_t(L.head_dim);
   p.total = p.update_bytes +
@@ -362,9 +366,17 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
                          snap_v + (idx % R) * snap_stride, d->max_state_len};
   };
 
+  // Updates run as persistent chains when the shape fits (one launch per
+  // batch of updates), else as per-update kernels.  KVM_AMD_CHAIN=0 forces
+  // the per-update kernels.
+  kvm::ChainPlan cp;
+  const char *chain_env = getenv("KVM_AMD_CHAIN");
+  const bool use_chain = !(chain_env && chain_env[0] == '0') &&
+                         kvm::chain_plan(L, C, d->max_state_len, &cp);
+
   // Initial state: the first min(T, C) tokens (model/kvm_mixer.py:434-447).
   if ((rc = mark(0)) != KVM_OK) return rc;
-  KVM_HIP(kvm::launch_zero_keys(L, C, sc, s), "key reset");
+  if (!use_chain) KVM_HIP(kvm::launch_zero_keys(L, C, sc, s), "key reset");
   KVM_HIP(kvm::launch_append_direct(L, d->kv, 0, L0, d->state, 0, snap_rows(0),
                                     L.gate_initial != 0, s),
           "initial state");
@@ -409,7 +421,38 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   };
 
   const size_t log_stride = size_t(L.batch * L.kv_heads) * size_t(C);
-  for (int64_t u = 0; u < d->n_updates; ++u) {
+  if (use_chain) {
+    // Batches of consecutive updates, one persistent launch each.  A batch
+    // [u, e) writes snapshots u+1..e into ring slots: every chunk reading a
+    // snapshot <= e - R is launched first, which needs e <= u + R.
+    const kvm::ChainScratch cs = kvm::carve_chain_scratch(ws, L, C);
+    // KVM_AMD_CHAIN_FIXED=0 keeps batches without appends on the token-split kernel.
+    const char *fixed_env = getenv("KVM_AMD_CHAIN_FIXED");
+    const kvm::SnapRing ring{snap_k, snap_v, snap_stride, R, d->max_state_len};
+    for (int64_t u = 0; u < d->n_updates;) {
+      const int64_t e = std::min({d->n_updates, u + int64_t(kvm::kChainMax), u + R});
+      if (e - R >= 0) {
+        if ((rc = flush(u + 1)) != KVM_OK) return rc;
+        if (next_chunk < n_chunks && next_chunk >= n && d->chunk_snapshot[next_chunk] <= e - R)
+          return fail(KVM_EINVAL, "snapshot ring too small for the schedule");
+      }
+      kvm::ChainList cl;
+      cl.u0 = int32_t(u);
+      cl.count = int32_t(e - u);
+      for (int64_t i = u; i < e; ++i) {
+        cl.tok_begin[i - u] = d->upd_token_begin[i];
+        cl.state_before[i - u] = d->upd_state_before[i];
+        cl.n_append[i - u] = d->upd_n_append[i];
+      }
+      kvm::ChainPlan bp = cp;
+      bp.fixed = !(fixed_env && fixed_env[0] == '0') && kvm::chain_fixed_ok(cp, cl, C);
+      KVM_HIP(kvm::launch_chain(L, d->kv, C, d->state, ring, cl, cs, bp, d->route_log,
+                                d->append_log, s),
+              "state update chain");
+      u = e;
+    }
+  }
+  for (int64_t u = 0; !use_chain && u < d->n_updates; ++u) {
     // Snapshot u + 1 overwrites ring slot (u + 1) % R: every chunk reading
     // snapshot u + 1 - R must have been launched (stream order does the rest).
     if (u + 1 - R >= 0) {

@@ -1,0 +1,1120 @@
+// Persistent chain of block-boundary memory updates on gfx950.
+//
+// Reference semantics are those of the per-update kernels: the update of
+// model/kvm_mixer.py:250-340 (append + merge) with the fp32 routing of
+// model/kvm_fp32_routing_reference.py:24-49, the overflow-token streams of
+// model/kvm_triton_mixer.py:429-446 and the Triton numeric contract of
+// model/kvm_triton_mixer.py:199-211.  This kernel runs a whole batch of
+// consecutive updates in one launch instead of two to four launches per
+// update, because a single update of a prefill is small (one row: 512
+// tokens x 512 slots) and a kernel boundary costs more than its work.
+//
+// Row groups.  Every row (b, kv_head) is served by a group of G workgroups
+// ("members") that sit on ONE XCD.  Workgroups are dispatched round-robin
+// over the XCDs (workgroup i runs on XCD i mod n, n | 8), so the members of
+// group g are the workgroups x + 8 * (q * G + m), x = g mod 8, q = g / 8.
+// Members share that XCD's L2, so one member's stores are visible to the
+// others once they have reached L2 (s_waitcnt) if the readers load them
+// with device-scope loads (sc1), which miss in the reader's L1 (a CU's L1
+// is not kept coherent with other CUs' stores; group-scope sc0 loads still
+// hit it).  No device-wide L2 writeback or invalidation is needed.
+// A group barrier is an L2 atomic counter; every wait is bounded and sets
+// an abort flag (all members then leave) instead of spinning forever.
+//
+// Work split of one update of a row:
+//   member m owns tokens [m * tpw, (m + 1) * tpw)  (prep, novelty, append,
+//                routing; tpw <= 64, the token operands stay in LDS)
+//   member m owns slots  [m * spm, (m + 1) * spm)  (merge sums, refreshed
+//                attention rows), spm = ceil(slots / G)
+// Phases, separated by group barriers (|):
+//   [novelty -> | -> rank, append my tokens -> |] -> route(my tokens) -> |
+//   -> merge(my slots) -> arrive, prep(my tokens of the next update), wait
+// The raw keys / values of the next update's tokens are loaded while the
+// routing scan runs, and the merge keys / values alternate between two
+// buffers, so the next update's prep overlaps the barrier that ends this
+// update.
+// The state (s_k, s_v, s_vlen) lives in the caller's arrays; snapshot u
+// holds the attention rows routing reads and snapshot u + 1 receives the
+// refreshed rows of every slot, as in the per-update path.
+
+#include "kvm_device.hpp"
+#include "kvm_internal.hpp"
+#include "kvm_seq.hpp"
+
+#include <algorithm>
+
+namespace kvm {
+namespace {
+
+constexpr int kChainThreads = 512;
+constexpr int kChainWaves = kChainThreads / 64;
+constexpr int kChainTok = 64;        // tokens per member at most
+constexpr int kTilesInFlight = 4;    // 16-slot tiles a wave loads at once
+constexpr unsigned kMaxPolls = 1u << 22;
+constexpr int kCounterStride = 32;   // words between group counters (128 B)
+
+// Group barrier, split so that independent work can run between arriving
+// and waiting.  arrive: this workgroup's global stores have reached L2,
+// then one L2 atomic increment.
+__device__ __forceinline__ void group_arrive(unsigned *ctr) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait: until `target` arrivals (G per barrier).  False when the wait timed
+// out or another group aborted.
+__device__ __forceinline__ bool group_wait(unsigned *ctr, unsigned target, unsigned *abort_flag,
+                                           int *ok_lds) {
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    for (unsigned p = 0; p < kMaxPolls; ++p) {
+      if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+        ok = 1;
+        break;
+      }
+      if ((p & 255u) == 255u &&
+          __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *ok_lds = ok;
+  }
+  __syncthreads();
+  return *ok_lds != 0;
+}
+
+// Loads of data that other members wrote during this launch: buffer loads
+// with device scope (sc1), served by the XCD's L2.  Offsets at or past the
+// resource's byte count read zero.
+constexpr int kBufWord3 = 0x00020000;
+constexpr int kScopeDevice = 16;  // cache-policy bits: sc1
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0,
+                                           int(bytes < 0x7fffffff ? bytes : 0x7fffffff), kBufWord3);
+}
+__device__ __forceinline__ uint4 l2_ld16(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScopeDevice);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t l2_ld4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScopeDevice);
+}
+
+// Lane exchanges across 16 / 32 lanes with v_permlane{16,32}_swap (VALU,
+// no LDS round trip): the value of lane l ^ 16 (l ^ 32).
+__device__ __forceinline__ uint32_t xor16_lane(uint32_t x, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return (lane & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t xor32_lane(uint32_t x, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (lane & 32) ? r[0] : r[1];
+}
+
+__device__ __forceinline__ AttnRows snap_at(const SnapRing &r, int64_t idx) {
+  const int64_t o = (idx % r.ring) * r.stride;
+  return AttnRows{r.k + o, r.v + o, r.cap};
+}
+
+// Scan of the member's tokens (operand rows in LDS, ntk <= 64 of them)
+// against slots [0, hi) of one row's attention keys (written by other
+// members) on MFMA 16x16x32 bf16, computed transposed (slot x token) with
+// the same operand roles and k-step order as the per-update routing kernel,
+// so the fp32 scores are bit-identical.  Wave w takes the 16-slot tiles
+// w + 8 * (4p + s), s < 4, in pass p and loads a pass's four tiles at once;
+// `hook` runs once, right after the first pass's loads are issued.
+//   NOVELTY: max over slots of the bf16-rounded score
+//            (model/kvm_mixer.py:66-68);
+//   route:   first argmax of the fp32 score over slots [lo, hi)
+//            (model/kvm_fp32_routing_reference.py:30-34).
+// Result of local token lt: best_v[lt] (and best_i[lt]).
+template <int D, bool NOVELTY, typename Hook>
+__device__ __forceinline__ void scan_slots(const uint16_t *op, const uint16_t *keys, int lo,
+                                           int hi, int ntk, float (*red_v)[kChainTok],
+                                           int (*red_i)[kChainTok], float *best_v, int *best_i,
+                                           Hook &&hook) {
+  constexpr int STR = D + 8;
+  constexpr int KS = D / 32;
+  constexpr int TF = kTilesInFlight;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_tt = (ntk + 15) >> 4;
+  const int n_st = (hi + 15) >> 4;
+  // Rows j >= hi lie past the resource and read zero (and are masked).
+  const __amdgpu_buffer_rsrc_t kr = l2_rsrc(keys, int64_t(hi) * D * 2);
+
+  float best[4];
+  int bidx[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    best[tt] = -INFINITY;
+    bidx[tt] = -1;
+  }
+  for (int p0 = 0; p0 < n_st; p0 += kChainWaves * TF) {
+    uint4 a[TF][KS];
+#pragma unroll
+    for (int s = 0; s < TF; ++s) {
+      const int j = (p0 + wave + kChainWaves * s) * 16 + (lane & 15);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) a[s][ks] = l2_ld16(kr, (j * D + ks * 32 + (lane >> 4) * 8) * 2);
+    }
+    if (p0 == 0) hook();
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      if (tt < n_tt) {
+        bf16x8 bx[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          bx[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
+              &op[(tt * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
+        f32x4 acc[TF];
+#pragma unroll
+        for (int s = 0; s < TF; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int s = 0; s < TF; ++s)
+            acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s][ks]), bx[ks], acc[s], 0,
+                                                             0, 0);
+        // Slots in increasing order within the lane: a strict > keeps the
+        // first maximum.
+#pragma unroll
+        for (int s = 0; s < TF; ++s) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = (p0 + wave + kChainWaves * s) * 16 + (lane >> 4) * 4 + i;
+            // Selects, not branches: slots outside [lo, hi) score -inf.
+            if constexpr (NOVELTY) {
+              best[tt] = fmaxf(best[tt], j < hi ? rbf(acc[s][i]) : -INFINITY);
+            } else {
+              const float sc = (j >= lo) & (j < hi) ? acc[s][i] : -INFINITY;
+              const bool take = sc > best[tt];
+              best[tt] = take ? sc : best[tt];
+              bidx[tt] = take ? j : bidx[tt];
+            }
+          }
+        }
+      }
+    }
+  }
+  if (n_st == 0) hook();
+
+  // Lane groups (slots 4q..4q+3 of every tile), then waves (interleaved
+  // tiles): larger score wins, equal scores go to the lower slot.
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    float bv = best[tt];
+    int bi = bidx[tt];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t vb = __float_as_uint(bv), ib = uint32_t(bi);
+      const float ob = __uint_as_float(r == 0 ? xor16_lane(vb, lane) : xor32_lane(vb, lane));
+      const int oi = int(r == 0 ? xor16_lane(ib, lane) : xor32_lane(ib, lane));
+      if constexpr (NOVELTY) {
+        bv = fmaxf(bv, ob);
+      } else if (oi >= 0 && (bi < 0 || ob > bv || (ob == bv && oi < bi))) {
+        bv = ob;
+        bi = oi;
+      }
+    }
+    if (lane < 16) {
+      red_v[wave][tt * 16 + lane] = bv;
+      red_i[wave][tt * 16 + lane] = bi;
+    }
+  }
+  __syncthreads();
+  if (tid < kChainTok) {
+    float vv[kChainWaves];
+    int ii[kChainWaves];
+#pragma unroll
+    for (int w = 0; w < kChainWaves; ++w) {
+      vv[w] = red_v[w][tid];
+      ii[w] = red_i[w][tid];
+    }
+    float bv = vv[0];
+    int bi = ii[0];
+#pragma unroll
+    for (int w = 1; w < kChainWaves; ++w) {
+      if constexpr (NOVELTY) {
+        bv = fmaxf(bv, vv[w]);
+      } else if (ii[w] >= 0 && (bi < 0 || vv[w] > bv || (vv[w] == bv && ii[w] < bi))) {
+        bv = vv[w];
+        bi = ii[w];
+      }
+    }
+    best_v[tid] = bv;
+    if (best_i) best_i[tid] = bi;
+  }
+  __syncthreads();
+}
+
+// Raw key / value / gate of the member's tokens, D/8 lanes per token.
+template <int D>
+struct RawTok {
+  static constexpr int IT = kChainTok * (D / 8) / kChainThreads;
+  uint4 k[IT], v[IT];
+  uint16_t g[IT];  // bf16 bits, converted where used (no wait at the load)
+};
+
+template <int D>
+__global__ __launch_bounds__(kChainThreads) void k_chain(
+    kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
+    ChainScratch cs, int rows, int G, int tpw, int spm_max, int32_t *route_log,
+    int32_t *append_log, int64_t log_stride) {
+  constexpr int GL = D / 8;                 // lanes per D-wide row
+  constexpr int STR = D + 8;                // LDS row stride (elements)
+  constexpr int RPP = kChainThreads / GL;   // rows per pass
+  constexpr int IT = RawTok<D>::IT;         // passes over the member's tokens
+  static_assert(IT * RPP == kChainTok, "token passes");
+  __shared__ __attribute__((aligned(16))) uint16_t op_r[kChainTok * STR];  // merge keys
+  __shared__ __attribute__((aligned(16))) uint16_t op_n[kChainTok * STR];  // prep(k)
+  __shared__ float red_v[kChainWaves][kChainTok];
+  __shared__ int red_i[kChainWaves][kChainTok];
+  __shared__ float res_v[kChainTok];
+  __shared__ int res_i[kChainTok];
+  __shared__ int ok_lds;
+  extern __shared__ __attribute__((aligned(16))) int dyn[];
+  int *tok_a = dyn;               // [n_tok] novelty rank flag
+  int *mr = tok_a + n_tok;        // [n_tok] local slot of each token or -1
+  int *lst = mr + n_tok;          // [n_tok] tokens placed per slot
+  int *sorted = lst + n_tok;      // [n_tok] per-slot lists in token order
+  int *cnt = sorted + n_tok;      // [spm_max]
+  int *off = cnt + spm_max;       // [spm_max]
+  int *fill = off + spm_max;      // [spm_max]
+  float *novl = reinterpret_cast<float *>(lst);  // [n_tok] novelty of all tokens (rank phase)
+
+  const int tid = threadIdx.x, part = tid % GL;
+  const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
+  const int member = q % G, group = (q / G) * 8 + xcd;
+  if (group >= rows) return;
+  const int row = group;
+  const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
+  const int t0 = member * tpw;
+  const int ntk = max(0, min(n_tok, t0 + tpw) - t0);
+  const int64_t rb = int64_t(row) * n_tok;
+  const int64_t par_stride = int64_t(rows) * n_tok * D;  // elements between the two merge buffers
+  unsigned *ctr = cs.bar + group * kCounterStride;
+  unsigned target = 0;
+  auto arrive = [&]() __attribute__((always_inline)) {
+    target += unsigned(G);
+    group_arrive(ctr);
+  };
+  auto wait = [&]() __attribute__((always_inline)) {
+    return group_wait(ctr, target, cs.abort_flag, &ok_lds);
+  };
+  uint16_t *s_k = static_cast<uint16_t *>(st.s_k);
+  uint16_t *s_v = static_cast<uint16_t *>(st.s_v);
+  float *s_vlen = static_cast<float *>(st.s_vlen);
+  const int64_t srow = int64_t(row) * st.capacity;
+
+  // Raw tokens of update i (token 0 of the chunk for idle lanes).  Prefill
+  // tokens never come from a ring (src.ring == 0, checked by the host).
+  const uint16_t *k_row = static_cast<const uint16_t *>(src.k) + b * src.k_sb + h * src.k_sh;
+  const uint16_t *v_row = static_cast<const uint16_t *>(src.v) + b * src.v_sb + h * src.v_sh;
+  const uint16_t *g_row = static_cast<const uint16_t *>(src.gate) + b * src.g_sb + h * src.g_sh;
+  auto load_raw = [&](int i, RawTok<D> &rt) __attribute__((always_inline)) {
+    const int64_t tb = list.tok_begin[i];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int lt = (tid + it * kChainThreads) / GL;
+      const int64_t t = tb + (lt < ntk ? t0 + lt : 0);
+      rt.k[it] = *reinterpret_cast<const uint4 *>(k_row + t * src.k_st + part * 8);
+      rt.v[it] = *reinterpret_cast<const uint4 *>(v_row + t * src.v_st + part * 8);
+      rt.g[it] = g_row[t * src.g_st];
+    }
+  };
+  // prep (model/kvm_mixer.py:120-129, model/kvm_triton_mixer.py:429-446):
+  // merge key / value of my tokens into LDS (routing operand) and into the
+  // update's merge buffer; prep(k) into LDS when the update appends.
+  auto prep = [&](int i, const RawTok<D> &rt) __attribute__((always_inline)) {
+    const bool nov = list.n_append[i] > 0;
+    uint16_t *gkb = cs.gk + (i & 1) * par_stride;
+    uint16_t *gvb = cs.gv + (i & 1) * par_stride;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int lt = (tid + it * kChainThreads) / GL;
+      const bool valid = lt < ntk;
+      float k[8], v[8];
+      unpack8(rt.k[it], k);
+      unpack8(rt.v[it], v);
+      const float g = bf2f(rt.g[it]);
+      prep_key<D>(k, part, L);
+      float gk[8], gv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gk[e] = L.gate_keys ? rbf(k[e] * g) : k[e];
+        gv[e] = L.gate_values ? rbf(v[e] * g) : v[e];
+      }
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(&op_r[lt * STR + part * 8]) = valid ? pack8(gk) : z;
+      if (nov) *reinterpret_cast<uint4 *>(&op_n[lt * STR + part * 8]) = valid ? pack8(k) : z;
+      if (valid) {
+        const int64_t o = (rb + t0 + lt) * D + part * 8;
+        store8(gkb + o, gk);
+        store8(gvb + o, gv);
+      }
+    }
+  };
+
+  RawTok<D> rt;
+  load_raw(0, rt);
+  prep(0, rt);
+  __syncthreads();
+
+  for (int i = 0; i < list.count; ++i) {
+    const int64_t u = int64_t(list.u0) + i;
+    const int64_t tb = list.tok_begin[i];
+    const int sb = list.state_before[i], na = list.n_append[i];
+    const int s_after = sb + na;
+    const int protect = min(int(L.sink_len), s_after);
+    const AttnRows cur = snap_at(snaps, u), nxt = snap_at(snaps, u + 1);
+    const uint16_t *gkb = cs.gk + (i & 1) * par_stride;
+    const uint16_t *gvb = cs.gv + (i & 1) * par_stride;
+    int32_t *rlog = route_log ? route_log + u * log_stride + rb : nullptr;
+    int32_t *alog = append_log ? append_log + u * log_stride + rb : nullptr;
+    const uint16_t *cur_k = cur.k + int64_t(row) * cur.cap * D;
+
+    // ---- append (model/kvm_mixer.py:44-75, 231-248): the n_append least
+    // novel tokens, ties to the lower index, become slots sb.. in token order.
+    if (na > 0) {
+      scan_slots<D, true>(op_n, cur_k, 0, sb, ntk, red_v, red_i, res_v, nullptr, [] {});
+      if (tid < ntk) cs.nov[rb + t0 + tid] = res_v[tid];
+      arrive();
+      if (!wait()) return;
+      const __amdgpu_buffer_rsrc_t nr = l2_rsrc(cs.nov + rb, int64_t(n_tok) * 4);
+      for (int t = tid; t < n_tok; t += kChainThreads) novl[t] = __uint_as_float(l2_ld4(nr, t * 4));
+      __syncthreads();
+      for (int t = tid; t < n_tok; t += kChainThreads) {
+        const float x = novl[t];
+        int r = 0;
+        for (int w = 0; w < n_tok; ++w) {
+          const float y = novl[w];
+          r += (y < x) || (y == x && w < t);
+        }
+        tok_a[t] = r < na ? 1 : 0;
+      }
+      __syncthreads();
+      // Positions of my appended tokens (tokens before them that append).
+      if (tid < ntk) {
+        const int t = t0 + tid;
+        int p = 0;
+        for (int w = 0; w < t; ++w) p += tok_a[w];
+        res_i[tid] = tok_a[t] ? p : -1;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int lt = (tid + it * kChainThreads) / GL;
+        const bool valid = lt < ntk && res_i[lt] >= 0;
+        const int tl = lt < ntk ? t0 + lt : 0;  // token of this lane (token 0 when idle)
+        float k[8], v[8];
+        if (L.gate_appends) {
+          unpack8(*reinterpret_cast<const uint4 *>(&op_r[lt * STR + part * 8]), k);
+          unpack8(l2_ld16(l2_rsrc(gvb + rb * D, int64_t(n_tok) * D * 2), (tl * D + part * 8) * 2), v);
+        } else {
+          unpack8(*reinterpret_cast<const uint4 *>(&op_n[lt * STR + part * 8]), k);
+          load8(v_row + (tb + tl) * src.v_st + part * 8, v);
+        }
+        const float vlen = row_norm8<D>(v);
+        float ka[8], va[8];
+        attn_rows<D>(k, v, vlen, part, L, ka, va);
+        if (valid) {
+          const int64_t slot = sb + res_i[lt];
+          const int64_t so = (srow + slot) * D + part * 8;
+          store8(s_k + so, k);
+          store8(s_v + so, v);
+          if (part == 0) s_vlen[srow + slot] = vlen;
+          const int64_t ao = (int64_t(row) * cur.cap + slot) * D + part * 8;
+          store8(cur.k + ao, ka);
+          store8(cur.v + ao, va);
+        }
+      }
+      arrive();
+      if (!wait()) return;
+    }
+
+    // ---- route (model/kvm_fp32_routing_reference.py:30-34); the next
+    // update's raw tokens are loaded behind the scan's slot rows.
+    const bool more = i + 1 < list.count;
+    scan_slots<D, false>(op_r, cur_k, protect, s_after, ntk, red_v, red_i, res_v, res_i,
+                         [&]() __attribute__((always_inline)) {
+                           if (more) load_raw(i + 1, rt);
+                         });
+    if (tid < ntk) {
+      const int t = t0 + tid;
+      const bool app = na > 0 && tok_a[t] != 0;
+      cs.route[rb + t] = app ? -1 : res_i[tid];
+      if (alog) alog[t] = app ? 1 : 0;
+      if (rlog) {
+        int r = res_i[tid];
+        if (app) {
+          int p = 0;
+          for (int w = 0; w < t; ++w) p += tok_a[w];
+          r = sb + p;
+        }
+        rlog[t] = r;
+      }
+    }
+    arrive();
+    if (!wait()) return;
+
+    // ---- merge + refresh (model/kvm_mixer.py:329-335) of my slots
+    const int spm = (s_after + G - 1) / G;
+    const int j0 = member * spm;
+    const int nsl = max(0, min(s_after, j0 + spm) - j0);
+    const __amdgpu_buffer_rsrc_t skr = l2_rsrc(s_k + srow * D, st.capacity * D * 2);
+    const __amdgpu_buffer_rsrc_t svr = l2_rsrc(s_v + srow * D, st.capacity * D * 2);
+    const __amdgpu_buffer_rsrc_t slr = l2_rsrc(s_vlen + srow, st.capacity * 4);
+    const __amdgpu_buffer_rsrc_t gkr = l2_rsrc(gkb + rb * D, int64_t(n_tok) * D * 2);
+    const __amdgpu_buffer_rsrc_t gvr = l2_rsrc(gvb + rb * D, int64_t(n_tok) * D * 2);
+    const __amdgpu_buffer_rsrc_t rr = l2_rsrc(cs.route + rb, int64_t(n_tok) * 4);
+    // Current sums and vlen of the first two slot passes (independent of the
+    // routes; rows past the state read zero and are not stored).
+    auto ld_state = [&](int local, uint4 &kk, uint4 &vv, float &ll) __attribute__((always_inline)) {
+      const int j = j0 + local;
+      kk = l2_ld16(skr, (j * D + part * 8) * 2);
+      vv = l2_ld16(svr, (j * D + part * 8) * 2);
+      ll = __uint_as_float(l2_ld4(slr, j * 4));
+    };
+    uint4 k0, v0, k1, v1;
+    float l0, l1;
+    ld_state(tid / GL, k0, v0, l0);
+    ld_state(RPP + tid / GL, k1, v1, l1);
+
+    for (int e = tid; e < nsl; e += kChainThreads) {
+      cnt[e] = 0;
+      fill[e] = 0;
+    }
+    __syncthreads();
+    for (int t = tid; t < n_tok; t += kChainThreads) {
+      const int r = int(l2_ld4(rr, t * 4));
+      const int lr = (r >= j0 && r < j0 + nsl) ? r - j0 : -1;
+      mr[t] = lr;
+      if (lr >= 0) atomicAdd(&cnt[lr], 1);
+    }
+    __syncthreads();
+    // Exclusive prefix of the slot counts on one wave.
+    if (tid < 64) {
+      const int per = (nsl + 63) >> 6;
+      const int e0 = tid * per;
+      int sum = 0;
+      for (int e = 0; e < per; ++e)
+        if (e0 + e < nsl) sum += cnt[e0 + e];
+      int incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (tid >= o) incl += y;
+      }
+      int run = incl - sum;
+      for (int e = 0; e < per; ++e)
+        if (e0 + e < nsl) {
+          off[e0 + e] = run;
+          run += cnt[e0 + e];
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < n_tok; t += kChainThreads) {
+      const int lr = mr[t];
+      if (lr >= 0) lst[off[lr] + atomicAdd(&fill[lr], 1)] = t;
+    }
+    __syncthreads();
+    // Each slot's list in token order (rank sort), so the fp32 sums run in
+    // token order whatever order the LDS atomics placed them in.
+    for (int base = 0; base < nsl; base += RPP) {
+      const int local = base + tid / GL;
+      if (local < nsl) {
+        const int n = cnt[local], o = off[local];
+        for (int e = part; e < n; e += GL) {
+          const int x = lst[o + e];
+          int r = 0;
+          for (int f = 0; f < n; ++f) r += lst[o + f] < x;
+          sorted[o + r] = x;
+        }
+      }
+    }
+    __syncthreads();
+    auto merge_slot = [&](int local, const uint4 &k_raw, const uint4 &v_raw,
+                          float vlen) __attribute__((always_inline)) {
+      const bool valid = local < nsl;
+      const int j = j0 + (valid ? local : 0);
+      const int n = valid ? cnt[local] : 0;
+      const int o = valid ? off[local] : 0;
+      float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int i0 = 0; i0 < n; i0 += 4) {
+        uint4 xk[4], xv[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if (i0 + w < n) {
+            const int to = (sorted[o + i0 + w] * D + part * 8) * 2;
+            xk[w] = l2_ld16(gkr, to);
+            xv[w] = l2_ld16(gvr, to);
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if (i0 + w < n) {
+            float fk[8], fv[8];
+            unpack8(xk[w], fk);
+            unpack8(xv[w], fv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              sk[e] += fk[e];
+              sv[e] += fv[e];
+            }
+          }
+        }
+      }
+      float k[8], v[8];
+      unpack8(k_raw, k);
+      unpack8(v_raw, v);
+      const int64_t so = (srow + j) * D + part * 8;
+      if (n > 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          k[e] = rbf(k[e] + rbf(sk[e]));
+          v[e] = rbf(v[e] + rbf(sv[e]));
+        }
+        if (valid) {
+          store8(s_k + so, k);
+          store8(s_v + so, v);
+        }
+      }
+      float ka[8], va[8];
+      attn_rows<D>(k, v, vlen, part, L, ka, va);
+      if (valid) {
+        const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
+        store8(nxt.k + ao, ka);
+        store8(nxt.v + ao, va);
+      }
+    };
+    for (int base = 0; base < nsl; base += 2 * RPP) {
+      if (base > 0) {
+        ld_state(base + tid / GL, k0, v0, l0);
+        ld_state(base + RPP + tid / GL, k1, v1, l1);
+      }
+      merge_slot(base + tid / GL, k0, v0, l0);
+      if (base + RPP < nsl) merge_slot(base + RPP + tid / GL, k1, v1, l1);
+    }
+
+    // ---- next update's prep while the other members finish this merge.
+    if (more) {
+      arrive();
+      prep(i + 1, rt);
+      if (!wait()) return;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chain of updates that append nothing (a fixed budget, or a batch in which
+// the budget does not grow): routing is split by SLOT instead of by token.
+//
+// Member m owns the 16-slot blocks m, m + G, m + 2G, ... of its row for the
+// whole launch: their sums (s_k, s_v, vlen) and attention key rows live in
+// the member's LDS.  Phase p of the launch:
+//   combine(p - 1)  every member reads the G partial maxima of every token
+//                   of update p - 1 and keeps the first argmax (largest
+//                   score, lowest slot);
+//   merge(p - 1)    sums of the tokens routed to my slots (token order),
+//                   refreshed attention rows into LDS and snapshot u0 + p;
+//   route(p)        the merge keys of ALL tokens of update p against MY
+//                   slots (MFMA 16x16x32 bf16, the per-update kernel's
+//                   operand roles and k-step order, so the fp32 scores are
+//                   bit-identical) -> per-token maximum over my slots;
+//   prep(p + 1)     merge keys / values of my share of update p + 1's tokens;
+//   one group barrier.
+// Merge keys / values rotate through three buffers (prepared one phase
+// ahead, read by route and, a phase later, by the merge); the partial
+// maxima alternate between two.
+constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
+constexpr int kTokWave = 64;      // tokens per wave in route(p)
+constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
+constexpr int kStageRows = 64;    // routed token rows staged in LDS at once
+constexpr int kChainMaxG = 16;
+
+__device__ __forceinline__ int own_local_to_slot(int l, int G, int m) {
+  return (((l >> 4) * G + m) << 4) | (l & 15);
+}
+
+template <int D>
+__global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
+    kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
+    ChainScratch cs, int rows, int G, int32_t *route_log, int32_t *append_log,
+    int64_t log_stride) {
+  constexpr int GL = D / 8;                 // lanes per D-wide row
+  constexpr int STR = D + 8;                // LDS row stride of key rows (elements)
+  constexpr int KS = D / 32;
+  constexpr int RPP = kChainThreads / GL;   // rows per pass
+  constexpr int SP = kOwnMax / RPP;         // passes over the owned slots
+  constexpr int GP = kStageRows / RPP;      // passes over a chunk of staged token rows
+  constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
+  __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
+  __shared__ __attribute__((aligned(16))) uint16_t own_sk[kOwnMax * D];   // key sums
+  __shared__ __attribute__((aligned(16))) uint16_t own_sv[kOwnMax * D];   // value sums
+  __shared__ __attribute__((aligned(16))) uint16_t stage_k[kStageRows * D];  // routed token rows
+  __shared__ __attribute__((aligned(16))) uint16_t stage_v[kStageRows * D];
+  __shared__ float own_vl[kOwnMax];
+  __shared__ int loc[kFixedMaxTok];      // local slot of each token's route, or -1
+  __shared__ int lst[kFixedMaxTok], sorted[kFixedMaxTok];
+  __shared__ int cnt[kOwnMax], off[kOwnMax], fill[kOwnMax];
+  __shared__ int ok_lds;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = tid % GL;
+  const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
+  const int member = q % G, group = (q / G) * 8 + xcd;
+  if (group >= rows) return;
+  const int row = group;
+  const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
+  const int64_t rb = int64_t(row) * n_tok;
+  const int64_t buf_stride = int64_t(rows) * n_tok * D;  // elements between merge buffers
+  const int tpm = (n_tok + G - 1) / G;                   // prep tokens per member (<= 64)
+  const int pt0 = member * tpm;
+  const int pnt = max(0, min(n_tok, pt0 + tpm) - pt0);
+  unsigned *ctr = cs.bar + group * kCounterStride;
+  unsigned target = 0;
+  auto arrive = [&]() __attribute__((always_inline)) {
+    target += unsigned(G);
+    group_arrive(ctr);
+  };
+  auto wait = [&]() __attribute__((always_inline)) {
+    return group_wait(ctr, target, cs.abort_flag, &ok_lds);
+  };
+  uint16_t *s_k = static_cast<uint16_t *>(st.s_k);
+  uint16_t *s_v = static_cast<uint16_t *>(st.s_v);
+  float *s_vlen = static_cast<float *>(st.s_vlen);
+  const int64_t srow = int64_t(row) * st.capacity;
+  const int S = list.state_before[0];  // no appends: constant over the batch
+  const int protect = min(int(L.sink_len), S);
+  // Owned local slots: 16 per owned block below S.
+  const int nblk = (S + 15) >> 4;
+  const int nown = member < nblk ? ((nblk - 1 - member) / G + 1) * 16 : 0;
+  const uint16_t *k_row = static_cast<const uint16_t *>(src.k) + b * src.k_sb + h * src.k_sh;
+  const uint16_t *v_row = static_cast<const uint16_t *>(src.v) + b * src.v_sb + h * src.v_sh;
+  const uint16_t *g_row = static_cast<const uint16_t *>(src.gate) + b * src.g_sb + h * src.g_sh;
+
+  // ---- owned state and attention keys into LDS (slots >= S stay zero).
+  {
+    const AttnRows a0 = snap_at(snaps, list.u0);
+    for (int base = 0; base < kOwnMax; base += RPP) {
+      const int l = base + tid / GL;
+      const int j = own_local_to_slot(l, G, member);
+      const bool valid = l < nown && j < S;
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const int64_t so = (srow + j) * D + part * 8;
+      *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) =
+          valid ? *reinterpret_cast<const uint4 *>(s_k + so) : z;
+      *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) =
+          valid ? *reinterpret_cast<const uint4 *>(s_v + so) : z;
+      *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) =
+          valid ? *reinterpret_cast<const uint4 *>(a0.k + (int64_t(row) * a0.cap + j) * D + part * 8)
+                : z;
+      if (part == 0) own_vl[l] = valid ? s_vlen[srow + j] : 0.f;
+    }
+  }
+
+  // Raw tokens of my prep share of update i (token 0 of the chunk for idle
+  // lanes; prefill tokens never come from a ring).
+  auto load_raw = [&](int i, RawTok<D> &rt) __attribute__((always_inline)) {
+    const int64_t tb = list.tok_begin[i];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int lt = (tid + it * kChainThreads) / GL;
+      const int64_t t = tb + (lt < pnt ? pt0 + lt : 0);
+      rt.k[it] = *reinterpret_cast<const uint4 *>(k_row + t * src.k_st + part * 8);
+      rt.v[it] = *reinterpret_cast<const uint4 *>(v_row + t * src.v_st + part * 8);
+      rt.g[it] = g_row[t * src.g_st];
+    }
+  };
+  // prep (model/kvm_mixer.py:120-129, model/kvm_triton_mixer.py:429-446):
+  // merge keys / values of my share of update i into merge buffer i % 3.
+  auto prep = [&](int i, const RawTok<D> &rt) __attribute__((always_inline)) {
+    uint16_t *gkb = cs.gk + (i % 3) * buf_stride + rb * D;
+    uint16_t *gvb = cs.gv + (i % 3) * buf_stride + rb * D;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int lt = (tid + it * kChainThreads) / GL;
+      float k[8], v[8];
+      unpack8(rt.k[it], k);
+      unpack8(rt.v[it], v);
+      const float g = bf2f(rt.g[it]);
+      prep_key<D>(k, part, L);
+      float gk[8], gv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gk[e] = L.gate_keys ? rbf(k[e] * g) : k[e];
+        gv[e] = L.gate_values ? rbf(v[e] * g) : v[e];
+      }
+      if (lt < pnt) {
+        store8(gkb + (pt0 + lt) * D + part * 8, gk);
+        store8(gvb + (pt0 + lt) * D + part * 8, gv);
+      }
+    }
+  };
+
+  RawTok<D> rt;
+  load_raw(0, rt);
+  prep(0, rt);
+  arrive();
+  if (!wait()) return;
+
+  for (int p = 0; p <= list.count; ++p) {
+    const bool do_route = p < list.count;
+    const bool do_prep = p + 1 < list.count;
+    // The raw tokens of update p + 1 are loaded behind the latency-critical
+    // loads of the phase (the merge gathers), so waiting for those never
+    // waits for these.
+    auto load_late = [&]() __attribute__((always_inline)) {
+      if (do_prep) load_raw(p + 1, rt);
+    };
+    if (p == 0) load_late();
+
+    if (p >= 1) {
+      // ---- combine(p - 1): first argmax over the members' partial maxima.
+      const int pi = p - 1;
+      const int64_t u = int64_t(list.u0) + pi;
+      const __amdgpu_buffer_rsrc_t pr =
+          l2_rsrc(cs.part + (int64_t(pi & 1) * rows * n_tok + rb) * G, int64_t(n_tok) * G * 8);
+      uint4 pw[kChainMaxG / 2];
+#pragma unroll
+      for (int i = 0; i < kChainMaxG / 2; ++i)
+        if (2 * i < G) pw[i] = l2_ld16(pr, (tid * G + 2 * i) * 8);
+      if (tid < kOwnMax) {
+        cnt[tid] = 0;
+        fill[tid] = 0;
+      }
+      if (tid < n_tok) {
+        float bv = -INFINITY;
+        int bi = -1;
+#pragma unroll
+        for (int i = 0; i < kChainMaxG / 2; ++i) {
+          if (2 * i < G) {
+            const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
+            const int i0 = int(pw[i].y), i1 = int(pw[i].w);
+            if (i0 >= 0 && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
+              bv = v0;
+              bi = i0;
+            }
+            if (i1 >= 0 && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
+              bv = v1;
+              bi = i1;
+            }
+          }
+        }
+        const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
+        loc[tid] = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
+        if (member == 0) {
+          if (route_log) route_log[u * log_stride + rb + tid] = bi;
+          if (append_log) append_log[u * log_stride + rb + tid] = 0;
+        }
+      }
+      __syncthreads();
+      if (tid < n_tok && loc[tid] >= 0) atomicAdd(&cnt[loc[tid]], 1);
+      __syncthreads();
+      if (tid < 64) {  // exclusive prefix of the slot counts (kOwnMax == 64)
+        const int c = cnt[tid];
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o);
+          if (tid >= o) incl += y;
+        }
+        off[tid] = incl - c;
+      }
+      __syncthreads();
+      const int ntot = off[kOwnMax - 1] + cnt[kOwnMax - 1];  // tokens routed to my slots
+      if (tid < n_tok) {
+        const int l = loc[tid];
+        if (l >= 0) lst[off[l] + atomicAdd(&fill[l], 1)] = tid;
+      }
+      __syncthreads();
+      // Each slot's tokens in token order (rank sort), so the fp32 sums run
+      // in token order whatever order the LDS atomics placed them in.
+      for (int base = 0; base < nown; base += RPP) {
+        const int l = base + tid / GL;
+        if (l < nown) {
+          const int n = cnt[l], o = off[l];
+          for (int e = part; e < n; e += GL) {
+            const int x = lst[o + e];
+            int r = 0;
+            for (int f = 0; f < n; ++f) r += lst[o + f] < x;
+            sorted[o + r] = x;
+          }
+        }
+      }
+      __syncthreads();
+
+      // ---- merge(p - 1) (model/kvm_mixer.py:329-335).  The routed token
+      // rows are staged in LDS (all loads of a chunk in flight together),
+      // then each slot sums its rows in token order.
+      const __amdgpu_buffer_rsrc_t gkr =
+          l2_rsrc(cs.gk + (pi % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+      const __amdgpu_buffer_rsrc_t gvr =
+          l2_rsrc(cs.gv + (pi % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+      float sk[SP][8], sv[SP][8];
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sk[sp][e] = 0.f;
+          sv[sp][e] = 0.f;
+        }
+      for (int c0 = 0; c0 < ntot || c0 == 0; c0 += kStageRows) {
+        const int nrow = min(kStageRows, ntot - c0);
+        uint4 xk[GP], xv[GP];
+#pragma unroll
+        for (int gp = 0; gp < GP; ++gp) {
+          const int r = gp * RPP + tid / GL;
+          if (r < nrow) {
+            const int to = (sorted[c0 + r] * D + part * 8) * 2;
+            xk[gp] = l2_ld16(gkr, to);
+            xv[gp] = l2_ld16(gvr, to);
+          }
+        }
+        if (c0 == 0) load_late();
+#pragma unroll
+        for (int gp = 0; gp < GP; ++gp) {
+          const int r = gp * RPP + tid / GL;
+          if (r < nrow) {
+            *reinterpret_cast<uint4 *>(&stage_k[r * D + part * 8]) = xk[gp];
+            *reinterpret_cast<uint4 *>(&stage_v[r * D + part * 8]) = xv[gp];
+          }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int sp = 0; sp < SP; ++sp) {
+          const int l = sp * RPP + tid / GL;
+          if (l < nown) {
+            const int e0 = max(off[l], c0), e1 = min(off[l] + cnt[l], c0 + nrow);
+            for (int e = e0; e < e1; ++e) {
+              float fk[8], fv[8];
+              unpack8(*reinterpret_cast<const uint4 *>(&stage_k[(e - c0) * D + part * 8]), fk);
+              unpack8(*reinterpret_cast<const uint4 *>(&stage_v[(e - c0) * D + part * 8]), fv);
+#pragma unroll
+              for (int x = 0; x < 8; ++x) {
+                sk[sp][x] += fk[x];
+                sv[sp][x] += fv[x];
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+      const AttnRows nxt = snap_at(snaps, u + 1);
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        const int l = sp * RPP + tid / GL;
+        const int j = own_local_to_slot(l, G, member);
+        const bool valid = l < nown && j < S;
+        float k[8], v[8];
+        unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
+        unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
+        if (valid && cnt[l] > 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            k[e] = rbf(k[e] + rbf(sk[sp][e]));
+            v[e] = rbf(v[e] + rbf(sv[sp][e]));
+          }
+          *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = pack8(k);
+          *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = pack8(v);
+        }
+        float ka[8], va[8];
+        attn_rows<D>(k, v, own_vl[l], part, L, ka, va);
+        if (valid) {
+          *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = pack8(ka);
+          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
+          store8(nxt.k + ao, ka);
+          store8(nxt.v + ao, va);
+        }
+      }
+      __syncthreads();
+    }
+
+    if (do_route) {
+      // ---- route(p) (model/kvm_fp32_routing_reference.py:30-34) against my
+      // slots: per-lane maximum in increasing slot order (strict >), then
+      // across the lane groups; larger score wins, ties go to the lower slot.
+      // B operands: my wave's 64 tokens (tokens >= n_tok read zero).
+      uint4 bx[4][KS];
+      const __amdgpu_buffer_rsrc_t gr =
+          l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
+                                    (lane >> 4) * 8) * 2);
+      float best[4];
+      int bidx[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        best[tt] = -INFINITY;
+        bidx[tt] = -1;
+      }
+      for (int lt = 0; lt < nown; lt += 16) {
+        const int jb = own_local_to_slot(lt, G, member);  // first slot of the block
+        uint4 a[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          a[ks] = *reinterpret_cast<const uint4 *>(
+              &own_k[(lt + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]), acc,
+                                                          0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = jb + (lane >> 4) * 4 + i;
+            const float sc = ((j >= protect) && (j < S)) ? acc[i] : -INFINITY;
+            const bool take = sc > best[tt];
+            best[tt] = take ? sc : best[tt];
+            bidx[tt] = take ? j : bidx[tt];
+          }
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        float bv = best[tt];
+        int bi = bidx[tt];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const uint32_t vb = __float_as_uint(bv), ib = uint32_t(bi);
+          const float ob = __uint_as_float(r == 0 ? xor16_lane(vb, lane) : xor32_lane(vb, lane));
+          const int oi = int(r == 0 ? xor16_lane(ib, lane) : xor32_lane(ib, lane));
+          if (oi >= 0 && (bi < 0 || ob > bv || (ob == bv && oi < bi))) {
+            bv = ob;
+            bi = oi;
+          }
+        }
+        const int t = wave * kTokWave + tt * 16 + lane;
+        if (lane < 16 && t < n_tok)
+          cs.part[(int64_t(p & 1) * rows * n_tok + rb + t) * G + member] =
+              make_uint2(__float_as_uint(bv), uint32_t(bi));
+      }
+      if (do_prep) prep(p + 1, rt);
+      arrive();
+      if (!wait()) return;
+    }
+  }
+
+  // ---- owned state back to the caller's arrays.
+  for (int base = 0; base < nown; base += RPP) {
+    const int l = base + tid / GL;
+    if (l < nown) {
+      const int j = own_local_to_slot(l, G, member);
+      if (j < S) {
+        const int64_t so = (srow + j) * D + part * 8;
+        *reinterpret_cast<uint4 *>(s_k + so) = *reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]);
+        *reinterpret_cast<uint4 *>(s_v + so) = *reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_chain_reset(unsigned *bar, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) bar[i] = 0;
+}
+
+}  // namespace
+
+bool chain_plan(const kvm_layer &L, int64_t n_tok, int64_t max_slots, ChainPlan *p) {
+  // Every member of a group must be resident at once: at most one
+  // workgroup per compute unit of the current device.
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  const int64_t limit = std::min<int64_t>(kChainMaxWorkgroups, cus);
+  const int64_t rows = L.batch * L.kv_heads;
+  const int64_t groups = (rows + 7) / 8 * 8;
+  int G = groups * 16 <= limit ? 16 : 8;
+  const int64_t tpw = ((n_tok + G - 1) / G + 15) / 16 * 16;
+  if (tpw > kChainTok || groups * G > limit || n_tok < 1) return false;
+  p->fixed = false;
+  p->G = G;
+  p->tpw = int(tpw);
+  p->spm_max = int((max_slots + G - 1) / G);
+  p->workgroups = int(groups * G);
+  const int64_t dyn = (4 * n_tok + 3 * int64_t(p->spm_max)) * 4;
+  if (dyn > 48 * 1024) return false;
+  p->dyn_lds = size_t(dyn);
+  return true;
+}
+
+bool chain_fixed_ok(const ChainPlan &p, const ChainList &list, int64_t n_tok) {
+  if (n_tok > kFixedMaxTok || list.count < 1 || (p.G & 1)) return false;
+  const int S = list.state_before[0];
+  for (int i = 0; i < list.count; ++i)
+    if (list.n_append[i] != 0 || list.state_before[i] != S) return false;
+  const int nblk = (S + 15) / 16;
+  return (nblk + p.G - 1) / p.G * 16 <= kOwnMax;
+}
+
+int64_t chain_scratch_bytes(const kvm_layer &L, int64_t n_tok) {
+  const size_t tok = size_t(L.batch * L.kv_heads) * size_t(n_tok);
+  auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
+  // three merge buffers of keys, three of values (buffer b at gk + b * rows * n_tok * D),
+  // routes, novelty, two sets of per-member maxima (up to 16 members), counters
+  return int64_t(2 * a256(3 * tok * size_t(L.head_dim) * 2) + 2 * a256(tok * 4) +
+                 a256(2 * tok * 16 * 8) +
+                 a256(size_t(kChainMaxWorkgroups) * kCounterStride * 4 + 256));
+}
+
+ChainScratch carve_chain_scratch(void *base, const kvm_layer &L, int64_t n_tok) {
+  const size_t tok = size_t(L.batch * L.kv_heads) * size_t(n_tok);
+  auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
+  unsigned char *p = static_cast<unsigned char *>(base);
+  ChainScratch c;
+  const size_t kb = tok * size_t(L.head_dim) * 2, ib = a256(tok * 4);
+  const size_t kb3 = a256(3 * kb), pb = a256(2 * tok * 16 * 8);
+  c.gk = reinterpret_cast<uint16_t *>(p);
+  c.gv = reinterpret_cast<uint16_t *>(p + kb3);
+  c.route = reinterpret_cast<int32_t *>(p + 2 * kb3);
+  c.nov = reinterpret_cast<float *>(p + 2 * kb3 + ib);
+  c.part = reinterpret_cast<uint2 *>(p + 2 * kb3 + 2 * ib);
+  c.bar = reinterpret_cast<unsigned *>(p + 2 * kb3 + 2 * ib + pb);
+  c.abort_flag = c.bar + size_t(kChainMaxWorkgroups) * kCounterStride;
+  return c;
+}
+
+hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
+                        const kvm_state &st, const SnapRing &snaps, const ChainList &list,
+                        const ChainScratch &cs, const ChainPlan &p, int32_t *route_log,
+                        int32_t *append_log, hipStream_t stream) {
+  if (list.count <= 0) return hipSuccess;
+  const int nb = kChainMaxWorkgroups * kCounterStride + 64;
+  hipLaunchKernelGGL(k_chain_reset, dim3((nb + 255) / 256), dim3(256), 0, stream, cs.bar, nb);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int rows = int(L.batch * L.kv_heads);
+  const int64_t log_stride = int64_t(rows) * n_tok;
+  if (p.fixed && chain_fixed_ok(p, list, n_tok)) {
+    if (L.head_dim == 128)
+      hipLaunchKernelGGL(k_chain_fixed<128>, dim3(p.workgroups), dim3(kChainThreads), 0, stream, L,
+                         src, int(n_tok), st, snaps, list, cs, rows, p.G, route_log, append_log,
+                         log_stride);
+    else
+      hipLaunchKernelGGL(k_chain_fixed<64>, dim3(p.workgroups), dim3(kChainThreads), 0, stream, L,
+                         src, int(n_tok), st, snaps, list, cs, rows, p.G, route_log, append_log,
+                         log_stride);
+    return hipGetLastError();
+  }
+  if (L.head_dim == 128)
+    hipLaunchKernelGGL(k_chain<128>, dim3(p.workgroups), dim3(kChainThreads), p.dyn_lds, stream, L,
+                       src, int(n_tok), st, snaps, list, cs, rows, p.G, p.tpw, p.spm_max,
+                       route_log, append_log, log_stride);
+  else
+    hipLaunchKernelGGL(k_chain<64>, dim3(p.workgroups), dim3(kChainThreads), p.dyn_lds, stream, L,
+                       src, int(n_tok), st, snaps, list, cs, rows, p.G, p.tpw, p.spm_max,
+                       route_log, append_log, log_stride);
+  return hipGetLastError();
+}
+
+}  // namespace kvm

@@ -81,6 +81,54 @@ hipError_t launch_update(const kvm_layer &L, const kvm_seq &src,
                          int32_t *route_out, int32_t *append_out,
                          hipStream_t stream);
 
+// Persistent update chain (kvm_chain.hip): a batch of consecutive updates
+// of every row in one launch.
+constexpr int kChainMax = 128;             // updates per launch
+constexpr int kChainMaxWorkgroups = 256;   // one 512-thread workgroup per CU
+struct ChainList {
+  int32_t u0;     // update index of entry 0 (snapshot u0 -> u0 + 1, log offset)
+  int32_t count;
+  int32_t tok_begin[kChainMax];
+  int32_t state_before[kChainMax];
+  int32_t n_append[kChainMax];
+};
+// Snapshot ring of attention rows: snapshot i at k + (i % ring) * stride.
+struct SnapRing {
+  uint16_t *k;
+  uint16_t *v;
+  int64_t stride;  // elements between ring entries
+  int64_t ring;
+  int64_t cap;     // slots per row
+};
+struct ChainScratch {
+  uint16_t *gk;          // merge keys   bf16 [3][rows, n_tok, D] (rotating over updates)
+  uint16_t *gv;          // merge values bf16 [3][rows, n_tok, D]
+  int32_t *route;        // merge slot of each token, -1 if appended [rows, n_tok]
+  float *nov;            // novelty of each token [rows, n_tok]
+  uint2 *part;           // per-member route maxima (score bits, slot) [2][rows, n_tok, G]
+  unsigned *bar;         // group barrier counters
+  unsigned *abort_flag;  // set when a group wait timed out
+};
+struct ChainPlan {
+  bool fixed;     // slot-owner routing (no appends in the batch)
+  int G;          // workgroups per row
+  int tpw;        // tokens per workgroup (multiple of 16, <= 64)
+  int spm_max;    // slots per workgroup at max_slots
+  int workgroups;
+  size_t dyn_lds;
+};
+// False when the shape does not fit the chain (the per-update kernels then run).
+bool chain_plan(const kvm_layer &L, int64_t n_tok, int64_t max_slots, ChainPlan *p);
+// Whether a batch may use the slot-owner kernel: no appends, one state
+// length, at most 64 slots per member and 512 tokens per update.
+bool chain_fixed_ok(const ChainPlan &p, const ChainList &list, int64_t n_tok);
+int64_t chain_scratch_bytes(const kvm_layer &L, int64_t n_tok);
+ChainScratch carve_chain_scratch(void *base, const kvm_layer &L, int64_t n_tok);
+hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
+                        const kvm_state &st, const SnapRing &snaps, const ChainList &list,
+                        const ChainScratch &cs, const ChainPlan &p, int32_t *route_log,
+                        int32_t *append_log, hipStream_t stream);
+
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
                              void *ring_k, void *ring_v, void *ring_gate,
                              int64_t ring_cap, int64_t pos, hipStream_t stream);

@@ -427,3 +427,49 @@ def test_prefill_wide_chunks_match_oracle(lib, B, Hq, Hkv, Tn, D, C, mode):
     smx, smean = T.err_stats(sk, st[O.S_K])
     assert smx <= 2e-2 * scale and smean <= 2e-3 * scale, f"final s_k: max {smx:.3e}, mean {smean:.3e}, scale {scale:.3e}"
     T.log(f"[prefill-wide] out max {mx:.2e} mean {mean:.2e}; S={S}; s_k max {smx:.2e} mean {smean:.2e} (scale {scale:.2e})")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Tn,D,C,mode,sink,gate_app,budget", [
+    (1, 8, 8, 4096, 128, 256, "fixed", 1, 0, None),
+    (2, 4, 2, 3000, 64, 128, "power_law", 1, 0, None),
+    (1, 4, 2, 2000, 128, 100, "power_law", 3, 1, None),
+    (1, 32, 32, 8192, 128, 512, "fixed", 1, 0, None),
+    (1, 4, 4, 6000, 64, 256, "power_law", 2, 0, 3),
+])
+def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C, mode, sink, gate_app,
+                                          budget):
+    """The persistent update chains (slot-owner routing for batches without
+    appends, token-split routing otherwise) and the per-update kernels give
+    bit-identical routes, appends, state and outputs (same fp32 scores, same
+    token-order sums); `budget` snapshots force several chain launches."""
+    T.log(f"[chain] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode} sink {sink} ring {budget}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode=mode, sink=sink, min_len=C, n_max=4, factor=6.0,
+                         gate_appends=gate_app)
+    gen = torch.Generator().manual_seed(11)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = (t.to(DEV) for t in _random_inputs(B, Hq, Hkv, Tn, D, 17))
+    plan = m.make_plan(Tn)
+    snap_bytes = None
+    if budget is not None:
+        snap_bytes = budget * 2 * B * Hkv * plan.max_state_len * D * 2
+    res = {}
+    for name, chain, fixed in (("owner", "1", "1"), ("token", "1", "0"), ("per-update", "0", "1")):
+        monkeypatch.setenv("KVM_AMD_CHAIN", chain)
+        monkeypatch.setenv("KVM_AMD_CHAIN_FIXED", fixed)
+        with torch.no_grad():
+            res[name] = m.prefill_raw(q, k, v, g, route_log=True, snapshot_budget=snap_bytes)
+        torch.cuda.synchronize()
+    b = res["per-update"]
+    S = plan.final_state_len
+    assert plan.n_updates > 0
+    for name in ("owner", "token"):
+        a = res[name]
+        for key in ("route_log", "append_log", "out"):
+            assert torch.equal(a[key], b[key]), f"{name} chain: {key}"
+        for key in ("state_k", "state_v", "state_vlen", "state_k_attn", "state_v_attn"):
+            assert torch.equal(a[key][:, :S], b[key][:, :S]), f"{name} chain: {key}"
+    a = res["owner"]
+    n_app = int(a["append_log"].sum())
+    T.log(f"[chain] {plan.n_updates} updates, S={S}, {n_app} appended tokens: identical")
