@@ -275,6 +275,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
   __shared__ float res_v[kChainTok];
   __shared__ int res_i[kChainTok];
   __shared__ int ok_lds;
+  __shared__ float ln_w[D], ln_b[D];  // ln_s_k parameters (LDS: no wait on global loads)
   extern __shared__ __attribute__((aligned(16))) int dyn[];
   int *tok_a = dyn;               // [n_tok] novelty rank flag
   int *mr = tok_a + n_tok;        // [n_tok] local slot of each token or -1
@@ -289,6 +290,11 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int member = q % G, group = (q / G) * 8 + xcd;
   if (group >= rows) return;
+  for (int d = tid; d < D; d += kChainThreads) {
+    ln_w[d] = static_cast<const float *>(L.ln_weight)[d];
+    ln_b[d] = static_cast<const float *>(L.ln_bias)[d];
+  }
+  __syncthreads();
   const int row = group;
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int t0 = member * tpw;
@@ -340,7 +346,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
       unpack8(rt.k[it], k);
       unpack8(rt.v[it], v);
       const float g = bf2f(rt.g[it]);
-      prep_key<D>(k, part, L);
+      prep_key<D>(k, part, L, ln_w, ln_b);
       float gk[8], gv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -419,7 +425,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
         }
         const float vlen = row_norm8<D>(v);
         float ka[8], va[8];
-        attn_rows<D>(k, v, vlen, part, L, ka, va);
+        attn_rows<D>(k, v, vlen, part, L, ln_w, ln_b, ka, va);
         if (valid) {
           const int64_t slot = sb + res_i[lt];
           const int64_t so = (srow + slot) * D + part * 8;
@@ -584,7 +590,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
         }
       }
       float ka[8], va[8];
-      attn_rows<D>(k, v, vlen, part, L, ka, va);
+      attn_rows<D>(k, v, vlen, part, L, ln_w, ln_b, ka, va);
       if (valid) {
         const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
         store8(nxt.k + ao, ka);
@@ -629,22 +635,21 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 //   one group barrier.
 // Merge keys / values rotate through three buffers (prepared one phase
 // ahead, read by route and, a phase later, by the merge); the partial
-// maxima alternate between two.
+// maxima alternate between two.  The raw tokens a prep needs are loaded
+// while the member waits at the previous barrier.
 constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
 constexpr int kTokWave = 64;      // tokens per wave in route(p)
 constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
 constexpr int kStageRows = 64;    // routed token rows staged in LDS at once
-constexpr int kChainMaxG = 16;
 
 __device__ __forceinline__ int own_local_to_slot(int l, int G, int m) {
   return (((l >> 4) * G + m) << 4) | (l & 15);
 }
 
-template <int D>
+template <int D, int GM>  // GM: the group size G (8 or 16)
 __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
-    ChainScratch cs, int rows, int G, int32_t *route_log, int32_t *append_log,
-    int64_t log_stride) {
+    ChainScratch cs, int rows, int32_t *route_log, int32_t *append_log, int64_t log_stride) {
   constexpr int GL = D / 8;                 // lanes per D-wide row
   constexpr int STR = D + 8;                // LDS row stride of key rows (elements)
   constexpr int KS = D / 32;
@@ -662,7 +667,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   __shared__ int lst[kFixedMaxTok], sorted[kFixedMaxTok];
   __shared__ int cnt[kOwnMax], off[kOwnMax], fill[kOwnMax];
   __shared__ int ok_lds;
+  __shared__ float ln_w[D], ln_b[D];  // ln_s_k parameters (LDS: no wait on global loads)
 
+  constexpr int G = GM;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = tid % GL;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int member = q % G, group = (q / G) * 8 + xcd;
@@ -696,6 +703,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   const uint16_t *v_row = static_cast<const uint16_t *>(src.v) + b * src.v_sb + h * src.v_sh;
   const uint16_t *g_row = static_cast<const uint16_t *>(src.gate) + b * src.g_sb + h * src.g_sh;
 
+  for (int d = tid; d < D; d += kChainThreads) {
+    ln_w[d] = static_cast<const float *>(L.ln_weight)[d];
+    ln_b[d] = static_cast<const float *>(L.ln_bias)[d];
+  }
   // ---- owned state and attention keys into LDS (slots >= S stay zero).
   {
     const AttnRows a0 = snap_at(snaps, list.u0);
@@ -741,7 +752,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       unpack8(rt.k[it], k);
       unpack8(rt.v[it], v);
       const float g = bf2f(rt.g[it]);
-      prep_key<D>(k, part, L);
+      prep_key<D>(k, part, L, ln_w, ln_b);
       float gk[8], gv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -755,33 +766,52 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     }
   };
 
+  // Raw tokens of update i + 1 are loaded between arriving at the barrier
+  // that ends phase i - 1 and waiting for it; phase i starts with their prep.
   RawTok<D> rt;
   load_raw(0, rt);
+  __syncthreads();
   prep(0, rt);
   arrive();
+  if (list.count > 1) load_raw(1, rt);
   if (!wait()) return;
 
   for (int p = 0; p <= list.count; ++p) {
     const bool do_route = p < list.count;
     const bool do_prep = p + 1 < list.count;
-    // The raw tokens of update p + 1 are loaded behind the latency-critical
-    // loads of the phase (the merge gathers), so waiting for those never
-    // waits for these.
-    auto load_late = [&]() __attribute__((always_inline)) {
-      if (do_prep) load_raw(p + 1, rt);
+    // Loads are issued in the order they are needed (a wait for one load
+    // waits for every older one): the partial maxima first, the route
+    // operands of update p (my wave's 64 tokens; tokens >= n_tok read zero)
+    // behind the merge gathers.
+    uint4 bx[4][KS];
+    bool bx_issued = false;
+    auto load_bx = [&]() __attribute__((always_inline)) {
+      if (do_route && !bx_issued) {
+        const __amdgpu_buffer_rsrc_t gr =
+            l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
+                                      (lane >> 4) * 8) * 2);
+      }
+      bx_issued = true;
     };
-    if (p == 0) load_late();
+    uint4 pw[GM / 2];
+    if (p >= 1) {
+      const __amdgpu_buffer_rsrc_t pr = l2_rsrc(
+          cs.part + (int64_t((p - 1) & 1) * rows * n_tok + rb) * G, int64_t(n_tok) * G * 8);
+#pragma unroll
+      for (int i = 0; i < GM / 2; ++i) pw[i] = l2_ld16(pr, (tid * GM + 2 * i) * 8);
+    }
+    // The next update's prep while those loads are in flight.
+    if (do_prep) prep(p + 1, rt);
 
     if (p >= 1) {
       // ---- combine(p - 1): first argmax over the members' partial maxima.
       const int pi = p - 1;
       const int64_t u = int64_t(list.u0) + pi;
-      const __amdgpu_buffer_rsrc_t pr =
-          l2_rsrc(cs.part + (int64_t(pi & 1) * rows * n_tok + rb) * G, int64_t(n_tok) * G * 8);
-      uint4 pw[kChainMaxG / 2];
-#pragma unroll
-      for (int i = 0; i < kChainMaxG / 2; ++i)
-        if (2 * i < G) pw[i] = l2_ld16(pr, (tid * G + 2 * i) * 8);
       if (tid < kOwnMax) {
         cnt[tid] = 0;
         fill[tid] = 0;
@@ -790,18 +820,16 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         float bv = -INFINITY;
         int bi = -1;
 #pragma unroll
-        for (int i = 0; i < kChainMaxG / 2; ++i) {
-          if (2 * i < G) {
-            const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
-            const int i0 = int(pw[i].y), i1 = int(pw[i].w);
-            if (i0 >= 0 && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
-              bv = v0;
-              bi = i0;
-            }
-            if (i1 >= 0 && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
-              bv = v1;
-              bi = i1;
-            }
+        for (int i = 0; i < GM / 2; ++i) {
+          const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
+          const int i0 = int(pw[i].y), i1 = int(pw[i].w);
+          if (i0 >= 0 && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
+            bv = v0;
+            bi = i0;
+          }
+          if (i1 >= 0 && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
+            bv = v1;
+            bi = i1;
           }
         }
         const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
@@ -862,7 +890,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           sk[sp][e] = 0.f;
           sv[sp][e] = 0.f;
         }
-      for (int c0 = 0; c0 < ntot || c0 == 0; c0 += kStageRows) {
+      for (int c0 = 0; c0 < ntot; c0 += kStageRows) {
         const int nrow = min(kStageRows, ntot - c0);
         uint4 xk[GP], xv[GP];
 #pragma unroll
@@ -874,7 +902,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
             xv[gp] = l2_ld16(gvr, to);
           }
         }
-        if (c0 == 0) load_late();
+        load_bx();
 #pragma unroll
         for (int gp = 0; gp < GP; ++gp) {
           const int r = gp * RPP + tid / GL;
@@ -903,6 +931,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         }
         __syncthreads();
       }
+      load_bx();
       const AttnRows nxt = snap_at(snaps, u + 1);
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
@@ -922,31 +951,23 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = pack8(v);
         }
         float ka[8], va[8];
-        attn_rows<D>(k, v, own_vl[l], part, L, ka, va);
+        attn_rows<D>(k, v, own_vl[l], part, L, ln_w, ln_b, ka, va);
         if (valid) {
           *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = pack8(ka);
           const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
           store8(nxt.k + ao, ka);
           store8(nxt.v + ao, va);
         }
+        __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
       }
       __syncthreads();
     }
 
+    load_bx();
     if (do_route) {
       // ---- route(p) (model/kvm_fp32_routing_reference.py:30-34) against my
       // slots: per-lane maximum in increasing slot order (strict >), then
       // across the lane groups; larger score wins, ties go to the lower slot.
-      // B operands: my wave's 64 tokens (tokens >= n_tok read zero).
-      uint4 bx[4][KS];
-      const __amdgpu_buffer_rsrc_t gr =
-          l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
-                                    (lane >> 4) * 8) * 2);
       float best[4];
       int bidx[4];
 #pragma unroll
@@ -997,8 +1018,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           cs.part[(int64_t(p & 1) * rows * n_tok + rb + t) * G + member] =
               make_uint2(__float_as_uint(bv), uint32_t(bi));
       }
-      if (do_prep) prep(p + 1, rt);
       arrive();
+      if (p + 2 < list.count) load_raw(p + 2, rt);
       if (!wait()) return;
     }
   }
@@ -1049,7 +1070,7 @@ bool chain_plan(const kvm_layer &L, int64_t n_tok, int64_t max_slots, ChainPlan 
 }
 
 bool chain_fixed_ok(const ChainPlan &p, const ChainList &list, int64_t n_tok) {
-  if (n_tok > kFixedMaxTok || list.count < 1 || (p.G & 1)) return false;
+  if (n_tok > kFixedMaxTok || list.count < 1 || (p.G != 8 && p.G != 16)) return false;
   const int S = list.state_before[0];
   for (int i = 0; i < list.count; ++i)
     if (list.n_append[i] != 0 || list.state_before[i] != S) return false;
@@ -1096,14 +1117,20 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
   const int rows = int(L.batch * L.kv_heads);
   const int64_t log_stride = int64_t(rows) * n_tok;
   if (p.fixed && chain_fixed_ok(p, list, n_tok)) {
-    if (L.head_dim == 128)
-      hipLaunchKernelGGL(k_chain_fixed<128>, dim3(p.workgroups), dim3(kChainThreads), 0, stream, L,
-                         src, int(n_tok), st, snaps, list, cs, rows, p.G, route_log, append_log,
-                         log_stride);
+    const dim3 grid(p.workgroups), blk(kChainThreads);
+    const int nt = int(n_tok);
+    if (L.head_dim == 128 && p.G == 8)
+      hipLaunchKernelGGL((k_chain_fixed<128, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
+                         cs, rows, route_log, append_log, log_stride);
+    else if (L.head_dim == 128)
+      hipLaunchKernelGGL((k_chain_fixed<128, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
+                         cs, rows, route_log, append_log, log_stride);
+    else if (p.G == 8)
+      hipLaunchKernelGGL((k_chain_fixed<64, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
+                         cs, rows, route_log, append_log, log_stride);
     else
-      hipLaunchKernelGGL(k_chain_fixed<64>, dim3(p.workgroups), dim3(kChainThreads), 0, stream, L,
-                         src, int(n_tok), st, snaps, list, cs, rows, p.G, route_log, append_log,
-                         log_stride);
+      hipLaunchKernelGGL((k_chain_fixed<64, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
+                         cs, rows, route_log, append_log, log_stride);
     return hipGetLastError();
   }
   if (L.head_dim == 128)

@@ -28,35 +28,46 @@ __device__ __forceinline__ float seq_g(const kvm_seq &s, int b, int h,
 }
 
 // prep(k) = LayerNorm_s(k with dims < r zeroed), rounded to bf16
-// (model/kvm_mixer.py:120-129).
+// (model/kvm_mixer.py:120-129).  w / b: ln_s_k weight and bias (global or
+// LDS; kernels that keep many loads in flight pass an LDS copy so that
+// reading them does not wait for those loads).
 template <int D>
-__device__ __forceinline__ void prep_key(float (&k)[8], int part,
-                                         const kvm_layer &L) {
+__device__ __forceinline__ void prep_key(float (&k)[8], int part, const kvm_layer &L,
+                                         const float *w, const float *b) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (part * 8 + i < L.rope_partial_dim) k[i] = 0.f;
-  layer_norm8<D>(k, part, static_cast<const float *>(L.ln_weight),
-                 static_cast<const float *>(L.ln_bias), float(L.ln_eps));
+  layer_norm8<D>(k, part, w, b, float(L.ln_eps));
 #pragma unroll
   for (int i = 0; i < 8; ++i) k[i] = rbf(k[i]);
+}
+template <int D>
+__device__ __forceinline__ void prep_key(float (&k)[8], int part, const kvm_layer &L) {
+  prep_key<D>(k, part, L, static_cast<const float *>(L.ln_weight),
+              static_cast<const float *>(L.ln_bias));
 }
 
 // Attention rows of one slot from its (bf16) key / value sums and vlen.
 template <int D>
-__device__ __forceinline__ void attn_rows(const float (&sk)[8],
-                                          const float (&sv)[8], float vlen,
-                                          int part, const kvm_layer &L,
-                                          float (&ka)[8], float (&va)[8]) {
+__device__ __forceinline__ void attn_rows(const float (&sk)[8], const float (&sv)[8], float vlen,
+                                          int part, const kvm_layer &L, const float *w,
+                                          const float *b, float (&ka)[8], float (&va)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     ka[i] = sk[i];
     va[i] = sv[i];
   }
-  layer_norm8<D>(ka, part, static_cast<const float *>(L.ln_weight),
-                 static_cast<const float *>(L.ln_bias), float(L.ln_eps));
+  layer_norm8<D>(ka, part, w, b, float(L.ln_eps));
 #pragma unroll
   for (int i = 0; i < 8; ++i) ka[i] = rbf(ka[i]);
   attn_value8<D>(va, vlen);
+}
+template <int D>
+__device__ __forceinline__ void attn_rows(const float (&sk)[8], const float (&sv)[8], float vlen,
+                                          int part, const kvm_layer &L, float (&ka)[8],
+                                          float (&va)[8]) {
+  attn_rows<D>(sk, sv, vlen, part, L, static_cast<const float *>(L.ln_weight),
+               static_cast<const float *>(L.ln_bias), ka, va);
 }
 
 }  // namespace kvm
