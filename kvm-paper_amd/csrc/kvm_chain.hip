@@ -658,6 +658,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   constexpr int GP = kStageRows / RPP;      // passes over a chunk of staged token rows
   constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
   __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
+  __shared__ __attribute__((aligned(16))) uint16_t own_va[kOwnMax * D];   // attention values
   __shared__ __attribute__((aligned(16))) uint16_t own_sk[kOwnMax * D];   // key sums
   __shared__ __attribute__((aligned(16))) uint16_t own_sv[kOwnMax * D];   // value sums
   __shared__ __attribute__((aligned(16))) uint16_t stage_k[kStageRows * D];  // routed token rows
@@ -932,7 +933,6 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         __syncthreads();
       }
       load_bx();
-      const AttnRows nxt = snap_at(snaps, u + 1);
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
         const int l = sp * RPP + tid / GL;
@@ -954,14 +954,29 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         attn_rows<D>(k, v, own_vl[l], part, L, ln_w, ln_b, ka, va);
         if (valid) {
           *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = pack8(ka);
-          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
-          store8(nxt.k + ao, ka);
-          store8(nxt.v + ao, va);
+          *reinterpret_cast<uint4 *>(&own_va[l * D + part * 8]) = pack8(va);
         }
         __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
       }
       __syncthreads();
     }
+    // Refreshed rows of merge(p - 1) into snapshot u0 + p.  No other member
+    // reads them, so they are stored after arriving at the barrier (its
+    // s_waitcnt then waits only for what the other members need).
+    auto store_snapshot = [&]() __attribute__((always_inline)) {
+      if (p < 1) return;
+      const AttnRows nxt = snap_at(snaps, int64_t(list.u0) + p);
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        const int l = sp * RPP + tid / GL;
+        const int j = own_local_to_slot(l, G, member);
+        if (l < nown && j < S) {
+          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
+          *reinterpret_cast<uint4 *>(nxt.k + ao) = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
+          *reinterpret_cast<uint4 *>(nxt.v + ao) = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
+        }
+      }
+    };
 
     load_bx();
     if (do_route) {
@@ -982,6 +997,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         for (int ks = 0; ks < KS; ++ks)
           a[ks] = *reinterpret_cast<const uint4 *>(
               &own_k[(lt + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]);
+        // Only a block holding sink slots or slots >= S needs the mask.
+        const bool masked = jb < protect || jb + 16 > S;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -989,13 +1006,22 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           for (int ks = 0; ks < KS; ++ks)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]), acc,
                                                           0, 0, 0);
+          if (masked) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = jb + (lane >> 4) * 4 + i;
-            const float sc = ((j >= protect) && (j < S)) ? acc[i] : -INFINITY;
-            const bool take = sc > best[tt];
-            best[tt] = take ? sc : best[tt];
-            bidx[tt] = take ? j : bidx[tt];
+            for (int i = 0; i < 4; ++i) {
+              const int j = jb + (lane >> 4) * 4 + i;
+              const float sc = ((j >= protect) && (j < S)) ? acc[i] : -INFINITY;
+              const bool take = sc > best[tt];
+              best[tt] = take ? sc : best[tt];
+              bidx[tt] = take ? j : bidx[tt];
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const bool take = acc[i] > best[tt];
+              best[tt] = take ? acc[i] : best[tt];
+              bidx[tt] = take ? jb + (lane >> 4) * 4 + i : bidx[tt];
+            }
           }
         }
       }
@@ -1019,8 +1045,11 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
               make_uint2(__float_as_uint(bv), uint32_t(bi));
       }
       arrive();
+      store_snapshot();
       if (p + 2 < list.count) load_raw(p + 2, rt);
       if (!wait()) return;
+    } else {
+      store_snapshot();
     }
   }
 

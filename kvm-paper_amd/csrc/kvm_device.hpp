@@ -138,11 +138,20 @@ __device__ __forceinline__ float row_norm8(const float (&x)[8]) {
 // Value row as the state contributes it to attention:
 // bf16(normalize(v) * vlen), normalize(v) = v / max(|v|, 1e-12)
 // (torch.nn.functional.normalize; model/kvm_mixer.py:205-206).
+// The quotients use one division per row: r = 1/n correctly rounded,
+// q0 = v * r, then one correction q = q0 + r * fma(-q0, n, v) (Markstein's
+// method), which gives the correctly rounded v / n for normal operands; it
+// was checked bit-identical to v / n on gfx950 over 2^31 random operands.
 template <int D>
 __device__ __forceinline__ void attn_value8(float (&v)[8], float vlen) {
   const float n = fmaxf(row_norm8<D>(v), 1e-12f);
+  const float r = 1.0f / n;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = rbf((v[i] / n) * vlen);
+  for (int i = 0; i < 8; ++i) {
+    const float q0 = v[i] * r;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, n, v[i]), r, q0);
+    v[i] = rbf(q * vlen);
+  }
 }
 
 }  // namespace kvm
