@@ -785,19 +785,15 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     // operands of update p (my wave's 64 tokens; tokens >= n_tok read zero)
     // behind the merge gathers.
     uint4 bx[4][KS];
-    bool bx_issued = false;
     auto load_bx = [&]() __attribute__((always_inline)) {
-      if (do_route && !bx_issued) {
-        const __amdgpu_buffer_rsrc_t gr =
-            l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+      const __amdgpu_buffer_rsrc_t gr =
+          l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
-                                      (lane >> 4) * 8) * 2);
-      }
-      bx_issued = true;
+        for (int ks = 0; ks < KS; ++ks)
+          bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
+                                    (lane >> 4) * 8) * 2);
     };
     uint4 pw[GM / 2];
     if (p >= 1) {
@@ -808,6 +804,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     }
     // The next update's prep while those loads are in flight.
     if (do_prep) prep(p + 1, rt);
+    if (p == 0) load_bx();
 
     if (p >= 1) {
       // ---- combine(p - 1): first argmax over the members' partial maxima.
@@ -891,19 +888,23 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           sk[sp][e] = 0.f;
           sv[sp][e] = 0.f;
         }
-      for (int c0 = 0; c0 < ntot; c0 += kStageRows) {
-        const int nrow = min(kStageRows, ntot - c0);
-        uint4 xk[GP], xv[GP];
+      // Routed rows are staged kStageRows at a time.  The first chunk always
+      // runs and its loads are straight-line code (rows past ntot read zero
+      // through the resource bound), followed by the route operands of update
+      // p, so the waits for the gathered rows never wait for those.
+      uint4 xk[GP], xv[GP];
+      auto gather = [&](int c0) __attribute__((always_inline)) {
 #pragma unroll
         for (int gp = 0; gp < GP; ++gp) {
-          const int r = gp * RPP + tid / GL;
-          if (r < nrow) {
-            const int to = (sorted[c0 + r] * D + part * 8) * 2;
-            xk[gp] = l2_ld16(gkr, to);
-            xv[gp] = l2_ld16(gvr, to);
-          }
+          const int pos = c0 + gp * RPP + tid / GL;
+          const int tok = pos < ntot ? sorted[pos] : n_tok;  // n_tok: past the resource
+          const int to = (tok * D + part * 8) * 2;
+          xk[gp] = l2_ld16(gkr, to);
+          xv[gp] = l2_ld16(gvr, to);
         }
-        load_bx();
+      };
+      auto stage_sum = [&](int c0) __attribute__((always_inline)) {
+        const int nrow = min(kStageRows, ntot - c0);
 #pragma unroll
         for (int gp = 0; gp < GP; ++gp) {
           const int r = gp * RPP + tid / GL;
@@ -931,8 +932,14 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
         __syncthreads();
-      }
+      };
+      gather(0);
       load_bx();
+      stage_sum(0);
+      for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
+        gather(c0);
+        stage_sum(c0);
+      }
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
         const int l = sp * RPP + tid / GL;
@@ -963,6 +970,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     // Refreshed rows of merge(p - 1) into snapshot u0 + p.  No other member
     // reads them, so they are stored after arriving at the barrier (its
     // s_waitcnt then waits only for what the other members need).
+    // Non-temporal stores: the attention kernel reads them much later, and
+    // keeping them out of L2 leaves room for the merge buffers the group
+    // reads back over the next two phases.
     auto store_snapshot = [&]() __attribute__((always_inline)) {
       if (p < 1) return;
       const AttnRows nxt = snap_at(snaps, int64_t(list.u0) + p);
@@ -972,13 +982,15 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         const int j = own_local_to_slot(l, G, member);
         if (l < nown && j < S) {
           const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
-          *reinterpret_cast<uint4 *>(nxt.k + ao) = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
-          *reinterpret_cast<uint4 *>(nxt.v + ao) = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
+          const uint4 kk = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
+          const uint4 vv = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
+          typedef unsigned u4 __attribute__((ext_vector_type(4)));
+          __builtin_nontemporal_store(u4{kk.x, kk.y, kk.z, kk.w}, reinterpret_cast<u4 *>(nxt.k + ao));
+          __builtin_nontemporal_store(u4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<u4 *>(nxt.v + ao));
         }
       }
     };
 
-    load_bx();
     if (do_route) {
       // ---- route(p) (model/kvm_fp32_routing_reference.py:30-34) against my
       // slots: per-lane maximum in increasing slot order (strict >), then
