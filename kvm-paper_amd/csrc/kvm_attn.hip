@@ -14,28 +14,32 @@
 //   * window tokens [max(0, (m-n+1)C), query] causally, keys scaled by the
 //     front temperature.
 // Workgroup = NW waves = 32*NW queries of one (batch, q_head); each wave owns
-// 32 queries (two 16-row MFMA tiles).  Keys stream through LDS in blocks of
-// 64: K row-major (times temperature, rounded to bf16, as the reference
-// does), V transposed.  Scores are computed transposed, S^T = K Q^T, with
-// v_mfma_f32_16x16x32_bf16, so that each lane holds 4 consecutive keys of one
-// query row: the P^T tiles feed the O^T = V^T P^T product directly as the B
-// operand (the key order inside a 32-key step is permuted identically in the
-// A operand, which leaves the sum unchanged).  Online softmax in fp32
-// registers with exp2; P rounded to bf16 for the PV product.
+// 32 queries (two 16-row MFMA tiles).  Scores are computed transposed,
+// S^T = K Q^T, with v_mfma_f32_16x16x32_bf16, so that each lane holds 4
+// consecutive keys of one query row: the P^T tiles feed the O^T = V^T P^T
+// product directly as the B operand (the key order inside a 32-key step is
+// permuted identically in the A operand, which leaves the sum unchanged).
+// Online softmax in fp32 registers with exp2; P rounded to bf16 for the PV
+// product.
 //
-// Latency structure: a workgroup of 8 waves (256 queries) shares each staged
-// key block, so a block load feeds twice the MFMA work of a 4-wave tile and
-// each thread stages half as much.  A wave consumes a whole 64-key block per
-// step (8 independent MFMA chains, one max reduction per 64 keys) and keeps
-// a lazily moved reference maximum per row, so the O rescale is rare.  Global loads are buffer loads whose
-// range check zero-fills keys past the end of a range (no per-load
-// branches, 32-bit offsets).  Every 32-key step reads all of its K fragments
-// from LDS before the score MFMAs and all of its V fragments before the
-// softmax arithmetic, so LDS latency overlaps MFMA and VALU work instead of
-// serialising with it.  Two LDS buffers, one barrier per block.  Workgroups
-// are renumbered so that each XCD (dispatch is round-robin over the 8 XCDs)
-// runs a contiguous range of (head, chunk) tiles: the window keys shared by
-// neighbouring chunks stay in that XCD's L2.
+// Numerics against the Triton kernel: the temperature multiplies the fp32
+// score (scale * tau) instead of being rounded into a bf16 copy of K
+// (:1868, :1900); the row sums are fp32 sums of the unrounded weights, as
+// there (:1884).
+//
+// Data movement: key blocks of 64 go from HBM/L2 straight into LDS with
+// buffer_load_dwordx4 ... lds (no register staging, no VALU or ds_write
+// work).  The LDS image of a block keeps keys row-major in 64-byte column
+// groups with a per-key swap of 32-byte halves, so that the K fragment reads
+// (ds_read_b128) and the V^T fragment reads (ds_read_b64_tr_b16, the gfx950
+// transposing LDS read) are free of bank conflicts while each 1 KiB DMA
+// instruction still reads whole 64-byte runs of 16 keys.  Two buffers; the
+// DMA of block j+1 runs while block j is consumed; one barrier per block.
+// A workgroup of 4 waves (one per SIMD) uses 64 KiB of LDS, so two
+// independent workgroups share a CU and fill each other's stalls.
+// Workgroups are renumbered so that each XCD (dispatch is round-robin over
+// the 8 XCDs) runs a contiguous range of (head, chunk) tiles: the window keys
+// shared by neighbouring chunks stay in that XCD's L2.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -44,126 +48,90 @@ namespace kvm {
 namespace {
 
 constexpr int BN = 64;   // keys per block
+constexpr int NW = 4;    // waves per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;
 // Buffer resource word 3 for raw (unformatted, unswizzled) dword access with
-// range checking: out-of-range loads return zero.
+// range checking: out-of-range loads return zero (and LDS-DMA lanes out of
+// range write nothing).
 constexpr int kBufWord3 = 0x00020000;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const f32x2 v = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// LDS image of one K (or V) block of 64 keys: D/32 column groups of 4 KiB,
+// each [64 keys][64 bytes]; byte of (key r, 16-byte unit u) =
+// (u/4)*4096 + r*64 + ((u%4) ^ (2 * bit2(r)))*16.
 template <int D>
-struct AttnSmem {
-  static constexpr int KSTR = D + 8;   // K row stride (elements)
-  static constexpr int VSTR = BN + 8;  // V^T row stride (elements)
-  uint16_t k[BN * KSTR];
-  uint16_t vt[D * VSTR];
+struct Lay {
+  static constexpr int GROUPS = D / 32;
+  static constexpr int BLK = GROUPS * 4096;  // bytes of one K (or V) block
+  static constexpr int BUF = 2 * BLK;        // K block then V block
+  static constexpr int CHUNKS = BLK / 1024;  // DMA instructions per K (or V) block
 };
-
-// Register staging of one K/V block over NT threads: K in 16-byte pieces
-// (key p / (D/8), dims 8 * (p % (D/8))), V in units of 2 keys x 8 dims.
-template <int D, int NT>
-struct Stage {
-  static constexpr int KPIECES = BN * (D / 8);
-  static constexpr int KPT = (KPIECES + NT - 1) / NT;
-  static constexpr int VUNITS = (BN / 2) * (D / 8);
-  static constexpr int VPT = (VUNITS + NT - 1) / NT;
-  uint4 k[KPT];
-  uint4 v[VPT][2];
-};
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
-  return make_uint4(x[0], x[1], x[2], x[3]);
-}
 
 // Resource over keys [0, nvalid) of a range starting at p with row stride
-// `stride` elements: byte offsets key * stride * 2 + 16 * part of keys past
-// nvalid fall outside it and read as zero.
+// `stride` elements.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t key_rsrc(const uint16_t *p, int64_t stride,
                                                           int nvalid) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(p), (short)0,
                                            int(nvalid * stride * 2), kBufWord3);
 }
 
-template <int D, int NT>
-__device__ __forceinline__ void stage_load(Stage<D, NT> &sg, __amdgpu_buffer_rsrc_t kr,
-                                           uint32_t kstride_b, __amdgpu_buffer_rsrc_t vr,
-                                           uint32_t vstride_b) {
-  using S = Stage<D, NT>;
-  const int tid = threadIdx.x;
+// 16-byte-per-lane buffer load into LDS at M0 + 16 * lane.  Issued from
+// inline assembly: the compiler would otherwise order every later LDS read
+// behind it (it cannot tell the DMA target from the buffer being read).  Its
+// completion is awaited explicitly with s_waitcnt vmcnt(0).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
+}
+
+// DMA of one block (keys [0, nvalid) of both ranges, set by the resources)
+// into the buffer at LDS byte address `buf`.  Instruction c fills keys
+// 16*(c%4) .. +15 of column group c/4; wave w issues c = w, w + NW, ...
+// `ko`/`vo`: lane offsets within an instruction, key lane/4, unit
+// (lane%4) ^ swap of that key.
+template <int D>
+__device__ __forceinline__ void issue_block(uint32_t buf, __amdgpu_buffer_rsrc_t kr,
+                                            __amdgpu_buffer_rsrc_t vr, uint32_t ko, uint32_t vo,
+                                            uint32_t kstride_b, uint32_t vstride_b, int wave) {
+  constexpr int PER = Lay<D>::CHUNKS / NW;
+  static_assert(Lay<D>::CHUNKS % NW == 0, "DMA instructions split evenly over the waves");
 #pragma unroll
-  for (int i = 0; i < S::KPT; ++i) {
-    const int p = tid + i * NT;
-    if (S::KPIECES % NT == 0 || p < S::KPIECES) {
-      const int key = p / (D / 8), part = p % (D / 8);
-      sg.k[i] = buf_load16(kr, uint32_t(key) * kstride_b + uint32_t(part) * 16u);
-    }
+  for (int t = 0; t < PER; ++t) {
+    const int c = wave + NW * t;
+    const int cg = c >> 2, rq = c & 3;
+    dma16(kr, buf + uint32_t(cg * 4096 + rq * 1024),
+          ko + uint32_t(16 * rq) * kstride_b + uint32_t(cg * 64));
   }
 #pragma unroll
-  for (int i = 0; i < S::VPT; ++i) {
-    const int u = tid + i * NT;
-    if (S::VUNITS % NT == 0 || u < S::VUNITS) {
-      const int kp = u % (BN / 2), dg = u / (BN / 2);
-      const uint32_t off = uint32_t(2 * kp) * vstride_b + uint32_t(dg) * 16u;
-      sg.v[i][0] = buf_load16(vr, off);
-      sg.v[i][1] = buf_load16(vr, off + vstride_b);
-    }
+  for (int t = 0; t < PER; ++t) {
+    const int c = wave + NW * t;
+    const int cg = c >> 2, rq = c & 3;
+    dma16(vr, buf + uint32_t(Lay<D>::BLK + cg * 4096 + rq * 1024),
+          vo + uint32_t(16 * rq) * vstride_b + uint32_t(cg * 64));
   }
 }
 
-// bf16 pair (lo half of a, lo half of b) -> one word, etc.
-__device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
-template <int D, int NT>
-__device__ __forceinline__ void stage_store(AttnSmem<D> &sm, const Stage<D, NT> &sg,
-                                            float tau, bool scale) {
-  using S = Stage<D, NT>;
-  constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < S::KPT; ++i) {
-    const int p = tid + i * NT;
-    if (S::KPIECES % NT == 0 || p < S::KPIECES) {
-      const int key = p / (D / 8), part = p % (D / 8);
-      uint4 w = sg.k[i];
-      if (scale) {
-        float x[8];
-        unpack8(w, x);
-        w.x = pack_bf16x2(x[0] * tau, x[1] * tau);
-        w.y = pack_bf16x2(x[2] * tau, x[3] * tau);
-        w.z = pack_bf16x2(x[4] * tau, x[5] * tau);
-        w.w = pack_bf16x2(x[6] * tau, x[7] * tau);
-      }
-      *reinterpret_cast<uint4 *>(&sm.k[key * KSTR + part * 8]) = w;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < S::VPT; ++i) {
-    const int u = tid + i * NT;
-    if (S::VUNITS % NT == 0 || u < S::VUNITS) {
-      const int kp = u % (BN / 2), dg = u / (BN / 2);
-      const uint32_t a0[4] = {sg.v[i][0].x, sg.v[i][0].y, sg.v[i][0].z, sg.v[i][0].w};
-      const uint32_t a1[4] = {sg.v[i][1].x, sg.v[i][1].y, sg.v[i][1].z, sg.v[i][1].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // dims 2j (low halves) and 2j+1 (high halves) of keys 2kp, 2kp+1
-        *reinterpret_cast<uint32_t *>(&sm.vt[(dg * 8 + 2 * j) * VSTR + 2 * kp]) = lo_lo(a0[j], a1[j]);
-        *reinterpret_cast<uint32_t *>(&sm.vt[(dg * 8 + 2 * j + 1) * VSTR + 2 * kp]) = hi_hi(a0[j], a1[j]);
-      }
-    }
+// Zero the V rows [nv, 64) of a buffer (a block shorter than 64 keys): the
+// DMA leaves them untouched, and their P weights are zero, so stale bytes
+// must not be Inf or NaN.
+template <int D>
+__device__ __forceinline__ void zero_v_tail(unsigned char *vbuf, int nv) {
+  const int units = (BN - nv) * 4 * Lay<D>::GROUPS;  // 16-byte units
+  for (int i = threadIdx.x; i < units; i += NW * 64) {
+    const int cg = i / ((BN - nv) * 4), rem = i % ((BN - nv) * 4);
+    const int r = nv + (rem >> 2), u = rem & 3;
+    *reinterpret_cast<uint4 *>(vbuf + cg * 4096 + r * 64 + u * 16) = make_uint4(0, 0, 0, 0);
   }
 }
 
@@ -171,7 +139,7 @@ template <int D>
 struct AttnState {
   f32x4 o[2][D / 16];  // O^T tiles [row tile][dv tile]
   float m[2];          // reference maximum of each row (log2 domain), -inf before any key
-  float l[2];          // lane-partial running sum
+  float l[2];          // lane-partial running row sums (fp32, unrounded weights)
 };
 
 // A row's reference maximum moves only when a block's maximum exceeds it by
@@ -180,25 +148,18 @@ struct AttnState {
 // multiplies per lane) is skipped in almost every block.
 constexpr float kRescaleSlack = 8.0f;
 
-// Online-softmax update with the 64 keys of a staged block.  Masked path:
-// keys >= nvalid, or (causal ranges) keys past the query: key > qrel + row,
-// where qrel is the wave's first query minus the position of the block's
-// first key.
+// S^T tiles of the 64 keys of a buffered block: s[kt][rt], kt = 16-key
+// tile, rt = 16-query tile.  kbuf + kb addresses key lane&15, dims
+// 8*(lane>>4).. of column group 0.
 template <int D>
-__device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D> &as,
-                                              const bf16x8 (&qf)[2][D / 32], bool masked,
-                                              int nvalid, bool causal, int qrel, float scale) {
-  constexpr int KSTR = AttnSmem<D>::KSTR, VSTR = AttnSmem<D>::VSTR;
-  const int lane = threadIdx.x & 63;
-  // S^T tiles for 64 keys: s[kt][rt], kt = 16-key tile, rt = 16-query tile.
-  f32x4 s[4][2];
+__device__ __forceinline__ void score_block(const unsigned char *kbuf, const bf16x8 (&qf)[2][D / 32],
+                                            f32x4 (&s)[4][2]) {
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     bf16x8 kf[D / 32];
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks)
-      kf[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
-          &sm.k[(kt * 16 + (lane & 15)) * KSTR + ks * 32 + (lane >> 4) * 8]));
+      kf[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(kbuf + ks * 4096 + kt * 1024));
     s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -207,6 +168,16 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D
       s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[1][ks], s[kt][1], 0, 0, 0);
     }
   }
+}
+
+// Masking (keys >= nvalid, or causal keys > qrel + row, where qrel is the
+// wave's first query minus the position of the block's first key), row
+// maxima (v_permlane swaps across the 16-lane groups) and the lazy move of
+// the reference maximum with its O rescale.
+template <int D>
+__device__ __forceinline__ void block_max(f32x4 (&s)[4][2], AttnState<D> &as, bool masked,
+                                          int nvalid, bool causal, int qrel, float scale) {
+  const int lane = threadIdx.x & 63;
   if (masked) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
@@ -232,8 +203,11 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D
     mx = fmaxf(fmaxf(mx, s[2][rt][3]), s[3][rt][0]);
     mx = fmaxf(fmaxf(mx, s[3][rt][1]), s[3][rt][2]);
     mx = fmaxf(mx, s[3][rt][3]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // max with lane ^ 16, then lane ^ 32 (each swap returns both values)
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     m_new[rt] = mx * scale;
     need |= m_new[rt] > as.m[rt] + kRescaleSlack;
   }
@@ -248,8 +222,13 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D
       for (int dt = 0; dt < D / 16; ++dt) as.o[rt][dt] *= alpha;
     }
   }
-  // P^T in the B-operand layout: two 32-key steps, each lane 8 keys (4 per kt).
-  bf16x8 pb[2][2];  // [32-key step][rt]
+}
+
+// P^T = exp2(S^T * scale - m) in the B-operand layout (two 32-key steps,
+// each lane 8 keys, 4 per kt) and the lane-partial row sums.
+template <int D>
+__device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], AttnState<D> &as,
+                                            float scale, bf16x8 (&pb)[2][2]) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const float base = as.m[rt] == -INFINITY ? 0.f : as.m[rt];
@@ -266,38 +245,50 @@ __device__ __forceinline__ void consume_block(const AttnSmem<D> &sm, AttnState<D
       pk[kt][0] = pack_bf16x2(p[0], p[1]);
       pk[kt][1] = pack_bf16x2(p[2], p[3]);
     }
+    as.l[rt] += psum;
     pb[0][rt] = as_bf16x8(make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]));
     pb[1][rt] = as_bf16x8(make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]));
-    as.l[rt] += psum;
   }
-  // O^T += V^T P^T over the 64 keys (two 32-key steps).
+}
+
+// O^T += V^T P^T over the 64 keys (two 32-key steps).  The
+// V^T fragment (dims dt*16 + lane%16, the 8 keys of the lane's B slots) is
+// two ds_read_b64_tr_b16 reads of the key-major block: within each 16-lane
+// group, source lane s reads 4 dims of key 4*(lane/16) + s/4 and the
+// transpose hands lane l the 4 keys of dim l.  vbuf + vb0 / vb1: lane
+// offsets for even / odd dim tiles.
+template <int D>
+__device__ __forceinline__ void block_pv(const unsigned char *vbuf, uint32_t vb0, uint32_t vb1,
+                                         const bf16x8 (&pb)[2][2], AttnState<D> &as) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
-      const uint16_t *vrow = &sm.vt[(dt * 16 + (lane & 15)) * VSTR + h * 32 + (lane >> 4) * 4];
-      const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
-      const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16);
-      const bf16x8 vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+      const unsigned char *p = vbuf + ((dt & 1) ? vb1 : vb0) + (dt >> 1) * 4096 + h * 2048;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(p));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(p + 1024));
+      const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+      const bf16x8 vf = as_bf16x8(make_uint4(l2.x, l2.y, h2.x, h2.y));
       as.o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[h][0], as.o[0][dt], 0, 0, 0);
       as.o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[h][1], as.o[1][dt], 0, 0, 0);
     }
   }
 }
 
-template <int D, int NW>
+template <int D>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles, int n_chunks,
                     ChunkTable table) {
   constexpr int NT = NW * 64, BM = NW * 32;
-  __shared__ __attribute__((aligned(16))) AttnSmem<D> sm[2];
+  constexpr int BUF = Lay<D>::BUF;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * BUF];
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
   // XCD-contiguous renumbering of the 1-D grid: logical order (q row, chunk, q tile).
   const int N = gridDim.x;
-  const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int x = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
   const int q8 = N / kXcds, r8 = N % kXcds;
-  const int logical = x * q8 + min(x, r8) + j;
+  const int logical = x * q8 + min(x, r8) + jx;
   const int per_row = n_chunks * qtiles;
   const int qrow = logical / per_row;
   const int rem = logical % per_row;
@@ -314,6 +305,11 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t qpos0 = q0 + wave * 32;
 
+  // Zero both buffers once: rows past a short block are then zeros or
+  // earlier keys, never uninitialised bytes.
+  for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT)
+    reinterpret_cast<uint4 *>(lds)[i] = make_uint4(0, 0, 0, 0);
+
   // Q fragments (B operand of S^T): row rt*16 + lane%16, dims ks*32 + 8*(lane/16).
   bf16x8 qf[2][D / 32];
   const uint16_t *qbase = static_cast<const uint16_t *>(A.q) + b * A.q_sb + hq * A.q_sh;
@@ -328,6 +324,14 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
       qf[rt][ks] = as_bf16x8(u);
     }
   }
+  // Complete the Q loads here and hide them from the compiler's wait
+  // tracking: inside the key loop the only outstanding vector-memory
+  // operations are then the block DMAs, awaited explicitly.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) asm volatile("" : "+v"(qf[rt][ks]));
 
   AttnState<D> as;
 #pragma unroll
@@ -340,6 +344,20 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
   const float scale = kLog2e / sqrtf(float(D));
   const float tau_s = static_cast<const float *>(L.state_temp)[hq];
   const float tau_f = static_cast<const float *>(L.front_temp)[hq];
+
+  // Lane offsets in a block image.  K fragments: key lane&15, unit
+  // (lane>>4) ^ swap(key).  V^T transpose reads: key 4*(lane/16) +
+  // (lane%16)/4, 8-byte piece lane&3 of the 32-byte half (dt&1) ^ swap(key)
+  // (bit 2 of the key is bit 0 of lane/16).  DMA: key lane/4 of the
+  // instruction's 16, unit (lane&3) ^ swap(key).
+  const uint32_t kb = uint32_t((lane & 15) * 64 + (((lane >> 4) ^ (((lane >> 2) & 1) << 1)) * 16));
+  const int g = lane >> 4, s4 = lane & 15;
+  const uint32_t vrow = uint32_t((4 * g + (s4 >> 2)) * 64 + 8 * (s4 & 3));
+  const uint32_t vb0 = vrow + uint32_t(32 * (g & 1));
+  const uint32_t vb1 = vrow + uint32_t(32 * ((g & 1) ^ 1));
+  const uint32_t dcol = uint32_t(((lane & 3) ^ (((lane >> 4) & 1) << 1)) * 16);
+  const uint32_t drow = uint32_t(lane >> 2);
+  const uint32_t lds_base = uint32_t(uintptr_t((lds_void *)lds));
 
   // Key ranges: the memory slots (state temperature, never causal), then
   // the window tokens [wb, q_hi) (front temperature, causal).  One copy of
@@ -360,39 +378,45 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
     const int64_t kstride = st ? D : A.kv.k_st;
     const int64_t vstride = st ? D : A.kv.v_st;
     const uint32_t kstride_b = uint32_t(kstride * 2), vstride_b = uint32_t(vstride * 2);
-    const float tau = st ? tau_s : tau_f;
-    const bool do_scale = tau != 1.0f;
+    const uint32_t ko = drow * kstride_b + dcol, vo = drow * vstride_b + dcol;
+    const float sc = scale * (st ? tau_s : tau_f);
     const bool causal = !st;
     const int nb = (nkeys + BN - 1) / BN;
-    __syncthreads();  // both buffers are free
-    {
-      Stage<D, NT> sg;
-      const int nv = min(BN, nkeys);
-      stage_load<D, NT>(sg, key_rsrc(kp, kstride, nv), kstride_b, key_rsrc(vp, vstride, nv), vstride_b);
-      stage_store<D, NT>(sm[0], sg, tau, do_scale);
-    }
-    __syncthreads();
+    // Causal ranges: block jj's first key is at wb + jj * BN.
+    auto qrel_of = [&](int jj) -> int {
+      const int64_t q = causal ? qpos0 - (wb + int64_t(jj) * BN) : int64_t(BN);
+      return int(min(max(q, int64_t(-64)), int64_t(BN)));
+    };
+    auto issue = [&](int jj) {
+      const int jn = jj * BN;
+      const int nv = min(BN, nkeys - jn);
+      if (nv < BN) zero_v_tail<D>(lds + (jj & 1) * BUF + Lay<D>::BLK, nv);
+      issue_block<D>(lds_base + uint32_t((jj & 1) * BUF),
+                     key_rsrc(kp + int64_t(jn) * kstride, kstride, nv),
+                     key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), ko, vo, kstride_b,
+                     vstride_b, wave);
+    };
+    __syncthreads();  // both buffers are free (and zeroed, the first time)
+    issue(0);
+    // Block j is in buffer j & 1.  Step j: wait for this wave's DMA of block
+    // j, barrier (block j complete in LDS; every wave is past block j - 1),
+    // DMA of block j + 1 into the other buffer, then consume block j.
 #pragma unroll 1
     for (int j = 0; j < nb; ++j) {
-      const int j0 = j * BN;
-      const int nvalid = min(BN, nkeys - j0);
-      const bool more = j + 1 < nb;
-      Stage<D, NT> sg;
-      if (more) {
-        const int jn = (j + 1) * BN;
-        const int nv = min(BN, nkeys - jn);
-        stage_load<D, NT>(sg, key_rsrc(kp + int64_t(jn) * kstride, kstride, nv), kstride_b,
-                          key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), vstride_b);
-      }
-      // Causal ranges: position of the block's first key is wb + j0.
-      const int64_t qrel64 = causal ? qpos0 - (wb + j0) : int64_t(BN);
-      const int qrel = int(min(max(qrel64, int64_t(-64)), int64_t(BN)));
-      const bool masked = nvalid < BN || qrel < BN - 1;
-      // wave-uniform: skip blocks entirely above the wave's causal diagonal
-      if (qrel + 31 >= 0)
-        consume_block<D>(sm[j & 1], as, qf, masked, nvalid, causal, qrel, scale);
-      if (more) stage_store<D, NT>(sm[(j + 1) & 1], sg, tau, do_scale);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if (j + 1 < nb) issue(j + 1);
+      const int qrel = qrel_of(j);
+      if (qrel + 31 < 0) continue;  // wave-uniform: block above the wave's causal diagonal
+      const int nvalid = min(BN, nkeys - j * BN);
+      const bool masked = nvalid < BN || qrel < BN - 1;
+      const unsigned char *bc = lds + (j & 1) * BUF;
+      f32x4 s[4][2];
+      score_block<D>(bc + kb, qf, s);
+      block_max<D>(s, as, masked, nvalid, causal, qrel, sc);
+      bf16x8 pb[2][2];
+      block_probs<D>(s, as, sc, pb);
+      block_pv<D>(bc + Lay<D>::BLK, vb0, vb1, pb, as);
     }
   }
 
@@ -400,9 +424,12 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
   uint16_t *obase = static_cast<uint16_t *>(A.out) + b * A.o_sb + hq * A.o_sh;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
+    // row sum over the 4 lanes of the row (lane ^ 16, lane ^ 32)
     float l = as.l[rt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
     const float inv = 1.0f / l;
     const int64_t t = qpos0 + rt * 16 + (lane & 15);
     if (t < q_hi) {
@@ -417,13 +444,13 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
   }
 }
 
-template <int D, int NW>
-hipError_t launch_nw(const kvm_layer &L, const PrefillAttnArgs &a, int64_t chunk_begin,
-                     int64_t n_chunks, const ChunkTable &table, hipStream_t stream) {
+template <int D>
+hipError_t launch_d(const kvm_layer &L, const PrefillAttnArgs &a, int64_t chunk_begin,
+                    int64_t n_chunks, const ChunkTable &table, hipStream_t stream) {
   const int qtiles = int((L.chunk_len + NW * 32 - 1) / (NW * 32));
   const int64_t n_wg = n_chunks * qtiles * L.batch * L.q_heads;
   const dim3 grid{unsigned(n_wg), 1u, 1u};
-  hipLaunchKernelGGL((k_attn_prefill<D, NW>), grid, dim3(NW * 64), 0, stream, L, a,
+  hipLaunchKernelGGL((k_attn_prefill<D>), grid, dim3(NW * 64), 0, stream, L, a,
                      int(chunk_begin), qtiles, int(n_chunks), table);
   return hipGetLastError();
 }
@@ -434,12 +461,8 @@ hipError_t launch_prefill_attention(const kvm_layer &L, const PrefillAttnArgs &a
                                     int64_t chunk_begin, int64_t n_chunks,
                                     const ChunkTable &table, hipStream_t stream) {
   if (n_chunks <= 0) return hipSuccess;
-  const bool wide = L.chunk_len >= 256;
-  if (L.head_dim == 128)
-    return wide ? launch_nw<128, 8>(L, a, chunk_begin, n_chunks, table, stream)
-                : launch_nw<128, 4>(L, a, chunk_begin, n_chunks, table, stream);
-  return wide ? launch_nw<64, 8>(L, a, chunk_begin, n_chunks, table, stream)
-              : launch_nw<64, 4>(L, a, chunk_begin, n_chunks, table, stream);
+  if (L.head_dim == 128) return launch_d<128>(L, a, chunk_begin, n_chunks, table, stream);
+  return launch_d<64>(L, a, chunk_begin, n_chunks, table, stream);
 }
 
 }  // namespace kvm
