@@ -397,7 +397,7 @@ def test_prefill_deterministic(lib):
 ])
 def test_prefill_wide_chunks_match_oracle(lib, B, Hq, Hkv, Tn, D, C, mode):
     """Whole prefill (every query chunk, every update) at chunk lengths that
-    use the 8-wave attention tiles, against the CPU oracle."""
+    span several 128-query attention tiles per chunk, against the CPU oracle."""
     T.log(f"[prefill-wide] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode}")
     cfg = T.mixer_config(Hq, Hkv, D, C, mode=mode, min_len=C, n_max=2, factor=6.0)
     gen = torch.Generator().manual_seed(5)
