@@ -62,24 +62,33 @@ __device__ __forceinline__ void group_arrive(unsigned *ctr) {
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// wait: until `target` arrivals (G per barrier).  False when the wait timed
-// out or another group aborted.
+// Scalar load that misses in the scalar cache (glc) and reads L2, where the
+// members' atomic increments land.  It is counted by lgkmcnt, not vmcnt, so
+// a poll does not wait behind the wave's outstanding vector loads (which
+// return in order): the barrier is seen as soon as the last member arrives.
+__device__ __forceinline__ unsigned l2_scalar_load(const unsigned *p) {
+  unsigned v;
+  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+// wait: until `target` arrivals (G per barrier), polled by wave 0.  False
+// when the wait timed out or another group aborted.
 __device__ __forceinline__ bool group_wait(unsigned *ctr, unsigned target, unsigned *abort_flag,
                                            int *ok_lds) {
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64) {  // wave 0, wave-uniform
     int ok = 0;
     for (unsigned p = 0; p < kMaxPolls; ++p) {
-      if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+      if (l2_scalar_load(ctr) >= target) {
         ok = 1;
         break;
       }
-      if ((p & 255u) == 255u &&
-          __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-        break;
+      if ((p & 255u) == 255u && l2_scalar_load(abort_flag)) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (!ok) __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *ok_lds = ok;
+    if (threadIdx.x == 0) {
+      if (!ok) __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *ok_lds = ok;
+    }
   }
   __syncthreads();
   return *ok_lds != 0;
