@@ -112,6 +112,13 @@ __device__ __forceinline__ uint32_t l2_ld4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScopeDevice);
 }
 
+// Raw token rows are read once: non-temporal loads keep them from evicting
+// the merge buffers the group reads back from L2 one and two updates later.
+__device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
+  const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // Lane exchanges across 16 / 32 lanes with v_permlane{16,32}_swap (VALU,
 // no LDS round trip): the value of lane l ^ 16 (l ^ 32).
 __device__ __forceinline__ uint32_t xor16_lane(uint32_t x, int lane) {
@@ -335,8 +342,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
     for (int it = 0; it < IT; ++it) {
       const int lt = (tid + it * kChainThreads) / GL;
       const int64_t t = tb + (lt < ntk ? t0 + lt : 0);
-      rt.k[it] = *reinterpret_cast<const uint4 *>(k_row + t * src.k_st + part * 8);
-      rt.v[it] = *reinterpret_cast<const uint4 *>(v_row + t * src.v_st + part * 8);
+      rt.k[it] = ld_stream16(k_row + t * src.k_st + part * 8);
+      rt.v[it] = ld_stream16(v_row + t * src.v_st + part * 8);
       rt.g[it] = g_row[t * src.g_st];
     }
   };
@@ -745,8 +752,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     for (int it = 0; it < IT; ++it) {
       const int lt = (tid + it * kChainThreads) / GL;
       const int64_t t = tb + (lt < pnt ? pt0 + lt : 0);
-      rt.k[it] = *reinterpret_cast<const uint4 *>(k_row + t * src.k_st + part * 8);
-      rt.v[it] = *reinterpret_cast<const uint4 *>(v_row + t * src.v_st + part * 8);
+      rt.k[it] = ld_stream16(k_row + t * src.k_st + part * 8);
+      rt.v[it] = ld_stream16(v_row + t * src.v_st + part * 8);
       rt.g[it] = g_row[t * src.g_st];
     }
   };
