@@ -112,6 +112,20 @@ __device__ __forceinline__ uint32_t l2_ld4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScopeDevice);
 }
 
+// LDS byte address of a __shared__ object (wave-uniform).
+typedef __attribute__((address_space(3))) void lds_void;
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T *p) {
+  return __builtin_amdgcn_readfirstlane(uint32_t(uintptr_t((lds_void *)(p))));
+}
+// 16-byte-per-lane device-scope (sc1) buffer load from L2 straight into LDS
+// at M0 + 16 * lane.  Issued from inline assembly so that the compiler does
+// not order later LDS reads behind it; the caller waits with s_waitcnt vmcnt.
+__device__ __forceinline__ void dma16_l2(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r) : "memory");
+}
+
 // Raw token rows are read once: non-temporal loads keep them from evicting
 // the merge buffers the group reads back from L2 one and two updates later.
 __device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
@@ -656,7 +670,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
 constexpr int kTokWave = 64;      // tokens per wave in route(p)
 constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
-constexpr int kStageRows = 64;    // routed token rows staged in LDS at once
+constexpr int kStageRows = 128;   // routed token rows staged in LDS at once
 
 __device__ __forceinline__ int own_local_to_slot(int l, int G, int m) {
   return (((l >> 4) * G + m) << 4) | (l & 15);
@@ -671,7 +685,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   constexpr int KS = D / 32;
   constexpr int RPP = kChainThreads / GL;   // rows per pass
   constexpr int SP = kOwnMax / RPP;         // passes over the owned slots
-  constexpr int GP = kStageRows / RPP;      // passes over a chunk of staged token rows
+  constexpr int RPI = 1024 / (2 * D);        // token rows per 1 KiB DMA instruction
+  constexpr int KI = kStageRows / RPI;       // DMA instructions per staged chunk (keys or values)
+  constexpr int NBX = 4 * KS;               // route-operand loads per lane (load_bx)
   constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
   __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
   __shared__ __attribute__((aligned(16))) uint16_t own_va[kOwnMax * D];   // attention values
@@ -904,31 +920,35 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           sk[sp][e] = 0.f;
           sv[sp][e] = 0.f;
         }
-      // Routed rows are staged kStageRows at a time.  The first chunk always
-      // runs and its loads are straight-line code (rows past ntot read zero
-      // through the resource bound), followed by the route operands of update
-      // p, so the waits for the gathered rows never wait for those.
-      uint4 xk[GP], xv[GP];
+      // Routed rows are staged kStageRows at a time, straight from L2 into
+      // LDS (device-scope LDS-DMA loads, no registers): instruction c of a
+      // chunk fills staged rows RPI*c .. RPI*c + RPI - 1; wave w issues
+      // c = w, w + 8, ... of the keys, then of the values.  Rows past ntot
+      // point past the resource and are not written.
       auto gather = [&](int c0) __attribute__((always_inline)) {
+        const uint32_t kbase = lds_addr(stage_k), vbase = lds_addr(stage_v);
 #pragma unroll
-        for (int gp = 0; gp < GP; ++gp) {
-          const int pos = c0 + gp * RPP + tid / GL;
+        for (int t = 0; t < 2 * KI / kChainWaves; ++t) {
+          const int c = __builtin_amdgcn_readfirstlane(wave) + kChainWaves * t;
+          const int ci = c < KI ? c : c - KI;
+          const int pos = c0 + ci * RPI + lane / GL;
           const int tok = pos < ntot ? sorted[pos] : n_tok;  // n_tok: past the resource
-          const int to = (tok * D + part * 8) * 2;
-          xk[gp] = l2_ld16(gkr, to);
-          xv[gp] = l2_ld16(gvr, to);
+          const uint32_t to = uint32_t((tok * D + part * 8) * 2);
+          if (c < KI)
+            dma16_l2(gkr, kbase + uint32_t(ci * 1024), to);
+          else
+            dma16_l2(gvr, vbase + uint32_t(ci * 1024), to);
         }
       };
-      auto stage_sum = [&](int c0) __attribute__((always_inline)) {
+      // `outstanding`: vector loads issued after the gather that may stay in
+      // flight (loads return in order, so waiting for vmcnt <= outstanding
+      // waits for the gathered rows only).
+      auto stage_sum = [&](int c0, bool bx_behind) __attribute__((always_inline)) {
         const int nrow = min(kStageRows, ntot - c0);
-#pragma unroll
-        for (int gp = 0; gp < GP; ++gp) {
-          const int r = gp * RPP + tid / GL;
-          if (r < nrow) {
-            *reinterpret_cast<uint4 *>(&stage_k[r * D + part * 8]) = xk[gp];
-            *reinterpret_cast<uint4 *>(&stage_v[r * D + part * 8]) = xv[gp];
-          }
-        }
+        if (bx_behind)
+          asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NBX) : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 #pragma unroll
         for (int sp = 0; sp < SP; ++sp) {
@@ -951,10 +971,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       };
       gather(0);
       load_bx();
-      stage_sum(0);
+      stage_sum(0, true);
       for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
         gather(c0);
-        stage_sum(c0);
+        stage_sum(c0, false);
       }
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
