@@ -864,7 +864,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         }
         const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
         loc[tid] = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
-        if (member == 0) {
+        if (tid >= pt0 && tid < pt0 + pnt) {  // each member logs its prep share
           if (route_log) route_log[u * log_stride + rb + tid] = bi;
           if (append_log) append_log[u * log_stride + rb + tid] = 0;
         }
