@@ -90,6 +90,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t key_rsrc(const uint16_t *p, in
 // inline assembly: the compiler would otherwise order every later LDS read
 // behind it (it cannot tell the DMA target from the buffer being read).  Its
 // completion is awaited explicitly with s_waitcnt vmcnt(0).
+// M0 is written inside the statement and not declared clobbered (the compiler
+// rejects M0 as a clobber): this is sound only while no compiled code of the
+// kernel keeps a value of its own in M0, which holds for these kernels (their
+// only M0 writes are these statements; checked in the generated assembly).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");

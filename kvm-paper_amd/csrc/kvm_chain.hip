@@ -121,6 +121,10 @@ __device__ __forceinline__ uint32_t lds_addr(T *p) {
 // 16-byte-per-lane device-scope (sc1) buffer load from L2 straight into LDS
 // at M0 + 16 * lane.  Issued from inline assembly so that the compiler does
 // not order later LDS reads behind it; the caller waits with s_waitcnt vmcnt.
+// M0 is written inside the statement and not declared clobbered (the compiler
+// rejects M0 as a clobber): this is sound only while no compiled code of the
+// kernel keeps a value of its own in M0, which holds for these kernels (their
+// only M0 writes are these statements; checked in the generated assembly).
 __device__ __forceinline__ void dma16_l2(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r) : "memory");
