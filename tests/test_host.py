@@ -248,3 +248,34 @@ def test_product_never_imports_the_oracle():
         text = f.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle", text, flags=re.M), f"{f} imports the oracle"
         assert "kvm_oracle" not in text, f"{f} references the oracle"
+
+
+@pytest.mark.parametrize("src", ["kvm_attn.hip", "kvm_chain.hip"])
+def test_m0_only_written_by_the_lds_dma_helpers(src, tmp_path):
+    """The inline-assembly LDS-DMA loads set M0 without declaring it clobbered
+    (the compiler rejects M0 as a clobber); that is sound only while the
+    compiled kernels use M0 for nothing else.  Compile the device code and
+    check that every M0 write is one of those statements, immediately followed
+    by its buffer load into LDS."""
+    import shutil
+    import subprocess
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path / "k.s"
+    r = subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                        "-o", str(out), str(ROOT / "kvm-paper_amd" / "csrc" / src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln.strip() for ln in out.read_text().splitlines()]
+    code = [ln for ln in lines if ln and not ln.startswith((";", "."))]
+    writes = 0
+    for i, ln in enumerate(code):
+        if re.search(r"\bm0\b", ln):
+            assert re.fullmatch(r"s_mov_b32 m0, s\d+", ln), f"{src}: unexpected use of M0: {ln}"
+            nxt = code[i + 1]
+            assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith(" lds"), (src, ln, nxt)
+            writes += 1
+    assert writes > 0
