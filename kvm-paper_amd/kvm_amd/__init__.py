@@ -4,11 +4,18 @@ Public API:
   SequenceMixer            drop-in for model.kvm_triton_mixer.SequenceMixer
   KVMDecodeCache           carried decode state (TritonKVMDecodeCache API)
   DecodeCacheSnapshot      snapshot used to (re)initialise a decode cache
+  RWKV7BackboneForCausalLM decoder whose token mixers are SequenceMixer
+                           (model.rwkv7_backbone.RWKV7BackboneForCausalLM)
+  MixerConfig              its config (the reference's field names/defaults)
+  StatesDictCache          per-layer carried-state cache of the decoder
   load_library             load libkvm_amd.so (raises if it is not built)
 """
 
 from ._lib import load as load_library
+from .backbone import MixerConfig, RWKV7BackboneForCausalLM, RWKV7BackboneModel, init_random_
 from .decode_cache import DecodeCacheSnapshot, KVMDecodeCache, TritonKVMDecodeCache
 from .mixer import SequenceMixer
+from .states_cache import StatesDictCache
 
-__all__ = ["SequenceMixer", "KVMDecodeCache", "TritonKVMDecodeCache", "DecodeCacheSnapshot", "load_library"]
+__all__ = ["SequenceMixer", "KVMDecodeCache", "TritonKVMDecodeCache", "DecodeCacheSnapshot", "load_library",
+           "MixerConfig", "RWKV7BackboneForCausalLM", "RWKV7BackboneModel", "StatesDictCache", "init_random_"]

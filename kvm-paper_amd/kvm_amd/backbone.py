@@ -1,0 +1,415 @@
+"""GPTAlpha2-style decoder whose token mixers are the HIP KVM ``SequenceMixer``.
+
+Restates the reference's decoder around the mixer, so a whole model (token
+ids -> logits, prefill then cached greedy decode) runs with every KVM layer on
+the MI355X kernels:
+
+  * model/rwkv7_backbone.py:34-73     ``RotaryEmbedding`` (partial interleaved RoPE)
+  * model/rwkv7_backbone.py:103-177   ``MLP`` (relu^2, optional token shift)
+  * model/rwkv7_backbone.py:180-235   ``Block`` (pre-LN, residual scale, lambdas)
+  * model/rwkv7_backbone.py:276-405   ``MixerConfig`` fields and defaults
+  * model/rwkv7_backbone.py:417-685   ``RWKV7BackboneModel`` (embedding, layers,
+                                      U-net skips, head LayerNorm)
+  * model/rwkv7_backbone.py:688-775   ``RWKV7BackboneForCausalLM`` (LM head,
+                                      logit soft cap, fp32 logits)
+
+Parameter names and shapes equal the reference's, so its ``state_dict``
+loads unchanged.  The classes are plain ``nn.Module``s (no HuggingFace
+base classes); generation is ``generate_greedy`` (prefill, then one token
+per step through the layer caches), the loop HuggingFace's greedy
+``generate`` runs on the reference model.
+
+Token-mixer selection follows the reference's ``token_mixer_class_path`` /
+``token_mixer`` (model/rwkv7_backbone.py:186-201).  The reference's KVM mixer
+paths (``model.kvm_mixer``, ``model.kvm_triton_mixer``,
+``model.kvm_fp32_routing_reference``) and ``token_mixer: kvm`` resolve to
+``kvm_amd.mixer.SequenceMixer``; other reference mixers are not part of this
+build and raise ``ValueError``.  Any other importable class path is loaded
+as given.
+"""
+
+from __future__ import annotations
+
+import importlib
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .mixer import set_label
+from .states_cache import StatesDictCache
+
+_KVM_PATH = "kvm_amd.mixer.SequenceMixer"
+_KVM_ALIASES = {
+    "model.kvm_mixer.SequenceMixer",
+    "model.kvm_triton_mixer.SequenceMixer",
+    "model.kvm_fp32_routing_reference.SequenceMixer",
+}
+
+# MixerConfigDataclass defaults (model/rwkv7_backbone.py:276-405) of every
+# field this decoder or the KVM mixer reads.
+_DEFAULTS: dict[str, Any] = dict(
+    model_class_path="kvm_amd.backbone.RWKV7BackboneForCausalLM",
+    vocab_size=50304, num_hidden_layers=12, num_attention_heads=6, num_key_value_heads=None,
+    d_qk_head=None, d_v_head=None, d_head=None, hidden_size=768, mup_base_dim=768,
+    rope_theta=10_000.0, rope_partial_dim=64, ffn_expansion=4.0, token_mixer="kvm",
+    token_mixer_class_path=None, alt_token_mixer="swa", alt_token_mixer_class_path=None,
+    alt_layer_every=-1, use_tokenshift_ffn=False, use_block_lambdas=False, use_skip_connections=False,
+    use_l2wrap=False, logit_softcap=0.0, residual_scale=None,
+    use_value_residual=1, kvm_value_residual_mode="rwkv", kvm_token_shift_mode="rwkv",
+    kvm_apply_merge_gate_to_initial_state=0, kvm_apply_merge_gate_to_appends=0,
+    kvm_use_merge_gate_keys=1, kvm_use_merge_gate_values=1, kvm_use_head_temps=1, kvm_use_vlens=1,
+    kvm_aotriton_forward_attention=1, kvm_aotriton_precompiled_forward=0, use_tokenshift_att=0,
+    sink_len=1, chunk_len=256, n_max_d_chunks=1, n_bswa_chunks=2, state_budget_mode="fixed",
+    state_growth_factor=1.0, state_growth_exponent=0.5, state_round_down=1, state_min_len=-1,
+    state_saturation_n=None, param_dtype="bfloat16", pad_token_id=None, bos_token_id=None,
+    eos_token_id=None,
+)
+
+
+class MixerConfig:
+    """Model config with the reference's field names and defaults
+    (model/rwkv7_backbone.py:276-405).  Unknown keyword arguments are kept as
+    attributes, as the reference's ``PretrainedConfig`` base does."""
+
+    def __init__(self, **kwargs: Any):
+        for k, v in _DEFAULTS.items():
+            setattr(self, k, v)
+        for k, v in kwargs.items():
+            setattr(self, k, v)
+
+    def to_dict(self) -> dict[str, Any]:
+        return dict(vars(self))
+
+
+@dataclass
+class CausalLMOutput:
+    """Logits (fp32) and the cache the step used."""
+
+    logits: torch.Tensor
+    past_key_values: StatesDictCache | None = None
+
+
+def token_shift_delta(x: torch.Tensor, prev_token: torch.Tensor | None = None, *,
+                      fallback: str = "first") -> torch.Tensor:
+    """``shift(x) - x`` with the previous token carried across calls (model/tokenshift.py:11-28)."""
+    if prev_token is None:
+        if fallback == "first":
+            prev_token = x[:, :1]
+        elif fallback == "zero":
+            prev_token = torch.zeros_like(x[:, :1])
+        else:
+            raise ValueError(f"Unsupported token-shift fallback: {fallback!r}")
+    elif prev_token.dtype != x.dtype or prev_token.device != x.device:
+        prev_token = prev_token.to(device=x.device, dtype=x.dtype)
+    return torch.cat([prev_token, x[:, :-1]], dim=1) - x
+
+
+def _orthogonal_(weight: torch.Tensor, gain: float) -> None:
+    """utils/init.py:4-8: fp32 orthogonal init copied into the parameter."""
+    with torch.no_grad():
+        weight.copy_(torch.nn.init.orthogonal_(torch.empty_like(weight, dtype=torch.float), gain))
+
+
+class RotaryEmbedding(nn.Module):
+    """Partial RoPE over interleaved pairs (model/rwkv7_backbone.py:34-73).
+
+    Frequencies ``base^-linspace(0, 1, partial_dim/2)``, each repeated for
+    its pair, zero past ``partial_dim``; cos/sin rounded to bf16 with the odd
+    sine entries negated (the pair swap in ``apply_rotary_embeddings``)."""
+
+    def __init__(self, full_dim: int, partial_dim: int, base: float = 10000.0):
+        super().__init__()
+        self.full_dim, self.partial_dim, self.base = full_dim, partial_dim, base
+        self._freq: torch.Tensor | None = None
+
+    def forward(self, position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        dev = position_ids.device
+        if self._freq is None or self._freq.device != dev:
+            f = (1 / self.base) ** torch.linspace(0.0, 1.0, steps=self.partial_dim // 2,
+                                                  dtype=torch.float32, device=dev)
+            f = f.repeat_interleave(2)
+            self._freq = torch.cat([f, f.new_zeros(self.full_dim - self.partial_dim)])
+        B, T = position_ids.shape
+        # A K=1 product: one fp32 multiply per element, as the reference's matmul.
+        theta = position_ids.float().view(B, T, 1, 1) * self._freq.view(1, 1, 1, -1)
+        cos = theta.cos().bfloat16()
+        sin = theta.sin().bfloat16()
+        sin[..., 1::2] *= -1
+        return cos, sin
+
+
+class MLP(nn.Module):
+    """relu(x W_fc)^2 W_proj with an optional RWKV token shift (model/rwkv7_backbone.py:103-177)."""
+
+    _CACHE_FINAL = "mlp_final_token"
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        self.config, self.layer_idx = config, layer_idx
+        d_hidden = int(config.ffn_expansion * config.hidden_size) // 32 * 32
+        self.c_fc = set_label("matrix_params", nn.Linear(config.hidden_size, d_hidden, bias=False))
+        _orthogonal_(self.c_fc.weight, gain=1)
+        self.c_proj = set_label("matrix_params", nn.Linear(d_hidden, config.hidden_size, bias=False))
+        self.c_proj.weight.data.zero_()
+        if config.use_tokenshift_ffn:
+            with torch.no_grad():
+                ratio = 1.0 - (layer_idx / config.num_hidden_layers)
+                ddd = torch.arange(config.hidden_size, dtype=torch.float32).div_(config.hidden_size).view(1, 1, -1)
+                self.x_k = set_label("scalars", nn.Parameter(1.0 - torch.pow(ddd, ratio ** 4)))
+
+    def forward(self, x, past_key_values=None, **kwargs):
+        if self.config.use_tokenshift_ffn:
+            prev = None
+            if past_key_values is not None:
+                layer_len = past_key_values.get_seq_length(self.layer_idx)
+                cur = int(x.size(1))
+                if layer_len < cur:
+                    raise AssertionError("MLP cache invariant violated: the layer cache must already include "
+                                         "the current attention pass before the MLP runs.")
+                prev = past_key_values.get_states(self.layer_idx).get(self._CACHE_FINAL)
+                prior = layer_len - cur
+                if prior > 0 and prev is None:
+                    raise AssertionError("cached MLP decode requires 'mlp_final_token' from a prior MLP pass.")
+                if prior == 0 and prev is not None:
+                    raise AssertionError("MLP cache invariant violated: found 'mlp_final_token' although no "
+                                         "prior MLP tokens exist for this layer.")
+                if prev is not None and prev.shape != (x.shape[0], 1, x.shape[2]):
+                    raise AssertionError(f"cached MLP decode requires 'mlp_final_token' of shape "
+                                         f"{(x.shape[0], 1, x.shape[2])}, got {tuple(prev.shape)}.")
+                past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:]})
+            xk = x + self.x_k * token_shift_delta(x, prev, fallback="zero")
+        else:
+            xk = x
+        return self.c_proj(F.relu(self.c_fc(xk)).square())
+
+
+def _resolve_mixer_path(config, layer_idx: int) -> str:
+    """model/rwkv7_backbone.py:186-201, with the KVM paths mapped onto this build."""
+    alt = config.alt_layer_every > 1 and layer_idx % config.alt_layer_every == 0
+    if alt:
+        path = config.alt_token_mixer_class_path or f"model.{config.alt_token_mixer}_mixer.SequenceMixer"
+    else:
+        path = config.token_mixer_class_path or f"model.{config.token_mixer}_mixer.SequenceMixer"
+    if path in _KVM_ALIASES:
+        return _KVM_PATH
+    if path.startswith("model."):
+        raise ValueError(f"token mixer {path!r} is not part of this build; only the KVM mixer "
+                         f"({_KVM_PATH}) is provided")
+    return path
+
+
+def _load_class(class_path: str):
+    module_path, class_name = class_path.rsplit(".", 1)
+    return getattr(importlib.import_module(module_path), class_name)
+
+
+class Block(nn.Module):
+    """Pre-LN block: x + scale*mixer(LN(x)), then x + scale*MLP(LN(x)) (model/rwkv7_backbone.py:180-235)."""
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        self.config, self.layer_idx = config, layer_idx
+        self.residual_scale = config.residual_scale or 1.0
+        mixer_cls = _load_class(_resolve_mixer_path(config, layer_idx))
+        self.ln_attn = set_label("scalars", nn.LayerNorm(config.hidden_size))
+        self.attn = mixer_cls(config, layer_idx)
+        self.ln_mlp = set_label("scalars", nn.LayerNorm(config.hidden_size))
+        self.mlp = MLP(config, layer_idx)
+        if config.use_block_lambdas:
+            self.lambdas = set_label("scalars", nn.Parameter(torch.tensor([1.0, 0.0])))
+
+    def forward(self, x, x0, **kwargs):
+        if self.config.use_block_lambdas:
+            x = self.lambdas[0] * x + self.lambdas[1] * x0
+        cached = not self.training and kwargs.get("past_key_values") is not None
+        attn_fn = getattr(self.attn, "forward_inference", self.attn.forward) if cached else self.attn.forward
+        x = x + attn_fn(self.ln_attn(x), x0=x0, **kwargs) * self.residual_scale
+        return x + self.mlp(self.ln_mlp(x), x0=x0, **kwargs) * self.residual_scale
+
+
+class RWKV7BackboneModel(nn.Module):
+    """Embedding -> LayerNorm -> blocks (with optional U-net skips) -> LayerNorm
+    (model/rwkv7_backbone.py:417-685)."""
+
+    def __init__(self, config):
+        super().__init__()
+        if config.alt_layer_every > 0:
+            raise ValueError("alternating token mixers are not part of this build (alt_layer_every must be <= 0)")
+        self.config = config
+        self.padding_idx = config.pad_token_id
+        self.vocab_size = config.vocab_size
+        self.d_qk_head = config.d_qk_head or config.d_head or (config.hidden_size // config.num_attention_heads)
+        self.d_v_head = config.d_v_head or config.d_head or (config.hidden_size // config.num_attention_heads)
+        self.wte = set_label("wte_embed", nn.Embedding(config.vocab_size, config.hidden_size, self.padding_idx),
+                             mup_d_in_ratio=1.0)
+        self.h = nn.ModuleList([Block(config, i) for i in range(config.num_hidden_layers)])
+        with torch.no_grad():
+            nn.init.uniform_(self.wte.weight, a=-1e-4, b=1e-4)
+        if config.use_skip_connections:
+            self.encoder_layers = config.num_hidden_layers // 2
+            self.decoder_layers = config.num_hidden_layers - self.encoder_layers
+            self.skip_weights = set_label("scalars", nn.Parameter(torch.ones(self.decoder_layers)))
+        else:
+            self.encoder_layers, self.decoder_layers = config.num_hidden_layers, 0
+        self.ln_emb = set_label("scalars", nn.LayerNorm(config.hidden_size))
+        self.ln_head = set_label("scalars", nn.LayerNorm(config.hidden_size))
+        self.rotary = RotaryEmbedding(self.d_qk_head, config.rope_partial_dim, config.rope_theta)
+
+    def embed(self, input_ids):
+        return self.ln_emb(self.wte(input_ids))
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
+                inputs_embeds=None, use_cache=None, cache_position=None, **kwargs):
+        """Returns ``(last_hidden_state, past_key_values or None)`` (model/rwkv7_backbone.py:468-570)."""
+        if (input_ids is None) ^ (inputs_embeds is not None):
+            raise ValueError("You must specify exactly one of input_ids or inputs_embeds")
+        if inputs_embeds is None:
+            inputs_embeds = self.embed(input_ids)
+        if cache_position is not None and cache_position.numel() > 0:
+            past_seen = int(cache_position.reshape(-1)[0].item())
+        elif position_ids is not None and position_ids.numel() > 0:
+            past_seen = int(position_ids.reshape(-1)[0].item())
+        elif (attention_mask is not None and past_key_values is not None
+              and attention_mask.shape[-1] > inputs_embeds.shape[1]):
+            past_seen = int(attention_mask.shape[-1] - inputs_embeds.shape[1])
+        elif past_key_values is None:
+            past_seen = 0
+        else:
+            raise ValueError("Cannot infer cached token count from past_key_values alone. "
+                             "Pass cache_position or position_ids when using a layer-indexed cache.")
+        if use_cache and not isinstance(past_key_values, StatesDictCache):
+            past_key_values = StatesDictCache()
+        if position_ids is None:
+            position_ids = (torch.arange(inputs_embeds.shape[1], device=inputs_embeds.device) + past_seen).unsqueeze(0)
+        if attention_mask is not None:
+            if bool(torch.all(attention_mask.sum(dim=-1) == attention_mask.shape[-1]).item()):
+                attention_mask = None
+            else:
+                raise NotImplementedError("left or right padding attention_masks are not supported by the model code")
+        if past_seen > 0 and inputs_embeds.shape[1] > 1:
+            raise AssertionError("multi-token inputs with past_key_values are not supported; "
+                                 "decode one token per step")
+        x = self._forward_model(input_ids, inputs_embeds, position_ids=position_ids, attention_mask=attention_mask,
+                                past_key_values=past_key_values, use_cache=use_cache, **kwargs)
+        return x, (past_key_values if use_cache else None)
+
+    def _forward_model(self, input_ids, x, position_ids, **kwargs):
+        """model/rwkv7_backbone.py:585-685 (no alternating layers)."""
+        x0 = x
+        position_embeddings = self.rotary(position_ids)
+        first = self.h[0]
+        first_kwargs_fn = getattr(first.attn, "get_first_layer_kwargs", lambda x0, x, **kw: {})
+        first_kwargs = first_kwargs_fn(x0=x0, x=first.ln_attn(x0), input_ids=input_ids, **kwargs)
+        layer_kwargs = dict(x0=x0, **first_kwargs, **kwargs)
+        layer_kwargs["position_embeddings"] = position_embeddings
+        skips = []
+        for i in range(self.encoder_layers):
+            x = self.h[i](x, **layer_kwargs)
+            if self.config.use_skip_connections:
+                skips.append(x)
+        for i in range(self.decoder_layers):
+            # An odd layer count pops an empty list, as the reference does.
+            x = self.h[self.encoder_layers + i](x + self.skip_weights[i] * skips.pop(), **layer_kwargs)
+        return self.ln_head(x)
+
+
+class RWKV7BackboneForCausalLM(nn.Module):
+    """Decoder + LM head (model/rwkv7_backbone.py:688-775)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.config = config
+        self.transformer = RWKV7BackboneModel(config)
+        self.lm_head = set_label("lm_head", nn.Linear(config.hidden_size, config.vocab_size, bias=False))
+        _orthogonal_(self.lm_head.weight, gain=0.5 * (config.vocab_size / config.hidden_size) ** 0.5)
+
+    def get_input_embeddings(self):
+        return self.transformer.wte
+
+    def get_output_embeddings(self):
+        return self.lm_head
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
+                inputs_embeds=None, labels=None, use_cache=None, logits_to_keep: int | torch.Tensor = 0,
+                **kwargs) -> CausalLMOutput:
+        if labels is not None:
+            raise ValueError("this build runs the inference forward path only (no loss)")
+        hidden, cache = self.transformer(input_ids=input_ids, attention_mask=attention_mask,
+                                         position_ids=position_ids, past_key_values=past_key_values,
+                                         inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
+        keep = slice(-logits_to_keep, None) if isinstance(logits_to_keep, int) else logits_to_keep
+        logits = self.lm_head(hidden[:, keep, :])
+        if self.config.logit_softcap != 0:
+            logits = self.config.logit_softcap * torch.tanh(logits / self.config.logit_softcap)
+        return CausalLMOutput(logits=logits.float(), past_key_values=cache)
+
+    @torch.no_grad()
+    def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
+                        cache: StatesDictCache | None = None, on_step=None) -> torch.Tensor:
+        """Prefill ``input_ids`` [B, T], then append ``max_new_tokens`` argmax
+        tokens, one cached single-token step each.  Returns [B, max_new_tokens].
+        ``on_step(step, logits)`` (optional) sees each step's fp32 logits
+        [B, vocab]; step 0 is the prefill's last position."""
+        B, T = input_ids.shape
+        cache = StatesDictCache() if cache is None else cache
+        out = self(input_ids=input_ids, past_key_values=cache, use_cache=True,
+                   cache_position=torch.arange(T, device=input_ids.device), logits_to_keep=1)
+        logits = out.logits[:, -1]
+        tokens = torch.empty(B, max_new_tokens, dtype=torch.long, device=input_ids.device)
+        for s in range(max_new_tokens):
+            if on_step is not None:
+                on_step(s, logits)
+            tok = logits.argmax(-1)
+            tokens[:, s] = tok
+            if s + 1 == max_new_tokens:
+                break
+            pos = torch.tensor([T + s], device=input_ids.device)
+            logits = self(input_ids=tok[:, None], past_key_values=cache, use_cache=True,
+                          cache_position=pos, logits_to_keep=1).logits[:, -1]
+        return tokens
+
+
+@torch.no_grad()
+def init_random_(model: nn.Module, seed: int = 0) -> nn.Module:
+    """Seeded random weights for benchmarks and tests, generated on the
+    device the parameters live on (a model built under ``torch.device("meta")``
+    and materialised with ``to_empty`` gets every value here).
+
+    Linear / embedding matrices ~ N(0, 1/fan_in) (embedding N(0, 1)); LayerNorm
+    weight 1 + 0.1 N, bias 0.1 N; token-shift mixing coefficients U(0, 1);
+    every other parameter 1 + 0.1 N for scales (temperatures, lambdas, skip
+    weights) and 0.1 N otherwise.  Unlike the reference's initialisation, no
+    output projection is zero, so every layer contributes."""
+    p0 = next(model.parameters())
+    gen = torch.Generator(device=p0.device).manual_seed(seed)
+
+    def normal_(t, mean=0.0, std=1.0):
+        t.copy_(torch.randn(t.shape, generator=gen, device=t.device, dtype=torch.float32) * std + mean)
+
+    done = set()
+    for mod in model.modules():
+        if isinstance(mod, nn.LayerNorm):
+            normal_(mod.weight, 1.0, 0.1)
+            normal_(mod.bias, 0.0, 0.1)
+            done.update((id(mod.weight), id(mod.bias)))
+        elif isinstance(mod, (nn.Linear, nn.Embedding)):
+            normal_(mod.weight, 0.0, 1.0 if isinstance(mod, nn.Embedding) else mod.weight.shape[1] ** -0.5)
+            done.add(id(mod.weight))
+    for name, p in model.named_parameters():
+        if id(p) in done:
+            continue
+        leaf = name.rsplit(".", 1)[-1]
+        if leaf in ("x_q", "x_k", "x_v", "x_v_hidden"):
+            p.copy_(torch.rand(p.shape, generator=gen, device=p.device, dtype=torch.float32))
+        elif leaf in ("front_head_temp", "state_head_temp", "lambdas", "skip_weights", "lamb"):
+            normal_(p, 1.0, 0.1)
+        else:
+            normal_(p, 0.0, 0.1)
+    return model
+
+
+__all__ = ["MixerConfig", "RotaryEmbedding", "MLP", "Block", "RWKV7BackboneModel", "RWKV7BackboneForCausalLM",
+           "CausalLMOutput", "StatesDictCache", "init_random_", "token_shift_delta"]

@@ -53,3 +53,38 @@ def oracle_setup(fx: dict):
         front_temp=fx["in_front_temp"], state_temp=fx["in_state_temp"],
     )
     return cfg, p
+
+
+BACKBONE = GOLDEN / "backbone"
+
+
+def backbone_names():
+    return sorted(p.stem for p in BACKBONE.glob("*.npz"))
+
+
+def load_backbone(name: str) -> dict:
+    """Whole-decoder fixture of tests/golden/make_golden_backbone.py: meta,
+    bf16 ``params`` (reference state_dict names), ``input_ids`` [B,T],
+    fp32 ``prefill_logits`` [B,T,V], greedy ``decode_tokens`` [B,N] and
+    ``decode_logits`` [B,N,V] (logits after feeding decode token s)."""
+    z = np.load(BACKBONE / f"{name}.npz", allow_pickle=False)
+    out = {"meta": json.loads(str(z["meta_json"]))}
+    out["params"] = {k[len("param."):]: torch.from_numpy(np.array(z[k])).view(torch.bfloat16)
+                     for k in z.files if k.startswith("param.")}
+    for key in ("input_ids", "prefill_logits", "decode_tokens", "decode_logits"):
+        out[key] = torch.from_numpy(np.array(z[key]))
+    return out
+
+
+def backbone_model(fx: dict, mixer_path: str | None = None, device="cpu"):
+    """The build's decoder with a fixture's config and weights (bf16, eval).
+    ``mixer_path`` overrides the token mixer class path; by default the
+    reference's path in the fixture resolves to the HIP mixer."""
+    from kvm_amd.backbone import MixerConfig, RWKV7BackboneForCausalLM
+
+    m = dict(fx["meta"]["model"])
+    if mixer_path is not None:
+        m["token_mixer_class_path"] = mixer_path
+    model = RWKV7BackboneForCausalLM(MixerConfig(**m)).to(torch.bfloat16)
+    model.load_state_dict(fx["params"], strict=True)
+    return model.to(device).eval()
