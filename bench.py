@@ -13,6 +13,10 @@ Workloads:
            a chunk boundary is crossed, split-K attention).  The timed
            region is `--decode-steps` consecutive tokens from a fresh
            snapshot, so the one update per 256 tokens is included.
+  decoder  config 5: random-init 24-layer all-KVM decoder (d_model 2048,
+           16 heads of 128, vocab 65536, chunk 512, 512 fixed slots):
+           prefill 16384 random token ids at batch 8, then greedy decode
+           (`--e2e-decode` steps); reported in the "decoder_e2e" object.
 
 Prints ONE JSON line: value = prefill tokens/s; the decode figures are in
 the "decode" object.  roofline: achieved algorithmic FLOP/s (prefill
@@ -191,6 +195,49 @@ def bench_decode(args, torch, kvm_amd):
     )
 
 
+def bench_e2e(args, torch, kvm_amd):
+    """Config 5: random-init 24-layer all-KVM decoder (d_model 2048, 16 heads
+    of 128, vocab 65536, bf16, chunk 512, 512 fixed slots); prefill 16384
+    random token ids at batch 8, then greedy decode.  One untimed warm-up
+    (prefill + 8 decode steps), then the timed prefill and decode."""
+    from kvm_amd.backbone import MixerConfig, RWKV7BackboneForCausalLM, StatesDictCache, init_random_
+
+    cfg = MixerConfig(vocab_size=65536, num_hidden_layers=24, num_attention_heads=16, hidden_size=2048,
+                      mup_base_dim=2048, use_tokenshift_att=1, use_tokenshift_ffn=1, residual_scale=0.5,
+                      rope_partial_dim=64, chunk_len=512, n_bswa_chunks=2, state_min_len=512,
+                      state_budget_mode="fixed", sink_len=1)
+    with torch.device("meta"):
+        model = RWKV7BackboneForCausalLM(cfg)
+    model = init_random_(model.to_empty(device="cuda").to(torch.bfloat16), 0).eval()
+    B, T, n_dec = 8, 16384, args.e2e_decode
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=gen)
+
+    def run(n):
+        cache = StatesDictCache()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        e[0].record()
+        lg = model(input_ids=ids, past_key_values=cache, use_cache=True,
+                   cache_position=torch.arange(T, device="cuda"), logits_to_keep=1).logits[:, -1]
+        e[1].record()
+        for s in range(n):
+            tok = lg.argmax(-1)
+            lg = model(input_ids=tok[:, None], past_key_values=cache, use_cache=True,
+                       cache_position=torch.tensor([T + s], device="cuda"), logits_to_keep=1).logits[:, -1]
+        e[2].record()
+        torch.cuda.synchronize()
+        return e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+
+    with torch.no_grad():
+        run(8)
+        pre_ms, dec_ms = run(n_dec)
+    del model
+    torch.cuda.empty_cache()
+    return dict(prefill_ms=pre_ms, prefill_tok_s=B * T / (pre_ms * 1e-3), decode_ms_per_step=dec_ms / n_dec,
+                decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec)
+
+
 def cpu_baseline(torch, sample_T):
     """The CPU oracle (eager restatement of model/kvm_mixer.py with fp32
     routing) on the first sample_T tokens of the prefill workload."""
@@ -231,7 +278,10 @@ def main():
                     help="tokens of the prefill workload the CPU baseline runs (default: all)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+    ap.add_argument("--skip-e2e", action="store_true")
+    ap.add_argument("--e2e-decode", type=int, default=512,
+                    help="greedy decode steps of the config-5 decoder run (default 512)")
+    ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e"], default=None,
                     help="run one workload (profiling); 'copy' streams a known number of bytes "
                          "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -253,6 +303,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": 2 * n, "copy_bytes_written": 2 * n, "launches": 3}))
         return
+    if args.only == "e2e":
+        print(json.dumps(bench_e2e(args, torch, kvm_amd)))
+        return
     if args.only == "decode":
         dec = bench_decode(args, torch, kvm_amd)
         print(json.dumps({k: v for k, v in dec.items()}))
@@ -269,6 +322,12 @@ def main():
         print("bench: decode config 4 ...", file=sys.stderr, flush=True)
         dec = bench_decode(args, torch, kvm_amd)
         print(f"bench: decode {dec['ms_per_step']:.3f} ms/token-step (attention {dec['attn_ms']:.3f} ms)",
+              file=sys.stderr, flush=True)
+    e2e = None
+    if not args.skip_e2e:
+        print("bench: config 5 decoder (24 layers, B8 T16384 prefill + greedy decode) ...", file=sys.stderr, flush=True)
+        e2e = bench_e2e(args, torch, kvm_amd)
+        print(f"bench: decoder prefill {e2e['prefill_ms']:.1f} ms, decode {e2e['decode_ms_per_step']:.2f} ms/step",
               file=sys.stderr, flush=True)
     cpu = None
     if not args.skip_cpu:
@@ -314,6 +373,15 @@ def main():
                          "achieved": round(bw / 1e9, 1), "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s",
                          "frac": round(bw / PEAK_HBM_BYTES, 4),
                          "traffic": measured_traffic("k_decode_partial", "config4")},
+        }
+    if e2e is not None:
+        line["decoder_e2e"] = {
+            "workload": "config 5: random-init 24-layer all-KVM decoder, d_model 2048, 16 heads of 128, vocab 65536, "
+                        f"bf16, chunk 512, 512 fixed slots; prefill 16384 random token ids at batch 8, then "
+                        f"{e2e['decode_steps']} greedy decode steps (projections, MLP and LM head on torch/hipBLASLt)",
+            "prefill_tokens_per_s": round(e2e["prefill_tok_s"], 1), "prefill_ms": round(e2e["prefill_ms"], 2),
+            "decode_tokens_per_s": round(e2e["decode_tok_s"], 1),
+            "decode_ms_per_step": round(e2e["decode_ms_per_step"], 3),
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
