@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 1
+#define KVM_ABI_VERSION 2
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -140,9 +140,47 @@ typedef struct kvm_prefill_desc {
                                     after the last attention launch (for timing) */
 } kvm_prefill_desc;
 
+/* The mixer's pre-boundary elementwise work on the q/k/v projections, for
+ * one layer (model/value_residual_mixin.py:173-237 calc_qkv and
+ * model/kvm_mixer.py:367-401 forward_prefix after the GEMMs):
+ *   value residual (value_residual_mode 1 linear: (1-lamb) v + lamb v_first;
+ *     2 rwkv: v + (v_first - v) * sigmoid(v_gate0 + gate_lin), before the
+ *     token shift; 3 rwkv_post_tokenshift: the same after it);
+ *   RWKV token shift (token_shift 1): x + x_mix * (prev - x), prev = the
+ *     previous token, or q_prev/k_prev/v_prev for token 0, or token 0 itself
+ *     when those are NULL (fallback "first", model/tokenshift.py:11-28);
+ *   ln_q / ln_k (LayerNorm over head_dim), then interleaved-pair RoPE with
+ *     the caller's bf16 cos/sin [B, T, 1, head_dim] (model/rwkv7_backbone.py:76-88);
+ *   merge gate 1 + elu(key_weight).
+ * Every step rounds to bf16 where the reference's torch ops do.
+ * Inputs q_lin [B,T,Hq*D], k_lin [B,T,Hkv*D], v_lin / v_first / gate_lin
+ * [B,T,Hkv*Dv], key_weight [B,T,Hkv] are contiguous bf16; the per-channel
+ * parameters are bf16.  Outputs q_out [B,T,Hq,D], k_out [B,T,Hkv,D], v_out
+ * [B,T,Hkv,Dv], gate_out [B,T,Hkv] (bf16, contiguous); v_last_out
+ * (optional, [B,1,Hkv*Dv]) receives the last token's value after a value
+ * residual applied before the shift (the decode cache's carried value). */
+typedef struct kvm_prefix_desc {
+  int64_t batch, seq_len, q_heads, kv_heads, head_dim, value_dim;
+  int64_t value_residual_mode; /* 0 none, 1 linear, 2 rwkv, 3 rwkv_post_tokenshift */
+  int64_t token_shift;         /* 0 none, 1 rwkv */
+  double ln_eps;
+  const void *q_lin, *k_lin, *v_lin, *v_first, *gate_lin, *key_weight;
+  const void *q_prev, *k_prev, *v_prev; /* [B, 1, width] or NULL */
+  const void *x_q, *x_k, *x_v, *v_gate0, *lamb;
+  const void *ln_q_w, *ln_q_b, *ln_k_w, *ln_k_b;
+  const void *cos, *sin;
+  int64_t rope_sb, rope_st; /* element strides of cos/sin over batch and tokens */
+  void *q_out, *k_out, *v_out, *gate_out, *v_last_out;
+} kvm_prefix_desc;
+
+/* Run the pre-boundary elementwise work described above.  Replaces the
+ * torch op sequence of calc_qkv + forward_prefix after the projections
+ * (model/value_residual_mixin.py:173-237, model/kvm_mixer.py:367-401). */
+int kvm_prefix(const kvm_prefix_desc *d, void *stream);
+
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
-int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc */
+int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc */
 const char *kvm_last_error(void);
 
 /* Workspace of kvm_prefill for the given descriptor (snapshot_ring and

@@ -130,11 +130,49 @@ int64_t kvm_struct_size(int which) {
     case 1: return sizeof(kvm_seq);
     case 2: return sizeof(kvm_state);
     case 3: return sizeof(kvm_prefill_desc);
+    case 4: return sizeof(kvm_prefix_desc);
     default: return -1;
   }
 }
 
 const char *kvm_last_error(void) { return g_error.c_str(); }
+
+int kvm_prefix(const kvm_prefix_desc *d, void *stream) {
+  if (!d) return fail(KVM_EINVAL, "prefix descriptor is NULL");
+  if (d->batch < 1 || d->seq_len < 1 || d->q_heads < 1 || d->kv_heads < 1)
+    return fail(KVM_EINVAL, "batch, seq_len and head counts must be positive");
+  if (d->head_dim != 64 && d->head_dim != 128)
+    return fail(KVM_EINVAL, "head_dim must be 64 or 128, got %lld", (long long)d->head_dim);
+  if (d->value_dim != d->head_dim) return fail(KVM_EINVAL, "value_dim must equal head_dim");
+  if (d->value_residual_mode < 0 || d->value_residual_mode > 3)
+    return fail(KVM_EINVAL, "value_residual_mode must be 0..3, got %lld", (long long)d->value_residual_mode);
+  if (d->token_shift != 0 && d->token_shift != 1) return fail(KVM_EINVAL, "token_shift must be 0 or 1");
+  if (!(d->ln_eps > 0.0)) return fail(KVM_EINVAL, "ln_eps must be positive");
+  const void *rows[] = {d->q_lin, d->k_lin, d->v_lin, d->q_out, d->k_out, d->v_out, d->cos, d->sin,
+                        d->ln_q_w, d->ln_q_b, d->ln_k_w, d->ln_k_b};
+  for (const void *p : rows)
+    if (!p || !aligned16(p)) return fail(KVM_EINVAL, "projection, output, RoPE and LayerNorm pointers must be non-NULL and 16-byte aligned");
+  const int64_t mode = d->value_residual_mode;
+  if (mode >= 1 && (!d->v_first || !aligned16(d->v_first)))
+    return fail(KVM_EINVAL, "value residual needs a 16-byte aligned v_first");
+  if (mode == 1 && !d->lamb) return fail(KVM_EINVAL, "linear value residual needs lamb");
+  if (mode >= 2 && (!d->gate_lin || !d->v_gate0 || !aligned16(d->gate_lin) || !aligned16(d->v_gate0)))
+    return fail(KVM_EINVAL, "rwkv value residual needs 16-byte aligned gate_lin and v_gate0");
+  if (d->token_shift) {
+    const void *mix[] = {d->x_q, d->x_k, d->x_v};
+    for (const void *p : mix)
+      if (!p || !aligned16(p)) return fail(KVM_EINVAL, "token shift needs 16-byte aligned x_q, x_k, x_v");
+    const void *prev[] = {d->q_prev, d->k_prev, d->v_prev};
+    for (const void *p : prev)
+      if (p && !aligned16(p)) return fail(KVM_EINVAL, "previous-token rows must be 16-byte aligned");
+  }
+  if (d->v_last_out && !aligned16(d->v_last_out)) return fail(KVM_EINVAL, "v_last_out must be 16-byte aligned");
+  if (d->rope_sb % 8 || d->rope_st % 8 || d->rope_st < d->head_dim)
+    return fail(KVM_EINVAL, "cos/sin strides must be multiples of 8 elements covering head_dim");
+  if (d->key_weight && !d->gate_out) return fail(KVM_EINVAL, "key_weight needs gate_out");
+  KVM_HIP(kvm::launch_prefix(*d, as_stream(stream)), "prefix");
+  return KVM_OK;
+}
 
 int64_t kvm_update_workspace_bytes(const kvm_layer *layer, int64_t n_tok) {
   if (check_layer(layer) != KVM_OK || n_tok < 1) return -1;

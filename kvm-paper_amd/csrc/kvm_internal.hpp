@@ -162,6 +162,8 @@ struct PrefillAttnArgs {
   int64_t snap_cap;        // slots per row in a snapshot
 };
 
+hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);
+
 hipError_t launch_prefill_attention(const kvm_layer &L,
                                     const PrefillAttnArgs &a,
                                     int64_t chunk_begin, int64_t n_chunks,

@@ -1,0 +1,206 @@
+// The KVM mixer's pre-boundary elementwise work in one kernel on gfx950.
+//
+// Reference: model/value_residual_mixin.py:173-237 (calc_qkv: value
+// residual, RWKV token shift, ln_q / ln_k) and model/kvm_mixer.py:367-401
+// (forward_prefix: RoPE, merge gate), after the projection GEMMs.  In the
+// reference every step is one torch op over the whole [B, T, H*D] tensor
+// (about twenty launches per layer, each reading and writing the tensor);
+// here every element is read once and written once.
+//
+// Work split: a task is one (batch, head, token) row; q heads first, then kv
+// heads.  A row of D features is held by D/8 consecutive lanes, 8 features
+// per lane (one 16-byte access), so a wave works on 64/(D/8) rows of
+// consecutive tokens of one head.  The token shift needs the previous
+// token's row: it is loaded again by the row's own lanes (an L1/L2 hit: the
+// neighbouring lane group or the previous wave loaded it).  kv rows also
+// recompute the previous token's value residual.
+//
+// Rounding: each reference op computes in fp32 and rounds to bf16 (torch's
+// opmath for bf16 tensors); the same rounding points are kept here, so the
+// outputs match the torch sequence except where an fp32 result of a
+// transcendental or of the LayerNorm's reductions differs in its last bit.
+
+#include "kvm_device.hpp"
+#include "kvm_internal.hpp"
+
+namespace kvm {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ void load_row8(const void *base, int64_t elem, float (&x)[8]) {
+  load8(static_cast<const uint16_t *>(base) + elem, x);
+}
+
+__device__ __forceinline__ void param8(const void *p, int64_t elem, float (&x)[8]) {
+  load8(static_cast<const uint16_t *>(p) + elem, x);
+}
+
+__device__ __forceinline__ float param1(const void *p, int64_t elem) {
+  return bf2f(static_cast<const uint16_t *>(p)[elem]);
+}
+
+// value residual applied to one row (v in place)
+__device__ __forceinline__ void value_residual(int mode, float (&v)[8], const kvm_prefix_desc &P,
+                                               int64_t row_elem, int64_t chan) {
+  if (mode == 1) {  // (1 - lamb) * v + lamb * v_first
+    const float lamb = param1(P.lamb, 0);
+    const float c1 = rbf(1.f - lamb);
+    float vf[8];
+    load_row8(P.v_first, row_elem, vf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = rbf(rbf(c1 * v[i]) + rbf(lamb * vf[i]));
+  } else {  // v + (v_first - v) * sigmoid(v_gate0 + gate_lin)
+    float vf[8], gl[8], g0[8];
+    load_row8(P.v_first, row_elem, vf);
+    load_row8(P.gate_lin, row_elem, gl);
+    param8(P.v_gate0, chan, g0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float t = rbf(g0[i] + gl[i]);
+      const float g = rbf(1.f / (1.f + expf(-t)));
+      v[i] = rbf(v[i] + rbf(rbf(vf[i] - v[i]) * g));
+    }
+  }
+}
+
+// x + x_mix * (prev - x)
+__device__ __forceinline__ void token_shift(float (&x)[8], const float (&prev)[8], const float (&mix)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = rbf(x[i] + rbf(mix[i] * rbf(prev[i] - x[i])));
+}
+
+// LayerNorm over the row (bf16 output), then interleaved-pair RoPE:
+// bf16(bf16(cos * x) + bf16(sin * x_pair)).
+template <int D>
+__device__ __forceinline__ void norm_rope(float (&x)[8], int part, const void *w, const void *b, float eps,
+                                          const kvm_prefix_desc &P, int64_t bi, int64_t t) {
+  float wf[8], bfv[8], c[8], s[8];
+  param8(w, part * 8, wf);
+  param8(b, part * 8, bfv);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum += x[i];
+  sum = group_sum<D / 8>(sum);
+  const float mean = sum / float(D);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float d = x[i] - mean;
+    q += d * d;
+  }
+  q = group_sum<D / 8>(q);
+  const float rstd = 1.0f / sqrtf(q / float(D) + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = rbf((x[i] - mean) * rstd * wf[i] + bfv[i]);
+  const int64_t ro = bi * P.rope_sb + t * P.rope_st + part * 8;
+  load_row8(P.cos, ro, c);
+  load_row8(P.sin, ro, s);
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = rbf(rbf(c[i] * x[i]) + rbf(s[i] * x[i ^ 1]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = y[i];
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
+  constexpr int LPR = D / 8;          // lanes per row
+  constexpr int RPW = 64 / LPR;       // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int part = lane % LPR;
+  const int64_t T = P.seq_len, Hq = P.q_heads, Hkv = P.kv_heads;
+  const int64_t row = (int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  // row = ((b * (Hq + Hkv) + head) * T + t)
+  const int64_t t = row % T;
+  const int64_t bh = row / T;
+  const int64_t head = bh % (Hq + Hkv);
+  const int64_t bi = bh / (Hq + Hkv);
+  if (bi >= P.batch) return;
+  const int mode = int(P.value_residual_mode);
+  const bool shift = P.token_shift != 0;
+
+  if (head < Hq) {
+    const int64_t width = Hq * D;
+    const int64_t chan = head * D + part * 8;
+    const int64_t e = (bi * T + t) * width + chan;
+    float x[8];
+    load_row8(P.q_lin, e, x);
+    if (shift) {
+      float pv[8], mix[8];
+      if (t > 0) load_row8(P.q_lin, e - width, pv);
+      else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, pv);
+      else for (int i = 0; i < 8; ++i) pv[i] = x[i];
+      param8(P.x_q, chan, mix);
+      token_shift(x, pv, mix);
+    }
+    norm_rope<D>(x, part, P.ln_q_w, P.ln_q_b, float(P.ln_eps), P, bi, t);
+    store8(static_cast<uint16_t *>(P.q_out) + e, x);
+    return;
+  }
+  const int64_t hk = head - Hq;
+  const int64_t width = Hkv * D;
+  const int64_t chan = hk * D + part * 8;
+  const int64_t e = (bi * T + t) * width + chan;
+  // keys: token shift, ln_k, RoPE
+  {
+    float x[8];
+    load_row8(P.k_lin, e, x);
+    if (shift) {
+      float pv[8], mix[8];
+      if (t > 0) load_row8(P.k_lin, e - width, pv);
+      else if (P.k_prev) load_row8(P.k_prev, bi * width + chan, pv);
+      else for (int i = 0; i < 8; ++i) pv[i] = x[i];
+      param8(P.x_k, chan, mix);
+      token_shift(x, pv, mix);
+    }
+    norm_rope<D>(x, part, P.ln_k_w, P.ln_k_b, float(P.ln_eps), P, bi, t);
+    store8(static_cast<uint16_t *>(P.k_out) + e, x);
+  }
+  // values: value residual before / after the token shift
+  {
+    const bool pre = mode == 1 || mode == 2;
+    float v[8];
+    load_row8(P.v_lin, e, v);
+    if (pre) value_residual(mode, v, P, e, chan);
+    if (P.v_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
+    if (shift) {
+      float pv[8], mix[8];
+      if (t > 0) {
+        load_row8(P.v_lin, e - width, pv);
+        if (pre) value_residual(mode, pv, P, e - width, chan);
+      } else if (P.v_prev) {
+        load_row8(P.v_prev, bi * width + chan, pv);
+      } else {
+        for (int i = 0; i < 8; ++i) pv[i] = v[i];
+      }
+      param8(P.x_v, chan, mix);
+      token_shift(v, pv, mix);
+    }
+    if (mode == 3) value_residual(2, v, P, e, chan);
+    store8(static_cast<uint16_t *>(P.v_out) + e, v);
+  }
+  // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
+  if (part == 0 && P.key_weight && P.gate_out) {
+    const int64_t ge = (bi * T + t) * Hkv + hk;
+    const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[ge]);
+    const float el = rbf(kw > 0.f ? kw : expm1f(kw));
+    static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
+  }
+}
+
+}  // namespace
+
+hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream) {
+  const int64_t rows = P.batch * (P.q_heads + P.kv_heads) * P.seq_len;
+  const int rpw = 64 / int(P.head_dim / 8);
+  const int64_t waves = (rows + rpw - 1) / rpw;
+  const dim3 grid{unsigned((waves + kThreads / 64 - 1) / (kThreads / 64)), 1u, 1u};
+  if (P.head_dim == 128)
+    hipLaunchKernelGGL(k_prefix<128>, grid, dim3(kThreads), 0, stream, P);
+  else
+    hipLaunchKernelGGL(k_prefix<64>, grid, dim3(kThreads), 0, stream, P);
+  return hipGetLastError();
+}
+
+}  // namespace kvm

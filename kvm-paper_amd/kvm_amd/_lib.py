@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -78,6 +78,20 @@ class KvmPrefillDesc(ctypes.Structure):
     ]
 
 
+class KvmPrefixDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("seq_len", _i64), ("q_heads", _i64), ("kv_heads", _i64),
+        ("head_dim", _i64), ("value_dim", _i64), ("value_residual_mode", _i64), ("token_shift", _i64),
+        ("ln_eps", ctypes.c_double),
+        ("q_lin", _vp), ("k_lin", _vp), ("v_lin", _vp), ("v_first", _vp), ("gate_lin", _vp), ("key_weight", _vp),
+        ("q_prev", _vp), ("k_prev", _vp), ("v_prev", _vp),
+        ("x_q", _vp), ("x_k", _vp), ("x_v", _vp), ("v_gate0", _vp), ("lamb", _vp),
+        ("ln_q_w", _vp), ("ln_q_b", _vp), ("ln_k_w", _vp), ("ln_k_b", _vp),
+        ("cos", _vp), ("sin", _vp), ("rope_sb", _i64), ("rope_st", _i64),
+        ("q_out", _vp), ("k_out", _vp), ("v_out", _vp), ("gate_out", _vp), ("v_last_out", _vp),
+    ]
+
+
 # Exported symbols and their signatures (include/kvm_amd.h).
 _P = ctypes.POINTER
 SIGNATURES = {
@@ -86,6 +100,7 @@ SIGNATURES = {
     "kvm_last_error": (ctypes.c_char_p, []),
     "kvm_prefill_workspace_bytes": (_i64, [_P(KvmPrefillDesc)]),
     "kvm_prefill": (ctypes.c_int, [_P(KvmPrefillDesc), _vp]),
+    "kvm_prefix": (ctypes.c_int, [_P(KvmPrefixDesc), _vp]),
     "kvm_state_append_direct": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _i64, _i64, _P(KvmState), _i64, _vp]),
     "kvm_state_refresh": (ctypes.c_int, [_P(KvmLayer), _P(KvmState), _i64, _i64, _vp]),
     "kvm_update_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),
@@ -122,7 +137,7 @@ def load(path: str | os.PathLike | None = None):
         fn.argtypes = args
     if lib.kvm_abi_version() != ABI_VERSION:
         raise KvmLibraryError(f"{p}: ABI version {lib.kvm_abi_version()} != {ABI_VERSION}")
-    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc)):
+    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc)):
         if lib.kvm_struct_size(i) != ctypes.sizeof(st):
             raise KvmLibraryError(f"{p}: struct {st.__name__} size mismatch")
     if path is None:

@@ -296,9 +296,10 @@ class SequenceMixer(nn.Module):
         if past_key_values is not None:
             qp, kp = states.get(self._CACHE_Q_FINAL), states.get(self._CACHE_K_FINAL)
             vp, xp = states.get(self._CACHE_V_FINAL), states.get(self._CACHE_X_FINAL)
+            # Copies, not views: a view would keep the whole [B, T, d] tensors alive.
             past_key_values.update(self.layer_idx, offset=0, states_dict={
-                self._CACHE_Q_FINAL: q[:, -1:].detach(), self._CACHE_K_FINAL: k[:, -1:].detach(),
-                self._CACHE_V_FINAL: v[:, -1:].detach(), self._CACHE_X_FINAL: x[:, -1:].detach(),
+                self._CACHE_Q_FINAL: q[:, -1:].detach().clone(), self._CACHE_K_FINAL: k[:, -1:].detach().clone(),
+                self._CACHE_V_FINAL: v[:, -1:].detach().clone(), self._CACHE_X_FINAL: x[:, -1:].detach().clone(),
             })
         if self.tokenshift_mode == "rwkv":
             q = _token_shift(q, self.x_q, qp)
@@ -315,7 +316,105 @@ class SequenceMixer(nn.Module):
         return q, k, v
 
     def forward_prefix(self, x, v_first, position_embeddings, attention_mask, past_key_values=None, **kwargs):
-        """q/k/v/merge gate at the post-QKV boundary (model/kvm_mixer.py:367-401)."""
+        """q/k/v/merge gate at the post-QKV boundary (model/kvm_mixer.py:367-401).
+
+        bf16 inference on the GPU runs the projections as torch GEMMs and
+        everything after them in one ``kvm_prefix`` launch; CPU tensors and
+        autograd take the torch op sequence, which is the reference's."""
+        if self._use_fused_prefix(x, position_embeddings):
+            return self._fused_prefix(x, v_first, position_embeddings, past_key_values)
+        return self._torch_prefix(x, v_first, position_embeddings, past_key_values)
+
+    _VR_MODES = {"none": 0, "linear": 1, "rwkv": 2, "rwkv_post_tokenshift": 3}
+
+    def _use_fused_prefix(self, x, position_embeddings) -> bool:
+        if not x.is_cuda or x.dtype != torch.bfloat16 or position_embeddings is None:
+            return False
+        if self.c_q.weight.dtype != torch.bfloat16:
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        return self.d_qk_head == self.d_v_head and self.d_qk_head in (64, 128)
+
+    def _fused_prefix(self, x, v_first, position_embeddings, past_key_values):
+        """Projections (torch GEMMs), then value residual, token shift,
+        ln_q/ln_k, RoPE and merge gate in one HIP launch (include/kvm_amd.h
+        kvm_prefix).  Same outputs and cache entries as ``_torch_prefix``."""
+        B, T, _ = x.size()
+        states = past_key_values.get_states(self.layer_idx) if past_key_values is not None else {}
+        past = past_key_values.get_seq_length(self.layer_idx) if past_key_values is not None else 0
+        if past > 0 and T != 1:
+            raise AssertionError("cached decode expects single-token inputs.")
+        mode = self._VR_MODES[self.value_residual_mode]
+        Hq, Hkv, D = self.num_attention_heads, self.num_key_value_heads, self.d_qk_head
+        q_lin, k_lin, v_lin = self.c_q(x), self.c_k(x), self.c_v(x)
+        xp = states.get(self._CACHE_X_FINAL) if past_key_values is not None else None
+        gate_lin = None
+        if mode == 2:
+            gate_lin = self.v_gate2(self.v_gate1(x))
+        elif mode == 3:
+            shift = self.x_v if self.value_projection_size == self.hidden_size else self.x_v_hidden
+            gate_lin = self.v_gate2(self.v_gate1(_token_shift(x, shift.view(1, 1, self.hidden_size), xp)))
+        use_gate = bool(self.config.kvm_use_merge_gate_keys or self.config.kvm_use_merge_gate_values)
+        kw = self.key_weighting(x).contiguous() if use_gate else None
+        shift_on = self.tokenshift_mode == "rwkv"
+        prev = [states.get(k) for k in (self._CACHE_Q_FINAL, self._CACHE_K_FINAL, self._CACHE_V_FINAL)]
+        bf = dict(device=x.device, dtype=torch.bfloat16)
+        q = torch.empty(B, T, Hq, D, **bf)
+        k = torch.empty(B, T, Hkv, D, **bf)
+        v = torch.empty(B, T, Hkv, D, **bf)
+        gate = torch.empty(B, T, Hkv, **bf) if use_gate else None
+        v_last = torch.empty(B, 1, Hkv * D, **bf) if past_key_values is not None else None
+        cos, sin = position_embeddings
+        if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
+            cos, sin = cos.bfloat16(), sin.bfloat16()
+        if cos.stride(-1) != 1 or cos.stride() != sin.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        rope_sb = cos.stride(0) if cos.size(0) > 1 else 0
+        keep = []
+
+        def ptr(t):
+            if t is None:
+                return None
+            t = t.contiguous()
+            keep.append(t)
+            return t.data_ptr()
+
+        d = _lib.KvmPrefixDesc()
+        d.batch, d.seq_len, d.q_heads, d.kv_heads, d.head_dim, d.value_dim = B, T, Hq, Hkv, D, D
+        d.value_residual_mode, d.token_shift, d.ln_eps = mode, int(shift_on), float(self.ln_q.eps)
+        d.q_lin, d.k_lin, d.v_lin = ptr(q_lin), ptr(k_lin), ptr(v_lin)
+        d.v_first = ptr(v_first.to(torch.bfloat16).reshape(B, T, -1)) if mode else None
+        d.gate_lin, d.key_weight = ptr(gate_lin), ptr(kw)
+        if shift_on:
+            d.q_prev, d.k_prev, d.v_prev = (ptr(p.to(torch.bfloat16)) if p is not None else None for p in prev)
+            d.x_q, d.x_k, d.x_v = ptr(self.x_q), ptr(self.x_k), ptr(self.x_v)
+        if mode >= 2:
+            d.v_gate0 = ptr(self.v_gate0)
+        if mode == 1:
+            d.lamb = ptr(self.lamb.reshape(1))
+        d.ln_q_w, d.ln_q_b, d.ln_k_w, d.ln_k_b = (ptr(t) for t in (self.ln_q.weight, self.ln_q.bias,
+                                                                   self.ln_k.weight, self.ln_k.bias))
+        d.cos, d.sin = ptr(cos), ptr(sin)
+        d.rope_sb, d.rope_st = rope_sb, cos.stride(1)
+        d.q_out, d.k_out, d.v_out = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        d.gate_out = gate.data_ptr() if gate is not None else None
+        d.v_last_out = v_last.data_ptr() if v_last is not None else None
+        lib = _lib.load()
+        _lib.check(lib.kvm_prefix(ctypes.byref(d), _lib.stream_handle(x.device)), "kvm_prefix")
+        del keep
+        if past_key_values is not None:
+            past_key_values.update(self.layer_idx, offset=0, states_dict={
+                self._CACHE_Q_FINAL: q_lin[:, -1:].clone(), self._CACHE_K_FINAL: k_lin[:, -1:].clone(),
+                self._CACHE_V_FINAL: v_last, self._CACHE_X_FINAL: x[:, -1:].detach().clone(),
+            })
+        if use_gate:
+            merge_gate = gate.view(B, T, Hkv, 1).transpose(1, 2)
+        else:
+            merge_gate = torch.ones((B, Hkv, T, 1), device=x.device, dtype=torch.float)
+        return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), merge_gate
+
+    def _torch_prefix(self, x, v_first, position_embeddings, past_key_values):
         B, T, _ = x.size()
         q, k, v = self.calc_qkv(x, v_first, past_key_values)
         q = apply_rotary_embeddings(q, position_embeddings)
