@@ -473,3 +473,43 @@ def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C
     a = res["owner"]
     n_app = int(a["append_log"].sum())
     T.log(f"[chain] {plan.n_updates} updates, S={S}, {n_app} appended tokens: identical")
+
+
+@pytest.mark.parametrize("Tn", [1, 5, 63, 64, 65, 128, 129, 191, 300])
+def test_prefill_ragged_lengths_match_oracle(lib, Tn):
+    """Prompt lengths around the chunk and window boundaries (C = 64, window
+    2C): no update, the first update, partial last chunks; batch 3 with GQA.
+    Output against the CPU oracle, then one cached decode step from the
+    prefill's cache (output, state coverage and s_k) against the oracle's."""
+    B, Hq, Hkv, D, C = 3, 2, 1, 64, 64
+    T.log(f"[prefill-ragged] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="fixed", min_len=C)
+    gen = torch.Generator().manual_seed(Tn)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = _random_inputs(B, Hq, Hkv, Tn + 1, D, 100 + Tn)
+    ocfg = O.OracleConfig(
+        q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=cfg.n_bswa_chunks,
+        n_max_d_chunks=cfg.n_max_d_chunks, sink_len=cfg.sink_len, rope_partial_dim=cfg.rope_partial_dim,
+        state_min_len=C, append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
+    cache = T.LayerStatesCache()
+    dq, dk, dv, dg = (x.to(DEV) for x in (q, k, v, g))
+    with torch.no_grad():
+        y = m.forward_prefill(dq[:, :, :Tn], dk[:, :, :Tn], dv[:, :, :Tn], dg[:, :, :Tn], None, None, None, cache)
+        y_dec = m.forward_single(dq[:, :, Tn:], dk[:, :, Tn:], dv[:, :, Tn:], dg[:, :, Tn:], None, None, None, cache)
+    torch.cuda.synchronize()
+    y_ref, st = O.prefill(q[:, :, :Tn], k[:, :, :Tn], v[:, :, :Tn], g[:, :, :Tn], p, ocfg)
+    T.assert_close_bf16(y.cpu().view(B, Tn, Hq, D).transpose(1, 2), y_ref, f"T={Tn} prefill output")
+    dec_ref, st = O.decode_step(st, Tn, q[:, :, Tn:], k[:, :, Tn:], v[:, :, Tn:], g[:, :, Tn:], p, ocfg)
+    T.assert_close_bf16(y_dec.cpu().view(B, 1, Hq, D).transpose(1, 2), dec_ref, f"T={Tn} decode step")
+    c = cache.get_states(0)[m._CACHE_TRITON_DECODE]
+    got = c.logical_state_dict()
+    S = int(st[O.S_K].size(2))
+    assert int(got["kvm_state_coverage_len"]) == int(st[O.COVERAGE])
+    scale = max(1.0, float(st[O.S_K].float().abs().max()))
+    smx, _ = T.err_stats(got["kvm_s_k"][:, :, :S].cpu(), st[O.S_K])
+    assert smx <= 2e-2 * scale, f"T={Tn}: state s_k after the decode step: max err {smx:.3e} (scale {scale:.2e})"
