@@ -8,14 +8,19 @@ Public API:
                            (model.rwkv7_backbone.RWKV7BackboneForCausalLM)
   MixerConfig              its config (the reference's field names/defaults)
   StatesDictCache          per-layer carried-state cache of the decoder
+  load_reference_checkpoint  the decoder from a reference checkpoint
+                           (save_pretrained directory, trainer .pt, .safetensors)
+  snapshot_from_states     DecodeCacheSnapshot from the eager mixer's state dict
   load_library             load libkvm_amd.so (raises if it is not built)
 """
 
 from ._lib import load as load_library
 from .backbone import MixerConfig, RWKV7BackboneForCausalLM, RWKV7BackboneModel, init_random_
+from .checkpoint import load_reference_checkpoint, snapshot_from_states
 from .decode_cache import DecodeCacheSnapshot, KVMDecodeCache, TritonKVMDecodeCache
 from .mixer import SequenceMixer
 from .states_cache import StatesDictCache
 
 __all__ = ["SequenceMixer", "KVMDecodeCache", "TritonKVMDecodeCache", "DecodeCacheSnapshot", "load_library",
-           "MixerConfig", "RWKV7BackboneForCausalLM", "RWKV7BackboneModel", "StatesDictCache", "init_random_"]
+           "MixerConfig", "RWKV7BackboneForCausalLM", "RWKV7BackboneModel", "StatesDictCache", "init_random_",
+           "load_reference_checkpoint", "snapshot_from_states"]

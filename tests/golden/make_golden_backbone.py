@@ -18,6 +18,13 @@ and records, in bf16 on the CPU:
 The fixtures hold tensors only: the parameters (bf16 bits), the token ids,
 the logits and the decoded tokens, plus the model config as JSON.
 
+For the first case it also writes the checkpoint the reference's trainer
+leaves at the end of a run (``raw_model.save_pretrained(logdir)``,
+trainer.py:286): the model is saved into a temporary directory and only its
+data files, ``config.json`` and ``model.safetensors``, are kept, under
+``backbone/hf_<case>/`` (save_pretrained also copies code files; those are
+not kept).  ``--checkpoint-only`` writes just that checkpoint.
+
 The reference's ``StatesDictCache`` cannot be built with this container's
 transformers (its layer class misses an abstract method), so the decode uses
 a stand-in with the same three calls the model makes on it
@@ -30,7 +37,9 @@ from __future__ import annotations
 
 import json
 import os
+import shutil
 import sys
+import tempfile
 from pathlib import Path
 
 import numpy as np
@@ -120,7 +129,7 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().contiguous().to(torch.bfloat16).view(torch.int16).numpy()
 
 
-def run_case(case):
+def build_model(case):
     sys.path.insert(0, str(REF))
     import utils.grad_cp as grad_cp  # noqa: E402
     from model.rwkv7_backbone import MixerConfig, RWKV7BackboneForCausalLM  # noqa: E402
@@ -130,6 +139,24 @@ def run_case(case):
     torch.manual_seed(case["seed"])
     model = RWKV7BackboneForCausalLM(cfg).to(torch.bfloat16).eval()
     randomize_(model, case["seed"])
+    return cfg, model
+
+
+def save_checkpoint(case):
+    """config.json + model.safetensors exactly as the reference writes them."""
+    _, model = build_model(case)
+    out = OUT_DIR / f"hf_{case['name']}"
+    out.mkdir(parents=True, exist_ok=True)
+    with tempfile.TemporaryDirectory() as tmp:
+        model.save_pretrained(tmp)
+        for name in ("config.json", "model.safetensors"):
+            shutil.copyfile(Path(tmp) / name, out / name)
+    print(f"wrote {out.relative_to(HERE)}: " + ", ".join(
+        f"{p.name} {p.stat().st_size / 1024:.0f} KiB" for p in sorted(out.iterdir())))
+
+
+def run_case(case):
+    cfg, model = build_model(case)
 
     B, T, n_dec = case["B"], case["T"], case["decode_steps"]
     gen = torch.Generator().manual_seed(case["seed"] + 1000)
@@ -163,6 +190,9 @@ def run_case(case):
 
 def main():
     OUT_DIR.mkdir(exist_ok=True)
+    save_checkpoint(CASES[0])
+    if "--checkpoint-only" in sys.argv:
+        return
     for case in CASES:
         data = run_case(case)
         path = OUT_DIR / f"{case['name']}.npz"

@@ -119,3 +119,67 @@ def test_config5_architecture_on_meta():
     per_layer = (4 * d * d + 3 * d + d + r * d + d * r + 4 * 128 + 2 * 128 + 16 * d + 2 * 16 + 4 * d
                  + 2 * ffn * d + d)
     assert sum(p.numel() for p in model.parameters()) == 24 * per_layer + 2 * V * d + 4 * d
+
+
+HF_DIR = golden_io.BACKBONE / "hf_decoder_fixed_tokenshift"
+
+
+def test_reference_hf_checkpoint_loads_bit_exact():
+    """The checkpoint the reference's save_pretrained wrote (config.json +
+    model.safetensors) gives the golden prefill and decode logits."""
+    from kvm_amd.checkpoint import load_reference_checkpoint
+
+    fx = golden_io.load_backbone("decoder_fixed_tokenshift")
+    model = load_reference_checkpoint(HF_DIR, token_mixer_class_path=ORACLE_MIXER)
+    assert model.config.num_hidden_layers == 2 and model.config.chunk_len == 32
+    ids, T = fx["input_ids"], fx["input_ids"].shape[1]
+    cache = BB.StatesDictCache()
+    with torch.no_grad():
+        lg = model(input_ids=ids, past_key_values=cache, use_cache=True, cache_position=torch.arange(T)).logits
+        assert torch.equal(lg, fx["prefill_logits"])
+        tok = fx["decode_tokens"][:, :1]
+        lg = model(input_ids=tok, past_key_values=cache, use_cache=True, cache_position=torch.tensor([T])).logits
+        assert torch.equal(lg[:, -1], fx["decode_logits"][:, 0])
+
+
+def test_checkpoint_file_forms(tmp_path):
+    """Trainer .pt checkpoints (torch.save of {step, model, optimizers},
+    trainer.py:265-281), bare .safetensors / .pt state dicts and
+    torch.compile / DDP key prefixes all load to the same tensors."""
+    from safetensors.torch import save_file
+
+    from kvm_amd.checkpoint import load_reference_checkpoint, read_state_dict
+
+    ref = read_state_dict(HF_DIR)
+    torch.save({"step": 10, "model": ref, "optimizers": []}, tmp_path / "model_step000010.pt")
+    torch.save({"_orig_mod." + k: v for k, v in ref.items()}, tmp_path / "bare.pt")
+    save_file({"module." + k: v.contiguous() for k, v in ref.items()}, str(tmp_path / "bare.safetensors"))
+    (tmp_path / "config.json").write_text((HF_DIR / "config.json").read_text())
+    for f in ("model_step000010.pt", "bare.pt", "bare.safetensors"):
+        sd = read_state_dict(tmp_path / f)
+        assert sd.keys() == ref.keys() and all(torch.equal(sd[k], ref[k]) for k in ref), f
+    model = load_reference_checkpoint(tmp_path / "model_step000010.pt", token_mixer_class_path=ORACLE_MIXER)
+    for k, v in model.state_dict().items():
+        assert torch.equal(v, ref[k]), k
+
+
+def test_snapshot_from_eager_states():
+    """The eager carried-state dict (model/kvm_mixer.py:518-525) maps onto a
+    DecodeCacheSnapshot with total_len = window begin + window length."""
+    from kvm_amd.checkpoint import snapshot_from_states
+    from oracle import kvm_oracle as O
+
+    B, Hq, Hkv, D, C, Tn = 1, 2, 1, 64, 32, 150
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(B, Hq, Tn, D, generator=gen).bfloat16()
+    k = torch.randn(B, Hkv, Tn, D, generator=gen).bfloat16()
+    v = torch.randn(B, Hkv, Tn, D, generator=gen).bfloat16()
+    g = torch.ones(B, Hkv, Tn, 1).bfloat16()
+    cfg = O.OracleConfig(q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, state_min_len=C)
+    p = O.OracleParams(ln_weight=torch.ones(D).bfloat16(), ln_bias=torch.zeros(D).bfloat16(),
+                       front_temp=torch.ones(Hq).bfloat16(), state_temp=torch.ones(Hq).bfloat16())
+    _, st = O.prefill(q, k, v, g, p, cfg)
+    snap = snapshot_from_states(st)
+    assert snap.total_len == Tn and snap.recent_begin == st[O.BSWA_BEGIN]
+    assert snap.state_coverage_len == st[O.COVERAGE]
+    assert snap.state_k is st[O.S_K] and snap.recent_gate is st[O.BSWA_GATE]

@@ -142,3 +142,47 @@ def test_config5_full_size(lib):
     assert torch.equal(toks_a, toks_b), "greedy decoding is not deterministic"
     assert torch.equal(toks_a[:, 0], tok)
     T.log(f"[decoder] config 5: {steps} greedy tokens per row, deterministic")
+
+
+def test_decode_continues_eager_carried_state(lib):
+    """Carried-state interop: the eager mixer's state dict (here the CPU
+    oracle's, which uses the reference's keys, model/kvm_mixer.py:518-525)
+    becomes a HIP decode cache via snapshot_from_states; 80 decode steps
+    (one state update) then match the eager decode steps."""
+    from kvm_amd.checkpoint import snapshot_from_states
+    from oracle import kvm_oracle as O
+
+    B, Hq, Hkv, D, C, Tn, steps = 2, 4, 2, 128, 64, 300, 80
+    T.log(f"[decoder] eager-state interop B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn} steps {steps}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="fixed", min_len=C)
+    gen = torch.Generator().manual_seed(21)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    n = Tn + steps
+    q = (torch.randn(B, Hq, n, D, generator=gen) / D ** 0.5).bfloat16()
+    k = (torch.randn(B, Hkv, n, D, generator=gen) / D ** 0.5).bfloat16()
+    v = (torch.randn(B, Hkv, n, D, generator=gen) / D ** 0.5).bfloat16()
+    g = (1 + torch.nn.functional.elu(torch.randn(B, Hkv, n, 1, generator=gen))).bfloat16()
+    ocfg = O.OracleConfig(q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C,
+                          n_bswa_chunks=cfg.n_bswa_chunks, sink_len=cfg.sink_len,
+                          rope_partial_dim=cfg.rope_partial_dim, state_min_len=C, append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
+    _, st = O.prefill(q[:, :, :Tn], k[:, :, :Tn], v[:, :, :Tn], g[:, :, :Tn], p, ocfg)
+    snap = snapshot_from_states({key: (x.to(DEV) if torch.is_tensor(x) else x) for key, x in st.items()})
+    cache = m.make_decode_cache(snap)
+    got, ref = [], []
+    with torch.no_grad():
+        for s in range(steps):
+            t = Tn + s
+            sl = slice(t, t + 1)
+            out = m._decode_one_token(q[:, :, sl].to(DEV), k[:, :, sl].to(DEV), v[:, :, sl].to(DEV),
+                                      g[:, :, sl].to(DEV), cache)
+            got.append(out.float().cpu().reshape(B, Hq, 1, D))
+            y, st = O.decode_step(st, t, q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], p, ocfg)
+            ref.append(y)
+    assert cache.update_count >= 1 and cache.total_len == n
+    mx, mean = T.assert_close_bf16(torch.cat(got, 2), torch.cat(ref, 2), "decode from eager state")
+    T.log(f"[decoder] eager-state interop: {steps} steps, {cache.update_count} update(s), max {mx:.2e} mean {mean:.2e}")
