@@ -7,13 +7,12 @@
 // (about twenty launches per layer, each reading and writing the tensor);
 // here every element is read once and written once.
 //
-// Work split: a task is one (batch, head, token) row; q heads first, then kv
-// heads.  A row of D features is held by D/8 consecutive lanes, 8 features
-// per lane (one 16-byte access), so a wave works on 64/(D/8) rows of
-// consecutive tokens of one head.  The token shift needs the previous
-// token's row: it is loaded again by the row's own lanes (an L1/L2 hit: the
-// neighbouring lane group or the previous wave loaded it).  kv rows also
-// recompute the previous token's value residual.
+// Work split: a wave covers 32 consecutive tokens of one (batch, head), q
+// heads first, then kv heads.  A row of D features is held by D/8
+// consecutive lanes, 8 features per lane (one 16-byte access), so a pass
+// works on 64/(D/8) tokens.  The token shift takes the previous token's row
+// from the neighbouring lane group (or the pass before): every input row is
+// loaded once, and only a wave's first token loads its predecessor.
 //
 // Rounding: each reference op computes in fp32 and rounds to bf16 (torch's
 // opmath for bf16 tensors); the same rounding points are kept here, so the
@@ -103,98 +102,149 @@ __device__ __forceinline__ void norm_rope(float (&x)[8], int part, const void *w
   for (int i = 0; i < 8; ++i) x[i] = y[i];
 }
 
+// One wave covers kTokWave consecutive tokens of one (batch, head), RPW rows
+// (tokens) at a time.  The previous token of a row is the row below it in
+// the same pass (a lane move by D/8 lanes) or, for the first row of a pass,
+// the last row of the previous pass (carried): only a wave's first token
+// loads its predecessor from memory.
+constexpr int kTokWave = 32;
+
+// Value `x` of lane (lane - LPR) for lanes of row sub > 0; for sub == 0 the
+// value of the last row of the previous pass (`carry`).
+template <int LPR>
+__device__ __forceinline__ void prev_rows(const float (&x)[8], const float (&carry)[8], int lane,
+                                          float (&pv)[8]) {
+  const int src = lane >= LPR ? lane - LPR : lane;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float up = __shfl(x[i], src);
+    pv[i] = lane >= LPR ? up : carry[i];
+  }
+}
+// The last row's values (lanes 64 - LPR .. 63) into every lane of the same part.
+template <int LPR>
+__device__ __forceinline__ void last_row(const float (&x)[8], int part, float (&c)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = __shfl(x[i], 64 - LPR + part);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   constexpr int LPR = D / 8;          // lanes per row
-  constexpr int RPW = 64 / LPR;       // rows per wave
+  constexpr int RPW = 64 / LPR;       // rows per pass
+  constexpr int PASSES = kTokWave / RPW;
   const int lane = threadIdx.x & 63;
-  const int part = lane % LPR;
+  const int part = lane % LPR, sub = lane / LPR;
   const int64_t T = P.seq_len, Hq = P.q_heads, Hkv = P.kv_heads;
-  const int64_t row = (int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
-  // row = ((b * (Hq + Hkv) + head) * T + t)
-  const int64_t t = row % T;
-  const int64_t bh = row / T;
+  const int64_t tiles = (T + kTokWave - 1) / kTokWave;
+  const int64_t wv = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t tile = wv % tiles;
+  const int64_t bh = wv / tiles;
   const int64_t head = bh % (Hq + Hkv);
   const int64_t bi = bh / (Hq + Hkv);
-  if (bi >= P.batch) return;
+  if (bi >= P.batch) return;  // wave-uniform
   const int mode = int(P.value_residual_mode);
   const bool shift = P.token_shift != 0;
+  const bool pre = mode == 1 || mode == 2;
+  const int64_t t0 = tile * kTokWave;
 
   if (head < Hq) {
     const int64_t width = Hq * D;
     const int64_t chan = head * D + part * 8;
-    const int64_t e = (bi * T + t) * width + chan;
-    float x[8];
-    load_row8(P.q_lin, e, x);
+    float mix[8], carry[8];
     if (shift) {
-      float pv[8], mix[8];
-      if (t > 0) load_row8(P.q_lin, e - width, pv);
-      else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, pv);
-      else for (int i = 0; i < 8; ++i) pv[i] = x[i];
       param8(P.x_q, chan, mix);
-      token_shift(x, pv, mix);
+      // predecessor of the tile's first token
+      if (t0 > 0) load_row8(P.q_lin, (bi * T + t0 - 1) * width + chan, carry);
+      else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, carry);
     }
-    norm_rope<D>(x, part, P.ln_q_w, P.ln_q_b, float(P.ln_eps), P, bi, t);
-    store8(static_cast<uint16_t *>(P.q_out) + e, x);
+#pragma unroll 1
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int64_t t = t0 + ps * RPW + sub;
+      const bool live = t < T;
+      const int64_t e = (bi * T + (live ? t : T - 1)) * width + chan;
+      float x[8];
+      load_row8(P.q_lin, e, x);
+      if (shift) {
+        float pv[8];
+        if (ps == 0 && t0 == 0 && !P.q_prev)  // fallback "first": token 0 is its own predecessor
+          for (int i = 0; i < 8; ++i) carry[i] = __shfl(x[i], part);
+        prev_rows<LPR>(x, carry, lane, pv);
+        last_row<LPR>(x, part, carry);
+        token_shift(x, pv, mix);
+      }
+      norm_rope<D>(x, part, P.ln_q_w, P.ln_q_b, float(P.ln_eps), P, bi, live ? t : T - 1);
+      if (live) store8(static_cast<uint16_t *>(P.q_out) + e, x);
+    }
     return;
   }
   const int64_t hk = head - Hq;
   const int64_t width = Hkv * D;
   const int64_t chan = hk * D + part * 8;
-  const int64_t e = (bi * T + t) * width + chan;
-  // keys: token shift, ln_k, RoPE
-  {
+  float kmix[8], vmix[8], kcarry[8], vcarry[8];
+  if (shift) {
+    param8(P.x_k, chan, kmix);
+    param8(P.x_v, chan, vmix);
+    if (t0 > 0) {
+      const int64_t ep = (bi * T + t0 - 1) * width + chan;
+      load_row8(P.k_lin, ep, kcarry);
+      load_row8(P.v_lin, ep, vcarry);
+      if (pre) value_residual(mode, vcarry, P, ep, chan);
+    } else {
+      if (P.k_prev) load_row8(P.k_prev, bi * width + chan, kcarry);
+      if (P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
+    }
+  }
+#pragma unroll 1
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t t = t0 + ps * RPW + sub;
+    const bool live = t < T;
+    const int64_t tt = live ? t : T - 1;
+    const int64_t e = (bi * T + tt) * width + chan;
+    // keys: token shift, ln_k, RoPE
     float x[8];
     load_row8(P.k_lin, e, x);
     if (shift) {
-      float pv[8], mix[8];
-      if (t > 0) load_row8(P.k_lin, e - width, pv);
-      else if (P.k_prev) load_row8(P.k_prev, bi * width + chan, pv);
-      else for (int i = 0; i < 8; ++i) pv[i] = x[i];
-      param8(P.x_k, chan, mix);
-      token_shift(x, pv, mix);
+      float pv[8];
+      if (ps == 0 && t0 == 0 && !P.k_prev)
+        for (int i = 0; i < 8; ++i) kcarry[i] = __shfl(x[i], part);
+      prev_rows<LPR>(x, kcarry, lane, pv);
+      last_row<LPR>(x, part, kcarry);
+      token_shift(x, pv, kmix);
     }
-    norm_rope<D>(x, part, P.ln_k_w, P.ln_k_b, float(P.ln_eps), P, bi, t);
-    store8(static_cast<uint16_t *>(P.k_out) + e, x);
-  }
-  // values: value residual before / after the token shift
-  {
-    const bool pre = mode == 1 || mode == 2;
+    norm_rope<D>(x, part, P.ln_k_w, P.ln_k_b, float(P.ln_eps), P, bi, tt);
+    if (live) store8(static_cast<uint16_t *>(P.k_out) + e, x);
+    // values: value residual before / after the token shift
     float v[8];
     load_row8(P.v_lin, e, v);
     if (pre) value_residual(mode, v, P, e, chan);
-    if (P.v_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
+    if (live && P.v_last_out && t == T - 1)
+      store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
     if (shift) {
-      float pv[8], mix[8];
-      if (t > 0) {
-        load_row8(P.v_lin, e - width, pv);
-        if (pre) value_residual(mode, pv, P, e - width, chan);
-      } else if (P.v_prev) {
-        load_row8(P.v_prev, bi * width + chan, pv);
-      } else {
-        for (int i = 0; i < 8; ++i) pv[i] = v[i];
-      }
-      param8(P.x_v, chan, mix);
-      token_shift(v, pv, mix);
+      float pv[8];
+      if (ps == 0 && t0 == 0 && !P.v_prev)
+        for (int i = 0; i < 8; ++i) vcarry[i] = __shfl(v[i], part);
+      prev_rows<LPR>(v, vcarry, lane, pv);
+      last_row<LPR>(v, part, vcarry);
+      token_shift(v, pv, vmix);
     }
     if (mode == 3) value_residual(2, v, P, e, chan);
-    store8(static_cast<uint16_t *>(P.v_out) + e, v);
-  }
-  // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
-  if (part == 0 && P.key_weight && P.gate_out) {
-    const int64_t ge = (bi * T + t) * Hkv + hk;
-    const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[ge]);
-    const float el = rbf(kw > 0.f ? kw : expm1f(kw));
-    static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
+    if (live) store8(static_cast<uint16_t *>(P.v_out) + e, v);
+    // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
+    if (live && part == 0 && P.key_weight && P.gate_out) {
+      const int64_t ge = (bi * T + t) * Hkv + hk;
+      const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[ge]);
+      const float el = rbf(kw > 0.f ? kw : expm1f(kw));
+      static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
+    }
   }
 }
 
 }  // namespace
 
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream) {
-  const int64_t rows = P.batch * (P.q_heads + P.kv_heads) * P.seq_len;
-  const int rpw = 64 / int(P.head_dim / 8);
-  const int64_t waves = (rows + rpw - 1) / rpw;
+  const int64_t tiles = (P.seq_len + kTokWave - 1) / kTokWave;
+  const int64_t waves = P.batch * (P.q_heads + P.kv_heads) * tiles;
   const dim3 grid{unsigned((waves + kThreads / 64 - 1) / (kThreads / 64)), 1u, 1u};
   if (P.head_dim == 128)
     hipLaunchKernelGGL(k_prefix<128>, grid, dim3(kThreads), 0, stream, P);
