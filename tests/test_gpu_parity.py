@@ -513,3 +513,54 @@ def test_prefill_ragged_lengths_match_oracle(lib, Tn):
     scale = max(1.0, float(st[O.S_K].float().abs().max()))
     smx, _ = T.err_stats(got["kvm_s_k"][:, :, :S].cpu(), st[O.S_K])
     assert smx <= 2e-2 * scale, f"T={Tn}: state s_k after the decode step: max err {smx:.3e} (scale {scale:.2e})"
+
+
+def test_prefill_saturation_budget_matches_oracle(lib):
+    """The saturation budget (state_budget_mode "kvm_saturation",
+    floor(N t / (N + t)), model/kvm_mixer.py:131-165) grows the state with
+    appends over the prefill: state length, output and final state against
+    the CPU oracle."""
+    B, Hq, Hkv, D, C, Tn = 1, 4, 2, 64, 64, 1000
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="kvm_saturation", min_len=C, n_max=4, sat_n=2000)
+    T.log(f"[prefill-saturation] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} N=2000 cap {C * 4}")
+    gen = torch.Generator().manual_seed(41)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 43)
+    with torch.no_grad():
+        res = m.prefill_raw(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), route_log=True)
+    torch.cuda.synchronize()
+    ocfg = O.OracleConfig(
+        q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=cfg.n_bswa_chunks,
+        n_max_d_chunks=4, sink_len=cfg.sink_len, rope_partial_dim=cfg.rope_partial_dim,
+        state_budget_mode="kvm_saturation", state_min_len=C, state_saturation_n=2000,
+        append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
+    rec = O.Recorder()
+    y_ref, st = O.prefill(q, k, v, g, p, ocfg, rec)
+    S = res["plan"].final_state_len
+    assert S == int(st[O.S_K].size(2)) and S > C, (S, int(st[O.S_K].size(2)))
+    assert sum(u.n_append for u in rec.updates) == S - C
+    T.assert_close_bf16(res["out"].cpu().transpose(1, 2), y_ref, "saturation prefill output")
+    # append sets and merge routes of every update against the oracle's
+    rows = B * Hkv
+    n_diff = total = 0
+    for i, u in enumerate(rec.updates):
+        gr = res["route_log"][i].cpu()
+        ga = res["append_log"][i].cpu()
+        mi = u.merge_idx.reshape(rows, -1)
+        if u.append_idx is not None:
+            ai = u.append_idx.reshape(rows, -1)
+            for r in range(rows):
+                assert torch.equal(ga[r].nonzero().flatten(), ai[r]), f"update {i} row {r}: append sets differ"
+        if u.route is None:  # every token of this update was appended
+            assert mi.size(1) == 0
+            continue
+        g_sel = torch.stack([gr[r, mi[r]] for r in range(rows)])
+        n_diff += int((g_sel != u.route.reshape(rows, -1).to(torch.int32)).sum())
+        total += g_sel.numel()
+    T.log(f"[prefill-saturation] S {C} -> {S}, {len(rec.updates)} updates, {n_diff}/{total} merge routes differ")
+    assert n_diff == 0
