@@ -330,7 +330,12 @@ class SequenceMixer(nn.Module):
     def _use_fused_prefix(self, x, position_embeddings) -> bool:
         if not x.is_cuda or x.dtype != torch.bfloat16 or position_embeddings is None:
             return False
-        if self.c_q.weight.dtype != torch.bfloat16:
+        # The kernel reads every parameter it uses as raw bf16.
+        used = [self.c_q.weight, self.ln_q.weight, self.ln_q.bias, self.ln_k.weight, self.ln_k.bias]
+        used += [getattr(self, n) for n in ("x_q", "x_k", "x_v", "v_gate0") if hasattr(self, n)]
+        if self.lamb is not None:
+            used.append(self.lamb)
+        if any(p.dtype != torch.bfloat16 for p in used):
             return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
