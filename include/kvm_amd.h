@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 2
+#define KVM_ABI_VERSION 3
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -153,8 +153,10 @@ typedef struct kvm_prefill_desc {
  *     the caller's bf16 cos/sin [B, T, 1, head_dim] (model/rwkv7_backbone.py:76-88);
  *   merge gate 1 + elu(key_weight).
  * Every step rounds to bf16 where the reference's torch ops do.
- * Inputs q_lin [B,T,Hq*D], k_lin [B,T,Hkv*D], v_lin / v_first / gate_lin
- * [B,T,Hkv*Dv], key_weight [B,T,Hkv] are contiguous bf16; the per-channel
+ * Inputs q_lin [B,T,Hq*D], k_lin [B,T,Hkv*D], v_lin [B,T,Hkv*Dv] are bf16
+ * rows qkv_st elements apart (the three may be column ranges of one
+ * concatenated projection), key_weight [B,T,Hkv] rows kw_st apart;
+ * v_first / gate_lin [B,T,Hkv*Dv] are contiguous; the per-channel
  * parameters are bf16.  Outputs q_out [B,T,Hq,D], k_out [B,T,Hkv,D], v_out
  * [B,T,Hkv,Dv], gate_out [B,T,Hkv] (bf16, contiguous); v_last_out
  * (optional, [B,1,Hkv*Dv]) receives the last token's value after a value
@@ -170,6 +172,7 @@ typedef struct kvm_prefix_desc {
   const void *ln_q_w, *ln_q_b, *ln_k_w, *ln_k_b;
   const void *cos, *sin;
   int64_t rope_sb, rope_st; /* element strides of cos/sin over batch and tokens */
+  int64_t qkv_st, kw_st;     /* token strides (elements) of q/k/v_lin and key_weight */
   void *q_out, *k_out, *v_out, *gate_out, *v_last_out;
 } kvm_prefix_desc;
 

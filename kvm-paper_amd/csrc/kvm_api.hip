@@ -170,6 +170,10 @@ int kvm_prefix(const kvm_prefix_desc *d, void *stream) {
   if (d->rope_sb % 8 || d->rope_st % 8 || d->rope_st < d->head_dim)
     return fail(KVM_EINVAL, "cos/sin strides must be multiples of 8 elements covering head_dim");
   if (d->key_weight && !d->gate_out) return fail(KVM_EINVAL, "key_weight needs gate_out");
+  const int64_t widest = std::max(d->q_heads, d->kv_heads) * d->head_dim;
+  if (d->qkv_st % 8 || d->qkv_st < widest)
+    return fail(KVM_EINVAL, "qkv_st must be a multiple of 8 elements covering the widest projection");
+  if (d->key_weight && d->kw_st < d->kv_heads) return fail(KVM_EINVAL, "kw_st must cover kv_heads");
   KVM_HIP(kvm::launch_prefix(*d, as_stream(stream)), "prefix");
   return KVM_OK;
 }

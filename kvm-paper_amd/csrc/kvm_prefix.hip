@@ -39,7 +39,8 @@ __device__ __forceinline__ float param1(const void *p, int64_t elem) {
   return bf2f(static_cast<const uint16_t *>(p)[elem]);
 }
 
-// value residual applied to one row (v in place)
+// value residual applied to one row (v in place); row_elem indexes the
+// contiguous v_first / gate_lin rows
 __device__ __forceinline__ void value_residual(int mode, float (&v)[8], const kvm_prefix_desc &P,
                                                int64_t row_elem, int64_t chan) {
   if (mode == 1) {  // (1 - lamb) * v + lamb * v_first
@@ -155,16 +156,17 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     if (shift) {
       param8(P.x_q, chan, mix);
       // predecessor of the tile's first token
-      if (t0 > 0) load_row8(P.q_lin, (bi * T + t0 - 1) * width + chan, carry);
+      if (t0 > 0) load_row8(P.q_lin, (bi * T + t0 - 1) * P.qkv_st + chan, carry);
       else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, carry);
     }
 #pragma unroll 1
     for (int ps = 0; ps < PASSES; ++ps) {
       const int64_t t = t0 + ps * RPW + sub;
       const bool live = t < T;
-      const int64_t e = (bi * T + (live ? t : T - 1)) * width + chan;
+      const int64_t r = bi * T + (live ? t : T - 1);
+      const int64_t e = r * width + chan;
       float x[8];
-      load_row8(P.q_lin, e, x);
+      load_row8(P.q_lin, r * P.qkv_st + chan, x);
       if (shift) {
         float pv[8];
         if (ps == 0 && t0 == 0 && !P.q_prev)  // fallback "first": token 0 is its own predecessor
@@ -186,10 +188,10 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     param8(P.x_k, chan, kmix);
     param8(P.x_v, chan, vmix);
     if (t0 > 0) {
-      const int64_t ep = (bi * T + t0 - 1) * width + chan;
-      load_row8(P.k_lin, ep, kcarry);
-      load_row8(P.v_lin, ep, vcarry);
-      if (pre) value_residual(mode, vcarry, P, ep, chan);
+      const int64_t rp = bi * T + t0 - 1;
+      load_row8(P.k_lin, rp * P.qkv_st + chan, kcarry);
+      load_row8(P.v_lin, rp * P.qkv_st + chan, vcarry);
+      if (pre) value_residual(mode, vcarry, P, rp * width + chan, chan);
     } else {
       if (P.k_prev) load_row8(P.k_prev, bi * width + chan, kcarry);
       if (P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
@@ -200,10 +202,11 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     const int64_t t = t0 + ps * RPW + sub;
     const bool live = t < T;
     const int64_t tt = live ? t : T - 1;
-    const int64_t e = (bi * T + tt) * width + chan;
+    const int64_t r = bi * T + tt;
+    const int64_t e = r * width + chan, ein = r * P.qkv_st + chan;
     // keys: token shift, ln_k, RoPE
     float x[8];
-    load_row8(P.k_lin, e, x);
+    load_row8(P.k_lin, ein, x);
     if (shift) {
       float pv[8];
       if (ps == 0 && t0 == 0 && !P.k_prev)
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     if (live) store8(static_cast<uint16_t *>(P.k_out) + e, x);
     // values: value residual before / after the token shift
     float v[8];
-    load_row8(P.v_lin, e, v);
+    load_row8(P.v_lin, ein, v);
     if (pre) value_residual(mode, v, P, e, chan);
     if (live && P.v_last_out && t == T - 1)
       store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
@@ -233,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
     if (live && part == 0 && P.key_weight && P.gate_out) {
       const int64_t ge = (bi * T + t) * Hkv + hk;
-      const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[ge]);
+      const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[(bi * T + t) * P.kw_st + hk]);
       const float el = rbf(kw > 0.f ? kw : expm1f(kw));
       static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
     }

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -87,7 +87,7 @@ class KvmPrefixDesc(ctypes.Structure):
         ("q_prev", _vp), ("k_prev", _vp), ("v_prev", _vp),
         ("x_q", _vp), ("x_k", _vp), ("x_v", _vp), ("v_gate0", _vp), ("lamb", _vp),
         ("ln_q_w", _vp), ("ln_q_b", _vp), ("ln_k_w", _vp), ("ln_k_b", _vp),
-        ("cos", _vp), ("sin", _vp), ("rope_sb", _i64), ("rope_st", _i64),
+        ("cos", _vp), ("sin", _vp), ("rope_sb", _i64), ("rope_st", _i64), ("qkv_st", _i64), ("kw_st", _i64),
         ("q_out", _vp), ("k_out", _vp), ("v_out", _vp), ("gate_out", _vp), ("v_last_out", _vp),
     ]
 

@@ -352,16 +352,32 @@ class SequenceMixer(nn.Module):
             raise AssertionError("cached decode expects single-token inputs.")
         mode = self._VR_MODES[self.value_residual_mode]
         Hq, Hkv, D = self.num_attention_heads, self.num_key_value_heads, self.d_qk_head
-        q_lin, k_lin, v_lin = self.c_q(x), self.c_k(x), self.c_v(x)
+        use_gate = bool(self.config.kvm_use_merge_gate_keys or self.config.kvm_use_merge_gate_values)
         xp = states.get(self._CACHE_X_FINAL) if past_key_values is not None else None
+        # Every projection of x in one GEMM (c_q, c_k, c_v, key_weighting and,
+        # for the rwkv value residual, v_gate1); the kernel reads the column
+        # ranges of its output in place.
+        mods = [self.c_q, self.c_k, self.c_v]
+        if use_gate:
+            mods.append(self.key_weighting)
+        if mode == 2:
+            mods.append(self.v_gate1)
+        if self._CONCAT_PROJ:
+            y = F.linear(x, self._projection_weight(mods))
+            sizes = [m.out_features for m in mods]
+            parts = torch.split(y, sizes + [y.size(-1) - sum(sizes)], dim=-1)[:len(mods)]
+        else:
+            parts = [m(x) for m in mods]
+            # the kernel reads q/k/v with one token stride
+            parts[:3] = torch.split(torch.cat(parts[:3], dim=-1), [m.out_features for m in mods[:3]], dim=-1)
+        q_lin, k_lin, v_lin = parts[:3]
+        kw = parts[3] if use_gate else None
         gate_lin = None
         if mode == 2:
-            gate_lin = self.v_gate2(self.v_gate1(x))
+            gate_lin = self.v_gate2(parts[-1])
         elif mode == 3:
             shift = self.x_v if self.value_projection_size == self.hidden_size else self.x_v_hidden
             gate_lin = self.v_gate2(self.v_gate1(_token_shift(x, shift.view(1, 1, self.hidden_size), xp)))
-        use_gate = bool(self.config.kvm_use_merge_gate_keys or self.config.kvm_use_merge_gate_values)
-        kw = self.key_weighting(x).contiguous() if use_gate else None
         shift_on = self.tokenshift_mode == "rwkv"
         prev = [states.get(k) for k in (self._CACHE_Q_FINAL, self._CACHE_K_FINAL, self._CACHE_V_FINAL)]
         bf = dict(device=x.device, dtype=torch.bfloat16)
@@ -388,9 +404,20 @@ class SequenceMixer(nn.Module):
         d = _lib.KvmPrefixDesc()
         d.batch, d.seq_len, d.q_heads, d.kv_heads, d.head_dim, d.value_dim = B, T, Hq, Hkv, D, D
         d.value_residual_mode, d.token_shift, d.ln_eps = mode, int(shift_on), float(self.ln_q.eps)
-        d.q_lin, d.k_lin, d.v_lin = ptr(q_lin), ptr(k_lin), ptr(v_lin)
+        st = q_lin.stride(1)
+        if not (all(t.stride(-1) == 1 and t.stride(1) == st and t.stride(0) == T * st for t in (q_lin, k_lin, v_lin))
+                and st % 8 == 0 and all(t.data_ptr() % 16 == 0 for t in (q_lin, k_lin, v_lin))):
+            raise AssertionError("q/k/v projections must share one token stride (a multiple of 8 elements)")
+        keep.extend((q_lin, k_lin, v_lin))
+        d.q_lin, d.k_lin, d.v_lin = q_lin.data_ptr(), k_lin.data_ptr(), v_lin.data_ptr()
+        d.qkv_st = q_lin.stride(1)
         d.v_first = ptr(v_first.to(torch.bfloat16).reshape(B, T, -1)) if mode else None
-        d.gate_lin, d.key_weight = ptr(gate_lin), ptr(kw)
+        d.gate_lin = ptr(gate_lin)
+        if kw is not None:
+            if kw.stride(-1) != 1 or kw.stride(0) != T * kw.stride(1):
+                kw = kw.contiguous()
+            keep.append(kw)
+            d.key_weight, d.kw_st = kw.data_ptr(), kw.stride(1)
         if shift_on:
             d.q_prev, d.k_prev, d.v_prev = (ptr(p.to(torch.bfloat16)) if p is not None else None for p in prev)
             d.x_q, d.x_k, d.x_v = ptr(self.x_q), ptr(self.x_k), ptr(self.x_v)
@@ -418,6 +445,25 @@ class SequenceMixer(nn.Module):
         else:
             merge_gate = torch.ones((B, Hkv, T, 1), device=x.device, dtype=torch.float)
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), merge_gate
+
+    # One concatenated projection GEMM in the fused path (fewer launches;
+    # same products, rounded by a different GEMM kernel than separate ones).
+    _CONCAT_PROJ = True
+
+    def _projection_weight(self, mods):
+        """torch.cat of the modules' weights, padded with zero rows to a
+        multiple of 8 outputs (16-byte aligned output rows), rebuilt whenever
+        one of them is replaced or modified in place (data pointer or version
+        counter)."""
+        key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.device) for m in mods)
+        cached = self.__dict__.get("_proj_cat")
+        if cached is None or cached[0] != key:
+            w0 = mods[0].weight
+            pad = -sum(m.out_features for m in mods) % 8
+            with torch.no_grad():
+                cached = (key, torch.cat([m.weight for m in mods] + [w0.new_zeros(pad, w0.size(1))], dim=0))
+            self.__dict__["_proj_cat"] = cached
+        return cached[1]
 
     def _torch_prefix(self, x, v_first, position_embeddings, past_key_values):
         B, T, _ = x.size()
