@@ -31,6 +31,7 @@ as given.
 from __future__ import annotations
 
 import importlib
+import math
 from dataclasses import dataclass
 from typing import Any
 
@@ -221,13 +222,22 @@ class Block(nn.Module):
         if config.use_block_lambdas:
             self.lambdas = set_label("scalars", nn.Parameter(torch.tensor([1.0, 0.0])))
 
+    def _residual(self, x, y):
+        """x + y * residual_scale.  For a power-of-two scale the product is
+        exact, so one fused add (alpha) gives the same bf16 result as the
+        reference's two ops."""
+        sc = float(self.residual_scale)
+        if sc > 0 and math.frexp(sc)[0] == 0.5:
+            return torch.add(x, y, alpha=sc)
+        return x + y * self.residual_scale
+
     def forward(self, x, x0, **kwargs):
         if self.config.use_block_lambdas:
             x = self.lambdas[0] * x + self.lambdas[1] * x0
         cached = not self.training and kwargs.get("past_key_values") is not None
         attn_fn = getattr(self.attn, "forward_inference", self.attn.forward) if cached else self.attn.forward
-        x = x + attn_fn(self.ln_attn(x), x0=x0, **kwargs) * self.residual_scale
-        return x + self.mlp(self.ln_mlp(x), x0=x0, **kwargs) * self.residual_scale
+        x = self._residual(x, attn_fn(self.ln_attn(x), x0=x0, **kwargs))
+        return self._residual(x, self.mlp(self.ln_mlp(x), x0=x0, **kwargs))
 
 
 class RWKV7BackboneModel(nn.Module):
