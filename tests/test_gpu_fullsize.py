@@ -35,10 +35,20 @@ def lib():
     return _lib.load()
 
 
-def _gpu_inputs(B, Hq, Hkv, Tn, D, seed):
+def _gpu_inputs(B, Hq, Hkv, Tn, D, seed, clustered=False):
+    """q/k/v ~ N(0,1)/sqrt(D), gate 1+elu(N(0,1)).  clustered:
+    10% of the keys are one of 8 centres shared by every head, N(0,1)/sqrt(D),
+    plus N(0, 0.05^2)/sqrt(D) noise, which stresses routing with near-equal keys."""
     gen = torch.Generator(device=DEV).manual_seed(seed)
     q = (torch.randn(B, Hq, Tn, D, device=DEV, generator=gen) / math.sqrt(D)).bfloat16()
-    k = (torch.randn(B, Hkv, Tn, D, device=DEV, generator=gen) / math.sqrt(D)).bfloat16()
+    kf = torch.randn(B, Hkv, Tn, D, device=DEV, generator=gen)
+    if clustered:
+        centres = torch.randn(8, D, device=DEV, generator=gen)
+        pick = torch.randint(0, 8, (B, Hkv, Tn), device=DEV, generator=gen)
+        sel = torch.rand(B, Hkv, Tn, device=DEV, generator=gen) < 0.1
+        noisy = centres[pick] + 0.05 * torch.randn(B, Hkv, Tn, D, device=DEV, generator=gen)
+        kf = torch.where(sel.unsqueeze(-1), noisy, kf)
+    k = (kf / math.sqrt(D)).bfloat16()
     v = (torch.randn(B, Hkv, Tn, D, device=DEV, generator=gen) / math.sqrt(D)).bfloat16()
     g = (1.0 + torch.nn.functional.elu(torch.randn(B, Hkv, Tn, 1, device=DEV, generator=gen))).bfloat16()
     return q, k, v, g
@@ -65,7 +75,7 @@ def test_full_size_prefill(lib, monkeypatch, name, B, Hq, Hkv, Tn, D, C, mode, n
     ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
     stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
     m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
-    q, k, v, g = _gpu_inputs(B, Hq, Hkv, Tn, D, 29)
+    q, k, v, g = _gpu_inputs(B, Hq, Hkv, Tn, D, 29, clustered=name.startswith("config3"))
     plan = m.make_plan(Tn)
     res = {}
     for which, chain in (("chain", "1"), ("per-update", "0")):
