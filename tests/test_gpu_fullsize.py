@@ -21,6 +21,10 @@ import torch
 
 import kvm_testlib as T
 
+
+def _rows(x):
+    return x.reshape(-1, x.size(-2), x.size(-1))
+
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
@@ -187,3 +191,85 @@ def test_full_size_decode_attention(lib):
                                            max_abs=1e-2, mean_abs=1e-3)
             worst = (max(worst[0], mx), max(worst[1], mean))
     T.log(f"[full-size] decode sampled rows: max {worst[0]:.2e} mean {worst[1]:.2e}")
+
+
+@pytest.mark.parametrize("name,B,Hq,Hkv,Tn,D,C,mode,n_max,factor", [
+    ("config2", 1, 32, 32, 32768, 128, 512, "fixed", 1, 1.0),
+    ("config3-growth", 2, 16, 16, 65536, 128, 512, "power_law", 2, 16.0),
+])
+def test_full_size_prefill_matches_oracle(lib, name, B, Hq, Hkv, Tn, D, C, mode, n_max, factor):
+    """The whole full-size prefill against the CPU oracle on the same inputs
+    (config 2: 61 updates, ~1M merge routes; config 3: 125 updates with
+    appends, clustered keys): routes and append sets (logged: the first update
+    with a difference), output within the bf16 tolerance, state rows.  Route
+    exactness from an identical state, with near ties classified against the
+    fp32 rounding bound, is tests/test_gpu_parity.py's per-update test."""
+    from oracle import kvm_oracle as O
+
+    T.log(f"[full-size-oracle] {name}: B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode=mode, min_len=C, n_max=n_max, factor=factor, expo=0.5)
+    gen = torch.Generator().manual_seed(23)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.1 * torch.randn(Hq, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = _gpu_inputs(B, Hq, Hkv, Tn, D, 29, clustered=name.startswith("config3"))
+    with torch.no_grad():
+        res = m.prefill_raw(q, k, v, g, route_log=True)
+    torch.cuda.synchronize()
+    ocfg = O.OracleConfig(
+        q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=cfg.n_bswa_chunks,
+        n_max_d_chunks=n_max, sink_len=cfg.sink_len, rope_partial_dim=cfg.rope_partial_dim,
+        state_budget_mode=mode, state_growth_factor=factor, state_growth_exponent=0.5, state_min_len=C,
+        append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
+    rec = O.Recorder()
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    qc, kc, vc, gc = q.cpu(), k.cpu(), v.cpu(), g.cpu()
+    y_ref, st = O.prefill(qc, kc, vc, gc, p, ocfg, rec)
+    rows = B * Hkv
+    assert len(rec.updates) == res["plan"].n_updates
+    sched = O.prefill_schedule(ocfg, Tn)["updates"]
+    first = None          # first update whose routes or appends differ
+    n_diff = n_route = n_app_diff = 0
+    for i, u in enumerate(rec.updates):
+        gr = res["route_log"][i].cpu()
+        ga = res["append_log"][i].cpu()
+        ai = u.append_idx.reshape(rows, -1)
+        app_ok = all(torch.equal(ga[r].nonzero().flatten(), ai[r]) for r in range(rows))
+        if u.route is None:
+            mism = torch.zeros(rows, 0, dtype=torch.bool)
+        else:
+            mi = u.merge_idx.reshape(rows, -1)
+            g_sel = torch.gather(gr, 1, mi)
+            mism = g_sel != u.route.reshape(rows, -1).to(torch.int32)
+            n_diff += int(mism.sum())
+            n_route += mism.numel()
+        if first is None and (not app_ok or bool(mism.any())):
+            first = i
+        n_app_diff += 0 if app_ok else 1
+    S = res["plan"].final_state_len
+    out = res["out"].cpu().transpose(1, 2)
+    mx, mean = T.assert_close_bf16(out, y_ref, f"{name} full-size output")
+    T.log(f"[full-size-oracle] {name}: {len(rec.updates)} updates, {n_route} merge routes, {n_diff} differ, "
+          f"{n_app_diff} updates with a different append set; bit-exact through update "
+          f"{len(rec.updates) - 1 if first is None else first - 1}; out max {mx:.2e} mean {mean:.2e}")
+    # The two sides sum each slot's tokens in different orders (the reference's bf16
+    # one-hot matmul, the kernels' token-order fp32 sums), so their states may differ by
+    # a bf16 ulp and a route near a tie may flip; from there the trajectories differ in
+    # the slots involved, most with config 3's clustered keys (near-identical slots).
+    # Measured: config 2 0.015% of the routes (bit-exact through update 37 of 61),
+    # config 3 1.0% (through update 15 of 125).  Bar: append sets equal, at most 2% of
+    # the routes, outputs within the bf16 tolerance (checked above).
+    assert n_app_diff == 0 and n_diff <= n_route // 50
+    # After a near tie the two trajectories hold different sums in the slots involved; everywhere
+    # else the state agrees: at least 99% of the slot rows within the bf16 tolerance.
+    sk = res["state_k"][:, :S].cpu().view(B, Hkv, S, D).float()
+    ref_sk = st[O.S_K].float()
+    scale = float(ref_sk.abs().max())
+    row_err = (sk - ref_sk).abs().amax(-1)
+    frac = float((row_err <= 2e-2 * scale).float().mean())
+    assert frac >= 0.99, f"{name}: only {frac:.4f} of the state rows agree"
+    if first is None:
+        assert n_diff == 0
