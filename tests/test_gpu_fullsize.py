@@ -201,9 +201,10 @@ def test_full_size_prefill_matches_oracle(lib, name, B, Hq, Hkv, Tn, D, C, mode,
     """The whole full-size prefill against the CPU oracle on the same inputs
     (config 2: 61 updates, ~1M merge routes; config 3: 125 updates with
     appends, clustered keys): routes and append sets (logged: the first update
-    with a difference), output within the bf16 tolerance, state rows.  Route
-    exactness from an identical state, with near ties classified against the
-    fp32 rounding bound, is tests/test_gpu_parity.py's per-update test."""
+    with a difference), output within the bf16 tolerance, state rows; and, for
+    the first, middle, last and first-differing updates, one update from the
+    oracle's own state, where every differing route must be an fp32 near tie
+    or a bf16 operand rounding (test_gpu_parity.update_parity)."""
     from oracle import kvm_oracle as O
 
     T.log(f"[full-size-oracle] {name}: B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C} {mode}")
@@ -224,7 +225,7 @@ def test_full_size_prefill_matches_oracle(lib, name, B, Hq, Hkv, Tn, D, C, mode,
         state_budget_mode=mode, state_growth_factor=factor, state_growth_exponent=0.5, state_min_len=C,
         append_tie_break="lower_index")
     p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=ft, state_temp=stt)
-    rec = O.Recorder()
+    rec = O.Recorder(keep_states=True)
     torch.set_num_threads(min(16, torch.get_num_threads()))
     qc, kc, vc, gc = q.cpu(), k.cpu(), v.cpu(), g.cpu()
     y_ref, st = O.prefill(qc, kc, vc, gc, p, ocfg, rec)
@@ -249,6 +250,24 @@ def test_full_size_prefill_matches_oracle(lib, name, B, Hq, Hkv, Tn, D, C, mode,
         if first is None and (not app_ok or bool(mism.any())):
             first = i
         n_app_diff += 0 if app_ok else 1
+    # Route exactness from an identical state at full size: the first update with a
+    # difference (where the trajectories part), the first, middle and last updates.
+    from kvm_amd import _lib
+    from test_gpu_parity import update_parity
+
+    layer = m._layer_struct(B, torch.device(DEV))
+    seq, keep = _lib.seq4(k, v, g)
+    nu = len(rec.updates)
+    pc = [0, 0, 0, 0]
+    for i in sorted({0, nu // 2, nu - 1} | ({first} if first is not None else set())):
+        u = rec.updates[i]
+        nxt = rec.updates[i + 1] if i + 1 < nu else None
+        ref_next = (nxt.s_k_before, nxt.s_v_before) if nxt is not None else (st[O.S_K], st[O.S_V])
+        c = update_parity(lib, layer, seq, u, sched[i][0] * C, kc, gc, p, ocfg, C, D, ref_next, f"{name} update {i}")
+        pc = [x + y for x, y in zip(pc, c)]
+    del keep
+    T.log(f"[full-size-oracle] {name}: sampled updates from the oracle's state: {pc[0]} merged tokens, "
+          f"{pc[1]} route mismatches ({pc[2]} fp32 near ties, {pc[3]} bf16 operand roundings)")
     S = res["plan"].final_state_len
     out = res["out"].cpu().transpose(1, 2)
     mx, mean = T.assert_close_bf16(out, y_ref, f"{name} full-size output")
