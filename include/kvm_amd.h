@@ -181,6 +181,18 @@ typedef struct kvm_prefix_desc {
  * (model/value_residual_mixin.py:173-237, model/kvm_mixer.py:367-401). */
 int kvm_prefix(const kvm_prefix_desc *d, void *stream);
 
+/* RWKV token shift out = x + mix * (shift(x) - x) over x [B, T, width]
+ * (bf16, contiguous, width a multiple of 8): shift(x) is the previous token,
+ * prev [B, width] for token 0, or when prev is NULL zeros (zero_fallback != 0)
+ * or token 0 itself.  Replaces model/tokenshift.py:11-37 as the decoder's MLP
+ * calls it (model/rwkv7_backbone.py:163-170, fallback "zero"). */
+int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t batch,
+                    int64_t seq_len, int64_t width, int zero_fallback, void *stream);
+
+/* out = relu(x)^2 over n bf16 elements (n a multiple of 8): the decoder MLP's
+ * activation, F.relu(x).square() (model/rwkv7_backbone.py:174-175). */
+int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
+
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
 int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc */

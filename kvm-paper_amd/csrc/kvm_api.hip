@@ -137,6 +137,25 @@ int64_t kvm_struct_size(int which) {
 
 const char *kvm_last_error(void) { return g_error.c_str(); }
 
+int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t batch,
+                    int64_t seq_len, int64_t width, int zero_fallback, void *stream) {
+  if (batch < 1 || seq_len < 1 || width < 8 || width % 8)
+    return fail(KVM_EINVAL, "token shift needs positive batch / seq_len and a width that is a multiple of 8");
+  if (!x || !mix || !out || !aligned16(x) || !aligned16(mix) || !aligned16(out) || (prev && !aligned16(prev)))
+    return fail(KVM_EINVAL, "token shift pointers must be non-NULL (prev may be NULL) and 16-byte aligned");
+  KVM_HIP(kvm::launch_token_shift(x, prev, mix, out, batch, seq_len, width, zero_fallback, as_stream(stream)),
+          "token shift");
+  return KVM_OK;
+}
+
+int kvm_relu_square(const void *x, void *out, int64_t n, void *stream) {
+  if (n < 8 || n % 8) return fail(KVM_EINVAL, "relu_square needs a positive element count that is a multiple of 8");
+  if (!x || !out || !aligned16(x) || !aligned16(out))
+    return fail(KVM_EINVAL, "relu_square pointers must be non-NULL and 16-byte aligned");
+  KVM_HIP(kvm::launch_relu_square(x, out, n, as_stream(stream)), "relu square");
+  return KVM_OK;
+}
+
 int kvm_prefix(const kvm_prefix_desc *d, void *stream) {
   if (!d) return fail(KVM_EINVAL, "prefix descriptor is NULL");
   if (d->batch < 1 || d->seq_len < 1 || d->q_heads < 1 || d->kv_heads < 1)

@@ -163,6 +163,9 @@ struct PrefillAttnArgs {
 };
 
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);
+hipError_t launch_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t B,
+                              int64_t T, int64_t width, int zero_fallback, hipStream_t stream);
+hipError_t launch_relu_square(const void *x, void *out, int64_t n, hipStream_t stream);
 
 hipError_t launch_prefill_attention(const kvm_layer &L,
                                     const PrefillAttnArgs &a,

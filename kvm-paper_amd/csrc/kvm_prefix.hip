@@ -257,3 +257,75 @@ hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream) {
 }
 
 }  // namespace kvm
+
+// ---------------------------------------------------------------------------
+// Elementwise ops of the decoder's MLP (model/rwkv7_backbone.py:163-177):
+// the RWKV token shift x + mix * (shift(x) - x) (model/tokenshift.py:11-37)
+// and relu(x)^2, one read and one write per element, with the reference's
+// bf16 rounding points.
+
+namespace kvm {
+namespace {
+
+// One thread per 8 channels of one token row.  prev: the row before token 0
+// ([B, width]), or NULL for the fallback: zeros (zero_fallback) or token 0
+// itself ("first").
+__global__ __launch_bounds__(256) void k_token_shift(const uint16_t *__restrict__ x,
+                                                     const uint16_t *__restrict__ prev,
+                                                     const uint16_t *__restrict__ mix,
+                                                     uint16_t *__restrict__ out, int64_t B, int64_t T,
+                                                     int64_t width, int zero_fallback) {
+  const int64_t per_row = width / 8;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= B * T * per_row) return;
+  const int64_t c = (i % per_row) * 8, r = i / per_row, t = r % T, b = r / T;
+  float xv[8], pv[8], mv[8];
+  load8(x + r * width + c, xv);
+  load8(mix + c, mv);
+  if (t > 0) {
+    load8(x + (r - 1) * width + c, pv);
+  } else if (prev) {
+    load8(prev + b * width + c, pv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[e] = zero_fallback ? 0.f : xv[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) xv[e] = rbf(xv[e] + rbf(mv[e] * rbf(pv[e] - xv[e])));
+  store8(out + r * width + c, xv);
+}
+
+// relu(x)^2: the relu is exact, the square rounds once (as torch's two ops).
+__global__ __launch_bounds__(256) void k_relu_square(const uint16_t *__restrict__ x, uint16_t *__restrict__ out,
+                                                     int64_t n8) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  float v[8];
+  load8(x + i * 8, v);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float r = fmaxf(v[e], 0.f);
+    v[e] = rbf(r * r);
+  }
+  store8(out + i * 8, v);
+}
+
+}  // namespace
+
+hipError_t launch_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t B,
+                              int64_t T, int64_t width, int zero_fallback, hipStream_t stream) {
+  const int64_t n = B * T * (width / 8);
+  hipLaunchKernelGGL(k_token_shift, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(prev),
+                     static_cast<const uint16_t *>(mix), static_cast<uint16_t *>(out), B, T, width, zero_fallback);
+  return hipGetLastError();
+}
+
+hipError_t launch_relu_square(const void *x, void *out, int64_t n, hipStream_t stream) {
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(k_relu_square, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint16_t *>(x), static_cast<uint16_t *>(out), n8);
+  return hipGetLastError();
+}
+
+}  // namespace kvm

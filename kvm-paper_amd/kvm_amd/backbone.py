@@ -180,11 +180,55 @@ class MLP(nn.Module):
                 if prev is not None and prev.shape != (x.shape[0], 1, x.shape[2]):
                     raise AssertionError(f"cached MLP decode requires 'mlp_final_token' of shape "
                                          f"{(x.shape[0], 1, x.shape[2])}, got {tuple(prev.shape)}.")
-                past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:]})
-            xk = x + self.x_k * token_shift_delta(x, prev, fallback="zero")
+                # a copy, not a view: a view would keep the whole [B, T, d] input alive
+                past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:].clone()})
+            if self._use_kernels(x):
+                xk = _kernel_token_shift(x, prev, self.x_k)
+            else:
+                xk = x + self.x_k * token_shift_delta(x, prev, fallback="zero")
         else:
             xk = x
-        return self.c_proj(F.relu(self.c_fc(xk)).square())
+        h = self.c_fc(xk)
+        if self._use_kernels(h):
+            return self.c_proj(_kernel_relu_square(h))
+        return self.c_proj(F.relu(h).square())
+
+    def _use_kernels(self, t: torch.Tensor) -> bool:
+        """bf16 inference on the GPU takes the HIP elementwise kernels (same
+        bf16 rounding points as the torch ops); CPU tensors and autograd take
+        the torch ops."""
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.size(-1) % 8:
+            return False
+        if self.config.use_tokenshift_ffn and self.x_k.dtype != torch.bfloat16:
+            return False
+        return not (torch.is_grad_enabled() and (t.requires_grad or any(p.requires_grad for p in self.parameters())))
+
+
+def _kernel_token_shift(x: torch.Tensor, prev: torch.Tensor | None, mix: torch.Tensor) -> torch.Tensor:
+    """x + mix * (shift(x) - x), fallback "zero", in one HIP launch (kvm_token_shift)."""
+    from . import _lib
+
+    x = x.contiguous()
+    B, T, d = x.shape
+    out = torch.empty_like(x)
+    if prev is not None:
+        prev = prev.to(device=x.device, dtype=x.dtype).reshape(B, d).contiguous()
+    mix = mix.reshape(d).contiguous()
+    _lib.check(_lib.load().kvm_token_shift(x.data_ptr(), prev.data_ptr() if prev is not None else None,
+                                           mix.data_ptr(), out.data_ptr(), B, T, d, 1,
+                                           _lib.stream_handle(x.device)), "kvm_token_shift")
+    return out
+
+
+def _kernel_relu_square(h: torch.Tensor) -> torch.Tensor:
+    """relu(h)^2 in one HIP launch (kvm_relu_square)."""
+    from . import _lib
+
+    h = h.contiguous()
+    out = torch.empty_like(h)
+    _lib.check(_lib.load().kvm_relu_square(h.data_ptr(), out.data_ptr(), h.numel(), _lib.stream_handle(h.device)),
+               "kvm_relu_square")
+    return out
 
 
 def _resolve_mixer_path(config, layer_idx: int) -> str:

@@ -122,3 +122,23 @@ def test_concatenated_projection_matches_separate_gemms(lib):
         mx, mean = T.err_stats(u, w)
         T.log(f"[prefix] concatenated vs separate projections, {name}: max {mx:.2e} mean {mean:.2e}")
         assert mx <= 0.1 and mean <= 2e-3, (name, mx, mean)
+
+
+@pytest.mark.parametrize("with_prev", [False, True])
+def test_mlp_kernels_match_torch_ops(lib, with_prev):
+    """The decoder MLP's token shift (fallback "zero", or a carried previous
+    token) and relu^2 kernels against the torch ops on the same GPU: bit-exact
+    (elementwise, same bf16 rounding points)."""
+    from kvm_amd.backbone import _kernel_relu_square, _kernel_token_shift, token_shift_delta
+
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    B, Tn, d = 3, 77, 256
+    x = torch.randn(B, Tn, d, device=DEV, generator=gen).bfloat16()
+    mix = torch.rand(1, 1, d, device=DEV, generator=gen).bfloat16()
+    prev = torch.randn(B, 1, d, device=DEV, generator=gen).bfloat16() if with_prev else None
+    with torch.no_grad():
+        got = _kernel_token_shift(x, prev, mix)
+        ref = x + mix * token_shift_delta(x, prev, fallback="zero")
+        assert torch.equal(got, ref), float((got.float() - ref.float()).abs().max())
+        h = torch.randn(B, Tn, 4 * d, device=DEV, generator=gen).bfloat16()
+        assert torch.equal(_kernel_relu_square(h), torch.nn.functional.relu(h).square())
