@@ -86,11 +86,22 @@ class MixerConfig:
 
 
 @dataclass
+class BaseModelOutput:
+    """The decoder's final hidden states and the cache the step used (the
+    fields of transformers' BaseModelOutputWithPast the reference returns)."""
+
+    last_hidden_state: torch.Tensor
+    past_key_values: StatesDictCache | None = None
+
+
+@dataclass
 class CausalLMOutput:
-    """Logits (fp32) and the cache the step used."""
+    """Logits (fp32) and the cache the step used (the fields of the
+    reference's CausalLMOutputWithPastAndAccuracy this build fills; no loss)."""
 
     logits: torch.Tensor
     past_key_values: StatesDictCache | None = None
+    loss: torch.Tensor | None = None
 
 
 def token_shift_delta(x: torch.Tensor, prev_token: torch.Tensor | None = None, *,
@@ -317,7 +328,7 @@ class RWKV7BackboneModel(nn.Module):
 
     def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
                 inputs_embeds=None, use_cache=None, cache_position=None, **kwargs):
-        """Returns ``(last_hidden_state, past_key_values or None)`` (model/rwkv7_backbone.py:468-570)."""
+        """BaseModelOutput(last_hidden_state, past_key_values or None) (model/rwkv7_backbone.py:468-570)."""
         if (input_ids is None) ^ (inputs_embeds is not None):
             raise ValueError("You must specify exactly one of input_ids or inputs_embeds")
         if inputs_embeds is None:
@@ -348,7 +359,7 @@ class RWKV7BackboneModel(nn.Module):
                                  "decode one token per step")
         x = self._forward_model(input_ids, inputs_embeds, position_ids=position_ids, attention_mask=attention_mask,
                                 past_key_values=past_key_values, use_cache=use_cache, **kwargs)
-        return x, (past_key_values if use_cache else None)
+        return BaseModelOutput(last_hidden_state=x, past_key_values=past_key_values if use_cache else None)
 
     def _forward_model(self, input_ids, x, position_ids, **kwargs):
         """model/rwkv7_backbone.py:585-685 (no alternating layers)."""
@@ -391,9 +402,10 @@ class RWKV7BackboneForCausalLM(nn.Module):
                 **kwargs) -> CausalLMOutput:
         if labels is not None:
             raise ValueError("this build runs the inference forward path only (no loss)")
-        hidden, cache = self.transformer(input_ids=input_ids, attention_mask=attention_mask,
-                                         position_ids=position_ids, past_key_values=past_key_values,
-                                         inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
+        base = self.transformer(input_ids=input_ids, attention_mask=attention_mask, position_ids=position_ids,
+                                past_key_values=past_key_values, inputs_embeds=inputs_embeds, use_cache=use_cache,
+                                **kwargs)
+        hidden, cache = base.last_hidden_state, base.past_key_values
         keep = slice(-logits_to_keep, None) if isinstance(logits_to_keep, int) else logits_to_keep
         logits = self.lm_head(hidden[:, keep, :])
         if self.config.logit_softcap != 0:
@@ -466,4 +478,4 @@ def init_random_(model: nn.Module, seed: int = 0) -> nn.Module:
 
 
 __all__ = ["MixerConfig", "RotaryEmbedding", "MLP", "Block", "RWKV7BackboneModel", "RWKV7BackboneForCausalLM",
-           "CausalLMOutput", "StatesDictCache", "init_random_", "token_shift_delta"]
+           "BaseModelOutput", "CausalLMOutput", "StatesDictCache", "init_random_", "token_shift_delta"]

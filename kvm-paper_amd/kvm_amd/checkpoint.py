@@ -110,6 +110,10 @@ def load_reference_checkpoint(path: str | Path, config: MixerConfig | dict | Non
     with torch.device("meta"):
         model = RWKV7BackboneForCausalLM(config)
     model.load_state_dict(sd, strict=strict, assign=True)
+    missing = [n for n, t in list(model.named_parameters()) + list(model.named_buffers()) if t.is_meta]
+    if missing:
+        raise ValueError(f"{path}: the checkpoint has no tensor for {missing[:8]}"
+                         f"{' ...' if len(missing) > 8 else ''} (nothing to initialise them from)")
     model = model.to(dtype=dtype)
     if device is not None:
         model = model.to(device)
