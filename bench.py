@@ -158,7 +158,9 @@ def bench_decode(args, torch, kvm_amd):
     gs = (1 + torch.nn.functional.elu(torch.randn(steps, B, H, 1, 1, generator=gen, device=dev))).bfloat16()
     cache = mixer.make_decode_cache(snap, state_capacity=S)
 
-    def run(timed):
+    def run(inner):
+        """One event pair per token (the reference's protocol); with `inner`,
+        a second pair around each attention launch (for the attention time)."""
         cache.reset_(snap)
         torch.cuda.synchronize()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -166,9 +168,11 @@ def bench_decode(args, torch, kvm_amd):
         for i in range(steps):
             ev[i][0].record()
             mixer._decode_advance(ks[i], vs[i], gs[i], cache)
-            ea[i][0].record()
+            if inner:
+                ea[i][0].record()
             mixer._decode_attention(qs[i], cache)
-            ea[i][1].record()
+            if inner:
+                ea[i][1].record()
             ev[i][1].record()
         torch.cuda.synchronize()
         return ev, ea
@@ -176,7 +180,8 @@ def bench_decode(args, torch, kvm_amd):
     with torch.no_grad():
         for _ in range(max(1, args.warmup)):
             run(False)
-        ev, ea = run(True)
+        ev, _ = run(False)
+        _, ea = run(True)
     step_ms = [a.elapsed_time(b) for a, b in ev]
     attn_ms = [a.elapsed_time(b) for a, b in ea]
     total_ms = sum(step_ms)
