@@ -106,16 +106,19 @@ def bench_prefill(args, torch, kvm_amd):
         for _ in range(args.warmup):
             mixer.prefill_raw(q, k, v, g, plan=plan)
         torch.cuda.synchronize()
-        # Timed steps: one event pair around all of them, nothing inside.
+        # Timed steps: one event pair around all of them, nothing inside.  The
+        # device status word is sticky, so it is read once after the timed
+        # steps (a failed update chain raises there).
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record()
         for i in range(args.steps):
-            mixer.prefill_raw(q, k, v, g, plan=plan)
+            mixer.prefill_raw(q, k, v, g, plan=plan, check_status=False)
         end.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        mixer.check_prefill_status()
         # Breakdown (update chain, attention launches) from separate steps whose
         # events kvm_prefill records on its launch stream.
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
@@ -123,8 +126,9 @@ def bench_prefill(args, torch, kvm_amd):
             for x in e:
                 x.record()
         for i in range(args.steps):
-            mixer.prefill_raw(q, k, v, g, plan=plan, events=evs[i])
+            mixer.prefill_raw(q, k, v, g, plan=plan, events=evs[i], check_status=False)
         torch.cuda.synchronize()
+        mixer.check_prefill_status()
     ms = start.elapsed_time(end) / args.steps
     attn_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
     chain_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
@@ -249,34 +253,67 @@ def bench_e2e(args, torch, kvm_amd):
                 decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec)
 
 
+def _cpu_prefill_inputs(torch, B, H, D, T, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, H, T, D, generator=gen) / math.sqrt(D)).to(dtype)
+    k = (torch.randn(B, H, T, D, generator=gen) / math.sqrt(D)).to(dtype)
+    v = (torch.randn(B, H, T, D, generator=gen) / math.sqrt(D)).to(dtype)
+    g = (1 + torch.nn.functional.elu(torch.randn(B, H, T, 1, generator=gen))).to(dtype)
+    return q, k, v, g
+
+
+def _time_cpu(fn, runs=3):
+    """One untimed warm-up, then the median of `runs` timed calls (seconds)."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], times
+
+
 def cpu_baseline(torch, sample_T):
     """The CPU oracle (eager restatement of model/kvm_mixer.py with fp32
-    routing) on the first sample_T tokens of the prefill workload."""
+    routing) on the host cores of this process: the first sample_T tokens of
+    the config-2 prefill (bf16), and BASELINE config 1 (fp32, B1 H4 D64
+    T4096 C256, 64 configured slots -> 256 effective, rope_partial_dim 32)."""
     from oracle import kvm_oracle as O
 
     threads = len(os.sched_getaffinity(0))
-    threads = min(threads, int(os.environ.get("KVM_CPU_THREADS", "16")))
     torch.set_num_threads(threads)
+
+    def params(D, H, dtype):
+        return O.OracleParams(ln_weight=torch.ones(D).to(dtype), ln_bias=torch.zeros(D).to(dtype),
+                              front_temp=torch.ones(H).to(dtype), state_temp=torch.ones(H).to(dtype))
+
     B, H, D, C = 1, 32, 128, 512
-    gen = torch.Generator().manual_seed(0)
-    q = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
-    k = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
-    v = (torch.randn(B, H, sample_T, D, generator=gen) / math.sqrt(D)).bfloat16()
-    g = (1 + torch.nn.functional.elu(torch.randn(B, H, sample_T, 1, generator=gen))).bfloat16()
-    cfg = O.OracleConfig(q_heads=H, kv_heads=H, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=2,
-                         sink_len=1, rope_partial_dim=64, state_min_len=256)
-    p = O.OracleParams(ln_weight=torch.ones(D).bfloat16(), ln_bias=torch.zeros(D).bfloat16(),
-                       front_temp=torch.ones(H).bfloat16(), state_temp=torch.ones(H).bfloat16())
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        O.prefill(q, k, v, g, p, cfg)
-        times.append(time.perf_counter() - t0)
-    sec = min(times)
-    return dict(value=B * sample_T / sec, unit="tokens/s", cores=threads, kind="port",
+    x2 = _cpu_prefill_inputs(torch, B, H, D, sample_T, torch.bfloat16, 0)
+    cfg2 = O.OracleConfig(q_heads=H, kv_heads=H, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=2,
+                          sink_len=1, rope_partial_dim=64, state_min_len=256)
+    p2 = params(D, H, torch.bfloat16)
+    sec2, all2 = _time_cpu(lambda: O.prefill(*x2, p2, cfg2))
+    x1 = _cpu_prefill_inputs(torch, 1, 4, 64, 4096, torch.float32, 0)
+    cfg1 = O.OracleConfig(q_heads=4, kv_heads=4, head_dim=64, value_dim=64, chunk_len=256, n_bswa_chunks=2,
+                          sink_len=1, rope_partial_dim=32, state_min_len=64)
+    p1 = params(64, 4, torch.float32)
+    sec1, all1 = _time_cpu(lambda: O.prefill(*x1, p1, cfg1))
+    quota = None
+    try:
+        q_, per = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        quota = None if q_ == "max" else round(int(q_) / int(per), 2)
+    except (OSError, ValueError):
+        pass
+    return dict(value=B * sample_T / sec2, unit="tokens/s", cores=threads, kind="port",
                 sample=f"CPU oracle (eager restatement of model/kvm_mixer.py, fp32 routing) prefill of "
-                       f"{sample_T} tokens of the config-2 layer (B1 H32 D128 C512, 512 slots), "
-                       f"best of 2 runs: {sec:.2f} s")
+                       f"{sample_T} tokens of the config-2 layer (B1 H32 D128 C512, 512 slots, bf16) on "
+                       f"{threads} threads (all cores in this process's affinity): 1 warm-up, median of "
+                       f"3 runs {sec2:.2f} s (runs {', '.join(f'{t:.2f}' for t in all2)} s)",
+                host={"affinity_cpus": threads, "os_cpu_count": os.cpu_count(), "cgroup_cpu_quota": quota,
+                      "omp_num_threads": os.environ.get("OMP_NUM_THREADS")},
+                config1={"value": 4096 / sec1, "unit": "tokens/s", "dtype": "f32", "seconds": round(sec1, 4),
+                         "sample": "BASELINE config 1 whole: B1 H4 D64 T4096 C256 fp32, 64 configured slots "
+                                   "(256 effective), rope_partial_dim 32; 1 warm-up, median of 3"})
 
 
 def main():

@@ -8,9 +8,10 @@
  * single-token decode.  Every entry point takes plain device pointers,
  * element strides and sizes; nothing here names a torch type.  All work is
  * enqueued on the caller's HIP stream (`stream`, a hipStream_t; NULL is the
- * legacy default stream) and no entry point synchronises the device or
- * allocates device memory: scratch space is passed in as `workspace`, sized
- * by the matching *_workspace_bytes() query.
+ * legacy default stream).  No entry point allocates device memory: scratch
+ * space is passed in as `workspace`, sized by the matching
+ * *_workspace_bytes() query.  No entry point synchronises, except
+ * kvm_prefill when the caller passes no status word (see kvm_prefill_desc).
  *
  * Tensors
  *   bf16 tensors are stored as raw 16-bit bfloat16; the last (feature) axis
@@ -26,7 +27,8 @@
  *   KVM_EINVAL marks an argument the reference would reject with ValueError
  *   or AssertionError, KVM_EHIP a HIP runtime failure, KVM_ESPACE a
  *   workspace or capacity that is too small (RuntimeError in the reference,
- *   model/kvm_triton_decode.py:207-211).
+ *   model/kvm_triton_decode.py:207-211), KVM_EABORT a device-side failure
+ *   reported through a status word (RuntimeError in the Python binding).
  *
  * Numeric contract (the reference's Triton path, model/kvm_triton_mixer.py:199-211,
  * evaluated against the eager golden model/kvm_mixer.py with the FP32
@@ -51,12 +53,18 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 3
+#define KVM_ABI_VERSION 4
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
 #define KVM_EHIP (-2)
 #define KVM_ESPACE (-3)
+#define KVM_EABORT (-4) /* the device reported an incomplete result (see status words) */
+
+/* Bits of a device status word (kvm_prefill_desc.status). */
+#define KVM_STATUS_CHAIN_TIMEOUT 1 /* a persistent update chain gave up waiting for its
+                                      row group: state, snapshots and outputs of that
+                                      prefill are incomplete */
 
 /* Static description of one KVM layer (the mixer attributes the forward
  * path reads: model/kvm_mixer.py:79-118, model/rwkv7_backbone.py:319-373).
@@ -138,6 +146,13 @@ typedef struct kvm_prefill_desc {
   void *const *events;           /* optional hipEvent_t[4] recorded on `stream`: before the first
                                     and after the last memory update, before the first and
                                     after the last attention launch (for timing) */
+  int32_t *status;               /* optional device int32 status word.  Set: the call stays
+                                    asynchronous; failure bits (KVM_STATUS_*) are ORed into
+                                    the word on the device and never cleared, so the caller
+                                    zeroes it once and reads it at a point where it
+                                    synchronises anyway.  NULL: the library keeps the word in
+                                    the workspace, waits for `stream` at the end of the call
+                                    and returns KVM_EABORT when a failure bit is set. */
 } kvm_prefill_desc;
 
 /* The mixer's pre-boundary elementwise work on the q/k/v projections, for

@@ -98,6 +98,7 @@ struct PrefillLayout {
   size_t slice_bytes;
   size_t update_bytes;
   size_t snap_elems;  // elements of one snapshot array (keys or values)
+  size_t status_off;  // the status word used when the caller passes none
   size_t total;
 };
 
@@ -113,8 +114,8 @@ PrefillLayout prefill_layout(const kvm_prefill_desc *d) {
                                      size_t(kvm::chain_scratch_bytes(L, L.chunk_len))));
   p.snap_elems = size_t(L.batch * L.kv_heads) * size_t(d->max_state_len) *
                  size_t(L.head_dim);
-  p.total = p.update_bytes +
-            2 * size_t(d->snapshot_ring) * align256(p.snap_elems * 2);
+  p.status_off = p.update_bytes + 2 * size_t(d->snapshot_ring) * align256(p.snap_elems * 2);
+  p.total = p.status_off + 256;
   return p;
 }
 
@@ -407,6 +408,8 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   if (!d->workspace || d->workspace_bytes < int64_t(lay.total))
     return fail(KVM_ESPACE, "prefill workspace of %lld bytes is smaller than %lld",
                 (long long)d->workspace_bytes, (long long)lay.total);
+  if (reinterpret_cast<uintptr_t>(d->status) & 3u)
+    return fail(KVM_EINVAL, "status word must be 4-byte aligned");
 
   hipStream_t s = as_stream(stream);
   auto mark = [&](int i) -> int {
@@ -434,6 +437,13 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   const char *chain_env = getenv("KVM_AMD_CHAIN");
   const bool use_chain = !(chain_env && chain_env[0] == '0') &&
                          kvm::chain_plan(L, C, d->max_state_len, &cp);
+
+  // Status word of the chain: the caller's (sticky, never cleared here), or
+  // one in the workspace, cleared now and checked at the end of the call.
+  const bool own_status = d->status == nullptr;
+  unsigned *status = own_status ? reinterpret_cast<unsigned *>(ws + lay.status_off)
+                                : reinterpret_cast<unsigned *>(d->status);
+  if (own_status && use_chain) KVM_HIP(kvm::launch_fill_u32(status, 1, 0u, s), "status reset");
 
   // Initial state: the first min(T, C) tokens (model/kvm_mixer.py:434-447).
   if ((rc = mark(0)) != KVM_OK) return rc;
@@ -486,7 +496,13 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
     // Batches of consecutive updates, one persistent launch each.  A batch
     // [u, e) writes snapshots u+1..e into ring slots: every chunk reading a
     // snapshot <= e - R is launched first, which needs e <= u + R.
-    const kvm::ChainScratch cs = kvm::carve_chain_scratch(ws, L, C);
+    kvm::ChainScratch cs = kvm::carve_chain_scratch(ws, L, C);
+    cs.status = status;
+    // KVM_AMD_CHAIN_POLLS overrides the poll budget of a group wait (0 makes
+    // every wait give up at once: the error path, with every workgroup
+    // leaving normally).
+    if (const char *polls = getenv("KVM_AMD_CHAIN_POLLS"))
+      cs.max_polls = unsigned(strtoul(polls, nullptr, 10));
     // KVM_AMD_CHAIN_FIXED=0 keeps batches without appends on the token-split kernel.
     const char *fixed_env = getenv("KVM_AMD_CHAIN_FIXED");
     const kvm::SnapRing ring{snap_k, snap_v, snap_stride, R, d->max_state_len};
@@ -554,6 +570,15 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
     KVM_HIP(hipMemcpy2DAsync(d->state.s_v_attn, dpitch, last.v, spitch, row_bytes,
                              rows, hipMemcpyDeviceToDevice, s),
             "final value rows");
+  }
+  if (own_status && use_chain) {
+    unsigned word = 0;
+    KVM_HIP(hipMemcpyAsync(&word, status, sizeof(word), hipMemcpyDeviceToHost, s), "status read");
+    KVM_HIP(hipStreamSynchronize(s), "status read");
+    if (word & KVM_STATUS_CHAIN_TIMEOUT)
+      return fail(KVM_EABORT,
+                  "the persistent update chain timed out waiting for its row group (another "
+                  "workload held compute units); state and outputs of this prefill are incomplete");
   }
   return KVM_OK;
 }

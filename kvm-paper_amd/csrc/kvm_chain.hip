@@ -19,7 +19,17 @@
 // is not kept coherent with other CUs' stores; group-scope sc0 loads still
 // hit it).  No device-wide L2 writeback or invalidation is needed.
 // A group barrier is an L2 atomic counter; every wait is bounded and sets
-// an abort flag (all members then leave) instead of spinning forever.
+// an abort flag (all members then leave) instead of spinning forever.  A
+// member that gives up also ORs KVM_STATUS_CHAIN_TIMEOUT into the caller's
+// sticky status word, which is how the host learns that the state and the
+// snapshots of this launch are incomplete.
+//
+// Co-residency.  A group's members wait for each other, so all of them must
+// run at the same time: the launch has at most one 512-thread workgroup per
+// compute unit (chain_plan), and it relies on the GPU being otherwise idle
+// enough to place all of them.  Work of another stream or process that holds
+// compute units for longer than the poll budget makes the waits time out;
+// the result is then reported, never silently used.
 //
 // Work split of one update of a row:
 //   member m owns tokens [m * tpw, (m + 1) * tpw)  (prep, novelty, append,
@@ -50,7 +60,6 @@ constexpr int kChainThreads = 512;
 constexpr int kChainWaves = kChainThreads / 64;
 constexpr int kChainTok = 64;        // tokens per member at most
 constexpr int kTilesInFlight = 4;    // 16-slot tiles a wave loads at once
-constexpr unsigned kMaxPolls = 1u << 22;
 constexpr int kCounterStride = 32;   // words between group counters (128 B)
 
 // Group barrier, split so that independent work can run between arriving
@@ -73,20 +82,24 @@ __device__ __forceinline__ unsigned l2_scalar_load(const unsigned *p) {
 }
 // wait: until `target` arrivals (G per barrier), polled by wave 0.  False
 // when the wait timed out or another group aborted.
-__device__ __forceinline__ bool group_wait(unsigned *ctr, unsigned target, unsigned *abort_flag,
+__device__ __forceinline__ bool group_wait(unsigned *ctr, unsigned target, const ChainScratch &cs,
                                            int *ok_lds) {
   if (threadIdx.x < 64) {  // wave 0, wave-uniform
     int ok = 0;
-    for (unsigned p = 0; p < kMaxPolls; ++p) {
+    for (unsigned p = 0; p < cs.max_polls; ++p) {
       if (l2_scalar_load(ctr) >= target) {
         ok = 1;
         break;
       }
-      if ((p & 255u) == 255u && l2_scalar_load(abort_flag)) break;
+      if ((p & 255u) == 255u && l2_scalar_load(cs.abort_flag)) break;
       __builtin_amdgcn_s_sleep(1);
     }
     if (threadIdx.x == 0) {
-      if (!ok) __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!ok) {
+        __hip_atomic_store(cs.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(cs.status, unsigned(KVM_STATUS_CHAIN_TIMEOUT), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
       *ok_lds = ok;
     }
   }
@@ -342,7 +355,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
     group_arrive(ctr);
   };
   auto wait = [&]() __attribute__((always_inline)) {
-    return group_wait(ctr, target, cs.abort_flag, &ok_lds);
+    return group_wait(ctr, target, cs, &ok_lds);
   };
   uint16_t *s_k = static_cast<uint16_t *>(st.s_k);
   uint16_t *s_v = static_cast<uint16_t *>(st.s_v);
@@ -725,7 +738,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     group_arrive(ctr);
   };
   auto wait = [&]() __attribute__((always_inline)) {
-    return group_wait(ctr, target, cs.abort_flag, &ok_lds);
+    return group_wait(ctr, target, cs, &ok_lds);
   };
   uint16_t *s_k = static_cast<uint16_t *>(st.s_k);
   uint16_t *s_v = static_cast<uint16_t *>(st.s_v);
@@ -1119,9 +1132,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   }
 }
 
-__global__ __launch_bounds__(256) void k_chain_reset(unsigned *bar, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) bar[i] = 0;
+__global__ __launch_bounds__(256) void k_fill_u32(unsigned *p, int64_t n, unsigned v) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 }  // namespace
@@ -1183,7 +1196,15 @@ ChainScratch carve_chain_scratch(void *base, const kvm_layer &L, int64_t n_tok) 
   c.part = reinterpret_cast<uint2 *>(p + 2 * kb3 + 2 * ib);
   c.bar = reinterpret_cast<unsigned *>(p + 2 * kb3 + 2 * ib + pb);
   c.abort_flag = c.bar + size_t(kChainMaxWorkgroups) * kCounterStride;
+  c.status = nullptr;  // set by the caller
+  c.max_polls = kChainDefaultPolls;
   return c;
+}
+
+hipError_t launch_fill_u32(unsigned *p, int64_t n, unsigned v, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_u32, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, p, n, v);
+  return hipGetLastError();
 }
 
 hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
@@ -1191,9 +1212,8 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
                         const ChainScratch &cs, const ChainPlan &p, int32_t *route_log,
                         int32_t *append_log, hipStream_t stream) {
   if (list.count <= 0) return hipSuccess;
-  const int nb = kChainMaxWorkgroups * kCounterStride + 64;
-  hipLaunchKernelGGL(k_chain_reset, dim3((nb + 255) / 256), dim3(256), 0, stream, cs.bar, nb);
-  hipError_t e = hipGetLastError();
+  // Barrier counters and the abort flag start at zero in every launch.
+  hipError_t e = launch_fill_u32(cs.bar, kChainMaxWorkgroups * kCounterStride + 64, 0u, stream);
   if (e != hipSuccess) return e;
   const int rows = int(L.batch * L.kv_heads);
   const int64_t log_stride = int64_t(rows) * n_tok;

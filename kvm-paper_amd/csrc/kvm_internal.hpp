@@ -107,7 +107,9 @@ struct ChainScratch {
   float *nov;            // novelty of each token [rows, n_tok]
   uint2 *part;           // per-member route maxima (score bits, slot) [2][rows, n_tok, G]
   unsigned *bar;         // group barrier counters
-  unsigned *abort_flag;  // set when a group wait timed out
+  unsigned *abort_flag;  // set when a group wait timed out (cleared per launch)
+  unsigned *status;      // sticky: KVM_STATUS_CHAIN_TIMEOUT is ORed in on a time-out
+  unsigned max_polls;    // L2 polls a group wait makes before giving up
 };
 struct ChainPlan {
   bool fixed;     // slot-owner routing (no appends in the batch)
@@ -128,6 +130,11 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
                         const kvm_state &st, const SnapRing &snaps, const ChainList &list,
                         const ChainScratch &cs, const ChainPlan &p, int32_t *route_log,
                         int32_t *append_log, hipStream_t stream);
+
+// Default poll budget of a group wait (about a second of polling).
+constexpr unsigned kChainDefaultPolls = 1u << 22;
+// Fill n words at p with v (a kernel, so the work may be graph-captured).
+hipError_t launch_fill_u32(unsigned *p, int64_t n, unsigned v, hipStream_t stream);
 
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
                              void *ring_k, void *ring_v, void *ring_gate,

@@ -16,12 +16,14 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KVM_OK = 0
 KVM_EINVAL = -1
 KVM_EHIP = -2
 KVM_ESPACE = -3
+KVM_EABORT = -4
+KVM_STATUS_CHAIN_TIMEOUT = 1
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -75,6 +77,7 @@ class KvmPrefillDesc(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", _i64),
         ("route_log", _vp), ("append_log", _vp),
         ("events", _vp),
+        ("status", _vp),
     ]
 
 

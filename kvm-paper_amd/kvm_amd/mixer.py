@@ -497,9 +497,35 @@ class SequenceMixer(nn.Module):
         if needs_grad:
             raise ValueError("the HIP KVM mixer implements the forward path only; run it under torch.no_grad()")
 
+    def _status_word(self, device) -> torch.Tensor:
+        """This mixer's sticky device status word (int32[1]) on ``device``:
+        the library ORs failure bits into it and never clears it."""
+        words = self.__dict__.setdefault("_status_words", {})
+        key = str(device)
+        if key not in words:
+            words[key] = torch.zeros(1, device=device, dtype=torch.int32)
+        return words[key]
+
+    def check_prefill_status(self, device=None) -> None:
+        """Raise RuntimeError if a prefill on ``device`` (all devices when
+        None) reported a device-side failure since the last check.  Waits for
+        the work already queued, so call it where a synchronisation is
+        acceptable."""
+        for key, word in list(self.__dict__.get("_status_words", {}).items()):
+            if device is not None and key != str(device):
+                continue
+            bits = int(word.item())
+            if bits:
+                word.zero_()
+                if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT:
+                    raise _lib.KvmLibraryError(
+                        "kvm_prefill: the persistent update chain timed out waiting for its row group "
+                        "(another workload held compute units); the prefill's outputs and state are incomplete")
+                raise _lib.KvmLibraryError(f"kvm_prefill: device status word {bits:#x}")
+
     def prefill_raw(self, q, k, v, merge_gate, *, plan: PrefillPlan | None = None, state_capacity: int | None = None,
                     route_log: bool = False, snapshot_budget: int | None = None,
-                    events=None) -> dict:
+                    events=None, check_status: bool | None = True) -> dict:
         """Post-QKV prefill on the HIP library; returns the raw outputs.
 
         q [B,Hq,T,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] bf16 (any strides with a
@@ -510,6 +536,14 @@ class SequenceMixer(nn.Module):
         [n_updates, B*Hkv, C] int32.  ``events``: optional four recorded
         torch.cuda.Event objects bracketing the update chain and the
         attention launches (timing).
+
+        ``check_status``: read the device status word after the call (one
+        synchronisation) and raise RuntimeError if the update chain gave up.
+        Callers that issue many prefills back to back pass False and call
+        ``check_prefill_status()`` once afterwards; the word is sticky.
+        With ``check_status=None`` no status word is passed: the library then
+        waits for the stream itself and reports a failure as its return code
+        (the C ABI's synchronous mode).
         """
         if q.dtype != torch.bfloat16:
             raise ValueError("the HIP KVM mixer computes in bfloat16; got " + str(q.dtype))
@@ -569,8 +603,11 @@ class SequenceMixer(nn.Module):
         if events is not None:
             ev_arr = (ctypes.c_void_p * 4)(*[e.cuda_event if e is not None else None for e in events])
             d.events = ctypes.cast(ev_arr, ctypes.c_void_p)
+        d.status = None if check_status is None else self._status_word(dev).data_ptr()
         _lib.check(lib.kvm_prefill(ctypes.byref(d), _lib.stream_handle(dev)), "kvm_prefill")
         del keep, ws
+        if check_status:
+            self.check_prefill_status(dev)
         res = {"out": out, "plan": plan, "capacity": cap, **st, **logs}
         return res
 

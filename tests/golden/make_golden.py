@@ -68,6 +68,24 @@ CASES = [
         sink=1, rope=32, mode="fixed", min_len=32, n_max=1, factor=1.0, expo=0.5,
         decode_steps=90, temps=True, gate_appends=0, gate_initial=0,
     ),
+    # The saturating budget floor(N t / (N + t)) of the paper's saturate runs
+    # (configs/prolong/120M/kvm_swa_saturate1024_wd.yaml: state_min_len 1,
+    # state_saturation_n): the state grows by a few slots at every update, so
+    # most updates both append and merge; the decode steps cross further
+    # boundaries of the same budget.
+    dict(
+        name="saturation_bf16",
+        dtype="bf16", B=1, Hq=2, Hkv=2, D=64, T=1400, C=64, n_bswa=2,
+        sink=1, rope=32, mode="kvm_saturation", min_len=1, n_max=10, factor=1.0, expo=0.5,
+        sat_n=300, decode_steps=140, temps=True, gate_appends=0, gate_initial=0,
+    ),
+    # The same budget with state_round_down 16, GQA and gated appends / initial state.
+    dict(
+        name="saturation_round16_gqa_bf16",
+        dtype="bf16", B=2, Hq=4, Hkv=2, D=64, T=1000, C=64, n_bswa=2,
+        sink=2, rope=16, mode="kvm_saturation", min_len=1, n_max=8, factor=1.0, expo=0.5,
+        sat_n=500, round_down=16, decode_steps=70, temps=True, gate_appends=1, gate_initial=1,
+    ),
 ]
 
 
@@ -118,8 +136,8 @@ def _config(case):
         rope_partial_dim=case["rope"], sink_len=case["sink"], chunk_len=case["C"],
         n_max_d_chunks=case["n_max"], n_bswa_chunks=case["n_bswa"],
         state_budget_mode=case["mode"], state_growth_factor=case["factor"],
-        state_growth_exponent=case["expo"], state_round_down=1,
-        state_min_len=case["min_len"], state_saturation_n=None,
+        state_growth_exponent=case["expo"], state_round_down=case.get("round_down", 1),
+        state_min_len=case["min_len"], state_saturation_n=case.get("sat_n"),
         kvm_use_merge_gate_keys=1, kvm_use_merge_gate_values=1,
         kvm_apply_merge_gate_to_appends=case["gate_appends"],
         kvm_apply_merge_gate_to_initial_state=case["gate_initial"],
@@ -230,17 +248,29 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
             out["final_" + key] = _as_np(st[key])
         out["final_kvm_state_coverage_len"] = np.array(int(st["kvm_state_coverage_len"]))
         out["final_kvm_bswa_begin"] = np.array(int(st["kvm_bswa_begin"]))
-    # Pair split/merge records into per-update entries.
-    upd = []
-    cur = {}
-    for r in records:
-        if r["kind"] == "split":
-            cur = {"append_idx": r["append_idx"], "merge_idx": r["merge_idx"]}
-        else:
-            cur["route"] = r["route"]
-            cur["state_len_at_merge"] = r["state_len"]
-            upd.append(cur)
-            cur = {}
+    # Per-update entries.  An update that appends starts with a split record
+    # and merges afterwards unless every token was appended (then the
+    # reference skips the merge, kvm_mixer.py:307-308); an update without
+    # appends has only its merge record.  "state_len_at_merge" is the state
+    # length after the update's appends.
+    def per_update(recs):
+        upd = []
+        for r in recs:
+            if r["kind"] == "split":
+                n_merge = int(r["merge_idx"].size(-1))
+                route = torch.zeros(*r["merge_idx"].shape[:-1], 0, dtype=torch.int64)
+                upd.append({"append_idx": r["append_idx"], "merge_idx": r["merge_idx"], "route": route,
+                            "state_len_at_merge": r["state_len"] + r["n_append"], "open": n_merge > 0})
+            elif upd and upd[-1].get("open"):
+                upd[-1]["route"] = r["route"]
+                upd[-1]["open"] = False
+                assert upd[-1]["state_len_at_merge"] == r["state_len"]
+            else:
+                upd.append({"route": r["route"], "state_len_at_merge": r["state_len"]})
+        return upd
+
+    upd = per_update(records)
+    n_prefill_updates = len(per_update(records[:n_prefill_records]))
     for i, u in enumerate(upd):
         out[f"upd{i}_route"] = u["route"].numpy().astype(np.int32)
         out[f"upd{i}_state_len_at_merge"] = np.array(u["state_len_at_merge"])
@@ -249,7 +279,7 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
             out[f"upd{i}_merge_idx"] = u["merge_idx"].numpy().astype(np.int32)
     meta = dict(case)
     meta.update(
-        n_updates=len(upd), n_prefill_updates=sum(1 for r in records[:n_prefill_records] if r["kind"] == "merge"),
+        n_updates=len(upd), n_prefill_updates=n_prefill_updates,
         torch_version=torch.__version__, prefill_seconds=prefill_s,
         reference="SmerkyG/KVM-paper eager model.kvm_fp32_routing_reference.SequenceMixer",
     )
@@ -258,9 +288,13 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
 
 
 def main():
+    """Write every case, or only the cases named on the command line."""
     eager, fp32ref, StatesDictCache = _import_reference()
     torch.manual_seed(0)
+    wanted = set(sys.argv[1:])
     for case in CASES:
+        if wanted and case["name"] not in wanted:
+            continue
         data = _run_case(case, eager, fp32ref, StatesDictCache)
         path = HERE / f"{case['name']}.npz"
         np.savez_compressed(path, **data)

@@ -15,6 +15,16 @@ def names():
     return sorted(p.stem for p in GOLDEN.glob("*.npz"))
 
 
+def decode_names():
+    """Fixtures that also hold cached single-token decode steps."""
+    return [n for n in names() if meta(n).get("decode_steps", 0) > 0]
+
+
+def meta(name: str) -> dict:
+    z = np.load(GOLDEN / f"{name}.npz", allow_pickle=False)
+    return json.loads(str(z["meta_json"]))
+
+
 def _tensor(arr: np.ndarray, dtype: str) -> torch.Tensor:
     t = torch.from_numpy(np.array(arr))
     if dtype == "bf16" and t.dtype == torch.int16:
@@ -44,7 +54,8 @@ def oracle_setup(fx: dict):
         chunk_len=m["C"], n_bswa_chunks=m["n_bswa"], n_max_d_chunks=m["n_max"],
         sink_len=m["sink"], rope_partial_dim=m["rope"] if m["rope"] > 0 else m["D"],
         state_budget_mode=m["mode"], state_growth_factor=m["factor"],
-        state_growth_exponent=m["expo"], state_round_down=1, state_min_len=m["min_len"],
+        state_growth_exponent=m["expo"], state_round_down=m.get("round_down", 1), state_min_len=m["min_len"],
+        state_saturation_n=m.get("sat_n"),
         gate_appends=bool(m["gate_appends"]), gate_initial=bool(m["gate_initial"]),
         use_head_temps=bool(m["temps"]),
     )

@@ -19,7 +19,7 @@ def gpu_available() -> bool:
 
 def mixer_config(Hq, Hkv, D, C, n_bswa=2, sink=1, rope=32, mode="fixed", min_len=-1, n_max=1,
                  factor=1.0, expo=0.5, sat_n=None, temps=True, gate_appends=0, gate_initial=0,
-                 gate_keys=1, gate_values=1):
+                 gate_keys=1, gate_values=1, round_down=1):
     """Config namespace with every attribute the KVM mixer reads."""
     return SimpleNamespace(
         num_attention_heads=Hq, num_key_value_heads=Hkv, hidden_size=Hq * D, d_qk_head=D, d_v_head=D,
@@ -27,7 +27,7 @@ def mixer_config(Hq, Hkv, D, C, n_bswa=2, sink=1, rope=32, mode="fixed", min_len
         kvm_value_residual_mode="rwkv", kvm_token_shift_mode="rwkv", rope_partial_dim=rope,
         sink_len=sink, chunk_len=C, n_max_d_chunks=n_max, n_bswa_chunks=n_bswa,
         state_budget_mode=mode, state_growth_factor=factor, state_growth_exponent=expo,
-        state_round_down=1, state_min_len=min_len, state_saturation_n=sat_n,
+        state_round_down=round_down, state_min_len=min_len, state_saturation_n=sat_n,
         kvm_use_merge_gate_keys=gate_keys, kvm_use_merge_gate_values=gate_values,
         kvm_apply_merge_gate_to_appends=gate_appends, kvm_apply_merge_gate_to_initial_state=gate_initial,
         kvm_use_head_temps=int(temps), kvm_use_vlens=1, kvm_aotriton_forward_attention=0,
@@ -40,6 +40,7 @@ def fixture_config(meta):
         rope=meta["rope"], mode=meta["mode"], min_len=meta["min_len"], n_max=meta["n_max"],
         factor=meta["factor"], expo=meta["expo"], temps=meta["temps"],
         gate_appends=meta["gate_appends"], gate_initial=meta["gate_initial"],
+        sat_n=meta.get("sat_n"), round_down=meta.get("round_down", 1),
     )
 
 

@@ -1,0 +1,64 @@
+"""The persistent update chain's failure path, forced from the host.
+
+KVM_AMD_CHAIN_POLLS=0 gives every group wait of the chain a poll budget of
+zero: each member gives up at its first barrier, before reading anything
+another member wrote, and leaves normally.  The prefill must then report the
+failure (RuntimeError from the Python class, KVM_EABORT from the C ABI in its
+synchronous mode) instead of returning the incomplete state, and a later
+prefill with the normal budget must be correct again.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import kvm_testlib as T
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, Hq, Hkv, D, Tn, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, Hq, Tn, D, generator=gen) / math.sqrt(D)).bfloat16().cuda()
+    k = (torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16().cuda()
+    v = (torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16().cuda()
+    g = (1 + torch.nn.functional.elu(torch.randn(B, Hkv, Tn, 1, generator=gen))).bfloat16().cuda()
+    return q, k, v, g
+
+
+@pytest.mark.parametrize("mode", ["fixed", "power_law"])
+def test_chain_timeout_is_reported(monkeypatch, mode):
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd import _lib
+
+    B, Hq, Hkv, D, C, Tn = 1, 4, 2, 128, 64, 64 * 10
+    cfg = T.mixer_config(Hq, Hkv, D, C, rope=32, mode=mode, min_len=C, n_max=4, factor=4.0, expo=0.5)
+    mixer = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = _inputs(B, Hq, Hkv, D, Tn)
+    T.log(f"[status] {mode}: reference prefill B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn}")
+    with torch.no_grad():
+        good = mixer.prefill_raw(q, k, v, g)
+        assert good["plan"].n_updates >= 2
+        ref_out = good["out"].clone()
+        monkeypatch.setenv("KVM_AMD_CHAIN_POLLS", "0")
+        T.log(f"[status] {mode}: prefill with a zero poll budget (every member leaves at its first wait)")
+        with pytest.raises(RuntimeError, match="timed out"):
+            mixer.prefill_raw(q, k, v, g)
+        # The C ABI without a status word waits itself and returns KVM_EABORT.
+        with pytest.raises(_lib.KvmLibraryError, match="timed out"):
+            mixer.prefill_raw(q, k, v, g, check_status=None)
+        # Deferred checking: the word is sticky across calls.
+        mixer.prefill_raw(q, k, v, g, check_status=False)
+        mixer.prefill_raw(q, k, v, g, check_status=False)
+        with pytest.raises(RuntimeError, match="timed out"):
+            mixer.check_prefill_status()
+        monkeypatch.delenv("KVM_AMD_CHAIN_POLLS")
+        T.log(f"[status] {mode}: prefill with the normal poll budget after the failures")
+        again = mixer.prefill_raw(q, k, v, g)
+        torch.cuda.synchronize()
+    assert torch.equal(again["out"], ref_out), "a prefill after a reported failure must be exact again"
+    mixer.check_prefill_status()  # clear

@@ -53,6 +53,37 @@ def test_struct_layout_matches_binding():
     assert lib.kvm_struct_size(9) == -1
 
 
+def test_header_abi_version_matches_binding():
+    from kvm_amd import _lib as L
+
+    m = re.search(r"#define KVM_ABI_VERSION (\d+)", HEADER.read_text())
+    assert m and int(m.group(1)) == L.ABI_VERSION
+    for name in ("KVM_EABORT", "KVM_STATUS_CHAIN_TIMEOUT"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", HEADER.read_text())
+        assert m and int(m.group(1)) == getattr(L, name)
+
+
+def test_integration_stub_binds_the_library(monkeypatch):
+    """The ctypes stub printed in INTEGRATION.md section 3 runs against the
+    built library: its ABI assert, struct-size asserts and argument list."""
+    _lib()
+    from kvm_amd import _lib as L
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    sec = text[text.index("## 3. Binding the C ABI directly"):]
+    block = sec[sec.index("```python") + len("```python"):]
+    block = block[:block.index("```")]
+    monkeypatch.setenv("LIBKVM_AMD", str(L.LIB_PATH))
+    ns: dict = {}
+    exec(compile(block, "INTEGRATION.md:stub", "exec"), ns)
+    lib = ns["lib"]
+    assert ns["KVM_ABI_VERSION"] == L.ABI_VERSION
+    assert ctypes.sizeof(ns["KvmLayer"]) == ctypes.sizeof(L.KvmLayer)
+    assert ctypes.sizeof(ns["KvmState"]) == ctypes.sizeof(L.KvmState)
+    assert len(lib.kvm_decode_attention.argtypes) == len(L.SIGNATURES["kvm_decode_attention"][1])
+    assert callable(ns["kvm_decode_attention"])
+
+
 def _layer(**kw):
     from kvm_amd import _lib as L
 

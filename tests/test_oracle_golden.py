@@ -20,6 +20,13 @@ def _exact(fx):
     return fx["meta"]["torch_version"] == torch.__version__
 
 
+def _route(u):
+    """Slot per merged token; an update that appended every token has none."""
+    if u.route is None:
+        return torch.zeros(*u.merge_idx.shape[:-1], 0, dtype=torch.int32)
+    return u.route.to(torch.int32)
+
+
 def _cmp(a, b, exact, atol=2e-2):
     if exact:
         assert torch.equal(a, b), f"max diff {(a.float() - b.float()).abs().max()}"
@@ -42,7 +49,7 @@ def test_prefill_matches_reference(name):
     n_pre = m["n_prefill_updates"]
     assert len(rec.updates) == n_pre
     for i, u in enumerate(rec.updates):
-        assert torch.equal(u.route.to(torch.int32), fx[f"upd{i}_route"]), f"update {i} routes differ"
+        assert torch.equal(_route(u), fx[f"upd{i}_route"]), f"update {i} routes differ"
         if f"upd{i}_append_idx" in fx:
             assert torch.equal(u.append_idx.to(torch.int32), fx[f"upd{i}_append_idx"])
             assert torch.equal(u.merge_idx.to(torch.int32), fx[f"upd{i}_merge_idx"])
@@ -50,7 +57,43 @@ def test_prefill_matches_reference(name):
             assert u.n_append == 0
 
 
-@pytest.mark.parametrize("name", [n for n in golden_io.names() if n.startswith("decode")])
+@pytest.mark.parametrize("name", golden_io.names())
+def test_schedules_match_reference_state_lengths(name):
+    """The state length after every update that the reference ran (recorded
+    when it merged, prefill and decode updates alike) equals the oracle's
+    schedule and the product's plan: this pins every budget branch (fixed,
+    power law, saturation, round-down) to the reference's own arithmetic."""
+    from kvm_amd.schedule import StateBudget, prefill_plan
+
+    fx = golden_io.load(name)
+    m = fx["meta"]
+    cfg, _ = golden_io.oracle_setup(fx)
+    T, C, n = m["T"], m["C"], m["n_bswa"]
+    ref_after = [int(fx[f"upd{i}_state_len_at_merge"]) for i in range(m["n_updates"])]
+    sched = O.prefill_schedule(cfg, T)
+    assert [u[4] for u in sched["updates"]] == ref_after[:m["n_prefill_updates"]]
+    budget = StateBudget(cfg.state_budget_mode, cfg.state_growth_factor, cfg.state_growth_exponent,
+                         cfg.state_round_down, cfg.state_min_len, cfg.state_saturation_n, cfg.max_state_len)
+    plan = prefill_plan(T, C, n, budget)
+    assert [b + a for b, a in zip(plan.upd_state_before, plan.upd_n_append)] == ref_after[:m["n_prefill_updates"]]
+    # Decode-time updates: one per chunk boundary the window crosses, each
+    # with ctx = n*C + coverage and available = coverage + C (model/kvm_mixer.py:645-669).
+    cur, cov = sched["final_state_len"], sched["final_coverage"]
+    got = []
+    for s in range(m.get("decode_steps", 0)):
+        total = T + s + 1
+        direct = min(total, C)
+        if direct > cov:
+            cur, cov = cur + 1, direct
+        new_cov = max(direct, O.bswa_begin_for_total_len(total, C, n))
+        if new_cov > cov:
+            cur = budget.desired(n * C + cov, cov + C, cur)
+            got.append(cur)
+            cov = new_cov
+    assert got == ref_after[m["n_prefill_updates"]:]
+
+
+@pytest.mark.parametrize("name", golden_io.decode_names())
 def test_decode_matches_reference(name):
     fx = golden_io.load(name)
     m = fx["meta"]
@@ -72,4 +115,4 @@ def test_decode_matches_reference(name):
     assert st[O.BSWA_BEGIN] == int(fx["final_kvm_bswa_begin"])
     assert len(rec.updates) == m["n_updates"]
     for i, u in enumerate(rec.updates):
-        assert torch.equal(u.route.to(torch.int32), fx[f"upd{i}_route"]), f"update {i} routes differ"
+        assert torch.equal(_route(u), fx[f"upd{i}_route"]), f"update {i} routes differ"

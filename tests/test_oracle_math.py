@@ -24,6 +24,70 @@ def _params(D, Hq, seed=0):
     )
 
 
+# Hand-computed state budgets (model/kvm_mixer.py:131-165): budget, ctx_len,
+# available, current -> state length.  Saturation values are
+# floor(N t / (N + t)) worked out by hand: 1024*1024/2048 = 512 exactly;
+# 1024*3072/4096 = 768 exactly; 1024*1023/2047 = 511.75 -> 511 (a formula
+# that rounds instead of flooring gives 512); 300*192/492 = 117.07 -> 117;
+# 500*1000/1500 = 333.3 -> 333, rounded down to 16 -> 320; 1024*1e6/(1e6+1024)
+# = 1022.95 -> 1022.  Power law: floor(16 * sqrt(4096)) = 1024; floor(5 *
+# sqrt(1000)) = floor(158.11) = 158; floor(1 * sqrt(65535)) = 255 (sqrt is
+# 255.998).
+BUDGET_TABLE = [
+    # (mode, factor, exponent, round_down, min_len, saturation_n, max_state_len)
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 1024, 10**6), 1024, 10**6, 0, 512),
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 1024, 10**6), 3072, 10**6, 0, 768),
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 1024, 10**6), 1023, 10**6, 0, 511),
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 1024, 10**6), 1, 10**6, 0, 1),          # floor 0, raised to min_len 1
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 300, 640), 192, 128, 64, 117),
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 300, 640), 192, 100, 64, 100),         # capped by the available context
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 300, 640), 192, 1000, 130, 130),       # never below the current length
+    (("kvm_saturation", 1.0, 0.5, 16, 1, 500, 512), 1000, 10**6, 0, 320),
+    (("kvm_saturation", 1.0, 0.5, 16, 1, 500, 256), 1000, 10**6, 0, 256),      # capped by max_state_len
+    (("kvm_saturation", 1.0, 0.5, 1, 1, 1024, 10**7), 10**6, 10**7, 0, 1022),
+    (("power_law", 16.0, 0.5, 1, -1, None, 1024), 4096, 10**6, 0, 1024),
+    (("power_law", 5.0, 0.5, 1, 64, None, 192), 1000, 10**6, 0, 158),
+    (("power_law", 5.0, 0.5, 32, 64, None, 192), 1000, 10**6, 0, 128),
+    (("power_law", 1.0, 0.5, 1, -1, None, 1024), 65535, 10**6, 0, 255),
+    (("power_law", 1.0, 0.5, 1, 300, None, 1024), 65535, 10**6, 0, 300),       # min_len floor
+    (("fixed", 1.0, 0.5, 1, 256, None, 512), 32768, 10**6, 512, 512),          # current 512 > floor 256
+    (("fixed", 1.0, 0.5, 1, 64, None, 256), 4096, 10**6, 0, 64),
+]
+
+
+@pytest.mark.parametrize("budget,ctx,avail,cur,want", BUDGET_TABLE)
+def test_state_budget_closed_forms(budget, ctx, avail, cur, want):
+    from kvm_amd.schedule import StateBudget
+
+    mode, f, e, rd, mn, sat, mx = budget
+    assert StateBudget(mode, f, e, rd, mn, sat, mx).desired(ctx, avail, cur) == want
+    C = 64
+    cfg = O.OracleConfig(q_heads=1, kv_heads=1, head_dim=64, value_dim=64, chunk_len=C, n_max_d_chunks=1,
+                         state_budget_mode=mode, state_growth_factor=f, state_growth_exponent=e,
+                         state_round_down=rd, state_min_len=mn, state_saturation_n=sat)
+    cfg_max = type(cfg).max_state_len
+    try:
+        type(cfg).max_state_len = property(lambda self: mx)
+        assert O.desired_state_len(cfg, ctx, avail, cur) == want
+    finally:
+        type(cfg).max_state_len = cfg_max
+
+
+def test_saturation_budget_properties():
+    """floor(N t / (N + t)) rises with t, stays below N and below t, and
+    reaches N - 1 only for t > N (N - 1) (brute force over t)."""
+    from kvm_amd.schedule import StateBudget
+
+    N = 97
+    b = StateBudget("kvm_saturation", 1.0, 0.5, 1, 0, N, 10**9)
+    prev = 0
+    for t in range(0, 20000):
+        s = b.desired(t, 10**9, 0)
+        assert prev <= s < N and s <= t
+        assert (s == N - 1) == (N * t >= (N - 1) * (N + t))
+        prev = s
+
+
 def test_prep_k_is_layernorm_of_rope_zeroed_key():
     D, r = 64, 24
     p = _params(D, 1)
