@@ -286,6 +286,27 @@ int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
                          int64_t o_sb, int64_t o_sh, void *workspace,
                          int64_t workspace_bytes, void *stream);
 
+/* Size of the library-owned scratch of kvm_decode_attention_noalloc, per GPU. */
+#define KVM_DECODE_SCRATCH_BYTES (16 << 20)
+
+/* kvm_decode_attention without a workspace argument: the split-K partials go
+ * to a scratch array the library holds on each GPU (KVM_DECODE_SCRATCH_BYTES,
+ * kept until the process ends), so the call performs no device allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  The scratch must hold B * q_heads * ceil((active_state_len +
+ * recent_len) / 256) * (head_dim + 2) * 4 bytes (kvm_decode_workspace_bytes);
+ * larger calls return KVM_ESPACE.  All calls on one GPU share its array and
+ * keep no state in it between calls, so calls that overlap on one GPU (two
+ * streams, two threads) race.  Arguments and results are those of
+ * kvm_decode_attention. */
+int kvm_decode_attention_noalloc(const kvm_layer *layer, const void *q, int64_t q_sb,
+                                 int64_t q_sh, const kvm_state *st,
+                                 int64_t active_state_len, const void *ring_k,
+                                 const void *ring_v, int64_t ring_cap,
+                                 int64_t ring_start, int64_t recent_len, void *out,
+                                 int64_t o_sb, int64_t o_sh, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -312,6 +312,26 @@ int kvm_ring_write(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
   return KVM_OK;
 }
 
+int kvm_decode_attention_noalloc(const kvm_layer *layer, const void *q, int64_t q_sb,
+                                 int64_t q_sh, const kvm_state *st,
+                                 int64_t active_state_len, const void *ring_k,
+                                 const void *ring_v, int64_t ring_cap,
+                                 int64_t ring_start, int64_t recent_len, void *out,
+                                 int64_t o_sb, int64_t o_sh, void *stream) {
+  if (check_layer(layer) != KVM_OK) return KVM_EINVAL;
+  const int64_t need = kvm::decode_workspace_bytes(*layer, active_state_len + recent_len);
+  if (need > int64_t(KVM_DECODE_SCRATCH_BYTES))
+    return fail(KVM_ESPACE,
+                "decode needs %lld bytes of scratch; the allocation-free entry point holds %lld "
+                "(use kvm_decode_attention with a workspace)",
+                (long long)need, (long long)KVM_DECODE_SCRATCH_BYTES);
+  void *scratch = nullptr;
+  KVM_HIP(kvm::decode_scratch(&scratch), "decode scratch address");
+  return kvm_decode_attention(layer, q, q_sb, q_sh, st, active_state_len, ring_k, ring_v,
+                              ring_cap, ring_start, recent_len, out, o_sb, o_sh, scratch,
+                              int64_t(KVM_DECODE_SCRATCH_BYTES), stream);
+}
+
 int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
                          int64_t q_sh, const kvm_state *st,
                          int64_t active_state_len, const void *ring_k,

@@ -15,6 +15,8 @@
 // fp32; the 4 waves merge (max, sum, acc) through LDS, and a second kernel
 // merges the segments in a fixed order (deterministic split-K).
 
+#include <mutex>
+
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
 
@@ -253,6 +255,38 @@ int64_t decode_segments(int64_t rows_total) {
 int64_t decode_workspace_bytes(const kvm_layer &L, int64_t max_rows) {
   const int64_t nseg = decode_segments(max_rows < 1 ? 1 : max_rows);
   return L.batch * L.q_heads * nseg * (L.head_dim + 2) * 4;
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned scratch of the allocation-free decode entry point
+// (kvm_decode_attention_noalloc): the split-K partials live in this
+// file-scope device array instead of a caller workspace.  Each GPU holds its
+// own copy at its own address, resolved once per device with
+// hipGetSymbolAddress; host code uses only that address, never the array's
+// name.  Every call on a device shares the array, so calls that overlap on
+// one device race.  The partial kernel writes every (query head, segment)
+// entry the combine kernel reads, so nothing needs clearing between calls.
+namespace {
+constexpr int kMaxScratchDevices = 64;
+__device__ __align__(256) unsigned char scratch[KVM_DECODE_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+hipError_t decode_scratch(void **ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,

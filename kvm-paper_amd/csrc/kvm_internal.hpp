@@ -141,6 +141,9 @@ hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
                              int64_t ring_cap, int64_t pos, hipStream_t stream);
 
 int64_t decode_segments(int64_t rows_total);
+// Address of this device's library-owned decode scratch
+// (KVM_DECODE_SCRATCH_BYTES, resolved once per device).
+hipError_t decode_scratch(void **ptr);
 int64_t decode_workspace_bytes(const kvm_layer &L, int64_t max_rows);
 hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
                          int64_t q_sh, const kvm_state &st, int64_t active,

@@ -115,7 +115,11 @@ SIGNATURES = {
     "kvm_decode_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),
     "kvm_decode_attention": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _i64, _vp, _vp,
                                             _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "kvm_decode_attention_noalloc": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _i64, _vp,
+                                                    _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp]),
 }
+# Library-owned scratch of kvm_decode_attention_noalloc per GPU (include/kvm_amd.h).
+KVM_DECODE_SCRATCH_BYTES = 16 << 20
 
 _LIB = None
 
