@@ -140,6 +140,44 @@ def bench_prefill(args, torch, kvm_amd):
     )
 
 
+def bench_backward(args, torch, kvm_amd, pf):
+    """Config 2 training step of the KVM layer at the post-QKV boundary: the
+    differentiable prefill (routes fixed by the forward) and its backward.
+    Reports the whole step and the HIP attention backward alone."""
+    from kvm_amd import training
+
+    mixer = pf["mixer"]
+    q, k, v, g = (x.detach().requires_grad_(True) for x in pf["inputs"])
+    B, H, T, D = q.shape
+    dout = (torch.randn(B, T, H, D, device=q.device) * 0.05).bfloat16()
+    for p in mixer.parameters():
+        p.requires_grad_(True)
+
+    def step():
+        y = training.prefill_with_grad(mixer, q, k, v, g)
+        y.backward(dout)
+
+    step()
+    torch.cuda.synchronize()
+    steps = max(1, min(args.steps, 3))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    with torch.no_grad():
+        res = mixer.prefill_raw(q, k, v, g, route_log=True, keep_snapshots=True, want_lse=True)
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        for _ in range(steps):
+            training.attention_backward(mixer, q, k, v, g, res, dout)
+        a1.record()
+        torch.cuda.synchronize()
+    return dict(step_ms=step_ms, attn_bwd_ms=a0.elapsed_time(a1) / steps, steps=steps)
+
+
 def bench_decode(args, torch, kvm_amd):
     B, H, D, C, n = 64, 32, 128, 256, 2
     S, total = 1024, 131072
@@ -327,9 +365,10 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--skip-e2e", action="store_true")
+    ap.add_argument("--skip-backward", action="store_true")
     ap.add_argument("--e2e-decode", type=int, default=512,
                     help="greedy decode steps of the config-5 decoder run (default 512)")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e", "backward"], default=None,
                     help="run one workload (profiling); 'copy' streams a known number of bytes "
                          "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -363,8 +402,17 @@ def main():
     if args.only == "prefill":
         print(json.dumps({"ms": pf["ms"], "attention_ms": pf["attn_ms"], "chain_ms": pf["chain_ms"]}))
         return
+    if args.only == "backward":
+        print(json.dumps(bench_backward(args, torch, kvm_amd, pf)))
+        return
     print(f"bench: prefill {pf['ms']:.3f} ms/step (attention {pf['attn_ms']:.3f} ms, updates {pf['chain_ms']:.3f} ms)",
           file=sys.stderr, flush=True)
+    bwd = None
+    if not args.skip_backward:
+        print("bench: config 2 training step (differentiable prefill + backward) ...", file=sys.stderr, flush=True)
+        bwd = bench_backward(args, torch, kvm_amd, pf)
+        print(f"bench: training step {bwd['step_ms']:.2f} ms (HIP attention backward {bwd['attn_bwd_ms']:.2f} ms)",
+              file=sys.stderr, flush=True)
     dec = None
     if not args.skip_decode:
         print("bench: decode config 4 ...", file=sys.stderr, flush=True)
@@ -421,6 +469,14 @@ def main():
                          "achieved": round(bw / 1e9, 1), "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s",
                          "frac": round(bw / PEAK_HBM_BYTES, 4),
                          "traffic": measured_traffic("k_decode_partial", "config4")},
+        }
+    if bwd is not None:
+        line["backward"] = {
+            "workload": "config 2 training step of the KVM layer at the post-QKV boundary: differentiable "
+                        "prefill (routes fixed by the forward) + backward of q, k, v, gate, ln_s_k and the "
+                        "head temperatures",
+            "step_ms": round(bwd["step_ms"], 3), "attention_backward_ms": round(bwd["attn_bwd_ms"], 3),
+            "tokens_per_s": round(32768 / (bwd["step_ms"] * 1e-3), 1),
         }
     if e2e is not None:
         line["decoder_e2e"] = {

@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 4
+#define KVM_ABI_VERSION 5
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -153,7 +153,55 @@ typedef struct kvm_prefill_desc {
                                     synchronises anyway.  NULL: the library keeps the word in
                                     the workspace, waits for `stream` at the end of the call
                                     and returns KVM_EABORT when a failure bit is set. */
+  float *lse;                    /* optional fp32 [B, Hq, T] (contiguous): log2-domain
+                                    log-sum-exp of every query's scaled scores,
+                                    log2(sum_j exp2(s_j)) with s = (q.k) * tau * log2(e) / sqrt(D);
+                                    the backward recomputes the probabilities from it */
+  void *snap_k;                  /* optional caller-held snapshots of the memory rows every query
+                                    chunk attends to: bf16 [n_updates + 1, rows, max_state_len,
+                                    head_dim] keys (LayerNorm_s(s_k)) and values; when set, they
+                                    replace the workspace's snapshot ring (snapshot_ring must be
+                                    n_updates + 1) and keep every snapshot for the backward */
+  void *snap_v;
 } kvm_prefill_desc;
+
+/* One prefill's attention backward (the gradient of
+ * model/kernels/kvm_triton_training_kernels.py:1803-1948; the reference's
+ * _kvm_attn_live_state_dq_kernel :1950-2090, _live_state_dkdv_to_raw_grad_kernel
+ * :2093-2305 and _kvm_attn_snapshot_bswa_dkdv_kernel :668-830), with the
+ * memory snapshots held fixed: gradients w.r.t. the queries, the window keys
+ * and values, every snapshot's key and value rows, and the two head
+ * temperatures.  The chain rule from the snapshot rows back to the tokens
+ * (LayerNorm_s, the value normalisation, the merge sums under the forward's
+ * routes) is the caller's. */
+typedef struct kvm_prefill_bwd_desc {
+  kvm_layer layer;
+  const void *q;                 /* bf16 [B, Hq, T, head_dim], strides as in kvm_prefill_desc */
+  int64_t q_sb, q_sh, q_st;
+  kvm_seq kv;                    /* window keys and values of the prompt (gate unused) */
+  int64_t seq_len;
+  const void *dout;              /* bf16 dL/d(out), out's layout: dout + b*do_sb + t*do_st + hq*do_sh */
+  int64_t do_sb, do_st, do_sh;
+  const float *lse;              /* fp32 [B, Hq, T] from the forward */
+  const float *delta;            /* fp32 [B, Hq, T]: sum over features of dout * out */
+  const void *snap_k, *snap_v;   /* bf16 [n_snap, rows, max_state_len, head_dim] from the forward */
+  int64_t max_state_len;
+  int64_t n_chunks;
+  const int32_t *chunk_state_len;/* host [n_chunks], as in kvm_prefill_desc */
+  const int32_t *chunk_snapshot; /* host [n_chunks] */
+  void *dq;                      /* bf16 out [B, Hq, T, head_dim] at dq + b*dq_sb + h*dq_sh + t*dq_st */
+  int64_t dq_sb, dq_sh, dq_st;
+  float *dk, *dv;                /* fp32 out [B, Hkv, T, head_dim] contiguous: window keys / values */
+  float *d_snap_k, *d_snap_v;    /* fp32 out [n_snap, rows, max_state_len, head_dim]: rows no
+                                    query chunk reads are zero */
+  float *d_state_temp;           /* fp32 out [q_heads] (summed over the batch) */
+  float *d_front_temp;           /* fp32 out [q_heads] */
+  void *workspace;               /* kvm_prefill_backward_workspace_bytes() */
+  int64_t workspace_bytes;
+} kvm_prefill_bwd_desc;
+
+int64_t kvm_prefill_backward_workspace_bytes(const kvm_prefill_bwd_desc *d);
+int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream);
 
 /* The mixer's pre-boundary elementwise work on the q/k/v projections, for
  * one layer (model/value_residual_mixin.py:173-237 calc_qkv and
@@ -210,7 +258,8 @@ int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
 
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
-int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc */
+int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc,
+                                        5 prefill_bwd_desc */
 const char *kvm_last_error(void);
 
 /* Workspace of kvm_prefill for the given descriptor (snapshot_ring and

@@ -114,7 +114,9 @@ PrefillLayout prefill_layout(const kvm_prefill_desc *d) {
                                      size_t(kvm::chain_scratch_bytes(L, L.chunk_len))));
   p.snap_elems = size_t(L.batch * L.kv_heads) * size_t(d->max_state_len) *
                  size_t(L.head_dim);
-  p.status_off = p.update_bytes + 2 * size_t(d->snapshot_ring) * align256(p.snap_elems * 2);
+  // Caller-held snapshots (d->snap_k / snap_v) replace the workspace ring.
+  const size_t ring = d->snap_k ? 0 : size_t(d->snapshot_ring);
+  p.status_off = p.update_bytes + 2 * ring * align256(p.snap_elems * 2);
   p.total = p.status_off + 256;
   return p;
 }
@@ -132,6 +134,7 @@ int64_t kvm_struct_size(int which) {
     case 2: return sizeof(kvm_state);
     case 3: return sizeof(kvm_prefill_desc);
     case 4: return sizeof(kvm_prefix_desc);
+    case 5: return sizeof(kvm_prefill_bwd_desc);
     default: return -1;
   }
 }
@@ -312,6 +315,89 @@ int kvm_ring_write(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
   return KVM_OK;
 }
 
+int64_t kvm_prefill_backward_workspace_bytes(const kvm_prefill_bwd_desc *d) {
+  if (!d || check_layer(&d->layer) != KVM_OK || d->n_chunks < 1) return -1;
+  return kvm::attn_bwd_workspace_bytes(d->layer, d->n_chunks);
+}
+
+int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream) {
+  if (!d) return fail(KVM_EINVAL, "backward descriptor is NULL");
+  int rc;
+  const kvm_layer &L = d->layer;
+  if ((rc = check_layer(&L)) || (rc = check_seq(&d->kv, "kv"))) return rc;
+  const int64_t T = d->seq_len, C = L.chunk_len, n = L.n_bswa_chunks;
+  if (T < 1) return fail(KVM_EINVAL, "seq_len must be positive");
+  const int64_t n_chunks = (T + C - 1) / C;
+  if (d->n_chunks != n_chunks)
+    return fail(KVM_EINVAL, "n_chunks %lld != ceil(T / C) = %lld", (long long)d->n_chunks,
+                (long long)n_chunks);
+  if (n_chunks > kvm::kMaxChunksPerLaunch)
+    return fail(KVM_EINVAL, "the backward handles at most %d query chunks", kvm::kMaxChunksPerLaunch);
+  const void *need[] = {d->q, d->dout, d->lse, d->delta, d->dq, d->dk, d->dv, d->d_state_temp,
+                        d->d_front_temp, d->chunk_state_len, d->chunk_snapshot};
+  for (const void *p : need)
+    if (!p) return fail(KVM_EINVAL, "backward: a required pointer is NULL");
+  if (!aligned16(d->q) || !aligned16(d->dout) || d->q_sb % 8 || d->q_sh % 8 || d->q_st % 8 ||
+      d->do_sb % 8 || d->do_sh % 8 || d->do_st % 8)
+    return fail(KVM_EINVAL, "q and dout must be 16-byte aligned with strides multiple of 8");
+  const bool has_state = n_chunks > n;
+  if (has_state && (!d->snap_k || !d->snap_v || !d->d_snap_k || !d->d_snap_v ||
+                    !aligned16(d->snap_k) || !aligned16(d->snap_v)))
+    return fail(KVM_EINVAL, "backward: snapshot arrays (and their gradients) must be set and aligned");
+  if (d->max_state_len < 1) return fail(KVM_EINVAL, "max_state_len must be positive");
+  kvm::ChunkTable table;
+  int64_t n_snap = 0;
+  for (int64_t m = 0; m < n_chunks; ++m) {
+    const int32_t s = d->chunk_state_len[m], snap = d->chunk_snapshot[m];
+    if (m < n) {
+      table.state_len[m] = 0;
+      table.snap_slot[m] = 0;
+      continue;
+    }
+    if (snap < 0 || s < 1 || s > d->max_state_len)
+      return fail(KVM_EINVAL, "chunk %lld schedule (state %d, snapshot %d) is invalid", (long long)m, s, snap);
+    table.state_len[m] = s;
+    table.snap_slot[m] = snap;
+    n_snap = std::max<int64_t>(n_snap, int64_t(snap) + 1);
+  }
+  const int64_t need_ws = kvm::attn_bwd_workspace_bytes(L, n_chunks);
+  if (!d->workspace || d->workspace_bytes < need_ws)
+    return fail(KVM_ESPACE, "backward workspace of %lld bytes is smaller than %lld",
+                (long long)d->workspace_bytes, (long long)need_ws);
+  kvm::BwdArgs a;
+  a.q = d->q;
+  a.q_sb = d->q_sb; a.q_sh = d->q_sh; a.q_st = d->q_st;
+  a.kv = d->kv;
+  a.T = T;
+  a.dout = d->dout;
+  a.do_sb = d->do_sb; a.do_st = d->do_st; a.do_sh = d->do_sh;
+  a.lse = d->lse;
+  a.delta = d->delta;
+  a.snap_k = static_cast<const uint16_t *>(d->snap_k);
+  a.snap_v = static_cast<const uint16_t *>(d->snap_v);
+  const int64_t rows = L.batch * L.kv_heads;
+  a.snap_stride = rows * d->max_state_len * L.head_dim;
+  a.snap_cap = d->max_state_len;
+  a.n_chunks = n_chunks;
+  a.dq = d->dq;
+  a.dq_sb = d->dq_sb; a.dq_sh = d->dq_sh; a.dq_st = d->dq_st;
+  a.dk = d->dk;
+  a.dv = d->dv;
+  a.d_snap_k = d->d_snap_k;
+  a.d_snap_v = d->d_snap_v;
+  a.dsnap_stride = a.snap_stride;
+  a.d_state_temp = d->d_state_temp;
+  a.d_front_temp = d->d_front_temp;
+  hipStream_t s = as_stream(stream);
+  if (has_state) {  // rows no query chunk reads keep a zero gradient
+    const int64_t words = n_snap * a.snap_stride;
+    KVM_HIP(kvm::launch_fill_u32(reinterpret_cast<unsigned *>(d->d_snap_k), words, 0u, s), "d_snap_k clear");
+    KVM_HIP(kvm::launch_fill_u32(reinterpret_cast<unsigned *>(d->d_snap_v), words, 0u, s), "d_snap_v clear");
+  }
+  KVM_HIP(kvm::launch_attn_backward(L, a, table, static_cast<float *>(d->workspace), s), "attention backward");
+  return KVM_OK;
+}
+
 int kvm_decode_attention_noalloc(const kvm_layer *layer, const void *q, int64_t q_sb,
                                  int64_t q_sh, const kvm_state *st,
                                  int64_t active_state_len, const void *ring_k,
@@ -388,6 +474,15 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
                                                 !d->upd_n_append)))
     return fail(KVM_EINVAL, "update schedule arrays must be set");
   if (d->snapshot_ring < 2) return fail(KVM_EINVAL, "snapshot_ring must be >= 2");
+  if (!d->snap_k != !d->snap_v) return fail(KVM_EINVAL, "snap_k and snap_v must be set together");
+  if (d->snap_k) {
+    if (d->snapshot_ring != std::max<int64_t>(2, d->n_updates + 1))
+      return fail(KVM_EINVAL, "caller-held snapshots need snapshot_ring = max(2, n_updates + 1)");
+    if (!aligned16(d->snap_k) || !aligned16(d->snap_v))
+      return fail(KVM_EINVAL, "snapshot arrays must be 16-byte aligned");
+  }
+  if (d->lse && (reinterpret_cast<uintptr_t>(d->lse) & 3u))
+    return fail(KVM_EINVAL, "lse must be 4-byte aligned");
   const int64_t L0 = std::min(T, C);
   if (d->max_state_len < L0 || d->max_state_len > d->state.capacity)
     return fail(KVM_ESPACE, "max_state_len %lld must be in [%lld, capacity %lld]",
@@ -440,9 +535,14 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   unsigned char *ws = static_cast<unsigned char *>(d->workspace);
   kvm::UpdateScratch sc = kvm::carve_update_scratch(ws, ws + lay.slices * lay.slice_bytes, L, C);
   uint16_t *snap_k = reinterpret_cast<uint16_t *>(ws + lay.update_bytes);
-  const size_t snap_bytes = align256(lay.snap_elems * 2);
+  size_t snap_bytes = align256(lay.snap_elems * 2);
   uint16_t *snap_v = reinterpret_cast<uint16_t *>(
       ws + lay.update_bytes + size_t(d->snapshot_ring) * snap_bytes);
+  if (d->snap_k) {  // the caller's dense [n_updates + 1, rows, max_state_len, D] arrays
+    snap_k = static_cast<uint16_t *>(d->snap_k);
+    snap_v = static_cast<uint16_t *>(d->snap_v);
+    snap_bytes = lay.snap_elems * 2;
+  }
   const int64_t snap_stride = int64_t(snap_bytes / 2);
   const int64_t R = d->snapshot_ring;
   auto snap_rows = [&](int64_t idx) {
@@ -483,6 +583,7 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   a.snap_v = snap_v;
   a.snap_stride = snap_stride;
   a.snap_cap = d->max_state_len;
+  a.lse = d->lse;
 
   int64_t next_chunk = 0;
   bool attn_marked = false;

@@ -436,6 +436,9 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
     l = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
     const float inv = 1.0f / l;
     const int64_t t = qpos0 + rt * 16 + (lane & 15);
+    // log2-domain log-sum-exp of the row: the probabilities are exp2(s - m) / l.
+    if (A.lse && lane < 16 && t < q_hi)
+      A.lse[(int64_t(b) * Hq + hq) * T + t] = as.m[rt] + log2f(l);
     if (t < q_hi) {
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {

@@ -170,7 +170,32 @@ struct PrefillAttnArgs {
   const uint16_t *snap_v;  // snapshot ring base (values)
   int64_t snap_stride;     // elements between consecutive snapshots
   int64_t snap_cap;        // slots per row in a snapshot
+  float *lse;              // optional fp32 [B, Hq, T]: log2-domain log-sum-exp per query
 };
+
+// Attention backward (kvm_attn_bwd.hip).
+struct BwdArgs {
+  const void *q;
+  int64_t q_sb, q_sh, q_st;
+  kvm_seq kv;
+  int64_t T;
+  const void *dout;
+  int64_t do_sb, do_st, do_sh;
+  const float *lse, *delta;  // [B, Hq, T]
+  const uint16_t *snap_k, *snap_v;
+  int64_t snap_stride;       // elements between snapshots
+  int64_t snap_cap;          // slots per row in a snapshot
+  int64_t n_chunks;
+  void *dq;
+  int64_t dq_sb, dq_sh, dq_st;
+  float *dk, *dv;            // [B*Hkv, T, D]
+  float *d_snap_k, *d_snap_v;
+  int64_t dsnap_stride;
+  float *d_state_temp, *d_front_temp;
+};
+int64_t attn_bwd_workspace_bytes(const kvm_layer &L, int64_t n_chunks);
+hipError_t launch_attn_backward(const kvm_layer &L, const BwdArgs &a, const ChunkTable &table,
+                                float *tpart, hipStream_t stream);
 
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);
 hipError_t launch_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t B,

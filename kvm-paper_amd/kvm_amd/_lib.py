@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -78,6 +78,29 @@ class KvmPrefillDesc(ctypes.Structure):
         ("route_log", _vp), ("append_log", _vp),
         ("events", _vp),
         ("status", _vp),
+        ("lse", _vp),
+        ("snap_k", _vp), ("snap_v", _vp),
+    ]
+
+
+class KvmPrefillBwdDesc(ctypes.Structure):
+    _fields_ = [
+        ("layer", KvmLayer),
+        ("q", _vp), ("q_sb", _i64), ("q_sh", _i64), ("q_st", _i64),
+        ("kv", KvmSeq),
+        ("seq_len", _i64),
+        ("dout", _vp), ("do_sb", _i64), ("do_st", _i64), ("do_sh", _i64),
+        ("lse", _vp), ("delta", _vp),
+        ("snap_k", _vp), ("snap_v", _vp),
+        ("max_state_len", _i64),
+        ("n_chunks", _i64),
+        ("chunk_state_len", ctypes.POINTER(ctypes.c_int32)),
+        ("chunk_snapshot", ctypes.POINTER(ctypes.c_int32)),
+        ("dq", _vp), ("dq_sb", _i64), ("dq_sh", _i64), ("dq_st", _i64),
+        ("dk", _vp), ("dv", _vp),
+        ("d_snap_k", _vp), ("d_snap_v", _vp),
+        ("d_state_temp", _vp), ("d_front_temp", _vp),
+        ("workspace", _vp), ("workspace_bytes", _i64),
     ]
 
 
@@ -103,6 +126,8 @@ SIGNATURES = {
     "kvm_last_error": (ctypes.c_char_p, []),
     "kvm_prefill_workspace_bytes": (_i64, [_P(KvmPrefillDesc)]),
     "kvm_prefill": (ctypes.c_int, [_P(KvmPrefillDesc), _vp]),
+    "kvm_prefill_backward_workspace_bytes": (_i64, [_P(KvmPrefillBwdDesc)]),
+    "kvm_prefill_backward": (ctypes.c_int, [_P(KvmPrefillBwdDesc), _vp]),
     "kvm_prefix": (ctypes.c_int, [_P(KvmPrefixDesc), _vp]),
     "kvm_token_shift": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
@@ -146,7 +171,7 @@ def load(path: str | os.PathLike | None = None):
         fn.argtypes = args
     if lib.kvm_abi_version() != ABI_VERSION:
         raise KvmLibraryError(f"{p}: ABI version {lib.kvm_abi_version()} != {ABI_VERSION}")
-    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc)):
+    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc, KvmPrefillBwdDesc)):
         if lib.kvm_struct_size(i) != ctypes.sizeof(st):
             raise KvmLibraryError(f"{p}: struct {st.__name__} size mismatch")
     if path is None:

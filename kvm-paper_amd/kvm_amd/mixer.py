@@ -489,13 +489,15 @@ class SequenceMixer(nn.Module):
             return self.forward_prefill(q, k, v, g, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
         return self.forward_single(q, k, v, g, v_first, position_embeddings, attention_mask, past_key_values, **kwargs)
 
-    def _check_no_grad(self, *tensors):
-        needs_grad = torch.is_grad_enabled() and any(
+    def _needs_grad(self, *tensors) -> bool:
+        return torch.is_grad_enabled() and any(
             t.requires_grad for t in (*tensors, self.ln_s_k.weight, self.ln_s_k.bias,
                                       getattr(self, "state_head_temp", tensors[0]),
                                       getattr(self, "front_head_temp", tensors[0])))
-        if needs_grad:
-            raise ValueError("the HIP KVM mixer implements the forward path only; run it under torch.no_grad()")
+
+    def _check_no_grad(self, *tensors):
+        if self._needs_grad(*tensors):
+            raise ValueError("the HIP KVM mixer's cached decode is inference only; run it under torch.no_grad()")
 
     def _status_word(self, device) -> torch.Tensor:
         """This mixer's sticky device status word (int32[1]) on ``device``:
@@ -525,7 +527,8 @@ class SequenceMixer(nn.Module):
 
     def prefill_raw(self, q, k, v, merge_gate, *, plan: PrefillPlan | None = None, state_capacity: int | None = None,
                     route_log: bool = False, snapshot_budget: int | None = None,
-                    events=None, check_status: bool | None = True) -> dict:
+                    events=None, check_status: bool | None = True, keep_snapshots: bool = False,
+                    want_lse: bool = False) -> dict:
         """Post-QKV prefill on the HIP library; returns the raw outputs.
 
         q [B,Hq,T,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] bf16 (any strides with a
@@ -544,6 +547,11 @@ class SequenceMixer(nn.Module):
         With ``check_status=None`` no status word is passed: the library then
         waits for the stream itself and reports a failure as its return code
         (the C ABI's synchronous mode).
+
+        Training (``kvm_amd.training``): ``keep_snapshots`` returns every
+        memory snapshot the query chunks read (``snap_k`` / ``snap_v``, bf16
+        [n_updates + 1, B*Hkv, max_state_len, D]); ``want_lse`` returns the
+        log2-domain log-sum-exp of every query (``lse``, fp32 [B, Hq, T]).
         """
         if q.dtype != torch.bfloat16:
             raise ValueError("the HIP KVM mixer computes in bfloat16; got " + str(q.dtype))
@@ -572,6 +580,14 @@ class SequenceMixer(nn.Module):
         per_snap = 2 * rows * plan.max_state_len * D * 2
         budget = _SNAPSHOT_BUDGET if snapshot_budget is None else int(snapshot_budget)
         ring = max(2, min(n_snaps, budget // max(per_snap, 1)))
+        extra = {}
+        if keep_snapshots:
+            ring = max(2, n_snaps)
+            shape = (n_snaps, rows, plan.max_state_len, D)
+            extra["snap_k"] = torch.empty(shape, **bf)
+            extra["snap_v"] = torch.empty(shape, **bf)
+        if want_lse:
+            extra["lse"] = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
         arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin,
                                                plan.upd_state_before, plan.upd_n_append)]
         d = _lib.KvmPrefillDesc()
@@ -588,6 +604,10 @@ class SequenceMixer(nn.Module):
         d.upd_token_begin, d.upd_state_before, d.upd_n_append = arrs[2], arrs[3], arrs[4]
         d.max_state_len = plan.max_state_len
         d.snapshot_ring = ring
+        if keep_snapshots:
+            d.snap_k, d.snap_v = extra["snap_k"].data_ptr(), extra["snap_v"].data_ptr()
+        if want_lse:
+            d.lse = extra["lse"].data_ptr()
         nbytes = int(lib.kvm_prefill_workspace_bytes(ctypes.byref(d)))
         if nbytes < 0:
             raise ValueError("invalid prefill descriptor: " + lib.kvm_last_error().decode())
@@ -608,7 +628,7 @@ class SequenceMixer(nn.Module):
         del keep, ws
         if check_status:
             self.check_prefill_status(dev)
-        res = {"out": out, "plan": plan, "capacity": cap, **st, **logs}
+        res = {"out": out, "plan": plan, "capacity": cap, **st, **logs, **extra}
         return res
 
     def forward_prefill(self, q, k, v, merge_gate, v_first, position_embeddings, attention_mask,
@@ -616,8 +636,16 @@ class SequenceMixer(nn.Module):
         """Prefill at the post-QKV boundary (model/kvm_triton_mixer.py:560-666)."""
         if attention_mask is not None:
             raise ValueError("the HIP KVM mixer does not support attention_mask")
-        self._check_no_grad(q, k, v, merge_gate)
         B, _, T, _ = q.size()
+        if self._needs_grad(q, k, v, merge_gate):
+            # Training (model/kvm_triton_mixer.py:24-195): the differentiable prefill with
+            # the forward's routes as fixed metadata; no decode cache is built.
+            if past_key_values is not None:
+                raise ValueError("the HIP KVM mixer's training path does not build a decode cache")
+            from .training import prefill_with_grad
+
+            y = prefill_with_grad(self, q, k, v, merge_gate)
+            return self.c_proj(y.reshape(B, T, -1))
         plan = self.make_plan(int(T))
         cap = None
         if past_key_values is not None:

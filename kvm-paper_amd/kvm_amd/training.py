@@ -1,0 +1,212 @@
+"""Training path of the HIP KVM mixer: the prefill as a differentiable op.
+
+Reference: ``_KvmTritonTrainingFunction`` (model/kvm_triton_mixer.py:24-195)
+with ``run_training_backward_reconstruct_live_state``
+(model/kernels/kvm_triton_training_kernels.py:3621-4153).  As there, the
+routing decisions of the forward (which slot every overflow token was
+appended to or merged into) are fixed metadata: the argmax and the append
+ranking are not differentiated, and the bf16 roundings of the forward are
+taken as the identity in the backward.
+
+Forward: ``kvm_prefill`` on the HIP library, keeping every memory snapshot
+the query chunks read, the routes of every update and the log-sum-exp of
+every query.
+
+Backward:
+  * attention (HIP, ``kvm_prefill_backward``): dq, the window keys' and
+    values' gradients, the gradients of every snapshot's key and value rows,
+    and the two head temperatures' gradients;
+  * memory state (this module): the snapshot rows are functions of the
+    tokens through LayerNorm_s(s_k), normalize(s_v) * vlen and the merge sums
+    under the fixed routes.  ``replay_snapshot_rows`` rebuilds them in fp32
+    with torch autograd from the token streams and the forward's routes, and
+    the snapshot-row gradients are pulled back through it to k, v, the merge
+    gate and the ln_s_k parameters.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def replay_snapshot_rows(k, v, gate, ln_w, ln_b, plan, route_log, append_log, cfg):
+    """Attention rows of every snapshot, rebuilt in fp32 from the tokens and
+    the forward's routes (differentiable in k, v, gate, ln_w, ln_b).
+
+    k, v: [rows, T, D]; gate: [rows, T]; route_log / append_log:
+    [n_updates, rows, C] (slot of every overflow token; 1 if appended).
+    ``cfg`` carries eps, rope_partial_dim, gate_keys, gate_values,
+    gate_appends, gate_initial.  Returns a list of (k_rows, v_rows), one per
+    snapshot, each [rows, S_snapshot, D].  The state follows
+    model/kvm_mixer.py:434-447 (initial state), :231-248 (append) and
+    :321-340 (merge sums) with the routes given.
+    """
+    rows, T, D = k.shape
+    C = plan.chunk_len
+    r = int(cfg["rope_partial_dim"])
+    kz = torch.cat([torch.zeros_like(k[..., :r]), k[..., r:]], dim=-1)
+    prep = F.layer_norm(kz, (D,), ln_w, ln_b, cfg["eps"])
+    g = gate.unsqueeze(-1)
+    gk = prep * g if cfg["gate_keys"] else prep
+    gv = v * g if cfg["gate_values"] else v
+    ak, av = (gk, gv) if cfg["gate_appends"] else (prep, v)
+
+    def attn_rows(s_k, s_v, vlen):
+        return (F.layer_norm(s_k, (D,), ln_w, ln_b, cfg["eps"]),
+                F.normalize(s_v, dim=-1) * vlen.unsqueeze(-1))
+
+    L0 = plan.initial_state_len
+    s_k = (prep * g if cfg["gate_initial"] else prep)[:, :L0]
+    s_v = (v * g if cfg["gate_initial"] else v)[:, :L0]
+    vlen = v[:, :L0].norm(dim=-1)
+    snaps = [attn_rows(s_k, s_v, vlen)]
+    ridx = torch.arange(rows, device=k.device).unsqueeze(1)
+    for u in range(plan.n_updates):
+        tb, before, n_app = plan.upd_token_begin[u], plan.upd_state_before[u], plan.upd_n_append[u]
+        route = route_log[u].long()                 # [rows, C]
+        app = append_log[u].bool()
+        after = before + n_app
+        if n_app:
+            # Appended tokens take slots before .. after - 1 in token order.
+            tok = app.nonzero()[:, 1].view(rows, n_app) + tb
+            new_k = ak[ridx, tok]
+            new_v = av[ridx, tok]
+            s_k = torch.cat([s_k, new_k], dim=1)
+            s_v = torch.cat([s_v, new_v], dim=1)
+            vlen = torch.cat([vlen, new_v.norm(dim=-1)], dim=1)
+        merged = ~app
+        flat = (ridx * after + route).masked_select(merged)
+        tok_rows = (ridx * T + tb + torch.arange(C, device=k.device)).masked_select(merged)
+        dk = torch.zeros(rows * after, D, device=k.device, dtype=k.dtype).index_add(
+            0, flat, gk.reshape(rows * T, D).index_select(0, tok_rows))
+        dv = torch.zeros(rows * after, D, device=k.device, dtype=k.dtype).index_add(
+            0, flat, gv.reshape(rows * T, D).index_select(0, tok_rows))
+        s_k = s_k + dk.view(rows, after, D)
+        s_v = s_v + dv.view(rows, after, D)
+        snaps.append(attn_rows(s_k, s_v, vlen))
+    return snaps
+
+
+def _layer_cfg(mixer):
+    return {
+        "eps": float(mixer.ln_s_k.eps), "rope_partial_dim": int(mixer.rope_partial_dim),
+        "gate_keys": bool(mixer.config.kvm_use_merge_gate_keys),
+        "gate_values": bool(mixer.config.kvm_use_merge_gate_values),
+        "gate_appends": bool(mixer.config.kvm_apply_merge_gate_to_appends),
+        "gate_initial": bool(mixer.config.kvm_apply_merge_gate_to_initial_state),
+    }
+
+
+def attention_backward(mixer, q, k, v, gate, res, dout):
+    """The HIP attention backward of one prefill (kvm_prefill_backward).
+
+    Returns dq [B,Hq,T,D] bf16, dk / dv of the window tokens [B,Hkv,T,D]
+    fp32, d_snap_k / d_snap_v [n_snap, B*Hkv, S_max, D] fp32 and the
+    temperature gradients [Hq] fp32."""
+    B, Hq, T, D = q.shape
+    Hkv = k.size(1)
+    plan = res["plan"]
+    dev = q.device
+    out = res["out"]                                  # [B, T, Hq, D] bf16
+    dout = dout.to(torch.bfloat16).contiguous()
+    delta = (dout.float() * out.float()).sum(-1).permute(0, 2, 1).contiguous()  # [B, Hq, T]
+    qv = _lib._bf16_view(q, "q")
+    seq, keep = _lib.seq4(k, v, gate)
+    layer = mixer._layer_struct(B, dev)
+    dq = torch.empty(B, Hq, T, D, device=dev, dtype=torch.bfloat16)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dk = torch.empty(B, Hkv, T, D, **f32)
+    dv = torch.empty(B, Hkv, T, D, **f32)
+    snap_k, snap_v = res["snap_k"], res["snap_v"]
+    d_snap_k = torch.empty(snap_k.shape, **f32)
+    d_snap_v = torch.empty(snap_v.shape, **f32)
+    d_ts = torch.empty(Hq, **f32)
+    d_tf = torch.empty(Hq, **f32)
+    arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot)]
+    d = _lib.KvmPrefillBwdDesc()
+    d.layer = layer.struct
+    d.q, d.q_sb, d.q_sh, d.q_st = qv.data_ptr(), qv.stride(0), qv.stride(1), qv.stride(2)
+    d.kv = seq
+    d.seq_len = T
+    d.dout, d.do_sb, d.do_st, d.do_sh = dout.data_ptr(), dout.stride(0), dout.stride(1), dout.stride(2)
+    d.lse, d.delta = res["lse"].data_ptr(), delta.data_ptr()
+    d.snap_k, d.snap_v = snap_k.data_ptr(), snap_v.data_ptr()
+    d.max_state_len = plan.max_state_len
+    d.n_chunks = plan.n_chunks
+    d.chunk_state_len, d.chunk_snapshot = arrs[0], arrs[1]
+    d.dq, d.dq_sb, d.dq_sh, d.dq_st = dq.data_ptr(), dq.stride(0), dq.stride(1), dq.stride(2)
+    d.dk, d.dv = dk.data_ptr(), dv.data_ptr()
+    d.d_snap_k, d.d_snap_v = d_snap_k.data_ptr(), d_snap_v.data_ptr()
+    d.d_state_temp, d.d_front_temp = d_ts.data_ptr(), d_tf.data_ptr()
+    lib = _lib.load()
+    nws = int(lib.kvm_prefill_backward_workspace_bytes(ctypes.byref(d)))
+    if nws < 0:
+        raise ValueError("invalid backward descriptor: " + lib.kvm_last_error().decode())
+    ws = torch.empty(max(nws, 16), device=dev, dtype=torch.uint8)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), nws
+    _lib.check(lib.kvm_prefill_backward(ctypes.byref(d), _lib.stream_handle(dev)), "kvm_prefill_backward")
+    del keep, ws
+    return dq, dk, dv, d_snap_k, d_snap_v, d_ts, d_tf
+
+
+class KVMPrefillFunction(torch.autograd.Function):
+    """y = prefill(q, k, v, gate; ln_s_k, temperatures) at the post-QKV
+    boundary, differentiable in all of them (routes fixed by the forward).
+    Returns the attention output [B, T, Hq, Dv] bf16 (before c_proj)."""
+
+    @staticmethod
+    def forward(ctx, mixer, q, k, v, gate, ln_w, ln_b, state_temp, front_temp):
+        with torch.no_grad():
+            res = mixer.prefill_raw(q, k, v, gate, route_log=True, keep_snapshots=True, want_lse=True)
+        ctx.mixer = mixer
+        ctx.res = res
+        ctx.save_for_backward(q, k, v, gate, ln_w, ln_b, state_temp, front_temp)
+        return res["out"]
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, gate, ln_w, ln_b, state_temp, front_temp = ctx.saved_tensors
+        mixer, res = ctx.mixer, ctx.res
+        plan = res["plan"]
+        B, Hkv, T, D = k.shape
+        rows = B * Hkv
+        dq, dk_w, dv_w, d_snap_k, d_snap_v, d_ts, d_tf = attention_backward(mixer, q, k, v, gate, res, dout)
+        # Memory state: pull the snapshot-row gradients back to the tokens.
+        with torch.enable_grad():
+            kf = k.detach().float().reshape(rows, T, D).requires_grad_(True)
+            vf = v.detach().float().reshape(rows, T, D).requires_grad_(True)
+            gf = gate.detach().float().reshape(rows, T).requires_grad_(True)
+            lw = ln_w.detach().float().requires_grad_(True)
+            lb = ln_b.detach().float().requires_grad_(True)
+            snaps = replay_snapshot_rows(kf, vf, gf, lw, lb, plan, res["route_log"], res["append_log"],
+                                         _layer_cfg(mixer))
+            total = kf.new_zeros(())
+            for s, (ka, va) in enumerate(snaps):
+                S = ka.size(1)
+                total = total + (ka * d_snap_k[s, :, :S]).sum() + (va * d_snap_v[s, :, :S]).sum()
+            gk, gv, gg, glw, glb = torch.autograd.grad(total, (kf, vf, gf, lw, lb), allow_unused=True)
+        zero = lambda t, ref: torch.zeros_like(ref, dtype=torch.float32) if t is None else t  # noqa: E731
+        dk = (dk_w + zero(gk, kf).view(B, Hkv, T, D)).to(k.dtype)
+        dv = (dv_w + zero(gv, vf).view(B, Hkv, T, D)).to(v.dtype)
+        dgate = zero(gg, gf).view(gate.shape).to(gate.dtype)
+        return (None, dq.to(q.dtype), dk, dv, dgate, zero(glw, lw).to(ln_w.dtype), zero(glb, lb).to(ln_b.dtype),
+                d_ts.to(state_temp.dtype), d_tf.to(front_temp.dtype))
+
+
+def prefill_with_grad(mixer, q, k, v, gate):
+    """Differentiable post-QKV prefill of ``mixer`` (routes fixed by the forward)."""
+    Hq = mixer.num_attention_heads
+    dev = q.device
+    ones = torch.ones(Hq, device=dev, dtype=torch.float32)
+    temps = bool(mixer.config.kvm_use_head_temps)
+    ts = mixer.state_head_temp.view(-1) if temps else ones
+    tf = mixer.front_head_temp.view(-1) if temps else ones
+    return KVMPrefillFunction.apply(mixer, q, k, v, gate, mixer.ln_s_k.weight, mixer.ln_s_k.bias, ts, tf)
+
+
+__all__ = ["KVMPrefillFunction", "prefill_with_grad", "replay_snapshot_rows", "attention_backward"]
