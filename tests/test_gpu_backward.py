@@ -100,6 +100,8 @@ def test_mixer_forward_trains_through_the_hip_prefill():
     cfg = T.mixer_config(Hq, Hkv, D, C, rope=16, mode="power_law", min_len=C, n_max=4, factor=8.0)
     torch.manual_seed(3)
     m = SequenceMixer(cfg, 0).to(DEV, torch.bfloat16).train()
+    with torch.no_grad():  # the output projection starts at zero, which would stop every gradient upstream
+        m.c_proj.weight.normal_(0.0, 0.02)
     x = (torch.randn(2, Tn, Hq * D, device=DEV) * 0.5).bfloat16().requires_grad_(True)
     T.log(f"[backward] mixer.forward B2 T{Tn} Hq{Hq} Hkv{Hkv} D{D} with gradients")
     ang = torch.arange(Tn, device=DEV).view(1, Tn, 1, 1) * torch.linspace(0.01, 1.0, D, device=DEV)
