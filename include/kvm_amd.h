@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 5
+#define KVM_ABI_VERSION 6
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -203,6 +203,51 @@ typedef struct kvm_prefill_bwd_desc {
 int64_t kvm_prefill_backward_workspace_bytes(const kvm_prefill_bwd_desc *d);
 int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream);
 
+/* The memory state's part of the backward (the reference's
+ * _live_state_dkdv_to_raw_grad_kernel, _reverse_route_scatter_grad_split_kernel,
+ * _restore_refresh_from_undo_routes_kernel and _initial_state_grad_kernel,
+ * model/kernels/kvm_triton_training_kernels.py:2093-2745), under the forward's
+ * routes.  Snapshot s (s = 0 .. n_updates) holds slot rows
+ * LayerNorm_s(s_k) and normalize(s_v) * vlen of the state after s updates;
+ * the state starts from the initial token rows (slots < initial_state_len),
+ * update u appends the tokens marked in append_log to slots
+ * upd_state_before[u] .. + upd_n_append[u] - 1 (in token order, vlen =
+ * |appended value row|) and then adds every other token's merge rows to the
+ * slot route_log names.  Given the gradients of every snapshot's rows
+ * (d_snap_k / d_snap_v, as kvm_prefill_backward writes them), this writes
+ * the gradients of the token rows that built the state: the merge rows, the
+ * appended rows (and the vlen each appended slot took), the initial rows
+ * (and their vlen), and the two LayerNorm parameters.  The sums are taken in
+ * fp32 and the forward's bf16 roundings as the identity. */
+typedef struct kvm_state_bwd_desc {
+  int64_t rows;                  /* batch * kv_heads */
+  int64_t seq_len, head_dim, chunk_len;
+  double ln_eps;
+  const float *ln_w, *ln_b;      /* fp32 [head_dim] */
+  const float *mk, *mv;          /* fp32 [rows, T, D] merge key / value rows of every token */
+  const float *ak, *av;          /* fp32 [rows, T, D] append key / value rows */
+  const float *avl;              /* fp32 [rows, T]: vlen an appended token's slot takes */
+  const float *ik, *iv;          /* fp32 [rows, L0, D] initial key / value rows */
+  const float *ivl;              /* fp32 [rows, L0]: vlen of the initial slots */
+  int64_t initial_state_len;     /* L0 */
+  int64_t n_updates;
+  const int32_t *upd_token_begin, *upd_state_before, *upd_n_append;  /* host [n_updates], n_updates < 256 */
+  const int32_t *route_log, *append_log;   /* device [n_updates, rows, chunk_len] */
+  int64_t max_state_len;
+  const float *d_snap_k, *d_snap_v;        /* fp32 [n_updates + 1, rows, max_state_len, D] */
+  float *d_mk, *d_mv, *d_ak, *d_av;        /* fp32 out [rows, T, D]: rows of tokens of that kind
+                                              (others are left as they are: zero them first) */
+  float *d_avl;                            /* fp32 out [rows, T] */
+  float *d_ik, *d_iv;                      /* fp32 out [rows, L0, D] */
+  float *d_ivl;                            /* fp32 out [rows, L0] */
+  float *d_ln;                             /* fp32 out [2, D]: d ln_w, d ln_b */
+  void *workspace;                         /* kvm_state_backward_workspace_bytes() */
+  int64_t workspace_bytes;
+} kvm_state_bwd_desc;
+
+int64_t kvm_state_backward_workspace_bytes(const kvm_state_bwd_desc *d);
+int kvm_state_backward(const kvm_state_bwd_desc *d, void *stream);
+
 /* The mixer's pre-boundary elementwise work on the q/k/v projections, for
  * one layer (model/value_residual_mixin.py:173-237 calc_qkv and
  * model/kvm_mixer.py:367-401 forward_prefix after the GEMMs):
@@ -259,7 +304,7 @@ int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
 int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc,
-                                        5 prefill_bwd_desc */
+                                        5 prefill_bwd_desc, 6 state_bwd_desc */
 const char *kvm_last_error(void);
 
 /* Workspace of kvm_prefill for the given descriptor (snapshot_ring and

@@ -197,6 +197,31 @@ int64_t attn_bwd_workspace_bytes(const kvm_layer &L, int64_t n_chunks);
 hipError_t launch_attn_backward(const kvm_layer &L, const BwdArgs &a, const ChunkTable &table,
                                 float *tpart, hipStream_t stream);
 
+// Memory-state backward (kvm_state_bwd.hip).  Token-row arrays are
+// [rows, T, D] fp32, per-token scalars [rows, T]; the initial rows
+// [rows, L0, D]; snapshot gradients [n_updates + 1, rows, max_state_len, D].
+struct StateBwdArgs {
+  int64_t rows, T, head_dim, chunk_len, L0, n_updates, max_state_len;
+  double ln_eps;
+  const float *ln_w, *ln_b;
+  const float *mk, *mv, *ak, *av, *avl, *ik, *iv, *ivl;
+  const int32_t *route_log, *append_log;  // [n_updates, rows, chunk_len]
+  const float *d_snap_k, *d_snap_v;
+  float *d_mk, *d_mv, *d_ak, *d_av, *d_avl, *d_ik, *d_iv, *d_ivl;
+  float *d_ln;                            // [2, D]
+};
+// Per-update schedule, passed by value as a kernel argument (3 KiB).
+struct UpdTable {
+  int32_t token_begin[kMaxChunksPerLaunch];
+  int32_t state_before[kMaxChunksPerLaunch];
+  int32_t n_append[kMaxChunksPerLaunch];
+};
+int64_t state_bwd_workspace_bytes(int64_t head_dim, int64_t rows, int64_t max_state_len);
+int64_t state_bwd_max_chunk();
+// part: the per-workgroup LayerNorm partials (the workspace).
+hipError_t launch_state_backward(const StateBwdArgs &a, const UpdTable &sched, float *part,
+                                 hipStream_t stream);
+
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);
 hipError_t launch_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t B,
                               int64_t T, int64_t width, int zero_fallback, hipStream_t stream);

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -104,6 +104,27 @@ class KvmPrefillBwdDesc(ctypes.Structure):
     ]
 
 
+class KvmStateBwdDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i64), ("seq_len", _i64), ("head_dim", _i64), ("chunk_len", _i64),
+        ("ln_eps", ctypes.c_double),
+        ("ln_w", _vp), ("ln_b", _vp),
+        ("mk", _vp), ("mv", _vp), ("ak", _vp), ("av", _vp), ("avl", _vp),
+        ("ik", _vp), ("iv", _vp), ("ivl", _vp),
+        ("initial_state_len", _i64), ("n_updates", _i64),
+        ("upd_token_begin", ctypes.POINTER(ctypes.c_int32)),
+        ("upd_state_before", ctypes.POINTER(ctypes.c_int32)),
+        ("upd_n_append", ctypes.POINTER(ctypes.c_int32)),
+        ("route_log", _vp), ("append_log", _vp),
+        ("max_state_len", _i64),
+        ("d_snap_k", _vp), ("d_snap_v", _vp),
+        ("d_mk", _vp), ("d_mv", _vp), ("d_ak", _vp), ("d_av", _vp), ("d_avl", _vp),
+        ("d_ik", _vp), ("d_iv", _vp), ("d_ivl", _vp),
+        ("d_ln", _vp),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
 class KvmPrefixDesc(ctypes.Structure):
     _fields_ = [
         ("batch", _i64), ("seq_len", _i64), ("q_heads", _i64), ("kv_heads", _i64),
@@ -128,6 +149,8 @@ SIGNATURES = {
     "kvm_prefill": (ctypes.c_int, [_P(KvmPrefillDesc), _vp]),
     "kvm_prefill_backward_workspace_bytes": (_i64, [_P(KvmPrefillBwdDesc)]),
     "kvm_prefill_backward": (ctypes.c_int, [_P(KvmPrefillBwdDesc), _vp]),
+    "kvm_state_backward_workspace_bytes": (_i64, [_P(KvmStateBwdDesc)]),
+    "kvm_state_backward": (ctypes.c_int, [_P(KvmStateBwdDesc), _vp]),
     "kvm_prefix": (ctypes.c_int, [_P(KvmPrefixDesc), _vp]),
     "kvm_token_shift": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
@@ -171,7 +194,8 @@ def load(path: str | os.PathLike | None = None):
         fn.argtypes = args
     if lib.kvm_abi_version() != ABI_VERSION:
         raise KvmLibraryError(f"{p}: ABI version {lib.kvm_abi_version()} != {ABI_VERSION}")
-    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc, KvmPrefillBwdDesc)):
+    for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc, KvmPrefillBwdDesc,
+                              KvmStateBwdDesc)):
         if lib.kvm_struct_size(i) != ctypes.sizeof(st):
             raise KvmLibraryError(f"{p}: struct {st.__name__} size mismatch")
     if path is None:

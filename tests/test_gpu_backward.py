@@ -174,3 +174,64 @@ def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gate
         worst.append(f"{name} {rmax:.1e}/{rmean:.1e}")
         assert rmax <= 5e-2 and rmean <= 2e-2, f"d{name}: relative max {rmax:.3e}, mean {rmean:.3e}"
     T.log(f"[backward] relative max/mean error per gradient: {', '.join(worst)}")
+
+
+@pytest.mark.parametrize("B,Hkv,D,C,Tn,mode,gates", [
+    (2, 2, 64, 64, 640, "power_law", (1, 1, 0, 0)),
+    (1, 2, 128, 128, 1300, "power_law", (1, 0, 1, 1)),
+    (1, 1, 64, 64, 400, "fixed", (0, 1, 1, 0)),
+])
+def test_state_backward_matches_replay_autograd(B, Hkv, D, C, Tn, mode, gates):
+    """kvm_state_backward against torch autograd through replay_snapshot_rows
+    (both fp32, the same routes): random snapshot-row gradients pulled back to
+    k, v, the gate and the LayerNorm parameters."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd import training
+
+    gk_, gv_, ga_, gi_ = gates
+    Hq = Hkv
+    T.log(f"[state-backward] B{B} Hkv{Hkv} D{D} C{C} T{Tn} {mode} gates {gates}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, rope=16, mode=mode, min_len=C, n_max=4, factor=8.0, expo=0.5,
+                         gate_keys=gk_, gate_values=gv_, gate_appends=ga_, gate_initial=gi_)
+    gen = torch.Generator().manual_seed(5)
+    lnw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    lnb = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ones = torch.ones(Hq).bfloat16()
+    m = T.make_mixer(cfg, lnw, lnb, ones, ones)
+    q = torch.randn(B, Hq, Tn, D, generator=gen).bfloat16()
+    k = torch.randn(B, Hkv, Tn, D, generator=gen).bfloat16()
+    v = torch.randn(B, Hkv, Tn, D, generator=gen).bfloat16()
+    g = (1 + F.elu(torch.randn(B, Hkv, Tn, 1, generator=gen))).bfloat16()
+    with torch.no_grad():
+        res = m.prefill_raw(*(t.to(DEV) for t in (q, k, v, g)), route_log=True)
+    plan = res["plan"]
+    rows = B * Hkv
+    assert plan.n_updates > 0
+    if mode != "fixed":
+        assert sum(plan.upd_n_append) > 0
+    n_snap = plan.n_updates + 1
+    shape = (n_snap, rows, plan.max_state_len, D)
+    dsk = torch.randn(shape, generator=gen).to(DEV)
+    dsv = torch.randn(shape, generator=gen).to(DEV)
+    lcfg = {"eps": 1e-5, "rope_partial_dim": 16, "gate_keys": gk_, "gate_values": gv_, "gate_appends": ga_,
+            "gate_initial": gi_}
+    kk, vv, gg = (x.to(DEV).reshape(rows, Tn, -1) for x in (k, v, g))
+    gg = gg.reshape(rows, Tn)
+    got = training.state_backward(kk, vv, gg, lnw.to(DEV), lnb.to(DEV), plan, res["route_log"],
+                                  res["append_log"], dsk, dsv, lcfg)
+    torch.cuda.synchronize()
+    leaves = [x.float().requires_grad_(True) for x in (kk, vv, gg, lnw.to(DEV), lnb.to(DEV))]
+    snaps = training.replay_snapshot_rows(*leaves, plan, res["route_log"], res["append_log"], lcfg)
+    total = sum((ka * dsk[s, :, :ka.size(1)]).sum() + (va * dsv[s, :, :va.size(1)]).sum()
+                for s, (ka, va) in enumerate(snaps))
+    ref = torch.autograd.grad(total, leaves)
+    worst = []
+    for name, a, b in zip(["k", "v", "gate", "ln_w", "ln_b"], got, ref):
+        assert a.shape == b.shape, name
+        err = (a - b).abs()
+        rmax = float(err.max() / b.abs().max().clamp_min(1e-12))
+        rmean = float(err.mean() / b.abs().mean().clamp_min(1e-12))
+        worst.append(f"{name} {rmax:.1e}/{rmean:.1e}")
+        assert rmax <= 2e-3 and rmean <= 2e-4, f"d{name}: relative max {rmax:.3e}, mean {rmean:.3e}"
+    T.log(f"[state-backward] relative max/mean error: {', '.join(worst)}")

@@ -48,7 +48,8 @@ def test_struct_layout_matches_binding():
     from kvm_amd import _lib as L
 
     assert lib.kvm_abi_version() == L.ABI_VERSION
-    for i, st in enumerate((L.KvmLayer, L.KvmSeq, L.KvmState, L.KvmPrefillDesc, L.KvmPrefixDesc, L.KvmPrefillBwdDesc)):
+    for i, st in enumerate((L.KvmLayer, L.KvmSeq, L.KvmState, L.KvmPrefillDesc, L.KvmPrefixDesc, L.KvmPrefillBwdDesc,
+                              L.KvmStateBwdDesc)):
         assert lib.kvm_struct_size(i) == ctypes.sizeof(st)
     assert lib.kvm_struct_size(9) == -1
 
