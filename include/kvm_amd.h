@@ -213,34 +213,28 @@ int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream);
  * update u appends the tokens marked in append_log to slots
  * upd_state_before[u] .. + upd_n_append[u] - 1 (in token order, vlen =
  * |appended value row|) and then adds every other token's merge rows to the
- * slot route_log names.  Given the gradients of every snapshot's rows
- * (d_snap_k / d_snap_v, as kvm_prefill_backward writes them), this writes
- * the gradients of the token rows that built the state: the merge rows, the
- * appended rows (and the vlen each appended slot took), the initial rows
- * (and their vlen), and the two LayerNorm parameters.  The sums are taken in
- * fp32 and the forward's bf16 roundings as the identity. */
+ * slot route_log names.  Token rows are prep = LayerNorm_s(k with dims <
+ * rope_partial_dim zeroed) and v, times the merge gate as the layer's gate
+ * flags say.  Given the gradients of every snapshot's rows (d_snap_k /
+ * d_snap_v, as kvm_prefill_backward writes them), this adds the state's
+ * share of the gradient to dk and dv (the attention backward's window
+ * gradients), writes dgate for the tokens the state holds, and writes the
+ * LayerNorm parameters' gradient (both uses of ln_s_k).  The sums are taken
+ * in fp32 and the forward's bf16 roundings as the identity. */
 typedef struct kvm_state_bwd_desc {
-  int64_t rows;                  /* batch * kv_heads */
-  int64_t seq_len, head_dim, chunk_len;
-  double ln_eps;
-  const float *ln_w, *ln_b;      /* fp32 [head_dim] */
-  const float *mk, *mv;          /* fp32 [rows, T, D] merge key / value rows of every token */
-  const float *ak, *av;          /* fp32 [rows, T, D] append key / value rows */
-  const float *avl;              /* fp32 [rows, T]: vlen an appended token's slot takes */
-  const float *ik, *iv;          /* fp32 [rows, L0, D] initial key / value rows */
-  const float *ivl;              /* fp32 [rows, L0]: vlen of the initial slots */
-  int64_t initial_state_len;     /* L0 */
-  int64_t n_updates;
-  const int32_t *upd_token_begin, *upd_state_before, *upd_n_append;  /* host [n_updates], n_updates < 256 */
-  const int32_t *route_log, *append_log;   /* device [n_updates, rows, chunk_len] */
+  kvm_layer layer;               /* shapes, ln_s_k (fp32), rope_partial_dim, gate flags, chunk_len */
+  kvm_seq kv;                    /* the prefill's keys, values and merge gates (bf16) */
+  int64_t seq_len;
+  int64_t initial_state_len;     /* L0 = min(seq_len, chunk_len) */
+  int64_t n_updates;             /* < 256 */
+  const int32_t *upd_token_begin, *upd_state_before, *upd_n_append;  /* host [n_updates] */
+  const int32_t *route_log, *append_log;   /* device [n_updates, rows, chunk_len] (kvm_prefill's logs) */
   int64_t max_state_len;
-  const float *d_snap_k, *d_snap_v;        /* fp32 [n_updates + 1, rows, max_state_len, D] */
-  float *d_mk, *d_mv, *d_ak, *d_av;        /* fp32 out [rows, T, D]: rows of tokens of that kind
-                                              (others are left as they are: zero them first) */
-  float *d_avl;                            /* fp32 out [rows, T] */
-  float *d_ik, *d_iv;                      /* fp32 out [rows, L0, D] */
-  float *d_ivl;                            /* fp32 out [rows, L0] */
-  float *d_ln;                             /* fp32 out [2, D]: d ln_w, d ln_b */
+  const float *d_snap_k, *d_snap_v;        /* fp32 [n_updates + 1, rows, max_state_len, head_dim] */
+  float *dk, *dv;                          /* fp32 [B, Hkv, seq_len, head_dim], in/out: the state's share is added */
+  float *dgate;                            /* fp32 out [B, Hkv, seq_len]: written for the tokens the state
+                                              holds (others are left as they are: zero them first) */
+  float *d_ln;                             /* fp32 out [2, head_dim]: d ln_w, d ln_b */
   void *workspace;                         /* kvm_state_backward_workspace_bytes() */
   int64_t workspace_bytes;
 } kvm_state_bwd_desc;

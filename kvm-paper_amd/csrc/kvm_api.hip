@@ -400,60 +400,56 @@ int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream) {
 }
 
 int64_t kvm_state_backward_workspace_bytes(const kvm_state_bwd_desc *d) {
-  if (!d || (d->head_dim != 64 && d->head_dim != 128) || d->rows < 1 || d->max_state_len < 1) return -1;
-  return kvm::state_bwd_workspace_bytes(d->head_dim, d->rows, d->max_state_len);
+  if (!d || check_layer(&d->layer) != KVM_OK || d->max_state_len < 1) return -1;
+  return kvm::state_bwd_workspace_bytes(d->layer.head_dim, d->layer.batch * d->layer.kv_heads, d->max_state_len);
 }
 
 int kvm_state_backward(const kvm_state_bwd_desc *d, void *stream) {
   if (!d) return fail(KVM_EINVAL, "state backward descriptor is NULL");
-  const int64_t D = d->head_dim, T = d->seq_len, C = d->chunk_len, L0 = d->initial_state_len,
-                nu = d->n_updates, S = d->max_state_len, rows = d->rows;
-  if (D != 64 && D != 128) return fail(KVM_EINVAL, "state backward: head_dim must be 64 or 128");
-  if (rows < 1 || T < 1 || C < 1 || L0 < 1 || L0 > T || S < L0 || nu < 0)
-    return fail(KVM_EINVAL, "state backward: sizes out of range");
+  int rc;
+  const kvm_layer &L = d->layer;
+  if ((rc = check_layer(&L)) || (rc = check_seq(&d->kv, "kv"))) return rc;
+  if (d->kv.ring) return fail(KVM_EINVAL, "state backward: the token source cannot be a ring");
+  const int64_t D = L.head_dim, T = d->seq_len, C = L.chunk_len, L0 = d->initial_state_len,
+                nu = d->n_updates, S = d->max_state_len, rows = L.batch * L.kv_heads;
+  if (T < 1 || L0 != std::min(T, C) || S < L0 || nu < 0)
+    return fail(KVM_EINVAL, "state backward: sizes out of range (initial_state_len must be min(T, chunk_len))");
   if (C > kvm::state_bwd_max_chunk())
     return fail(KVM_EINVAL, "state backward: chunk_len above %lld", (long long)kvm::state_bwd_max_chunk());
   if (nu >= kvm::kMaxChunksPerLaunch)
     return fail(KVM_EINVAL, "state backward handles at most %d updates", kvm::kMaxChunksPerLaunch - 1);
-  const void *f32[] = {d->ln_w, d->ln_b, d->ik, d->iv, d->ivl, d->d_snap_k, d->d_snap_v,
-                       d->d_ik, d->d_iv, d->d_ivl, d->d_ln};
-  for (const void *p : f32)
+  const void *need[] = {d->d_snap_k, d->d_snap_v, d->dk, d->dv, d->dgate, d->d_ln};
+  for (const void *p : need)
     if (!p || !aligned16(p)) return fail(KVM_EINVAL, "state backward: a required pointer is NULL or unaligned");
   kvm::UpdTable U;
-  int64_t len = L0;
+  int64_t len = L0, prev_end = L0;
   for (int64_t u = 0; u < nu; ++u) {
     if (!d->upd_token_begin || !d->upd_state_before || !d->upd_n_append)
       return fail(KVM_EINVAL, "state backward: the update schedule is NULL");
     const int32_t tb = d->upd_token_begin[u], before = d->upd_state_before[u], na = d->upd_n_append[u];
-    if (tb < 0 || tb + C > T || before != len || na < 0 || na > C || before + na > S)
+    // Update chunks are disjoint, follow the initial tokens and hold C tokens each.
+    if (tb < prev_end || tb + C > T || before != len || na < 0 || na > C || before + na > S)
       return fail(KVM_EINVAL, "update %lld schedule (token %d, state %d + %d) is invalid", (long long)u, tb,
                   before, na);
     U.token_begin[u] = tb;
     U.state_before[u] = before;
     U.n_append[u] = na;
     len = before + na;
+    prev_end = tb + C;
   }
-  if (nu > 0) {
-    const void *tok[] = {d->mk, d->mv, d->ak, d->av, d->avl, d->route_log, d->append_log,
-                         d->d_mk, d->d_mv, d->d_ak, d->d_av, d->d_avl};
-    for (const void *p : tok)
-      if (!p || !aligned16(p)) return fail(KVM_EINVAL, "state backward: token arrays must be set and aligned");
-  }
-  const int64_t need = kvm::state_bwd_workspace_bytes(D, rows, S);
-  if (!d->workspace || d->workspace_bytes < need || !aligned16(d->workspace))
+  if (nu > 0 && (!d->route_log || !d->append_log))
+    return fail(KVM_EINVAL, "state backward: route_log and append_log are required");
+  const int64_t need_ws = kvm::state_bwd_workspace_bytes(D, rows, S);
+  if (!d->workspace || d->workspace_bytes < need_ws || !aligned16(d->workspace))
     return fail(KVM_ESPACE, "state backward workspace of %lld bytes is smaller than %lld",
-                (long long)d->workspace_bytes, (long long)need);
+                (long long)d->workspace_bytes, (long long)need_ws);
   kvm::StateBwdArgs a;
-  a.rows = rows; a.T = T; a.head_dim = D; a.chunk_len = C; a.L0 = L0; a.n_updates = nu;
-  a.max_state_len = S;
-  a.ln_eps = d->ln_eps;
-  a.ln_w = d->ln_w; a.ln_b = d->ln_b;
-  a.mk = d->mk; a.mv = d->mv; a.ak = d->ak; a.av = d->av; a.avl = d->avl;
-  a.ik = d->ik; a.iv = d->iv; a.ivl = d->ivl;
+  a.L = L;
+  a.kv = d->kv;
+  a.rows = rows; a.T = T; a.L0 = L0; a.n_updates = nu; a.max_state_len = S;
   a.route_log = d->route_log; a.append_log = d->append_log;
   a.d_snap_k = d->d_snap_k; a.d_snap_v = d->d_snap_v;
-  a.d_mk = d->d_mk; a.d_mv = d->d_mv; a.d_ak = d->d_ak; a.d_av = d->d_av; a.d_avl = d->d_avl;
-  a.d_ik = d->d_ik; a.d_iv = d->d_iv; a.d_ivl = d->d_ivl;
+  a.dk = d->dk; a.dv = d->dv; a.dgate = d->dgate;
   a.d_ln = d->d_ln;
   KVM_HIP(kvm::launch_state_backward(a, U, static_cast<float *>(d->workspace), as_stream(stream)),
           "state backward");

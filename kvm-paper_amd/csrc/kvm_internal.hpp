@@ -197,17 +197,16 @@ int64_t attn_bwd_workspace_bytes(const kvm_layer &L, int64_t n_chunks);
 hipError_t launch_attn_backward(const kvm_layer &L, const BwdArgs &a, const ChunkTable &table,
                                 float *tpart, hipStream_t stream);
 
-// Memory-state backward (kvm_state_bwd.hip).  Token-row arrays are
-// [rows, T, D] fp32, per-token scalars [rows, T]; the initial rows
-// [rows, L0, D]; snapshot gradients [n_updates + 1, rows, max_state_len, D].
+// Memory-state backward (kvm_state_bwd.hip).  dk / dv are [rows, T, D]
+// fp32 (added to), dgate [rows, T]; snapshot gradients
+// [n_updates + 1, rows, max_state_len, D].
 struct StateBwdArgs {
-  int64_t rows, T, head_dim, chunk_len, L0, n_updates, max_state_len;
-  double ln_eps;
-  const float *ln_w, *ln_b;
-  const float *mk, *mv, *ak, *av, *avl, *ik, *iv, *ivl;
+  kvm_layer L;
+  kvm_seq kv;
+  int64_t rows, T, L0, n_updates, max_state_len;
   const int32_t *route_log, *append_log;  // [n_updates, rows, chunk_len]
   const float *d_snap_k, *d_snap_v;
-  float *d_mk, *d_mv, *d_ak, *d_av, *d_avl, *d_ik, *d_iv, *d_ivl;
+  float *dk, *dv, *dgate;
   float *d_ln;                            // [2, D]
 };
 // Per-update schedule, passed by value as a kernel argument (3 KiB).

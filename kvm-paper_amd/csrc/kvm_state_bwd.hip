@@ -16,20 +16,31 @@
 //   an appended token gets the same for the slot's base row, plus the vlen
 //   gradient sum_{s'} G_v . normalize(s_v) of the snapshots holding it;
 //   the initial rows get dL/ds(0).
+// The token rows themselves are functions of the raw tokens
+// (model/kvm_mixer.py:120-129, 231-248, 321-340, 434-447):
+//   prep = LayerNorm_s(k with dims < rope_partial_dim zeroed),
+//   merge rows   (prep * g if gate_keys, v * g if gate_values),
+//   append rows  (the merge rows if gate_appends, else prep, v), vlen = |append value row|,
+//   initial rows (prep * g, v * g if gate_initial, else prep, v), vlen = |v|,
+// and this kernel recomputes them from the bf16 tokens and carries the chain
+// rule down to dk, dv (added to the attention backward's window gradients),
+// the merge gate and the LayerNorm parameters (both uses of ln_s_k).
 // One workgroup owns RPW slots of one row and holds their sums and gradient
 // accumulators in registers (D/8 lanes per slot row): a forward scan over the
 // updates rebuilds the final sums, a reverse scan accumulates H and undoes
-// each update's merges.  Every token is routed to exactly one slot, so each
-// output row has exactly one writer (no atomics).
+// each update's merges.  Every state token is routed to exactly one slot, so
+// each token row of dk / dv / dgate has exactly one writer (no atomics).
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
+#include "kvm_seq.hpp"
 
 namespace kvm {
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxChunk = 4096;
+constexpr float kNormEps = 1e-12f;  // torch.nn.functional.normalize
 
 __device__ __forceinline__ void load8f(const float *p, float (&x)[8]) {
   const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
@@ -41,64 +52,215 @@ __device__ __forceinline__ void store8f(float *p, const float (&x)[8]) {
   *reinterpret_cast<float4 *>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
 }
 
+enum TokKind { kMerged = 0, kAppended = 1, kInitial = 2 };
+
+// One raw token of the row, recomputed in fp32: xh = normalised rope-zeroed
+// key, prep = xh * w + b, the value row and the gate.
+struct Tok {
+  float xh[8], prep[8], v[8];
+  float r, g;
+};
+
+template <int D>
+__device__ __forceinline__ void load_tok(const StateBwdArgs &A, int b, int h, int64_t t, int part,
+                                         const float (&w)[8], const float (&bb)[8], Tok &x) {
+  float k[8];
+  load8(seq_k(A.kv, b, h, t) + part * 8, k);
+  load8(seq_v(A.kv, b, h, t) + part * 8, x.v);
+  x.g = seq_g(A.kv, b, h, t);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (part * 8 + e < A.L.rope_partial_dim) k[e] = 0.f;
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += k[e];
+  const float mean = group_sum<D / 8>(s) / float(D);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q += (k[e] - mean) * (k[e] - mean);
+  x.r = 1.0f / sqrtf(group_sum<D / 8>(q) / float(D) + float(A.L.ln_eps));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x.xh[e] = (k[e] - mean) * x.r;
+    x.prep[e] = x.xh[e] * w[e] + bb[e];
+  }
+}
+
+// Whether the gate multiplies a token's key / value row: merge rows follow
+// gate_keys / gate_values, appended rows are the merge rows when
+// gate_appends is set (else ungated), initial rows follow gate_initial
+// (model/kvm_mixer.py:264-281, 434-441).
+__device__ __forceinline__ bool gate_k(const kvm_layer &L, int kind) {
+  return kind == kMerged ? L.gate_keys != 0
+         : kind == kAppended ? (L.gate_appends != 0 && L.gate_keys != 0)
+                             : L.gate_initial != 0;
+}
+__device__ __forceinline__ bool gate_v(const kvm_layer &L, int kind) {
+  return kind == kMerged ? L.gate_values != 0
+         : kind == kAppended ? (L.gate_appends != 0 && L.gate_values != 0)
+                             : L.gate_initial != 0;
+}
+
+// The key / value rows a token contributes to the state.
+__device__ __forceinline__ void tok_rows(const kvm_layer &L, const Tok &x, int kind, float (&rk)[8],
+                                         float (&rv)[8]) {
+  const bool gk = gate_k(L, kind), gv = gate_v(L, kind);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    rk[e] = gk ? x.prep[e] * x.g : x.prep[e];
+    rv[e] = gv ? x.v[e] * x.g : x.v[e];
+  }
+}
+
+// Chain rule from the gradients of a token's state rows (dk_row, dv_row and
+// the vlen gradient dl) to dk, dv, dgate of the token and the LayerNorm
+// parameters; adds into A.dk / A.dv (one writer per token row).
+template <int D>
+__device__ __forceinline__ void tok_backward(const StateBwdArgs &A, const Tok &x, int kind, int64_t tok_row,
+                                             int part, const float (&w)[8], const float (&dk_row)[8],
+                                             const float (&dv_row)[8], float dl, float (&dlw)[8],
+                                             float (&dlb)[8]) {
+  const bool gk = gate_k(A.L, kind), gv = gate_v(A.L, kind);
+  float dxv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dxv[e] = dv_row[e];
+  float dvl[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // vlen gradient on the raw value (initial)
+  if (kind != kMerged) {
+    // vlen = |append value row| (appended) or |v| (initial)
+    float rv[8], n2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      rv[e] = (kind == kAppended && gv) ? x.v[e] * x.g : x.v[e];
+      n2 += rv[e] * rv[e];
+    }
+    const float n = sqrtf(group_sum<D / 8>(n2));
+    const float c = n > 0.f ? dl / n : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (kind == kAppended)
+        dxv[e] += c * rv[e];
+      else
+        dvl[e] = c * rv[e];
+    }
+  }
+  float dg = 0.f, dprep[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dprep[e] = gk ? dk_row[e] * x.g : dk_row[e];
+    if (gk) dg += dk_row[e] * x.prep[e];
+    if (gv) dg += dxv[e] * x.v[e];
+  }
+  dg = group_sum<D / 8>(dg);
+  float m1 = 0.f, m2 = 0.f, dxh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dxh[e] = dprep[e] * w[e];
+    m1 += dxh[e];
+    m2 += dxh[e] * x.xh[e];
+    dlw[e] += dprep[e] * x.xh[e];
+    dlb[e] += dprep[e];
+  }
+  m1 = group_sum<D / 8>(m1) / float(D);
+  m2 = group_sum<D / 8>(m2) / float(D);
+  const int64_t o = tok_row * D + part * 8;
+  float dk[8], dv[8];
+  load8f(A.dk + o, dk);
+  load8f(A.dv + o, dv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (part * 8 + e >= A.L.rope_partial_dim) dk[e] += x.r * (dxh[e] - m1 - x.xh[e] * m2);
+    dv[e] += (gv ? dxv[e] * x.g : dxv[e]) + dvl[e];
+  }
+  store8f(A.dk + o, dk);
+  store8f(A.dv + o, dv);
+  if (part == 0) A.dgate[tok_row] = dg;
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable U, float *__restrict__ dln_part) {
   constexpr int GL = D / 8;            // lanes per slot row
   constexpr int RPW = kThreads / GL;   // slot rows per workgroup
-  __shared__ int32_t rt[kMaxChunk];    // route_log of the current update
-  __shared__ int32_t ap[kMaxChunk];    // append_log of the current update
+  // Tokens of the current update routed to this workgroup's slots, in token
+  // order: (token << 8) | (local slot << 1) | appended.
+  __shared__ int32_t lst[kMaxChunk];
+  __shared__ int wsum[kThreads / 64];
   __shared__ float red[kThreads / 64][2][D];
   const int tid = threadIdx.x, part = tid % GL, lane = tid & 63, wave = tid >> 6;
   const int row = blockIdx.y;
-  const int j = blockIdx.x * RPW + tid / GL;  // this thread's slot
-  const int C = int(A.chunk_len), T = int(A.T), L0 = int(A.L0), nu = int(A.n_updates);
-  const int64_t rowT = int64_t(row) * T;
-  const float eps = float(A.ln_eps);
-  float w[8];
-  load8f(A.ln_w + part * 8, w);
+  const int hb = row / int(A.L.kv_heads), hh = row % int(A.L.kv_heads);
+  const int j0 = blockIdx.x * RPW, my = tid / GL;
+  const int j = j0 + my;  // this thread's slot
+  const int C = int(A.L.chunk_len), L0 = int(A.L0), nu = int(A.n_updates);
+  const int64_t rowT = int64_t(row) * A.T;
+  const float eps = float(A.L.ln_eps);
+  float w[8], bb[8];
+  load8f(static_cast<const float *>(A.L.ln_weight) + part * 8, w);
+  load8f(static_cast<const float *>(A.L.ln_bias) + part * 8, bb);
   auto tb_of = [&](int u) { return U.token_begin[u]; };
   auto before_of = [&](int u) { return U.state_before[u]; };
   auto napp_of = [&](int u) { return U.n_append[u]; };
+  // Ordered compaction of update u's routes onto [j0, j0 + RPW); returns the
+  // list length (the same in every thread).
   auto stage = [&](int u) {
     const int64_t o = (int64_t(u) * A.rows + row) * C;
-    __syncthreads();
-    for (int t = tid; t < C; t += kThreads) {
-      rt[t] = A.route_log[o + t];
-      ap[t] = A.append_log[o + t];
+    int n = 0;
+    __syncthreads();  // the previous list has been read
+    for (int t0 = 0; t0 < C; t0 += kThreads) {
+      const int t = t0 + tid;
+      int r = -1, a = 0;
+      if (t < C) {
+        r = A.route_log[o + t];
+        a = A.append_log[o + t];
+      }
+      const bool hit = r >= j0 && r < j0 + RPW;
+      const uint64_t m = __ballot(hit);
+      if (lane == 0) wsum[wave] = __popcll(m);
+      __syncthreads();
+      int woff = 0, tot = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < kThreads / 64; ++w2) {
+        woff += w2 < wave ? wsum[w2] : 0;
+        tot += wsum[w2];
+      }
+      if (hit)
+        lst[n + woff + __popcll(m & ((uint64_t(1) << lane) - 1))] = (t << 8) | ((r - j0) << 1) | (a ? 1 : 0);
+      n += tot;
+      __syncthreads();  // wsum is rewritten next round; lst complete after the last
     }
-    __syncthreads();
+    return n;
   };
-  auto ld_row = [&](const float *base, int64_t r, float (&x)[8]) { load8f(base + r * D + part * 8, x); };
 
   // ---- forward scan: final fp32 sums of my slot, and its vlen.
   float sk[8], sv[8];
   float vlen = 0.f;
   if (j < L0) {
-    ld_row(A.ik, int64_t(row) * L0 + j, sk);
-    ld_row(A.iv, int64_t(row) * L0 + j, sv);
-    vlen = A.ivl[int64_t(row) * L0 + j];
+    Tok x;
+    load_tok<D>(A, hb, hh, j, part, w, bb, x);
+    tok_rows(A.L, x, kInitial, sk, sv);
+    vlen = row_norm8<D>(x.v);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) sk[e] = sv[e] = 0.f;
   }
   for (int u = 0; u < nu; ++u) {
-    stage(u);
+    const int n = stage(u);
     const int tb = tb_of(u);
     float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int t = 0; t < C; ++t) {
-      if (rt[t] != j) continue;
-      float xk[8], xv[8];
-      if (ap[t]) {  // the slot's base row (appended before this update's merges)
-        ld_row(A.ak, rowT + tb + t, sk);
-        ld_row(A.av, rowT + tb + t, sv);
-        vlen = A.avl[rowT + tb + t];
+    for (int i = 0; i < n; ++i) {
+      const int e = lst[i];
+      if (((e >> 1) & 127) != my) continue;
+      Tok x;
+      load_tok<D>(A, hb, hh, tb + (e >> 8), part, w, bb, x);
+      if (e & 1) {  // the slot's base row (appended before this update's merges)
+        tok_rows(A.L, x, kAppended, sk, sv);
+        vlen = row_norm8<D>(sv);
       } else {
-        ld_row(A.mk, rowT + tb + t, xk);
-        ld_row(A.mv, rowT + tb + t, xv);
+        float xk[8], xv[8];
+        tok_rows(A.L, x, kMerged, xk, xv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          dk[e] += xk[e];
-          dv[e] += xv[e];
+        for (int c = 0; c < 8; ++c) {
+          dk[c] += xk[c];
+          dv[c] += xv[c];
         }
       }
     }
@@ -144,41 +306,42 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
       m2 = group_sum<GL>(m2) / float(D);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acck[e] += r * (dxh[e] - m1 - xh[e] * m2);
+      // va = sv / max(|sv|, eps) * vlen
       float nn = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) nn += sv[e] * sv[e];
       const float nrm = sqrtf(group_sum<GL>(nn));
-      const float inv = nrm > 0.f ? 1.0f / nrm : 0.f;
+      const float inv = 1.0f / fmaxf(nrm, kNormEps);
       float gs = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) gs += gv[e] * sv[e] * inv;
       gs = group_sum<GL>(gs);
       accl += gs;
+      const float proj = nrm > kNormEps ? gs * inv : 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) accv[e] += vlen * inv * (gv[e] - gs * sv[e] * inv);
+      for (int e = 0; e < 8; ++e) accv[e] += vlen * inv * (gv[e] - proj * sv[e]);
     }
     if (s == 0) break;
     // Undo update s - 1, which built snapshot s from snapshot s - 1.
     const int u = s - 1;
-    stage(u);
+    const int n = stage(u);
     const int tb = tb_of(u);
-    for (int t = 0; t < C; ++t) {
-      if (rt[t] != j) continue;
-      const int64_t o = (rowT + tb + t) * D + part * 8;
-      if (ap[t]) {
-        store8f(A.d_ak + o, acck);
-        store8f(A.d_av + o, accv);
-        if (part == 0) A.d_avl[rowT + tb + t] = accl;
+    for (int i = 0; i < n; ++i) {
+      const int e = lst[i];
+      if (((e >> 1) & 127) != my) continue;
+      const int64_t t = tb + (e >> 8);
+      Tok x;
+      load_tok<D>(A, hb, hh, t, part, w, bb, x);
+      if (e & 1) {
+        tok_backward<D>(A, x, kAppended, rowT + t, part, w, acck, accv, accl, dlw, dlb);
       } else {
-        store8f(A.d_mk + o, acck);
-        store8f(A.d_mv + o, accv);
+        tok_backward<D>(A, x, kMerged, rowT + t, part, w, acck, accv, 0.f, dlw, dlb);
         float xk[8], xv[8];
-        ld_row(A.mk, rowT + tb + t, xk);
-        ld_row(A.mv, rowT + tb + t, xv);
+        tok_rows(A.L, x, kMerged, xk, xv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          sk[e] -= xk[e];
-          sv[e] -= xv[e];
+        for (int c = 0; c < 8; ++c) {
+          sk[c] -= xk[c];
+          sv[c] -= xv[c];
         }
       }
     }
@@ -189,10 +352,9 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
     }
   }
   if (j < L0) {
-    const int64_t o = (int64_t(row) * L0 + j) * D + part * 8;
-    store8f(A.d_ik + o, acck);
-    store8f(A.d_iv + o, accv);
-    if (part == 0) A.d_ivl[int64_t(row) * L0 + j] = accl;
+    Tok x;
+    load_tok<D>(A, hb, hh, j, part, w, bb, x);
+    tok_backward<D>(A, x, kInitial, rowT + j, part, w, acck, accv, accl, dlw, dlb);
   }
   // LayerNorm parameter gradients: sum over my slots, then this workgroup's partial.
 #pragma unroll
@@ -218,13 +380,18 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   }
 }
 
-template <int D>
-__global__ void k_state_bwd_ln(const float *part, int nwg, float *out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= 2 * D) return;
+// d ln_w / d ln_b: feature blockIdx.x of the 2D outputs summed over the
+// workgroups' partials (fixed order: strided per thread, then a tree).
+__global__ __launch_bounds__(256) void k_state_bwd_ln(const float *part, int nwg, int width, float *out) {
+  __shared__ float wred[4];
+  const int f = blockIdx.x, tid = threadIdx.x;
   float a = 0.f;
-  for (int w = 0; w < nwg; ++w) a += part[int64_t(w) * 2 * D + i];
-  out[i] = a;
+  for (int w = tid; w < nwg; w += 256) a += part[int64_t(w) * width + f];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o);
+  if ((tid & 63) == 0) wred[tid >> 6] = a;
+  __syncthreads();
+  if (tid == 0) out[f] = (wred[0] + wred[1]) + (wred[2] + wred[3]);
 }
 
 template <int D>
@@ -234,8 +401,8 @@ hipError_t launch_d(const StateBwdArgs &a, const UpdTable &sched, float *part, h
   hipLaunchKernelGGL((k_state_bwd<D>), grid, dim3(kThreads), 0, s, a, sched, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_state_bwd_ln<D>), dim3((2 * D + 127) / 128), dim3(128), 0, s, part,
-                     int(grid.x * grid.y), a.d_ln);
+  hipLaunchKernelGGL(k_state_bwd_ln, dim3(2 * D), dim3(256), 0, s, part, int(grid.x * grid.y), 2 * D,
+                     a.d_ln);
   return hipGetLastError();
 }
 
@@ -251,7 +418,7 @@ int64_t state_bwd_max_chunk() { return kMaxChunk; }
 
 hipError_t launch_state_backward(const StateBwdArgs &a, const UpdTable &sched, float *part,
                                  hipStream_t stream) {
-  if (a.head_dim == 128) return launch_d<128>(a, sched, part, stream);
+  if (a.L.head_dim == 128) return launch_d<128>(a, sched, part, stream);
   return launch_d<64>(a, sched, part, stream);
 }
 

@@ -106,20 +106,16 @@ class KvmPrefillBwdDesc(ctypes.Structure):
 
 class KvmStateBwdDesc(ctypes.Structure):
     _fields_ = [
-        ("rows", _i64), ("seq_len", _i64), ("head_dim", _i64), ("chunk_len", _i64),
-        ("ln_eps", ctypes.c_double),
-        ("ln_w", _vp), ("ln_b", _vp),
-        ("mk", _vp), ("mv", _vp), ("ak", _vp), ("av", _vp), ("avl", _vp),
-        ("ik", _vp), ("iv", _vp), ("ivl", _vp),
-        ("initial_state_len", _i64), ("n_updates", _i64),
+        ("layer", KvmLayer),
+        ("kv", KvmSeq),
+        ("seq_len", _i64), ("initial_state_len", _i64), ("n_updates", _i64),
         ("upd_token_begin", ctypes.POINTER(ctypes.c_int32)),
         ("upd_state_before", ctypes.POINTER(ctypes.c_int32)),
         ("upd_n_append", ctypes.POINTER(ctypes.c_int32)),
         ("route_log", _vp), ("append_log", _vp),
         ("max_state_len", _i64),
         ("d_snap_k", _vp), ("d_snap_v", _vp),
-        ("d_mk", _vp), ("d_mv", _vp), ("d_ak", _vp), ("d_av", _vp), ("d_avl", _vp),
-        ("d_ik", _vp), ("d_iv", _vp), ("d_ivl", _vp),
+        ("dk", _vp), ("dv", _vp), ("dgate", _vp),
         ("d_ln", _vp),
         ("workspace", _vp), ("workspace_bytes", _i64),
     ]

@@ -17,14 +17,11 @@ Backward:
     values' gradients, the gradients of every snapshot's key and value rows,
     and the two head temperatures' gradients;
   * memory state (HIP, ``kvm_state_backward``): the snapshot rows are
-    functions of the token rows through LayerNorm_s(s_k), normalize(s_v) *
-    vlen and the merge sums under the fixed routes; the kernel pulls the
-    snapshot-row gradients back to the merge, append and initial token rows
-    (and the snapshot LayerNorm's parameters);
-  * token rows (torch autograd, elementwise): the token rows are
-    LayerNorm_s of the rope-zeroed keys, the values and the merge gate's
-    products, so their gradients reach k, v, the gate and ln_s_k through
-    one vectorised autograd call.
+    functions of the tokens through LayerNorm_s(s_k), normalize(s_v) * vlen,
+    the merge sums under the fixed routes and the token rows (LayerNorm_s of
+    the rope-zeroed keys, the values, the merge gate's products); the kernel
+    pulls the snapshot-row gradients back through all of it to k, v (added
+    to the window gradients), the gate and the ln_s_k parameters.
 
 ``replay_snapshot_rows`` restates the snapshots in torch (fp32, differentiable)
 and serves as the reference the state kernel is tested against.
@@ -98,16 +95,6 @@ def replay_snapshot_rows(k, v, gate, ln_w, ln_b, plan, route_log, append_log, cf
     return snaps
 
 
-def _layer_cfg(mixer):
-    return {
-        "eps": float(mixer.ln_s_k.eps), "rope_partial_dim": int(mixer.rope_partial_dim),
-        "gate_keys": bool(mixer.config.kvm_use_merge_gate_keys),
-        "gate_values": bool(mixer.config.kvm_use_merge_gate_values),
-        "gate_appends": bool(mixer.config.kvm_apply_merge_gate_to_appends),
-        "gate_initial": bool(mixer.config.kvm_apply_merge_gate_to_initial_state),
-    }
-
-
 def attention_backward(mixer, q, k, v, gate, res, dout):
     """The HIP attention backward of one prefill (kvm_prefill_backward).
 
@@ -179,82 +166,51 @@ class KVMPrefillFunction(torch.autograd.Function):
         q, k, v, gate, ln_w, ln_b, state_temp, front_temp = ctx.saved_tensors
         mixer, res = ctx.mixer, ctx.res
         plan = res["plan"]
-        B, Hkv, T, D = k.shape
-        rows = B * Hkv
         dq, dk_w, dv_w, d_snap_k, d_snap_v, d_ts, d_tf = attention_backward(mixer, q, k, v, gate, res, dout)
         if plan.n_chunks > mixer.config.n_bswa_chunks:  # some query chunk read the memory state
-            gk, gv, gg, glw, glb = state_backward(
-                k.detach().reshape(rows, T, D), v.detach().reshape(rows, T, D), gate.detach().reshape(rows, T),
-                ln_w.detach(), ln_b.detach(), plan, res["route_log"], res["append_log"], d_snap_k, d_snap_v,
-                _layer_cfg(mixer))
-            dk = (dk_w + gk.view(B, Hkv, T, D)).to(k.dtype)
-            dv = (dv_w + gv.view(B, Hkv, T, D)).to(v.dtype)
-            dgate = gg.view(gate.shape).to(gate.dtype)
+            dgate, d_ln = state_backward(mixer, k, v, gate, res, d_snap_k, d_snap_v, dk_w, dv_w)
+            glw, glb = d_ln[0], d_ln[1]
         else:
-            dk, dv = dk_w.to(k.dtype), dv_w.to(v.dtype)
-            dgate = torch.zeros_like(gate)
+            dgate = torch.zeros(gate.shape, device=gate.device, dtype=torch.float32)
             glw, glb = torch.zeros_like(ln_w, dtype=torch.float32), torch.zeros_like(ln_b, dtype=torch.float32)
-        return (None, dq.to(q.dtype), dk, dv, dgate, glw.to(ln_w.dtype), glb.to(ln_b.dtype),
-                d_ts.to(state_temp.dtype), d_tf.to(front_temp.dtype))
+        return (None, dq.to(q.dtype), dk_w.to(k.dtype), dv_w.to(v.dtype), dgate.view(gate.shape).to(gate.dtype),
+                glw.to(ln_w.dtype), glb.to(ln_b.dtype), d_ts.to(state_temp.dtype), d_tf.to(front_temp.dtype))
 
 
-def token_rows(k, v, gate, ln_w, ln_b, L0, cfg):
-    """The token rows the memory state is built from (fp32, differentiable):
-    merge rows (mk, mv), append rows (ak, av) and their vlen |av|, initial
-    rows (ik, iv) and their vlen |v| (model/kvm_mixer.py:403-447 prep and
-    initial state; :231-248 append; :321-340 merge)."""
-    D = k.size(-1)
-    r = int(cfg["rope_partial_dim"])
-    kz = torch.cat([torch.zeros_like(k[..., :r]), k[..., r:]], dim=-1)
-    prep = F.layer_norm(kz, (D,), ln_w, ln_b, cfg["eps"])
-    g = gate.unsqueeze(-1)
-    mk = prep * g if cfg["gate_keys"] else prep
-    mv = v * g if cfg["gate_values"] else v
-    ak, av = (mk, mv) if cfg["gate_appends"] else (prep, v)
-    ik = (prep * g if cfg["gate_initial"] else prep)[:, :L0]
-    iv = (v * g if cfg["gate_initial"] else v)[:, :L0]
-    return {"mk": mk, "mv": mv, "ak": ak, "av": av, "avl": av.norm(dim=-1),
-            "ik": ik, "iv": iv, "ivl": v[:, :L0].norm(dim=-1)}
+def state_backward(mixer, k, v, gate, res, d_snap_k, d_snap_v, dk, dv):
+    """The memory state's share of the backward (``kvm_state_backward``).
 
-
-def state_backward(k, v, gate, ln_w, ln_b, plan, route_log, append_log, d_snap_k, d_snap_v, cfg):
-    """Gradients of sum_s <rows(snapshot s), d_snap[s]> with respect to k, v
-    [rows, T, D], gate [rows, T], ln_w and ln_b (fp32), the routes fixed.
-
-    The memory-state part runs in ``kvm_state_backward`` (HIP); the token
-    rows' own LayerNorm / gate products are differentiated by torch.
+    k, v: [B, Hkv, T, D] bf16 and gate [B, Hkv, T, 1] as the forward read
+    them; ``res`` the forward's ``prefill_raw`` result (plan, route_log,
+    append_log); d_snap_k / d_snap_v the snapshot-row gradients; dk / dv
+    fp32 [B, Hkv, T, D] contiguous, to which the state's share is added in
+    place.  Returns dgate fp32 [B, Hkv, T] and the ln_s_k gradients [2, D].
     Reference: _live_state_dkdv_to_raw_grad_kernel, _reverse_route_scatter_grad_split_kernel,
     _initial_state_grad_kernel (model/kernels/kvm_triton_training_kernels.py:2093-2745)."""
-    rows, T, D = k.shape
+    B, Hkv, T, D = k.shape
     dev = k.device
+    plan = res["plan"]
     nu = plan.n_updates
-    L0 = plan.initial_state_len
-    with torch.enable_grad():
-        leaves = [x.detach().float().requires_grad_(True) for x in (k, v, gate, ln_w, ln_b)]
-        kf, vf, gf, lw, lb = leaves
-        tr = token_rows(kf, vf, gf, lw, lb, L0, cfg)
-    names = ("mk", "mv", "ak", "av", "avl", "ik", "iv", "ivl")
-    vals = {n: tr[n].detach().contiguous() for n in names}
-    grads = {n: torch.zeros_like(vals[n]) for n in names}
+    for name, t in (("dk", dk), ("dv", dv)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (B, Hkv, T, D):
+            raise ValueError(f"{name} must be contiguous fp32 [B, Hkv, T, D]")
+    seq, keep = _lib.seq4(k, v, gate)
+    layer = mixer._layer_struct(B, dev)
+    dgate = torch.zeros(B, Hkv, T, device=dev, dtype=torch.float32)
     d_ln = torch.empty(2, D, device=dev, dtype=torch.float32)
-    lnw32, lnb32 = lw.detach().contiguous(), lb.detach().contiguous()
     d = _lib.KvmStateBwdDesc()
-    d.rows, d.seq_len, d.head_dim, d.chunk_len = rows, T, D, plan.chunk_len
-    d.ln_eps = float(cfg["eps"])
-    d.ln_w, d.ln_b = lnw32.data_ptr(), lnb32.data_ptr()
-    for n in names:
-        setattr(d, n, vals[n].data_ptr())
-        setattr(d, "d_" + n, grads[n].data_ptr())
-    d.initial_state_len, d.n_updates = L0, nu
+    d.layer = layer.struct
+    d.kv = seq
+    d.seq_len, d.initial_state_len, d.n_updates = T, plan.initial_state_len, nu
     sched = [_lib.int32_array(a) for a in (plan.upd_token_begin, plan.upd_state_before, plan.upd_n_append)]
     d.upd_token_begin, d.upd_state_before, d.upd_n_append = sched
     if nu:
-        rl = route_log.to(torch.int32).contiguous()
-        al = append_log.to(torch.int32).contiguous()
+        rl = res["route_log"].to(torch.int32).contiguous()
+        al = res["append_log"].to(torch.int32).contiguous()
         d.route_log, d.append_log = rl.data_ptr(), al.data_ptr()
     d.max_state_len = plan.max_state_len
     d.d_snap_k, d.d_snap_v = d_snap_k.data_ptr(), d_snap_v.data_ptr()
-    d.d_ln = d_ln.data_ptr()
+    d.dk, d.dv, d.dgate, d.d_ln = dk.data_ptr(), dv.data_ptr(), dgate.data_ptr(), d_ln.data_ptr()
     lib = _lib.load()
     nws = int(lib.kvm_state_backward_workspace_bytes(ctypes.byref(d)))
     if nws < 0:
@@ -262,10 +218,8 @@ def state_backward(k, v, gate, ln_w, ln_b, plan, route_log, append_log, d_snap_k
     ws = torch.empty(max(nws, 16), device=dev, dtype=torch.uint8)
     d.workspace, d.workspace_bytes = ws.data_ptr(), nws
     _lib.check(lib.kvm_state_backward(ctypes.byref(d), _lib.stream_handle(dev)), "kvm_state_backward")
-    outs = [tr[n] for n in names]
-    gk, gv, gg, glw, glb = torch.autograd.grad(outs, leaves, [grads[n] for n in names], allow_unused=True)
-    zero = lambda t, ref: torch.zeros_like(ref) if t is None else t  # noqa: E731
-    return (zero(gk, kf), zero(gv, vf), zero(gg, gf), zero(glw, lw) + d_ln[0], zero(glb, lb) + d_ln[1])
+    del keep, ws
+    return dgate, d_ln
 
 
 def prefill_with_grad(mixer, q, k, v, gate):
@@ -280,4 +234,4 @@ def prefill_with_grad(mixer, q, k, v, gate):
 
 
 __all__ = ["KVMPrefillFunction", "prefill_with_grad", "replay_snapshot_rows", "attention_backward",
-           "state_backward", "token_rows"]
+           "state_backward"]

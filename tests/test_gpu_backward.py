@@ -184,7 +184,8 @@ def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gate
 def test_state_backward_matches_replay_autograd(B, Hkv, D, C, Tn, mode, gates):
     """kvm_state_backward against torch autograd through replay_snapshot_rows
     (both fp32, the same routes): random snapshot-row gradients pulled back to
-    k, v, the gate and the LayerNorm parameters."""
+    k, v, the gate and the LayerNorm parameters (dk / dv start from zero, so
+    they hold the state's share alone)."""
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
     from kvm_amd import training
@@ -216,12 +217,14 @@ def test_state_backward_matches_replay_autograd(B, Hkv, D, C, Tn, mode, gates):
     dsv = torch.randn(shape, generator=gen).to(DEV)
     lcfg = {"eps": 1e-5, "rope_partial_dim": 16, "gate_keys": gk_, "gate_values": gv_, "gate_appends": ga_,
             "gate_initial": gi_}
-    kk, vv, gg = (x.to(DEV).reshape(rows, Tn, -1) for x in (k, v, g))
-    gg = gg.reshape(rows, Tn)
-    got = training.state_backward(kk, vv, gg, lnw.to(DEV), lnb.to(DEV), plan, res["route_log"],
-                                  res["append_log"], dsk, dsv, lcfg)
+    kd, vd, gd = (x.to(DEV) for x in (k, v, g))
+    dk = torch.zeros(B, Hkv, Tn, D, device=DEV)
+    dv = torch.zeros(B, Hkv, Tn, D, device=DEV)
+    dgate, d_ln = training.state_backward(m, kd, vd, gd, res, dsk, dsv, dk, dv)
     torch.cuda.synchronize()
-    leaves = [x.float().requires_grad_(True) for x in (kk, vv, gg, lnw.to(DEV), lnb.to(DEV))]
+    got = (dk.view(rows, Tn, D), dv.view(rows, Tn, D), dgate.view(rows, Tn), d_ln[0], d_ln[1])
+    leaves = [x.float().requires_grad_(True) for x in (kd.reshape(rows, Tn, D), vd.reshape(rows, Tn, D),
+                                                         gd.reshape(rows, Tn), lnw.to(DEV), lnb.to(DEV))]
     snaps = training.replay_snapshot_rows(*leaves, plan, res["route_log"], res["append_log"], lcfg)
     total = sum((ka * dsk[s, :, :ka.size(1)]).sum() + (va * dsv[s, :, :va.size(1)]).sum()
                 for s, (ka, va) in enumerate(snaps))
