@@ -41,103 +41,15 @@
 // the 8 XCDs) runs a contiguous range of (head, chunk) tiles: the window keys
 // shared by neighbouring chunks stay in that XCD's L2.
 
+#include "kvm_attn_tile.hpp"
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
 
 namespace kvm {
 namespace {
 
-constexpr int BN = 64;   // keys per block
-constexpr int NW = 4;    // waves per workgroup
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kXcds = 8;
-// Buffer resource word 3 for raw (unformatted, unswizzled) dword access with
-// range checking: out-of-range loads return zero (and LDS-DMA lanes out of
-// range write nothing).
-constexpr int kBufWord3 = 0x00020000;
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const f32x2 v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-}
-
-// LDS image of one K (or V) block of 64 keys: D/32 column groups of 4 KiB,
-// each [64 keys][64 bytes]; byte of (key r, 16-byte unit u) =
-// (u/4)*4096 + r*64 + ((u%4) ^ (2 * bit2(r)))*16.
-template <int D>
-struct Lay {
-  static constexpr int GROUPS = D / 32;
-  static constexpr int BLK = GROUPS * 4096;  // bytes of one K (or V) block
-  static constexpr int BUF = 2 * BLK;        // K block then V block
-  static constexpr int CHUNKS = BLK / 1024;  // DMA instructions per K (or V) block
-};
-
-// Resource over keys [0, nvalid) of a range starting at p with row stride
-// `stride` elements.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t key_rsrc(const uint16_t *p, int64_t stride,
-                                                          int nvalid) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(p), (short)0,
-                                           int(nvalid * stride * 2), kBufWord3);
-}
-
-// 16-byte-per-lane buffer load into LDS at M0 + 16 * lane.  Issued from
-// inline assembly: the compiler would otherwise order every later LDS read
-// behind it (it cannot tell the DMA target from the buffer being read).  Its
-// completion is awaited explicitly with s_waitcnt vmcnt(0).
-// M0 is written inside the statement and not declared clobbered (the compiler
-// rejects M0 as a clobber): this is sound only while no compiled code of the
-// kernel keeps a value of its own in M0, which holds for these kernels (their
-// only M0 writes are these statements; checked in the generated assembly).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
-}
-
-// DMA of one block (keys [0, nvalid) of both ranges, set by the resources)
-// into the buffer at LDS byte address `buf`.  Instruction c fills keys
-// 16*(c%4) .. +15 of column group c/4; wave w issues c = w, w + NW, ...
-// `ko`/`vo`: lane offsets within an instruction, key lane/4, unit
-// (lane%4) ^ swap of that key.
-template <int D>
-__device__ __forceinline__ void issue_block(uint32_t buf, __amdgpu_buffer_rsrc_t kr,
-                                            __amdgpu_buffer_rsrc_t vr, uint32_t ko, uint32_t vo,
-                                            uint32_t kstride_b, uint32_t vstride_b, int wave) {
-  constexpr int PER = Lay<D>::CHUNKS / NW;
-  static_assert(Lay<D>::CHUNKS % NW == 0, "DMA instructions split evenly over the waves");
-#pragma unroll
-  for (int t = 0; t < PER; ++t) {
-    const int c = wave + NW * t;
-    const int cg = c >> 2, rq = c & 3;
-    dma16(kr, buf + uint32_t(cg * 4096 + rq * 1024),
-          ko + uint32_t(16 * rq) * kstride_b + uint32_t(cg * 64));
-  }
-#pragma unroll
-  for (int t = 0; t < PER; ++t) {
-    const int c = wave + NW * t;
-    const int cg = c >> 2, rq = c & 3;
-    dma16(vr, buf + uint32_t(Lay<D>::BLK + cg * 4096 + rq * 1024),
-          vo + uint32_t(16 * rq) * vstride_b + uint32_t(cg * 64));
-  }
-}
-
-// Zero the V rows [nv, 64) of a buffer (a block shorter than 64 keys): the
-// DMA leaves them untouched, and their P weights are zero, so stale bytes
-// must not be Inf or NaN.
-template <int D>
-__device__ __forceinline__ void zero_v_tail(unsigned char *vbuf, int nv) {
-  const int units = (BN - nv) * 4 * Lay<D>::GROUPS;  // 16-byte units
-  for (int i = threadIdx.x; i < units; i += NW * 64) {
-    const int cg = i / ((BN - nv) * 4), rem = i % ((BN - nv) * 4);
-    const int r = nv + (rem >> 2), u = rem & 3;
-    *reinterpret_cast<uint4 *>(vbuf + cg * 4096 + r * 64 + u * 16) = make_uint4(0, 0, 0, 0);
-  }
-}
+constexpr int NW = 4;  // waves per workgroup
+using namespace tile;
 
 template <int D>
 struct AttnState {
@@ -394,8 +306,8 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
     auto issue = [&](int jj) {
       const int jn = jj * BN;
       const int nv = min(BN, nkeys - jn);
-      if (nv < BN) zero_v_tail<D>(lds + (jj & 1) * BUF + Lay<D>::BLK, nv);
-      issue_block<D>(lds_base + uint32_t((jj & 1) * BUF),
+      if (nv < BN) zero_v_tail<D, NT>(lds + (jj & 1) * BUF + Lay<D>::BLK, nv);
+      issue_block<D, NW>(lds_base + uint32_t((jj & 1) * BUF),
                      key_rsrc(kp + int64_t(jn) * kstride, kstride, nv),
                      key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), ko, vo, kstride_b,
                      vstride_b, wave);

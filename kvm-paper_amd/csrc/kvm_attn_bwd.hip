@@ -15,58 +15,37 @@
 // :668-830 (window dk/dv) and :2093-2305 (snapshot rows).
 //
 // Two kernels, each owning what it writes (no atomics, deterministic):
-//   k_attn_bwd_dq    one 64-query tile of one (batch, q head): loops over
-//                    its memory rows and window keys; writes dq and a
-//                    per-workgroup temperature partial;
-//   k_attn_bwd_dkdv  one 64-key block of one (batch, kv head), either rows of
-//                    one snapshot or window tokens: loops over every query
-//                    of every head of its GQA group that sees them; writes
-//                    dk and dv.
-// MFMA (v_mfma_f32_16x16x32_bf16) operands are arranged so that the
-// reduction axis is contiguous: S = Q K^T and dP = dO V^T read K / V / Q /
-// dO rows straight from row-major LDS tiles; the products over keys (dq) or
-// over queries (dk, dv) take their bf16 P / dS operand from a per-wave LDS
-// transpose tile and the second operand as 8 column reads.
+//   k_attn_bwd_dq    128 queries (4 waves x 32) of one (batch, q head) in
+//                    chunk m: streams the chunk's memory rows and window keys
+//                    as 64-row K / V blocks; writes dq and a per-workgroup
+//                    temperature partial;
+//   k_attn_bwd_dkdv  64 keys (4 waves x 16) of one (batch, kv head), either
+//                    rows of one snapshot or window tokens: streams every
+//                    query of every head of its GQA group that sees them as
+//                    64-row Q / dO blocks; writes dk and dv.
+// Both stream their blocks the way the forward does (kvm_attn_tile.hpp):
+// LDS-DMA into a swizzled double-buffered image, row fragments with
+// ds_read_b128, transposed fragments with ds_read_b64_tr_b16.  The score-like
+// products put the streamed rows in the A operand, so their C layout (4
+// consecutive rows per lane) is already the B operand of the next product:
+//   dq kernel:   S^T = K Q^T, dP^T = V dO^T, dq^T += K^T dS^T;
+//   dkdv kernel: S = Q K^T, dP = dO V^T, dv^T += dO^T P, dk^T += Q^T dS;
+// P and dS never leave registers.  Each 64-row block is consumed as two
+// 32-row halves (fewer live score registers).
 
+#include "kvm_attn_tile.hpp"
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
 
 namespace kvm {
 namespace {
 
-constexpr int BQ = 64;   // queries per dq workgroup / query block of dkdv
-constexpr int BK = 64;   // keys per key block
-constexpr int NWB = 4;   // waves per workgroup
-constexpr float kLog2e = 1.4426950408889634f;
+using namespace tile;
 
-__device__ __forceinline__ uint4 ld16_or_zero(const uint16_t *p, bool ok) {
-  return ok ? *reinterpret_cast<const uint4 *>(p) : make_uint4(0, 0, 0, 0);
-}
-
-// Row-major tile [rows x D] bf16 in LDS from global rows r0.. (row stride
-// `st` elements), rows >= nvalid zero-filled.
-template <int D, int ROWS>
-__device__ __forceinline__ void stage_rows(uint16_t *lds, const uint16_t *g, int64_t st, int nvalid) {
-  constexpr int PER_ROW = D / 8;
-  for (int i = threadIdx.x; i < ROWS * PER_ROW; i += NWB * 64) {
-    const int r = i / PER_ROW, c = i % PER_ROW;
-    *reinterpret_cast<uint4 *>(lds + r * D + c * 8) = ld16_or_zero(g + int64_t(r) * st + c * 8, r < nvalid);
-  }
-}
-
-// B operand (K x N = 32 x 16) whose K rows are 8 consecutive rows of a
-// row-major LDS tile `t` ([.. x D]) and whose N column is feature `col`:
-// lane l supplies rows k0 + 8 (l / 16) .. + 7 of column col.
-template <int D>
-__device__ __forceinline__ bf16x8 col_frag(const uint16_t *t, int k0, int col) {
-  const int lane = threadIdx.x & 63;
-  const int r = k0 + 8 * (lane >> 4);
-  uint16_t v[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = t[(r + j) * D + col];
-  return as_bf16x8(make_uint4(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16),
-                              v[4] | (uint32_t(v[5]) << 16), v[6] | (uint32_t(v[7]) << 16)));
-}
+constexpr int NWB = 4;            // waves per workgroup
+constexpr int NTB = NWB * 64;     // threads per workgroup
+constexpr int BQ = NWB * 32;      // queries per dq workgroup (32 per wave)
+constexpr int BKW = NWB * 16;     // keys per dk/dv workgroup (16 per wave)
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -74,130 +53,215 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-struct BwdKeySeg {
-  const uint16_t *k, *v;  // row 0 of the segment
-  int64_t kst, vst;       // row strides (elements)
-  int nkeys;
-  int64_t pos0;           // sequence position of row 0 (window); unused for memory rows
-  bool causal;
-  float tau;
-};
+// XCD-contiguous renumbering of a 1-D grid (dispatch is round-robin over the
+// 8 XCDs): each XCD runs a contiguous range of logical tiles, so tiles that
+// share streamed rows share that XCD's L2.
+__device__ __forceinline__ int xcd_logical(int bid, int N) {
+  const int x = bid % kXcds, jx = bid / kXcds;
+  const int q8 = N / kXcds, r8 = N % kXcds;
+  return x * q8 + min(x, r8) + jx;
+}
 
 // ---------------------------------------------------------------------------
-// dq: workgroup = 64 queries of one (batch, q head) in chunk m.
+// dq.  Logical tile order (b, hq, chunk, query tile); the temperature partial
+// of tile w goes to tpart[2 w + segment].
 template <int D>
-__global__ __launch_bounds__(NWB * 64) void k_attn_bwd_dq(kvm_layer L, BwdArgs A, int qtiles,
-                                                          ChunkTable table, float *tpart) {
+__global__ __launch_bounds__(NTB) __attribute__((amdgpu_waves_per_eu(2)))
+void k_attn_bwd_dq(kvm_layer L, BwdArgs A, int qtiles, ChunkTable table, float *tpart) {
   constexpr int KS = D / 32, DT = D / 16;
-  __shared__ __attribute__((aligned(16))) uint16_t kt[BK * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[BK * D];
-  __shared__ __attribute__((aligned(16))) uint16_t dst[NWB][16 * BK];
+  constexpr int BUF = Lay<D>::BUF, BLK = Lay<D>::BLK;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * BUF];
   __shared__ float red[NWB][2];
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
-  const int wg = blockIdx.x;
-  const int qt = wg % qtiles, m = (wg / qtiles) % int(A.n_chunks), qrow = wg / (qtiles * int(A.n_chunks));
+  const int n_chunks = int(A.n_chunks);
+  const int wg = xcd_logical(blockIdx.x, gridDim.x);
+  const int qt = wg % qtiles, m = (wg / qtiles) % n_chunks, qrow = wg / (qtiles * n_chunks);
   const int b = qrow / Hq, hq = qrow % Hq, hk = hq / (Hq / Hkv), kvrow = b * Hkv + hk;
   const int64_t T = A.T;
   const int64_t q0 = int64_t(m) * C + int64_t(qt) * BQ;
   const int64_t q_hi = min(int64_t(m + 1) * C, T);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int64_t qpos0 = q0 + wave * 32;
   const float scale_nat = 1.0f / sqrtf(float(D));
-  float tacc[2] = {0.f, 0.f};
-  if (q0 < q_hi) {
-    // A operands: Q and dO rows of this wave's 16 queries.
-    const int64_t tr = q0 + wave * 16 + (lane & 15);
-    const bool rok = tr < q_hi;
-    const uint16_t *qp = static_cast<const uint16_t *>(A.q) + b * A.q_sb + hq * A.q_sh + tr * A.q_st;
-    const uint16_t *dop = static_cast<const uint16_t *>(A.dout) + b * A.do_sb + hq * A.do_sh + tr * A.do_st;
-    bf16x8 qa[KS], da[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qa[ks] = as_bf16x8(ld16_or_zero(qp + ks * 32 + g * 8, rok));
-      da[ks] = as_bf16x8(ld16_or_zero(dop + ks * 32 + g * 8, rok));
-    }
-    // The lane's C-layout rows: queries q0 + 16 wave + 4 g + i.
-    float lse[4], dl[4];
-    int64_t tq[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      tq[i] = q0 + wave * 16 + 4 * g + i;
-      const bool ok = tq[i] < q_hi;
-      const int64_t o = (int64_t(b) * Hq + hq) * T + (ok ? tq[i] : 0);
-      lse[i] = ok ? A.lse[o] : INFINITY;
-      dl[i] = ok ? A.delta[o] : 0.f;
-    }
-    f32x4 dq[DT];
-#pragma unroll
-    for (int t = 0; t < DT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float t_state = 0.f, t_front = 0.f;  // temperature partials of the two key segments
 
+  // Zero both buffers once: rows past a short block are then zeros or
+  // earlier rows, never uninitialised bytes.
+  for (int i = threadIdx.x; i < 2 * BUF / 16; i += NTB)
+    reinterpret_cast<uint4 *>(lds)[i] = make_uint4(0, 0, 0, 0);
+
+  if (q0 < q_hi) {  // workgroup-uniform
+    // B operands: Q and dO rows rt*16 + lane%16, dims ks*32 + 8*(lane/16).
+    bf16x8 qf[2][KS], dof[2][KS];
+    float lse[2], dl[2];
+    const uint16_t *qb = static_cast<const uint16_t *>(A.q) + b * A.q_sb + hq * A.q_sh;
+    const uint16_t *db = static_cast<const uint16_t *>(A.dout) + b * A.do_sb + hq * A.do_sh;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t t = qpos0 + rt * 16 + (lane & 15);
+      const bool ok = t < q_hi;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        uint4 u = make_uint4(0, 0, 0, 0), w = make_uint4(0, 0, 0, 0);
+        if (ok) {
+          u = *reinterpret_cast<const uint4 *>(qb + t * A.q_st + ks * 32 + (lane >> 4) * 8);
+          w = *reinterpret_cast<const uint4 *>(db + t * A.do_st + ks * 32 + (lane >> 4) * 8);
+        }
+        qf[rt][ks] = as_bf16x8(u);
+        dof[rt][ks] = as_bf16x8(w);
+      }
+      const int64_t o = (int64_t(b) * Hq + hq) * T + (ok ? t : 0);
+      lse[rt] = ok ? A.lse[o] : INFINITY;  // p = 0 for rows past the chunk
+      dl[rt] = ok ? A.delta[o] : 0.f;
+    }
+    // Complete these loads and hide them from the compiler's wait tracking:
+    // inside the block loop the only vector-memory operations are the DMAs.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        asm volatile("" : "+v"(qf[rt][ks]));
+        asm volatile("" : "+v"(dof[rt][ks]));
+      }
+      asm volatile("" : "+v"(lse[rt]));
+      asm volatile("" : "+v"(dl[rt]));
+    }
+    f32x4 dq[2][DT];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dq[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const Lanes lo = lane_offsets(lane);
+    const uint32_t lds_base = uint32_t(uintptr_t((lds_void *)lds));
     const float tau_s = static_cast<const float *>(L.state_temp)[hq];
     const float tau_f = static_cast<const float *>(L.front_temp)[hq];
-    const int64_t wb = max(int64_t(0), int64_t(m - n + 1) * C);
-    BwdKeySeg segs[2];
     const int S = m >= n ? table.state_len[m] : 0;
+    const int64_t wb = max(int64_t(0), int64_t(m - n + 1) * C);
     const int64_t soff = int64_t(table.snap_slot[m]) * A.snap_stride + int64_t(kvrow) * A.snap_cap * D;
-    segs[0] = {A.snap_k + soff, A.snap_v + soff, D, D, S, 0, false, tau_s};
-    const uint16_t *kw = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
-    const uint16_t *vw = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
-    segs[1] = {kw + wb * A.kv.k_st, vw + wb * A.kv.v_st, A.kv.k_st, A.kv.v_st, int(q_hi - wb), wb, true, tau_f};
+    const uint16_t *kwin = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
+    const uint16_t *vwin = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
 #pragma unroll 1
-    for (int sg = 0; sg < 2; ++sg) {
-      const BwdKeySeg &sgm = segs[sg];
-      const float sc = kLog2e * scale_nat * sgm.tau;
-      const float dsc = scale_nat * sgm.tau;
+    for (int seg = 0; seg < 2; ++seg) {
+      const bool st = seg == 0;
       // Causal window: keys past the tile's last query are never visible.
-      const int nk = sgm.causal ? int(min(int64_t(sgm.nkeys), q0 + BQ - sgm.pos0)) : sgm.nkeys;
+      const int nkeys = st ? S : int(min(q_hi, q0 + BQ) - wb);
+      if (nkeys <= 0) continue;
+      const uint16_t *kp = st ? A.snap_k + soff : kwin + wb * A.kv.k_st;
+      const uint16_t *vp = st ? A.snap_v + soff : vwin + wb * A.kv.v_st;
+      const int64_t kstride = st ? D : A.kv.k_st, vstride = st ? D : A.kv.v_st;
+      const uint32_t kstride_b = uint32_t(kstride * 2), vstride_b = uint32_t(vstride * 2);
+      const uint32_t ko = lo.drow * kstride_b + lo.dcol, vo = lo.drow * vstride_b + lo.dcol;
+      const float tau = st ? tau_s : tau_f;
+      const float sc = kLog2e * scale_nat * tau, dsc = scale_nat * tau;
+      const bool causal = !st;
+      const int nb = (nkeys + BN - 1) / BN;
+      float tacc = 0.f;
+      auto issue = [&](int jj) {
+        const int jn = jj * BN;
+        const int nv = min(BN, nkeys - jn);
+        unsigned char *img = lds + (jj & 1) * BUF;
+        if (nv < BN) {  // both halves meet zero weights there
+          zero_v_tail<D, NTB>(img, nv);
+          zero_v_tail<D, NTB>(img + BLK, nv);
+        }
+        issue_block<D, NWB>(lds_base + uint32_t((jj & 1) * BUF), key_rsrc(kp + int64_t(jn) * kstride, kstride, nv),
+                            key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), ko, vo, kstride_b, vstride_b,
+                            wave);
+      };
+      __syncthreads();  // both buffers are free (and zeroed, the first time)
+      issue(0);
 #pragma unroll 1
-      for (int j0 = 0; j0 < nk; j0 += BK) {
-        const int nv = min(BK, nk - j0);
+      for (int j = 0; j < nb; ++j) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        stage_rows<D, BK>(kt, sgm.k + int64_t(j0) * sgm.kst, sgm.kst, nv);
-        stage_rows<D, BK>(vt, sgm.v + int64_t(j0) * sgm.vst, sgm.vst, nv);
-        __syncthreads();
+        if (j + 1 < nb) issue(j + 1);
+        // qrel: the wave's first query minus the block's first key (clamped).
+        const int qrel = causal ? int(min(max(qpos0 - (wb + int64_t(j) * BN), int64_t(-64)), int64_t(BN))) : BN;
+        const int nvalid = min(BN, nkeys - j * BN);
+        const bool masked = nvalid < BN || qrel < BN - 1;
+        const unsigned char *kimg = lds + (j & 1) * BUF, *vimg = kimg + BLK;
 #pragma unroll
-        for (int nt = 0; nt < BK / 16; ++nt) {
-          f32x4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-          const int key = nt * 16 + (lane & 15);
+        for (int hb = 0; hb < 2; ++hb) {
+          if (nvalid <= 32 * hb || qrel + 31 < 32 * hb) continue;  // wave-uniform: nothing visible
+          // One 16-key tile at a time: S^T and dP^T, then its dS^T pairs.
+          uint32_t pk[2][2][2];  // [rt][k2][pair]
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            const bf16x8 kb = as_bf16x8(*reinterpret_cast<const uint4 *>(kt + key * D + ks * 32 + g * 8));
-            const bf16x8 vb = as_bf16x8(*reinterpret_cast<const uint4 *>(vt + key * D + ks * 32 + g * 8));
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s, 0, 0, 0);
-            dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[ks], vb, dp, 0, 0, 0);
+          for (int k2 = 0; k2 < 2; ++k2) {
+            const int kt = 2 * hb + k2;
+            f32x4 s[2], dp[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+              s[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+              dp[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              const bf16x8 kf = row_frag(kimg, lo, kt, ks), vf = row_frag(vimg, lo, kt, ks);
+#pragma unroll
+              for (int rt = 0; rt < 2; ++rt) {
+                s[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[rt][ks], s[rt], 0, 0, 0);
+                dp[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, dof[rt][ks], dp[rt], 0, 0, 0);
+              }
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+              const int lim = qrel + rt * 16 + (lane & 15);
+              float d[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int key = kt * 16 + (lane >> 4) * 4 + i;
+                const bool vis = !masked || (key < nvalid && (!causal || key <= lim));
+                const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][i], sc, -lse[rt])) : 0.f;
+                const float ds = p * (dp[rt][i] - dl[rt]);
+                tacc += ds * s[rt][i];
+                d[i] = ds * dsc;
+              }
+              pk[rt][k2][0] = pack_bf16x2(d[0], d[1]);
+              pk[rt][k2][1] = pack_bf16x2(d[2], d[3]);
+            }
           }
+          // dS^T (scaled by tau / sqrt(D)) in the B-operand layout of step hb.
+          bf16x8 dsb[2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kj = j0 + key;
-            const bool vis = kj < nk && (!sgm.causal || sgm.pos0 + kj <= tq[i]);
-            const float p = vis ? exp2f(s[i] * sc - lse[i]) : 0.f;
-            const float ds = p * (dp[i] - dl[i]);
-            tacc[sg] += ds * s[i];
-            dst[wave][(4 * g + i) * BK + key] = uint16_t(f2bf(ds * dsc));
+          for (int rt = 0; rt < 2; ++rt)
+            dsb[rt] = as_bf16x8(make_uint4(pk[rt][0][0], pk[rt][0][1], pk[rt][1][0], pk[rt][1][1]));
+          // dq^T += K^T dS^T over the 32 keys of step hb.
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const bf16x8 kt_f = tr_frag(kimg, lo, hb, dt);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              dq[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt_f, dsb[rt], dq[rt][dt], 0, 0, 0);
           }
         }
-        __syncthreads();
-        // dq += dS K over the block's 64 keys (two 32-key steps).
+      }
+      if (st)
+        t_state = tacc;
+      else
+        t_front = tacc;
+    }
+    // dq rows: lane holds dims dt*16 + 4*(lane/16) + i of query rt*16 + lane%16.
+    uint16_t *dqp = static_cast<uint16_t *>(A.dq) + b * A.dq_sb + hq * A.dq_sh;
 #pragma unroll
-        for (int kk = 0; kk < BK / 32; ++kk) {
-          const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(
-              &dst[wave][(lane & 15) * BK + kk * 32 + g * 8]));
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t t = qpos0 + rt * 16 + (lane & 15);
+      if (t < q_hi) {
 #pragma unroll
-          for (int t = 0; t < DT; ++t)
-            dq[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, col_frag<D>(kt, kk * 32, t * 16 + (lane & 15)),
-                                                            dq[t], 0, 0, 0);
+        for (int dt = 0; dt < DT; ++dt) {
+          uint2 w;
+          w.x = pack_bf16x2(dq[rt][dt][0], dq[rt][dt][1]);
+          w.y = pack_bf16x2(dq[rt][dt][2], dq[rt][dt][3]);
+          *reinterpret_cast<uint2 *>(dqp + t * A.dq_st + dt * 16 + (lane >> 4) * 4) = w;
         }
       }
     }
-    uint16_t *dqp = static_cast<uint16_t *>(A.dq) + b * A.dq_sb + hq * A.dq_sh;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (tq[i] < q_hi)
-#pragma unroll
-        for (int t = 0; t < DT; ++t) dqp[tq[i] * A.dq_st + t * 16 + (lane & 15)] = uint16_t(f2bf(dq[t][i]));
   }
   // Temperature partials of this workgroup: sum of dS (q . k) / sqrt(D).
-  const float t0 = wave_sum(tacc[0]) * scale_nat, t1 = wave_sum(tacc[1]) * scale_nat;
+  const float t0 = wave_sum(t_state) * scale_nat, t1 = wave_sum(t_front) * scale_nat;
   if (lane == 0) {
     red[wave][0] = t0;
     red[wave][1] = t1;
@@ -228,24 +292,28 @@ __global__ void k_attn_bwd_temps(const float *tpart, int B, int Hq, int n_chunks
 }
 
 // ---------------------------------------------------------------------------
-// dk / dv: workgroup = 64 keys of one (batch, kv head).
-//   snapshot mode: rows [kb*64, +64) of the snapshot chunk m = n + blockIdx.x / kblocks
+// dk / dv: workgroup = 64 keys of one (batch, kv head); logical tile order
+// (kv row, key block).
+//   snapshot mode: rows [kb*64, +64) of the snapshot chunk m = n + kblock / kblocks
 //                  reads (all its queries, no causal mask, state temperature);
 //   window mode:   tokens [kb*64, +64): query t sees token p iff
 //                  wb(chunk(t)) <= p <= t (front temperature).
+// Q and dO of 64 queries stream as blocks; the block's lse and delta go into
+// LDS with the same DMA (wave 0, one float per lane).
 template <int D, bool SNAP>
-__global__ __launch_bounds__(NWB * 64) void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks,
-                                                            ChunkTable table) {
+__global__ __launch_bounds__(NTB) __attribute__((amdgpu_waves_per_eu(2)))
+void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
   constexpr int KS = D / 32, DT = D / 16;
-  __shared__ __attribute__((aligned(16))) uint16_t qt[BQ * D];
-  __shared__ __attribute__((aligned(16))) uint16_t dot[BQ * D];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[NWB][16 * BQ];
-  __shared__ __attribute__((aligned(16))) uint16_t dt[NWB][16 * BQ];
-  __shared__ float lse_s[BQ], dl_s[BQ];
+  constexpr int BUF = Lay<D>::BUF, BLK = Lay<D>::BLK;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * BUF];
+  __shared__ __attribute__((aligned(1024))) float stat[2][2][BN];  // [buffer][lse, delta][query]
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads), grp = Hq / Hkv;
-  const int kvrow = blockIdx.y, b = kvrow / Hkv, hk = kvrow % Hkv;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+  const int wg = xcd_logical(blockIdx.x, gridDim.x);
+  const int kvrow = wg / kblocks, kblk = wg % kblocks;
+  const int b = kvrow / Hkv, hk = kvrow % Hkv;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t T = A.T;
   const float scale_nat = 1.0f / sqrtf(float(D));
 
@@ -254,35 +322,47 @@ __global__ __launch_bounds__(NWB * 64) void k_attn_bwd_dkdv(kvm_layer L, BwdArgs
   const uint16_t *kbase, *vbase;
   int64_t kst, vst;
   if (SNAP) {
-    m_snap = n + int(blockIdx.x) / kblocks;
-    kb0 = int64_t(blockIdx.x % kblocks) * BK;
-    if (m_snap >= int(A.n_chunks)) return;
+    const int per = (int(A.snap_cap) + BKW - 1) / BKW;  // key blocks per snapshot
+    m_snap = n + kblk / per;
+    kb0 = int64_t(kblk % per) * BKW;
     nkeys = table.state_len[m_snap];
     const int64_t soff = int64_t(table.snap_slot[m_snap]) * A.snap_stride + int64_t(kvrow) * A.snap_cap * D;
     kbase = A.snap_k + soff;
     vbase = A.snap_v + soff;
     kst = vst = D;
   } else {
-    kb0 = int64_t(blockIdx.x) * BK;
+    kb0 = int64_t(kblk) * BKW;
     nkeys = int(T);
     kbase = static_cast<const uint16_t *>(A.kv.k) + b * A.kv.k_sb + hk * A.kv.k_sh;
     vbase = static_cast<const uint16_t *>(A.kv.v) + b * A.kv.v_sb + hk * A.kv.v_sh;
     kst = A.kv.k_st;
     vst = A.kv.v_st;
   }
-  if (kb0 >= nkeys) return;
-  // A operands: this wave's 16 keys (K for S^T = K Q^T, V for dP^T = V dO^T).
+  if (kb0 >= nkeys) return;  // workgroup-uniform, before any barrier
+
+  for (int i = threadIdx.x; i < 2 * BUF / 16; i += NTB)
+    reinterpret_cast<uint4 *>(lds)[i] = make_uint4(0, 0, 0, 0);
+
+  // B operands: K and V rows of this wave's 16 keys (row lane%16, dims ks*32 + 8*(lane/16)).
   const int64_t kr = kb0 + wave * 16 + (lane & 15);
   const bool kok = kr < nkeys;
-  bf16x8 ka[KS], va[KS];
+  bf16x8 kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    ka[ks] = as_bf16x8(ld16_or_zero(kbase + kr * kst + ks * 32 + g * 8, kok));
-    va[ks] = as_bf16x8(ld16_or_zero(vbase + kr * vst + ks * 32 + g * 8, kok));
+    uint4 u = make_uint4(0, 0, 0, 0), w = make_uint4(0, 0, 0, 0);
+    if (kok) {
+      u = *reinterpret_cast<const uint4 *>(kbase + kr * kst + ks * 32 + (lane >> 4) * 8);
+      w = *reinterpret_cast<const uint4 *>(vbase + kr * vst + ks * 32 + (lane >> 4) * 8);
+    }
+    kf[ks] = as_bf16x8(u);
+    vf[ks] = as_bf16x8(w);
   }
-  int64_t kp[4];  // the lane's C-layout keys: kb0 + 16 wave + 4 g + i
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < 4; ++i) kp[i] = kb0 + wave * 16 + 4 * g + i;
+  for (int ks = 0; ks < KS; ++ks) {
+    asm volatile("" : "+v"(kf[ks]));
+    asm volatile("" : "+v"(vf[ks]));
+  }
   f32x4 dk[DT], dv[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
@@ -295,10 +375,17 @@ __global__ __launch_bounds__(NWB * 64) void k_attn_bwd_dkdv(kvm_layer L, BwdArgs
     tq_lo = int64_t(m_snap) * C;
     tq_hi = min(int64_t(m_snap + 1) * C, T);
   } else {
-    tq_lo = kb0 / BQ * BQ;
-    const int64_t last_key = min(kb0 + BK, T) - 1;
+    tq_lo = kb0;
+    const int64_t last_key = min(kb0 + BKW, T) - 1;
     tq_hi = min(T, (last_key / C + n) * int64_t(C));
   }
+  const Lanes lo = lane_offsets(lane);
+  const uint32_t lds_base = uint32_t(uintptr_t((lds_void *)lds));
+  const uint32_t stat_base = uint32_t(uintptr_t((lds_void *)&stat[0][0][0]));
+  const uint32_t qstride_b = uint32_t(A.q_st * 2), dstride_b = uint32_t(A.do_st * 2);
+  const uint32_t qo = lo.drow * qstride_b + lo.dcol, doo = lo.drow * dstride_b + lo.dcol;
+  const int nqb = int((tq_hi - tq_lo + BN - 1) / BN);
+  const int64_t kp = kr;  // the lane's key (column lane%16 of every C tile)
 #pragma unroll 1
   for (int h = 0; h < grp; ++h) {
     const int hq = hk * grp + h;
@@ -308,76 +395,107 @@ __global__ __launch_bounds__(NWB * 64) void k_attn_bwd_dkdv(kvm_layer L, BwdArgs
     const uint16_t *dorow = static_cast<const uint16_t *>(A.dout) + b * A.do_sb + hq * A.do_sh;
     const float *lse_row = A.lse + (int64_t(b) * Hq + hq) * T;
     const float *dl_row = A.delta + (int64_t(b) * Hq + hq) * T;
+    auto issue = [&](int jj) {
+      const int64_t t0 = tq_lo + int64_t(jj) * BN;
+      const int nv = int(min(int64_t(BN), tq_hi - t0));
+      unsigned char *img = lds + (jj & 1) * BUF;
+      if (nv < BN) {
+        zero_v_tail<D, NTB>(img, nv);
+        zero_v_tail<D, NTB>(img + BLK, nv);
+      }
+      issue_block<D, NWB>(lds_base + uint32_t((jj & 1) * BUF), key_rsrc(qrow + t0 * A.q_st, A.q_st, nv),
+                          key_rsrc(dorow + t0 * A.do_st, A.do_st, nv), qo, doo, qstride_b, dstride_b, wave);
+      if (wave == 0) {  // lse and delta of the block: one float per lane, rows >= nv not written
+        const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(lse_row + t0), (short)0, nv * 4, kBufWord3);
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(dl_row + t0), (short)0, nv * 4, kBufWord3);
+        dma4(lr, stat_base + uint32_t(((jj & 1) * 2 + 0) * BN * 4), uint32_t(lane * 4));
+        dma4(dr, stat_base + uint32_t(((jj & 1) * 2 + 1) * BN * 4), uint32_t(lane * 4));
+      }
+    };
+    __syncthreads();  // both buffers are free (and zeroed, the first time)
+    issue(0);
 #pragma unroll 1
-    for (int64_t t0 = tq_lo; t0 < tq_hi; t0 += BQ) {
-      const int nq = int(min(int64_t(BQ), tq_hi - t0));
+    for (int j = 0; j < nqb; ++j) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      stage_rows<D, BQ>(qt, qrow + t0 * A.q_st, A.q_st, nq);
-      stage_rows<D, BQ>(dot, dorow + t0 * A.do_st, A.do_st, nq);
-      if (threadIdx.x < BQ) {
-        const bool ok = threadIdx.x < nq;
-        lse_s[threadIdx.x] = ok ? lse_row[t0 + threadIdx.x] : INFINITY;
-        dl_s[threadIdx.x] = ok ? dl_row[t0 + threadIdx.x] : 0.f;
-      }
-      __syncthreads();
+      if (j + 1 < nqb) issue(j + 1);
+      const int64_t t0 = tq_lo + int64_t(j) * BN;
+      const int nq = int(min(int64_t(BN), tq_hi - t0));
+      const unsigned char *qimg = lds + (j & 1) * BUF, *dimg = qimg + BLK;
+      const float *lse_s = &stat[j & 1][0][0], *dl_s = &stat[j & 1][1][0];
 #pragma unroll
-      for (int nt = 0; nt < BQ / 16; ++nt) {
-        f32x4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-        const int qi = nt * 16 + (lane & 15);
+      for (int hb = 0; hb < 2; ++hb) {
+        // wave-uniform: no valid query in the half, or (window) all of its
+        // queries before the wave's first key
+        if (nq <= 32 * hb) continue;
+        if (!SNAP && t0 + 32 * hb + 31 < kb0 + wave * 16) continue;
+        f32x4 s[2], dp[2];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 qb = as_bf16x8(*reinterpret_cast<const uint4 *>(qt + qi * D + ks * 32 + g * 8));
-          const bf16x8 db = as_bf16x8(*reinterpret_cast<const uint4 *>(dot + qi * D + ks * 32 + g * 8));
-          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[ks], qb, s, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[ks], db, dp, 0, 0, 0);
+        for (int q2 = 0; q2 < 2; ++q2) {
+          const int qt = 2 * hb + q2;
+          s[q2] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[q2] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            s[q2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(row_frag(qimg, lo, qt, ks), kf[ks], s[q2], 0, 0, 0);
+            dp[q2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(row_frag(dimg, lo, qt, ks), vf[ks], dp[q2], 0, 0, 0);
+          }
         }
-        const int64_t t = t0 + qi;
-        const int64_t wbt = max(int64_t(0), (t / C - n + 1) * int64_t(C));
+        // P and dS (scaled by tau / sqrt(D)) in the B-operand layout of step hb:
+        // lane holds queries qt*16 + 4*(lane/16) + i of key lane%16.
+        uint32_t pp[2][2], pd[2][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bool vis = t < tq_hi && kp[i] < nkeys;
-          if (!SNAP) vis = vis && kp[i] <= t && wbt <= kp[i];
-          const float p = vis ? exp2f(s[i] * sc - lse_s[qi]) : 0.f;
-          const float ds = p * (dp[i] - dl_s[qi]);
-          pt[wave][(4 * g + i) * BQ + qi] = uint16_t(f2bf(p));
-          dt[wave][(4 * g + i) * BQ + qi] = uint16_t(f2bf(ds * dsc));
+        for (int q2 = 0; q2 < 2; ++q2) {
+          const int qr = (2 * hb + q2) * 16 + (lane >> 4) * 4;  // block-relative query of i = 0
+          const float4 l4 = *reinterpret_cast<const float4 *>(lse_s + qr);
+          const float4 d4 = *reinterpret_cast<const float4 *>(dl_s + qr);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+          float p[4], d[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t t = t0 + qr + i;
+            bool vis = qr + i < nq && kp < nkeys;
+            if (!SNAP) vis = vis && kp <= t && max(int64_t(0), (t / C - n + 1) * int64_t(C)) <= kp;
+            p[i] = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[q2][i], sc, -lv[i])) : 0.f;
+            d[i] = p[i] * (dp[q2][i] - dv4[i]) * dsc;
+          }
+          pp[q2][0] = pack_bf16x2(p[0], p[1]);
+          pp[q2][1] = pack_bf16x2(p[2], p[3]);
+          pd[q2][0] = pack_bf16x2(d[0], d[1]);
+          pd[q2][1] = pack_bf16x2(d[2], d[3]);
         }
-      }
-      __syncthreads();
-      // dv += P^T dO, dk += dS^T Q over the block's 64 queries.
+        const bf16x8 pb = as_bf16x8(make_uint4(pp[0][0], pp[0][1], pp[1][0], pp[1][1]));
+        const bf16x8 db = as_bf16x8(make_uint4(pd[0][0], pd[0][1], pd[1][0], pd[1][1]));
+        // dv^T += dO^T P, dk^T += Q^T dS over the 32 queries of step hb.
 #pragma unroll
-      for (int kk = 0; kk < BQ / 32; ++kk) {
-        const bf16x8 pa = as_bf16x8(*reinterpret_cast<const uint4 *>(&pt[wave][(lane & 15) * BQ + kk * 32 + g * 8]));
-        const bf16x8 sa = as_bf16x8(*reinterpret_cast<const uint4 *>(&dt[wave][(lane & 15) * BQ + kk * 32 + g * 8]));
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const int col = t * 16 + (lane & 15);
-          dv[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, col_frag<D>(dot, kk * 32, col), dv[t], 0, 0, 0);
-          dk[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa, col_frag<D>(qt, kk * 32, col), dk[t], 0, 0, 0);
+        for (int dt = 0; dt < DT; ++dt) {
+          dv[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr_frag(dimg, lo, hb, dt), pb, dv[dt], 0, 0, 0);
+          dk[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr_frag(qimg, lo, hb, dt), db, dk[dt], 0, 0, 0);
         }
       }
     }
   }
-  // Owner writes (fp32).
-  float *dkp, *dvp;
-  int64_t rowst = D;
-  if (SNAP) {
-    const int64_t off = int64_t(table.snap_slot[m_snap]) * A.dsnap_stride + int64_t(kvrow) * A.snap_cap * D;
-    dkp = A.d_snap_k + off;
-    dvp = A.d_snap_v + off;
-  } else {
-    const int64_t off = int64_t(kvrow) * T * D;
-    dkp = A.dk + off;
-    dvp = A.dv + off;
+  // Owner writes (fp32): lane holds dims dt*16 + 4*(lane/16) + i of key kp.
+  if (kp < nkeys) {
+    float *dkp, *dvp;
+    if (SNAP) {
+      const int64_t off = int64_t(table.snap_slot[m_snap]) * A.dsnap_stride + int64_t(kvrow) * A.snap_cap * D;
+      dkp = A.d_snap_k + off;
+      dvp = A.d_snap_v + off;
+    } else {
+      const int64_t off = int64_t(kvrow) * T * D;
+      dkp = A.dk + off;
+      dvp = A.dv + off;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int64_t o = kp * D + dt * 16 + (lane >> 4) * 4;
+      *reinterpret_cast<float4 *>(dkp + o) = make_float4(dk[dt][0], dk[dt][1], dk[dt][2], dk[dt][3]);
+      *reinterpret_cast<float4 *>(dvp + o) = make_float4(dv[dt][0], dv[dt][1], dv[dt][2], dv[dt][3]);
+    }
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (kp[i] < nkeys)
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        dkp[kp[i] * rowst + t * 16 + (lane & 15)] = dk[t][i];
-        dvp[kp[i] * rowst + t * 16 + (lane & 15)] = dv[t][i];
-      }
 }
 
 template <int D>
@@ -386,22 +504,23 @@ hipError_t launch_bwd_d(const kvm_layer &L, const BwdArgs &a, const ChunkTable &
   const int n_chunks = int(a.n_chunks);
   const int qtiles = int((L.chunk_len + BQ - 1) / BQ);
   const int64_t rows = L.batch * L.kv_heads;
-  hipLaunchKernelGGL((k_attn_bwd_dq<D>), dim3(unsigned(L.batch * L.q_heads * n_chunks * qtiles)),
-                     dim3(NWB * 64), 0, stream, L, a, qtiles, table, tpart);
+  hipLaunchKernelGGL((k_attn_bwd_dq<D>), dim3(unsigned(L.batch * L.q_heads * n_chunks * qtiles)), dim3(NTB), 0,
+                     stream, L, a, qtiles, table, tpart);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_bwd_temps, dim3(unsigned((L.q_heads + 63) / 64)), dim3(64), 0, stream, tpart,
                      int(L.batch), int(L.q_heads), n_chunks, qtiles, a.d_state_temp, a.d_front_temp);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int wblocks = int((a.T + BK - 1) / BK);
-  hipLaunchKernelGGL((k_attn_bwd_dkdv<D, false>), dim3(unsigned(wblocks), unsigned(rows)), dim3(NWB * 64), 0,
-                     stream, L, a, 0, table);
+  const int wblocks = int((a.T + BKW - 1) / BKW);
+  hipLaunchKernelGGL((k_attn_bwd_dkdv<D, false>), dim3(unsigned(wblocks * rows)), dim3(NTB), 0, stream, L, a,
+                     wblocks, table);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const int n = int(L.n_bswa_chunks);
   if (n_chunks > n) {
-    const int kblocks = int((a.snap_cap + BK - 1) / BK);
-    hipLaunchKernelGGL((k_attn_bwd_dkdv<D, true>), dim3(unsigned((n_chunks - n) * kblocks), unsigned(rows)),
-                       dim3(NWB * 64), 0, stream, L, a, kblocks, table);
+    const int per = int((a.snap_cap + BKW - 1) / BKW);
+    const int kblocks = (n_chunks - n) * per;
+    hipLaunchKernelGGL((k_attn_bwd_dkdv<D, true>), dim3(unsigned(kblocks * rows)), dim3(NTB), 0, stream, L, a,
+                       kblocks, table);
     e = hipGetLastError();
   }
   return e;
