@@ -424,6 +424,12 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
       const int64_t t0 = tq_lo + int64_t(j) * BN;
       const int nq = int(min(int64_t(BN), tq_hi - t0));
       const unsigned char *qimg = lds + (j & 1) * BUF, *dimg = qimg + BLK;
+      // Window start of the chunks the block's queries lie in: with C >= 64
+      // a 64-query block spans at most two chunks, c0 and c0 + 1 (first
+      // query of c0 + 1 at `bnd`); shorter chunks take the division per query.
+      const int64_t c0 = t0 / C, bnd = (c0 + 1) * C;
+      const int64_t wb0 = max(int64_t(0), (c0 - n + 1) * int64_t(C)), wb1 = max(int64_t(0), (c0 - n + 2) * int64_t(C));
+      const bool two_chunks = C >= BN;
       const float *lse_s = &stat[j & 1][0][0], *dl_s = &stat[j & 1][1][0];
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
@@ -457,7 +463,10 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
           for (int i = 0; i < 4; ++i) {
             const int64_t t = t0 + qr + i;
             bool vis = qr + i < nq && kp < nkeys;
-            if (!SNAP) vis = vis && kp <= t && max(int64_t(0), (t / C - n + 1) * int64_t(C)) <= kp;
+            if (!SNAP) {
+              const int64_t wbt = two_chunks ? (t < bnd ? wb0 : wb1) : max(int64_t(0), (t / C - n + 1) * int64_t(C));
+              vis = vis && kp <= t && wbt <= kp;
+            }
             p[i] = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[q2][i], sc, -lv[i])) : 0.f;
             d[i] = p[i] * (dp[q2][i] - dv4[i]) * dsc;
           }

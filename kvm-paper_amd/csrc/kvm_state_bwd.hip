@@ -25,10 +25,15 @@
 // and this kernel recomputes them from the bf16 tokens and carries the chain
 // rule down to dk, dv (added to the attention backward's window gradients),
 // the merge gate and the LayerNorm parameters (both uses of ln_s_k).
-// One workgroup owns RPW slots of one row and holds their sums and gradient
-// accumulators in registers (D/8 lanes per slot row): a forward scan over the
-// updates rebuilds the final sums, a reverse scan accumulates H and undoes
-// each update's merges.  Every state token is routed to exactly one slot, so
+// One single-wave workgroup owns RPW slots of one row (a lane group of D/8
+// lanes per slot) and holds their sums and gradient accumulators in
+// registers: a forward scan over the updates rebuilds the final sums, a
+// reverse scan accumulates H and undoes each update's merges.  The tokens
+// routed to the workgroup's slots in one update are processed RPW at a time,
+// one per lane group whatever slot they belong to (the per-token LayerNorm
+// and chain rule keep every lane busy); their rows and the slots' gradients
+// cross between lane groups through LDS, and each owner folds its tokens in
+// list (token) order.  Every state token is routed to exactly one slot, so
 // each token row of dk / dv / dgate has exactly one writer (no atomics).
 
 #include "kvm_device.hpp"
@@ -38,7 +43,7 @@
 namespace kvm {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 64;  // one wave per workgroup: the per-update compaction needs no barrier
 constexpr int kMaxChunk = 4096;
 constexpr float kNormEps = 1e-12f;  // torch.nn.functional.normalize
 
@@ -61,13 +66,31 @@ struct Tok {
   float r, g;
 };
 
+// Raw bf16 loads of one token (issued early, used later).
+struct RawTok {
+  uint4 k, v;
+  uint32_t g;
+};
+// Token rows of one (batch, kv head): the prefill's k / v / gate views (no ring).
+struct RowSrc {
+  const uint16_t *k, *v, *g;
+  int64_t k_st, v_st, g_st;
+};
+__device__ __forceinline__ RawTok fetch_tok(const RowSrc &R, int64_t t, int part) {
+  RawTok r;
+  r.k = *reinterpret_cast<const uint4 *>(R.k + t * R.k_st + part * 8);
+  r.v = *reinterpret_cast<const uint4 *>(R.v + t * R.v_st + part * 8);
+  r.g = R.g[t * R.g_st];
+  return r;
+}
+
 template <int D>
-__device__ __forceinline__ void load_tok(const StateBwdArgs &A, int b, int h, int64_t t, int part,
-                                         const float (&w)[8], const float (&bb)[8], Tok &x) {
+__device__ __forceinline__ void make_tok(const StateBwdArgs &A, const RawTok &r, int part, const float (&w)[8],
+                                         const float (&bb)[8], Tok &x) {
   float k[8];
-  load8(seq_k(A.kv, b, h, t) + part * 8, k);
-  load8(seq_v(A.kv, b, h, t) + part * 8, x.v);
-  x.g = seq_g(A.kv, b, h, t);
+  unpack8(r.k, k);
+  unpack8(r.v, x.v);
+  x.g = bf2f(r.g);
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     if (part * 8 + e < A.L.rope_partial_dim) k[e] = 0.f;
@@ -178,21 +201,30 @@ __device__ __forceinline__ void tok_backward(const StateBwdArgs &A, const Tok &x
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable U, float *__restrict__ dln_part) {
-  constexpr int GL = D / 8;            // lanes per slot row
-  constexpr int RPW = kThreads / GL;   // slot rows per workgroup
+  constexpr int GL = D / 8;            // lanes per slot row (a lane group)
+  constexpr int RPW = kThreads / GL;   // slot rows per workgroup = lane groups
   // Tokens of the current update routed to this workgroup's slots, in token
   // order: (token << 8) | (local slot << 1) | appended.
   __shared__ int32_t lst[kMaxChunk];
-  __shared__ int wsum[kThreads / 64];
-  __shared__ float red[kThreads / 64][2][D];
-  const int tid = threadIdx.x, part = tid % GL, lane = tid & 63, wave = tid >> 6;
+  __shared__ __attribute__((aligned(16))) float rows[RPW][2][D];  // token rows, one per lane group
+  __shared__ __attribute__((aligned(16))) float accb[RPW][2][D];  // slot gradients (reverse scan)
+  __shared__ float accl_s[RPW];
+  __shared__ float red[2][D];
+  const int tid = threadIdx.x, part = tid % GL, lane = tid & 63;
   const int row = blockIdx.y;
   const int hb = row / int(A.L.kv_heads), hh = row % int(A.L.kv_heads);
   const int j0 = blockIdx.x * RPW, my = tid / GL;
-  const int j = j0 + my;  // this thread's slot
+  const int j = j0 + my;  // this lane group's slot
   const int C = int(A.L.chunk_len), L0 = int(A.L0), nu = int(A.n_updates);
   const int64_t rowT = int64_t(row) * A.T;
   const float eps = float(A.L.ln_eps);
+  RowSrc R;
+  R.k = static_cast<const uint16_t *>(A.kv.k) + hb * A.kv.k_sb + hh * A.kv.k_sh;
+  R.v = static_cast<const uint16_t *>(A.kv.v) + hb * A.kv.v_sb + hh * A.kv.v_sh;
+  R.g = static_cast<const uint16_t *>(A.kv.gate) + hb * A.kv.g_sb + hh * A.kv.g_sh;
+  R.k_st = A.kv.k_st;
+  R.v_st = A.kv.v_st;
+  R.g_st = A.kv.g_st;
   float w[8], bb[8];
   load8f(static_cast<const float *>(A.L.ln_weight) + part * 8, w);
   load8f(static_cast<const float *>(A.L.ln_bias) + part * 8, bb);
@@ -200,11 +232,12 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   auto before_of = [&](int u) { return U.state_before[u]; };
   auto napp_of = [&](int u) { return U.n_append[u]; };
   // Ordered compaction of update u's routes onto [j0, j0 + RPW); returns the
-  // list length (the same in every thread).
+  // list length (the same in every lane).
   auto stage = [&](int u) {
     const int64_t o = (int64_t(u) * A.rows + row) * C;
     int n = 0;
     __syncthreads();  // the previous list has been read
+#pragma unroll 8
     for (int t0 = 0; t0 < C; t0 += kThreads) {
       const int t = t0 + tid;
       int r = -1, a = 0;
@@ -214,28 +247,25 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
       }
       const bool hit = r >= j0 && r < j0 + RPW;
       const uint64_t m = __ballot(hit);
-      if (lane == 0) wsum[wave] = __popcll(m);
-      __syncthreads();
-      int woff = 0, tot = 0;
-#pragma unroll
-      for (int w2 = 0; w2 < kThreads / 64; ++w2) {
-        woff += w2 < wave ? wsum[w2] : 0;
-        tot += wsum[w2];
-      }
-      if (hit)
-        lst[n + woff + __popcll(m & ((uint64_t(1) << lane) - 1))] = (t << 8) | ((r - j0) << 1) | (a ? 1 : 0);
-      n += tot;
-      __syncthreads();  // wsum is rewritten next round; lst complete after the last
+      if (hit) lst[n + __popcll(m & ((uint64_t(1) << lane) - 1))] = (t << 8) | ((r - j0) << 1) | (a ? 1 : 0);
+      n += __popcll(m);
     }
+    __syncthreads();  // the list is complete
     return n;
   };
+  auto put_rows = [&](const float (&rk)[8], const float (&rv)[8]) {
+    store8f(&rows[my][0][part * 8], rk);
+    store8f(&rows[my][1][part * 8], rv);
+  };
 
-  // ---- forward scan: final fp32 sums of my slot, and its vlen.
+  // ---- forward scan: final fp32 sums of my slot, and its vlen.  Lane group
+  // g prepares the rows of list entry i0 + g; the owning group then folds
+  // them in list order.
   float sk[8], sv[8];
   float vlen = 0.f;
   if (j < L0) {
     Tok x;
-    load_tok<D>(A, hb, hh, j, part, w, bb, x);
+    make_tok<D>(A, fetch_tok(R, j, part), part, w, bb, x);
     tok_rows(A.L, x, kInitial, sk, sv);
     vlen = row_norm8<D>(x.v);
   } else {
@@ -246,23 +276,37 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
     const int n = stage(u);
     const int tb = tb_of(u);
     float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < n; ++i) {
-      const int e = lst[i];
-      if (((e >> 1) & 127) != my) continue;
+    for (int i0 = 0; i0 < n; i0 += RPW) {
+      const int i = i0 + my;
+      const int e = i < n ? lst[i] : 0;
       Tok x;
-      load_tok<D>(A, hb, hh, tb + (e >> 8), part, w, bb, x);
-      if (e & 1) {  // the slot's base row (appended before this update's merges)
-        tok_rows(A.L, x, kAppended, sk, sv);
-        vlen = row_norm8<D>(sv);
-      } else {
+      make_tok<D>(A, fetch_tok(R, tb + (e >> 8), part), part, w, bb, x);
+      float rk[8], rv[8];
+      tok_rows(A.L, x, (e & 1) ? kAppended : kMerged, rk, rv);
+      put_rows(rk, rv);
+      __syncthreads();
+      for (int g = 0; g < RPW && i0 + g < n; ++g) {
+        const int eg = lst[i0 + g];
+        if (((eg >> 1) & 127) != my) continue;
         float xk[8], xv[8];
-        tok_rows(A.L, x, kMerged, xk, xv);
+        load8f(&rows[g][0][part * 8], xk);
+        load8f(&rows[g][1][part * 8], xv);
+        if (eg & 1) {  // the slot's base row (appended before this update's merges)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          dk[c] += xk[c];
-          dv[c] += xv[c];
+          for (int c = 0; c < 8; ++c) {
+            sk[c] = xk[c];
+            sv[c] = xv[c];
+          }
+          vlen = row_norm8<D>(sv);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            dk[c] += xk[c];
+            dv[c] += xv[c];
+          }
         }
       }
+      __syncthreads();  // rows is rewritten by the next batch
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -275,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   float gk[8], gv[8], acck[8], accv[8], dlw[8], dlb[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acck[e] = accv[e] = dlw[e] = dlb[e] = 0.f;
-  float accl = 0.f;  // d vlen of my slot (row-reduced, replicated over the row's lanes)
+  float accl = 0.f;  // d vlen of my slot (row-reduced, replicated over the group's lanes)
   for (int s = nu; s >= 0; --s) {
     const int len = s == 0 ? L0 : before_of(s - 1) + napp_of(s - 1);
     if (j < len) {
@@ -322,28 +366,48 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
       for (int e = 0; e < 8; ++e) accv[e] += vlen * inv * (gv[e] - proj * sv[e]);
     }
     if (s == 0) break;
-    // Undo update s - 1, which built snapshot s from snapshot s - 1.
+    // Undo update s - 1, which built snapshot s from snapshot s - 1: lane
+    // group g runs the token-side chain rule of list entry i0 + g with the
+    // owning slot's gradient (published in accb), the owner subtracts the
+    // merged rows in list order.
     const int u = s - 1;
     const int n = stage(u);
     const int tb = tb_of(u);
-    for (int i = 0; i < n; ++i) {
-      const int e = lst[i];
-      if (((e >> 1) & 127) != my) continue;
+    store8f(&accb[my][0][part * 8], acck);
+    store8f(&accb[my][1][part * 8], accv);
+    if (part == 0) accl_s[my] = accl;
+    __syncthreads();
+    for (int i0 = 0; i0 < n; i0 += RPW) {
+      const int i = i0 + my;
+      const bool valid = i < n;
+      const int e = valid ? lst[i] : 0;
       const int64_t t = tb + (e >> 8);
+      const int ls = (e >> 1) & 127;
       Tok x;
-      load_tok<D>(A, hb, hh, t, part, w, bb, x);
-      if (e & 1) {
-        tok_backward<D>(A, x, kAppended, rowT + t, part, w, acck, accv, accl, dlw, dlb);
-      } else {
-        tok_backward<D>(A, x, kMerged, rowT + t, part, w, acck, accv, 0.f, dlw, dlb);
+      make_tok<D>(A, fetch_tok(R, t, part), part, w, bb, x);
+      float ak[8], av[8];
+      load8f(&accb[ls][0][part * 8], ak);
+      load8f(&accb[ls][1][part * 8], av);
+      const bool app = (e & 1) != 0;
+      if (valid) tok_backward<D>(A, x, app ? kAppended : kMerged, rowT + t, part, w, ak, av,
+                                 app ? accl_s[ls] : 0.f, dlw, dlb);
+      float rk[8], rv[8];
+      tok_rows(A.L, x, kMerged, rk, rv);
+      put_rows(rk, rv);
+      __syncthreads();
+      for (int g = 0; g < RPW && i0 + g < n; ++g) {
+        const int eg = lst[i0 + g];
+        if (((eg >> 1) & 127) != my || (eg & 1)) continue;
         float xk[8], xv[8];
-        tok_rows(A.L, x, kMerged, xk, xv);
+        load8f(&rows[g][0][part * 8], xk);
+        load8f(&rows[g][1][part * 8], xv);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           sk[c] -= xk[c];
           sv[c] -= xv[c];
         }
       }
+      __syncthreads();  // rows is rewritten by the next batch
     }
     if (j >= before_of(u) && j < before_of(u) + napp_of(u)) {  // the slot did not exist before
 #pragma unroll
@@ -353,10 +417,10 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   }
   if (j < L0) {
     Tok x;
-    load_tok<D>(A, hb, hh, j, part, w, bb, x);
+    make_tok<D>(A, fetch_tok(R, j, part), part, w, bb, x);
     tok_backward<D>(A, x, kInitial, rowT + j, part, w, acck, accv, accl, dlw, dlb);
   }
-  // LayerNorm parameter gradients: sum over my slots, then this workgroup's partial.
+  // LayerNorm parameter gradients: sum over the wave, then this workgroup's partial.
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float x = dlw[e], y = dlb[e];
@@ -367,17 +431,13 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
       y += __shfl_xor(y, o);
     }
     if (lane < GL) {
-      red[wave][0][part * 8 + e] = x;
-      red[wave][1][part * 8 + e] = y;
+      red[0][part * 8 + e] = x;
+      red[1][part * 8 + e] = y;
     }
   }
   __syncthreads();
-  for (int i = tid; i < 2 * D; i += kThreads) {
-    const int which = i / D, f = i % D;
-    float a = 0.f;
-    for (int w2 = 0; w2 < kThreads / 64; ++w2) a += red[w2][which][f];
-    dln_part[(int64_t(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * D + i] = a;
-  }
+  for (int i = tid; i < 2 * D; i += kThreads)
+    dln_part[(int64_t(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * D + i] = red[i / D][i % D];
 }
 
 // d ln_w / d ln_b: feature blockIdx.x of the 2D outputs summed over the

@@ -121,6 +121,7 @@ def test_mixer_forward_trains_through_the_hip_prefill():
     (1, 4, 2, 64, 64, 300, "fixed", 1.0, (1, 1, 0, 0)),
     (2, 4, 2, 64, 64, 450, "power_law", 8.0, (1, 1, 0, 0)),
     (1, 2, 1, 128, 128, 700, "power_law", 8.0, (1, 0, 1, 1)),
+    (1, 2, 2, 64, 32, 230, "fixed", 1.0, (1, 1, 0, 0)),  # chunks shorter than a 64-row block
 ])
 def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gates):
     if not torch.cuda.is_available():
