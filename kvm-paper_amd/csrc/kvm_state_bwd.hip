@@ -46,6 +46,7 @@ namespace {
 constexpr int kThreads = 64;  // one wave per workgroup: the per-update compaction needs no barrier
 constexpr int kMaxChunk = 4096;
 constexpr float kNormEps = 1e-12f;  // torch.nn.functional.normalize
+constexpr int kPf = 8;              // route entries per lane loaded one update ahead
 
 __device__ __forceinline__ void load8f(const float *p, float (&x)[8]) {
   const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
@@ -137,12 +138,14 @@ __device__ __forceinline__ void tok_rows(const kvm_layer &L, const Tok &x, int k
 
 // Chain rule from the gradients of a token's state rows (dk_row, dv_row and
 // the vlen gradient dl) to dk, dv, dgate of the token and the LayerNorm
-// parameters; adds into A.dk / A.dv (one writer per token row).
+// parameters.  dk / dv hold the token's current rows of A.dk / A.dv (loaded
+// by the caller ahead of time); the sums are stored back (one writer per
+// token row).
 template <int D>
 __device__ __forceinline__ void tok_backward(const StateBwdArgs &A, const Tok &x, int kind, int64_t tok_row,
                                              int part, const float (&w)[8], const float (&dk_row)[8],
                                              const float (&dv_row)[8], float dl, float (&dlw)[8],
-                                             float (&dlb)[8]) {
+                                             float (&dlb)[8], float (&dk)[8], float (&dv)[8]) {
   const bool gk = gate_k(A.L, kind), gv = gate_v(A.L, kind);
   float dxv[8];
 #pragma unroll
@@ -186,9 +189,6 @@ __device__ __forceinline__ void tok_backward(const StateBwdArgs &A, const Tok &x
   m1 = group_sum<D / 8>(m1) / float(D);
   m2 = group_sum<D / 8>(m2) / float(D);
   const int64_t o = tok_row * D + part * 8;
-  float dk[8], dv[8];
-  load8f(A.dk + o, dk);
-  load8f(A.dv + o, dv);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     if (part * 8 + e >= A.L.rope_partial_dim) dk[e] += x.r * (dxh[e] - m1 - x.xh[e] * m2);
@@ -204,8 +204,8 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   constexpr int GL = D / 8;            // lanes per slot row (a lane group)
   constexpr int RPW = kThreads / GL;   // slot rows per workgroup = lane groups
   // Tokens of the current update routed to this workgroup's slots, in token
-  // order: (token << 8) | (local slot << 1) | appended.
-  __shared__ int32_t lst[kMaxChunk];
+  // order: (token << 8) | (local slot << 1) | appended (dynamic LDS, chunk_len entries).
+  extern __shared__ int32_t lst[];
   __shared__ __attribute__((aligned(16))) float rows[RPW][2][D];  // token rows, one per lane group
   __shared__ __attribute__((aligned(16))) float accb[RPW][2][D];  // slot gradients (reverse scan)
   __shared__ float accl_s[RPW];
@@ -231,24 +231,37 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   auto tb_of = [&](int u) { return U.token_begin[u]; };
   auto before_of = [&](int u) { return U.state_before[u]; };
   auto napp_of = [&](int u) { return U.n_append[u]; };
-  // Ordered compaction of update u's routes onto [j0, j0 + RPW); returns the
-  // list length (the same in every lane).
+  // Route / append entries of the first kPf * 64 tokens of an update are
+  // loaded one update ahead (in registers); the rest, if any, when used.
+  int pr[kPf], pa[kPf];
+  auto prefetch = [&](int u) {
+    if (u < 0 || u >= nu) return;
+    const int64_t o = (int64_t(u) * A.rows + row) * C;
+#pragma unroll
+    for (int it = 0; it < kPf; ++it) {
+      const int t = it * kThreads + tid;
+      pr[it] = t < C ? A.route_log[o + t] : -1;
+      pa[it] = t < C ? A.append_log[o + t] : 0;
+    }
+  };
+  // Ordered compaction of update u's routes onto [j0, j0 + RPW) (the first
+  // part from the prefetched registers); returns the list length (the same
+  // in every lane).
   auto stage = [&](int u) {
     const int64_t o = (int64_t(u) * A.rows + row) * C;
     int n = 0;
     __syncthreads();  // the previous list has been read
-#pragma unroll 8
-    for (int t0 = 0; t0 < C; t0 += kThreads) {
-      const int t = t0 + tid;
-      int r = -1, a = 0;
-      if (t < C) {
-        r = A.route_log[o + t];
-        a = A.append_log[o + t];
-      }
+    auto add = [&](int t, int r, int a) {
       const bool hit = r >= j0 && r < j0 + RPW;
       const uint64_t m = __ballot(hit);
       if (hit) lst[n + __popcll(m & ((uint64_t(1) << lane) - 1))] = (t << 8) | ((r - j0) << 1) | (a ? 1 : 0);
       n += __popcll(m);
+    };
+#pragma unroll
+    for (int it = 0; it < kPf; ++it) add(it * kThreads + tid, pr[it], pa[it]);
+    for (int t0 = kPf * kThreads; t0 < C; t0 += kThreads) {
+      const int t = t0 + tid;
+      add(t, t < C ? A.route_log[o + t] : -1, t < C ? A.append_log[o + t] : 0);
     }
     __syncthreads();  // the list is complete
     return n;
@@ -272,8 +285,10 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
 #pragma unroll
     for (int e = 0; e < 8; ++e) sk[e] = sv[e] = 0.f;
   }
+  prefetch(0);
   for (int u = 0; u < nu; ++u) {
     const int n = stage(u);
+    prefetch(u + 1);
     const int tb = tb_of(u);
     float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int i0 = 0; i0 < n; i0 += RPW) {
@@ -320,13 +335,21 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
 #pragma unroll
   for (int e = 0; e < 8; ++e) acck[e] = accv[e] = dlw[e] = dlb[e] = 0.f;
   float accl = 0.f;  // d vlen of my slot (row-reduced, replicated over the group's lanes)
-  for (int s = nu; s >= 0; --s) {
-    const int len = s == 0 ? L0 : before_of(s - 1) + napp_of(s - 1);
-    if (j < len) {
-      // Local backward of snapshot s at my slot.
+  auto snap_len = [&](int s) { return s == 0 ? L0 : before_of(s - 1) + napp_of(s - 1); };
+  // Snapshot-row gradients of snapshot s at my slot (issued one step ahead).
+  auto load_snap = [&](int s) {
+    if (j < snap_len(s)) {
       const int64_t so = ((int64_t(s) * A.rows + row) * A.max_state_len + j) * D + part * 8;
       load8f(A.d_snap_k + so, gk);
       load8f(A.d_snap_v + so, gv);
+    }
+  };
+  prefetch(nu - 1);
+  load_snap(nu);
+  for (int s = nu; s >= 0; --s) {
+    const int len = snap_len(s);
+    if (j < len) {
+      // Local backward of snapshot s at my slot.
       float mean = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) mean += sk[e];
@@ -372,6 +395,8 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
     // merged rows in list order.
     const int u = s - 1;
     const int n = stage(u);
+    prefetch(u - 1);
+    load_snap(s - 1);  // used at the next step
     const int tb = tb_of(u);
     store8f(&accb[my][0][part * 8], acck);
     store8f(&accb[my][1][part * 8], accv);
@@ -383,14 +408,19 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
       const int e = valid ? lst[i] : 0;
       const int64_t t = tb + (e >> 8);
       const int ls = (e >> 1) & 127;
+      const RawTok raw = fetch_tok(R, t, part);
+      float cdk[8], cdv[8];  // the token's rows of A.dk / A.dv, loaded with its k / v
+      const int64_t o = (rowT + t) * D + part * 8;
+      load8f(A.dk + o, cdk);
+      load8f(A.dv + o, cdv);
       Tok x;
-      make_tok<D>(A, fetch_tok(R, t, part), part, w, bb, x);
+      make_tok<D>(A, raw, part, w, bb, x);
       float ak[8], av[8];
       load8f(&accb[ls][0][part * 8], ak);
       load8f(&accb[ls][1][part * 8], av);
       const bool app = (e & 1) != 0;
       if (valid) tok_backward<D>(A, x, app ? kAppended : kMerged, rowT + t, part, w, ak, av,
-                                 app ? accl_s[ls] : 0.f, dlw, dlb);
+                                 app ? accl_s[ls] : 0.f, dlw, dlb, cdk, cdv);
       float rk[8], rv[8];
       tok_rows(A.L, x, kMerged, rk, rv);
       put_rows(rk, rv);
@@ -418,7 +448,11 @@ __global__ __launch_bounds__(kThreads) void k_state_bwd(StateBwdArgs A, UpdTable
   if (j < L0) {
     Tok x;
     make_tok<D>(A, fetch_tok(R, j, part), part, w, bb, x);
-    tok_backward<D>(A, x, kInitial, rowT + j, part, w, acck, accv, accl, dlw, dlb);
+    float cdk[8], cdv[8];
+    const int64_t o = (rowT + j) * D + part * 8;
+    load8f(A.dk + o, cdk);
+    load8f(A.dv + o, cdv);
+    tok_backward<D>(A, x, kInitial, rowT + j, part, w, acck, accv, accl, dlw, dlb, cdk, cdv);
   }
   // LayerNorm parameter gradients: sum over the wave, then this workgroup's partial.
 #pragma unroll
@@ -458,7 +492,7 @@ template <int D>
 hipError_t launch_d(const StateBwdArgs &a, const UpdTable &sched, float *part, hipStream_t s) {
   constexpr int RPW = kThreads / (D / 8);
   const dim3 grid(unsigned((a.max_state_len + RPW - 1) / RPW), unsigned(a.rows));
-  hipLaunchKernelGGL((k_state_bwd<D>), grid, dim3(kThreads), 0, s, a, sched, part);
+  hipLaunchKernelGGL((k_state_bwd<D>), grid, dim3(kThreads), size_t(a.L.chunk_len) * 4, s, a, sched, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_state_bwd_ln, dim3(2 * D), dim3(256), 0, s, part, int(grid.x * grid.y), 2 * D,
