@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 6
+#define KVM_ABI_VERSION 7
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -183,7 +183,10 @@ typedef struct kvm_prefill_bwd_desc {
   const void *dout;              /* bf16 dL/d(out), out's layout: dout + b*do_sb + t*do_st + hq*do_sh */
   int64_t do_sb, do_st, do_sh;
   const float *lse;              /* fp32 [B, Hq, T] from the forward */
-  const float *delta;            /* fp32 [B, Hq, T]: sum over features of dout * out */
+  float *delta;                  /* fp32 [B, Hq, T]: sum over features of dout * out; filled by the
+                                    library when `out` is set, else read */
+  const void *out;               /* bf16 forward output (dout's layout) or NULL */
+  int64_t o_sb, o_st, o_sh;
   const void *snap_k, *snap_v;   /* bf16 [n_snap, rows, max_state_len, head_dim] from the forward */
   int64_t max_state_len;
   int64_t n_chunks;
@@ -193,7 +196,8 @@ typedef struct kvm_prefill_bwd_desc {
   int64_t dq_sb, dq_sh, dq_st;
   float *dk, *dv;                /* fp32 out [B, Hkv, T, head_dim] contiguous: window keys / values */
   float *d_snap_k, *d_snap_v;    /* fp32 out [n_snap, rows, max_state_len, head_dim]: rows no
-                                    query chunk reads are zero */
+                                    query chunk reads are zero (each snapshot is read by one chunk:
+                                    chunk_snapshot strictly increases over the chunks >= n_bswa) */
   float *d_state_temp;           /* fp32 out [q_heads] (summed over the batch) */
   float *d_front_temp;           /* fp32 out [q_heads] */
   void *workspace;               /* kvm_prefill_backward_workspace_bytes() */

@@ -341,13 +341,15 @@ int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream) {
   if (!aligned16(d->q) || !aligned16(d->dout) || d->q_sb % 8 || d->q_sh % 8 || d->q_st % 8 ||
       d->do_sb % 8 || d->do_sh % 8 || d->do_st % 8)
     return fail(KVM_EINVAL, "q and dout must be 16-byte aligned with strides multiple of 8");
+  if (d->out && (!aligned16(d->out) || d->o_sb % 8 || d->o_sh % 8 || d->o_st % 8))
+    return fail(KVM_EINVAL, "out must be 16-byte aligned with strides multiple of 8");
   const bool has_state = n_chunks > n;
   if (has_state && (!d->snap_k || !d->snap_v || !d->d_snap_k || !d->d_snap_v ||
                     !aligned16(d->snap_k) || !aligned16(d->snap_v)))
     return fail(KVM_EINVAL, "backward: snapshot arrays (and their gradients) must be set and aligned");
   if (d->max_state_len < 1) return fail(KVM_EINVAL, "max_state_len must be positive");
   kvm::ChunkTable table;
-  int64_t n_snap = 0;
+  int64_t first_snap = -1;
   for (int64_t m = 0; m < n_chunks; ++m) {
     const int32_t s = d->chunk_state_len[m], snap = d->chunk_snapshot[m];
     if (m < n) {
@@ -357,9 +359,13 @@ int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream) {
     }
     if (snap < 0 || s < 1 || s > d->max_state_len)
       return fail(KVM_EINVAL, "chunk %lld schedule (state %d, snapshot %d) is invalid", (long long)m, s, snap);
+    // Each snapshot's gradient has one writer: the chunk that reads it.
+    if (m > n && snap != table.snap_slot[m - 1] + 1)
+      return fail(KVM_EINVAL, "chunk %lld reads snapshot %d: snapshots must be read once each, in order",
+                  (long long)m, snap);
+    if (m == n) first_snap = snap;
     table.state_len[m] = s;
     table.snap_slot[m] = snap;
-    n_snap = std::max<int64_t>(n_snap, int64_t(snap) + 1);
   }
   const int64_t need_ws = kvm::attn_bwd_workspace_bytes(L, n_chunks);
   if (!d->workspace || d->workspace_bytes < need_ws)
@@ -390,11 +396,17 @@ int kvm_prefill_backward(const kvm_prefill_bwd_desc *d, void *stream) {
   a.d_state_temp = d->d_state_temp;
   a.d_front_temp = d->d_front_temp;
   hipStream_t s = as_stream(stream);
-  if (has_state) {  // rows no query chunk reads keep a zero gradient
-    const int64_t words = n_snap * a.snap_stride;
+  // Snapshots below the first one read keep a zero gradient (the snapshot
+  // kernel writes every row of the ones read, zeros past their length).
+  if (has_state && first_snap > 0) {
+    const int64_t words = first_snap * a.snap_stride;
     KVM_HIP(kvm::launch_fill_u32(reinterpret_cast<unsigned *>(d->d_snap_k), words, 0u, s), "d_snap_k clear");
     KVM_HIP(kvm::launch_fill_u32(reinterpret_cast<unsigned *>(d->d_snap_v), words, 0u, s), "d_snap_v clear");
   }
+  if (d->out)
+    KVM_HIP(kvm::launch_attn_delta(L, d->dout, d->do_sb, d->do_st, d->do_sh, d->out, d->o_sb, d->o_st, d->o_sh, T,
+                                   d->delta, s),
+            "delta");
   KVM_HIP(kvm::launch_attn_backward(L, a, table, static_cast<float *>(d->workspace), s), "attention backward");
   return KVM_OK;
 }

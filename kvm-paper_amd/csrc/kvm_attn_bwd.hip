@@ -274,6 +274,31 @@ void k_attn_bwd_dq(kvm_layer L, BwdArgs A, int qtiles, ChunkTable table, float *
   }
 }
 
+// delta[b, hq, t] = sum over features of dout * out (fp32 sum of the bf16
+// products), the row term of dS = p (dP - delta).  D/8 lanes per row, each
+// with 8 features (16-byte loads of both bf16 rows).
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_bwd_delta(const uint16_t *dout, int64_t do_sb, int64_t do_st,
+                                                        int64_t do_sh, const uint16_t *out, int64_t o_sb,
+                                                        int64_t o_st, int64_t o_sh, int Hq, int64_t T,
+                                                        int64_t n_rows, float *delta) {
+  constexpr int GL = D / 8;
+  const int64_t r = int64_t(blockIdx.x) * (256 / GL) + threadIdx.x / GL;  // row (b, hq, t)
+  const int part = threadIdx.x % GL;
+  const bool ok = r < n_rows;
+  const int64_t rr = ok ? r : 0;
+  const int64_t t = rr % T, bh = rr / T;
+  const int hq = int(bh % Hq), b = int(bh / Hq);
+  float x[8], y[8];
+  load8(dout + b * do_sb + t * do_st + hq * do_sh + part * 8, x);
+  load8(out + b * o_sb + t * o_st + hq * o_sh + part * 8, y);
+  float a = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a += x[e] * y[e];
+  a = group_sum<GL>(a);
+  if (ok && part == 0) delta[r] = a;
+}
+
 // Per-head temperature gradients: partials summed in a fixed order
 // (batch, chunk, tile).
 __global__ void k_attn_bwd_temps(const float *tpart, int B, int Hq, int n_chunks, int qtiles,
@@ -338,7 +363,17 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
     kst = A.kv.k_st;
     vst = A.kv.v_st;
   }
-  if (kb0 >= nkeys) return;  // workgroup-uniform, before any barrier
+  if (kb0 >= nkeys) {  // workgroup-uniform, before any barrier
+    if (SNAP) {  // rows past the snapshot's length get a zero gradient
+      const int64_t off = int64_t(table.snap_slot[m_snap]) * A.dsnap_stride + int64_t(kvrow) * A.snap_cap * D;
+      const int64_t nrow = min(int64_t(BKW), A.snap_cap - kb0);
+      for (int64_t i = threadIdx.x; i < nrow * D / 4; i += NTB) {
+        reinterpret_cast<float4 *>(A.d_snap_k + off + kb0 * D)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        reinterpret_cast<float4 *>(A.d_snap_v + off + kb0 * D)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    return;
+  }
 
   for (int i = threadIdx.x; i < 2 * BUF / 16; i += NTB)
     reinterpret_cast<uint4 *>(lds)[i] = make_uint4(0, 0, 0, 0);
@@ -486,8 +521,13 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
       }
     }
   }
-  // Owner writes (fp32): lane holds dims dt*16 + 4*(lane/16) + i of key kp.
-  if (kp < nkeys) {
+  // Owner writes (fp32): lane holds dims dt*16 + 4*(lane/16) + i of key kp;
+  // snapshot rows past the snapshot's length are written as zeros.
+  if (SNAP && kp >= nkeys) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (kp < nkeys || (SNAP && kp < A.snap_cap)) {
     float *dkp, *dvp;
     if (SNAP) {
       const int64_t off = int64_t(table.snap_slot[m_snap]) * A.dsnap_stride + int64_t(kvrow) * A.snap_cap * D;
@@ -540,6 +580,22 @@ hipError_t launch_bwd_d(const kvm_layer &L, const BwdArgs &a, const ChunkTable &
 int64_t attn_bwd_workspace_bytes(const kvm_layer &L, int64_t n_chunks) {
   const int64_t qtiles = (L.chunk_len + BQ - 1) / BQ;
   return L.batch * L.q_heads * n_chunks * qtiles * 2 * 4;
+}
+
+hipError_t launch_attn_delta(const kvm_layer &L, const void *dout, int64_t do_sb, int64_t do_st, int64_t do_sh,
+                             const void *out, int64_t o_sb, int64_t o_st, int64_t o_sh, int64_t T, float *delta,
+                             hipStream_t stream) {
+  const int64_t n_rows = L.batch * L.q_heads * T;
+  const int gl = int(L.head_dim / 8);
+  const unsigned grid = unsigned((n_rows + (256 / gl) - 1) / (256 / gl));
+  const uint16_t *dp = static_cast<const uint16_t *>(dout), *op = static_cast<const uint16_t *>(out);
+  if (L.head_dim == 128)
+    hipLaunchKernelGGL((k_attn_bwd_delta<128>), dim3(grid), dim3(256), 0, stream, dp, do_sb, do_st, do_sh, op,
+                       o_sb, o_st, o_sh, int(L.q_heads), T, n_rows, delta);
+  else
+    hipLaunchKernelGGL((k_attn_bwd_delta<64>), dim3(grid), dim3(256), 0, stream, dp, do_sb, do_st, do_sh, op,
+                       o_sb, o_st, o_sh, int(L.q_heads), T, n_rows, delta);
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_backward(const kvm_layer &L, const BwdArgs &a, const ChunkTable &table,

@@ -196,6 +196,10 @@ struct BwdArgs {
 int64_t attn_bwd_workspace_bytes(const kvm_layer &L, int64_t n_chunks);
 hipError_t launch_attn_backward(const kvm_layer &L, const BwdArgs &a, const ChunkTable &table,
                                 float *tpart, hipStream_t stream);
+// delta = rowsum(dout * out) over [B, Hq, T] rows (bf16 inputs, fp32 out).
+hipError_t launch_attn_delta(const kvm_layer &L, const void *dout, int64_t do_sb, int64_t do_st, int64_t do_sh,
+                             const void *out, int64_t o_sb, int64_t o_st, int64_t o_sh, int64_t T, float *delta,
+                             hipStream_t stream);
 
 // Memory-state backward (kvm_state_bwd.hip).  dk / dv are [rows, T, D]
 // fp32 (added to), dgate [rows, T]; snapshot gradients

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -91,6 +91,7 @@ class KvmPrefillBwdDesc(ctypes.Structure):
         ("seq_len", _i64),
         ("dout", _vp), ("do_sb", _i64), ("do_st", _i64), ("do_sh", _i64),
         ("lse", _vp), ("delta", _vp),
+        ("out", _vp), ("o_sb", _i64), ("o_st", _i64), ("o_sh", _i64),
         ("snap_k", _vp), ("snap_v", _vp),
         ("max_state_len", _i64),
         ("n_chunks", _i64),

@@ -107,7 +107,7 @@ def attention_backward(mixer, q, k, v, gate, res, dout):
     dev = q.device
     out = res["out"]                                  # [B, T, Hq, D] bf16
     dout = dout.to(torch.bfloat16).contiguous()
-    delta = (dout.float() * out.float()).sum(-1).permute(0, 2, 1).contiguous()  # [B, Hq, T]
+    delta = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)  # rowsum(dout * out), filled by the library
     qv = _lib._bf16_view(q, "q")
     seq, keep = _lib.seq4(k, v, gate)
     layer = mixer._layer_struct(B, dev)
@@ -128,6 +128,7 @@ def attention_backward(mixer, q, k, v, gate, res, dout):
     d.seq_len = T
     d.dout, d.do_sb, d.do_st, d.do_sh = dout.data_ptr(), dout.stride(0), dout.stride(1), dout.stride(2)
     d.lse, d.delta = res["lse"].data_ptr(), delta.data_ptr()
+    d.out, d.o_sb, d.o_st, d.o_sh = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
     d.snap_k, d.snap_v = snap_k.data_ptr(), snap_v.data_ptr()
     d.max_state_len = plan.max_state_len
     d.n_chunks = plan.n_chunks
