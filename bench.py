@@ -253,7 +253,7 @@ def bench_e2e(args, torch, kvm_amd):
     of 128, vocab 65536, bf16, chunk 512, 512 fixed slots); prefill 16384
     random token ids at batch 8, then greedy decode.  One untimed warm-up
     (prefill + 8 decode steps), then the timed prefill and decode."""
-    from kvm_amd.backbone import MixerConfig, RWKV7BackboneForCausalLM, StatesDictCache, init_random_
+    from kvm_amd.backbone import DecodeGraph, MixerConfig, RWKV7BackboneForCausalLM, StatesDictCache, init_random_
 
     cfg = MixerConfig(vocab_size=65536, num_hidden_layers=24, num_attention_heads=16, hidden_size=2048,
                       mup_base_dim=2048, use_tokenshift_att=1, use_tokenshift_ffn=1, residual_scale=0.5,
@@ -266,7 +266,7 @@ def bench_e2e(args, torch, kvm_amd):
     gen = torch.Generator(device="cuda").manual_seed(1)
     ids = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=gen)
 
-    def run(n):
+    def run(n, graph):
         cache = StatesDictCache()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         torch.cuda.synchronize()
@@ -274,21 +274,27 @@ def bench_e2e(args, torch, kvm_amd):
         lg = model(input_ids=ids, past_key_values=cache, use_cache=True,
                    cache_position=torch.arange(T, device="cuda"), logits_to_keep=1).logits[:, -1]
         e[1].record()
+        runner = DecodeGraph(model, cache) if graph else None
         for s in range(n):
             tok = lg.argmax(-1)
-            lg = model(input_ids=tok[:, None], past_key_values=cache, use_cache=True,
-                       cache_position=torch.tensor([T + s], device="cuda"), logits_to_keep=1).logits[:, -1]
+            if runner is not None:
+                lg = runner.step(tok)
+            else:
+                lg = model(input_ids=tok[:, None], past_key_values=cache, use_cache=True,
+                           cache_position=torch.tensor([T + s]), logits_to_keep=1).logits[:, -1]
         e[2].record()
         torch.cuda.synchronize()
         return e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
 
     with torch.no_grad():
-        run(8)
-        pre_ms, dec_ms = run(n_dec)
+        run(8, True)
+        pre_ms, dec_ms = run(n_dec, True)
+        _, eager_ms = run(min(n_dec, 64), False)
     del model
     torch.cuda.empty_cache()
     return dict(prefill_ms=pre_ms, prefill_tok_s=B * T / (pre_ms * 1e-3), decode_ms_per_step=dec_ms / n_dec,
-                decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec)
+                decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec, decode_path="hip_graph",
+                eager_decode_ms_per_step=eager_ms / min(n_dec, 64))
 
 
 def _cpu_prefill_inputs(torch, B, H, D, T, dtype, seed):

@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 7
+#define KVM_ABI_VERSION 8
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -377,6 +377,30 @@ int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
                          int64_t ring_start, int64_t recent_len, void *out,
                          int64_t o_sb, int64_t o_sh, void *workspace,
                          int64_t workspace_bytes, void *stream);
+
+/* Decode with the step counters in device memory, so that a decode step can
+ * be captured once in a HIP graph and replayed (the kernels read the counters
+ * when they run; the arguments of a replayed launch never change).  ctl is
+ * an int32 record {active_state_len, ring_start, recent_len, reserved} per
+ * layer, holding the values BEFORE the step's token is written: the ring
+ * write stores it at row (ring_start + recent_len) % ring_cap, the attention
+ * reads recent_len + pending window rows (pending = 1 after that write), and
+ * kvm_decode_advance moves recent_len past it.  Kernels clamp the counters to
+ * the ring and state capacities.  The same operations as kvm_ring_write and
+ * kvm_decode_attention (model/kvm_triton_mixer.py:717-757, whose counters are
+ * host values); the attention's grid covers st->capacity + ring_cap rows
+ * (workspace: kvm_decode_workspace_bytes of that many rows), and its result
+ * is bit-identical to kvm_decode_attention's for the same counters. */
+int kvm_ring_write_dev(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
+                       void *ring_v, void *ring_gate, int64_t ring_cap,
+                       const int32_t *ctl, void *stream);
+int kvm_decode_attention_dev(const kvm_layer *layer, const void *q, int64_t q_sb,
+                             int64_t q_sh, const kvm_state *st, const int32_t *ctl,
+                             int32_t pending, const void *ring_k, const void *ring_v,
+                             int64_t ring_cap, void *out, int64_t o_sb, int64_t o_sh,
+                             void *workspace, int64_t workspace_bytes, void *stream);
+/* recent_len += 1 in the n records at ctl (record i at ctl + 4 i). */
+int kvm_decode_advance(int32_t *ctl, int64_t n, void *stream);
 
 /* Size of the library-owned scratch of kvm_decode_attention_noalloc, per GPU. */
 #define KVM_DECODE_SCRATCH_BYTES (16 << 20)

@@ -316,6 +316,24 @@ int kvm_ring_write(const kvm_layer *layer, const kvm_seq *src, void *ring_k,
   return KVM_OK;
 }
 
+int kvm_ring_write_dev(const kvm_layer *layer, const kvm_seq *src, void *ring_k, void *ring_v,
+                       void *ring_gate, int64_t ring_cap, const int32_t *ctl, void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_seq(src, "src"))) return rc;
+  if (!ring_k || !ring_v || !ring_gate || !aligned16(ring_k) || !aligned16(ring_v) || ring_cap < 1)
+    return fail(KVM_EINVAL, "ring buffers must be set and 16-byte aligned");
+  if (!ctl) return fail(KVM_EINVAL, "ctl must point to the device counters");
+  KVM_HIP(kvm::launch_ring_write(*layer, *src, ring_k, ring_v, ring_gate, ring_cap, 0, as_stream(stream), ctl),
+          "kvm_ring_write_dev");
+  return KVM_OK;
+}
+
+int kvm_decode_advance(int32_t *ctl, int64_t n, void *stream) {
+  if (!ctl || n < 1) return fail(KVM_EINVAL, "decode advance needs counters");
+  KVM_HIP(kvm::launch_decode_advance(ctl, n, as_stream(stream)), "kvm_decode_advance");
+  return KVM_OK;
+}
+
 int64_t kvm_prefill_backward_workspace_bytes(const kvm_prefill_bwd_desc *d) {
   if (!d || check_layer(&d->layer) != KVM_OK || d->n_chunks < 1) return -1;
   return kvm::attn_bwd_workspace_bytes(d->layer, d->n_chunks);
@@ -465,6 +483,30 @@ int kvm_state_backward(const kvm_state_bwd_desc *d, void *stream) {
   a.d_ln = d->d_ln;
   KVM_HIP(kvm::launch_state_backward(a, U, static_cast<float *>(d->workspace), as_stream(stream)),
           "state backward");
+  return KVM_OK;
+}
+
+int kvm_decode_attention_dev(const kvm_layer *layer, const void *q, int64_t q_sb, int64_t q_sh,
+                             const kvm_state *st, const int32_t *ctl, int32_t pending, const void *ring_k,
+                             const void *ring_v, int64_t ring_cap, void *out, int64_t o_sb, int64_t o_sh,
+                             void *workspace, int64_t workspace_bytes, void *stream) {
+  int rc;
+  if ((rc = check_layer(layer)) || (rc = check_state(st, true))) return rc;
+  if (!q || !aligned16(q) || q_sb % 8 || q_sh % 8)
+    return fail(KVM_EINVAL, "q must be 16-byte aligned with strides multiple of 8");
+  if (!out) return fail(KVM_EINVAL, "out must be set");
+  if (!ring_k || !ring_v || !aligned16(ring_k) || !aligned16(ring_v) || ring_cap < 1)
+    return fail(KVM_EINVAL, "ring buffers must be set and 16-byte aligned");
+  if (!ctl) return fail(KVM_EINVAL, "ctl must point to the device counters");
+  if (pending < 0 || pending > 1) return fail(KVM_EINVAL, "pending must be 0 or 1");
+  const int64_t max_rows = st->capacity + ring_cap;
+  const int64_t need = kvm::decode_workspace_bytes(*layer, max_rows);
+  if (!workspace || workspace_bytes < need)
+    return fail(KVM_ESPACE, "decode workspace of %lld bytes is smaller than %lld",
+                (long long)workspace_bytes, (long long)need);
+  KVM_HIP(kvm::launch_decode(*layer, q, q_sb, q_sh, *st, 0, ring_k, ring_v, ring_cap, 0, 0, out, o_sb, o_sh,
+                             workspace, as_stream(stream), ctl, int(pending), max_rows),
+          "kvm_decode_attention_dev");
   return KVM_OK;
 }
 

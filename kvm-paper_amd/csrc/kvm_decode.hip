@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(
     int64_t cap, int active, const uint16_t *__restrict__ rk,
     const uint16_t *__restrict__ rv, int64_t ring_cap, int64_t ring_start,
     int recent_len, int nseg, float *__restrict__ part_acc,
-    float *__restrict__ part_ml) {
+    float *__restrict__ part_ml, const int32_t *__restrict__ ctl, int pending) {
   constexpr int G = D / 8;             // lanes per key row
   constexpr int RPS = 64 / G;          // rows per wave step
   constexpr int STEPS = kRowsPerWave / RPS;
@@ -59,7 +59,12 @@ __global__ __launch_bounds__(256) void k_decode_partial(
   const int hq0 = hk * group + blockIdx.z * GQ;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / G, part = lane % G;
-  const int total = active + recent_len;
+  if (ctl) {  // counters in device memory (graph-captured decode), clamped to the buffers
+    active = min(max(ctl[0], 0), int(cap));
+    ring_start = ((int64_t(ctl[1]) % ring_cap) + ring_cap) % ring_cap;
+    recent_len = min(max(ctl[2] + pending, 0), int(ring_cap));
+  }
+  const int total = min(active + recent_len, nseg * kSegRows);
   const float scale = kLog2e / sqrtf(float(D));
 
   float qv[GQ][8], ts[GQ], tf[GQ];
@@ -214,7 +219,7 @@ hipError_t launch_partial(const kvm_layer &L, const void *q, int64_t q_sb,
                           const void *ring_k, const void *ring_v,
                           int64_t ring_cap, int64_t ring_start,
                           int64_t recent_len, int nseg, float *pacc,
-                          float *pml, hipStream_t stream) {
+                          float *pml, const int32_t *ctl, int pending, hipStream_t stream) {
   const int group = int(L.q_heads / L.kv_heads);
   dim3 grid(unsigned(nseg), unsigned(L.batch * L.kv_heads),
             unsigned(group / GQ));
@@ -224,7 +229,7 @@ hipError_t launch_partial(const kvm_layer &L, const void *q, int64_t q_sb,
                      static_cast<const uint16_t *>(st.s_v_attn), st.capacity,
                      int(active), static_cast<const uint16_t *>(ring_k),
                      static_cast<const uint16_t *>(ring_v), ring_cap,
-                     ring_start, int(recent_len), nseg, pacc, pml);
+                     ring_start, int(recent_len), nseg, pacc, pml, ctl, pending);
   return hipGetLastError();
 }
 
@@ -234,12 +239,12 @@ hipError_t launch_partial_d(const kvm_layer &L, const void *q, int64_t q_sb,
                             const void *ring_k, const void *ring_v,
                             int64_t ring_cap, int64_t ring_start,
                             int64_t recent_len, int nseg, float *pacc,
-                            float *pml, hipStream_t stream) {
+                            float *pml, const int32_t *ctl, int pending, hipStream_t stream) {
   const int64_t group = L.q_heads / L.kv_heads;
 #define KVM_PARTIAL(GQ)                                                      \
   launch_partial<D, GQ>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,       \
                         ring_cap, ring_start, recent_len, nseg, pacc, pml, \
-                        stream)
+                        ctl, pending, stream)
   if (group % 4 == 0) return KVM_PARTIAL(4);
   if (group % 2 == 0) return KVM_PARTIAL(2);
   return KVM_PARTIAL(1);
@@ -294,8 +299,11 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
                          const void *ring_k, const void *ring_v,
                          int64_t ring_cap, int64_t ring_start,
                          int64_t recent_len, void *out, int64_t o_sb,
-                         int64_t o_sh, void *workspace, hipStream_t stream) {
-  const int nseg = int(decode_segments(active + recent_len));
+                         int64_t o_sh, void *workspace, hipStream_t stream,
+                         const int32_t *ctl, int pending, int64_t max_rows) {
+  // Host counters: segments for the rows present; device counters: for
+  // max_rows (segments past the live rows contribute nothing).
+  const int nseg = int(decode_segments(ctl ? max_rows : active + recent_len));
   const int64_t npid = L.batch * L.q_heads;
   float *pacc = static_cast<float *>(workspace);
   float *pml = pacc + npid * nseg * L.head_dim;
@@ -303,11 +311,11 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
   if (L.head_dim == 128)
     e = launch_partial_d<128>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
                               ring_cap, ring_start, recent_len, nseg, pacc,
-                              pml, stream);
+                              pml, ctl, pending, stream);
   else
     e = launch_partial_d<64>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
                              ring_cap, ring_start, recent_len, nseg, pacc, pml,
-                             stream);
+                             ctl, pending, stream);
   if (e != hipSuccess) return e;
   if (L.head_dim == 128)
     hipLaunchKernelGGL(k_decode_combine<128>, dim3(unsigned(npid)), dim3(128),
@@ -317,6 +325,19 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
     hipLaunchKernelGGL(k_decode_combine<64>, dim3(unsigned(npid)), dim3(64), 0,
                        stream, int(L.q_heads), nseg, pacc, pml,
                        static_cast<uint16_t *>(out), o_sb, o_sh);
+  return hipGetLastError();
+}
+
+namespace {
+// recent_len += 1 in n counter records (vector stores: one lane per record).
+__global__ __launch_bounds__(256) void k_decode_advance(int32_t *ctl, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) ctl[i * 4 + 2] += 1;
+}
+}  // namespace
+
+hipError_t launch_decode_advance(int32_t *ctl, int64_t n, hipStream_t stream) {
+  hipLaunchKernelGGL(k_decode_advance, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, ctl, n);
   return hipGetLastError();
 }
 

@@ -136,9 +136,12 @@ constexpr unsigned kChainDefaultPolls = 1u << 22;
 // Fill n words at p with v (a kernel, so the work may be graph-captured).
 hipError_t launch_fill_u32(unsigned *p, int64_t n, unsigned v, hipStream_t stream);
 
+// ctl (optional): device counters {.., ring_start, recent_len, ..}; the row is
+// then (ring_start + recent_len) % ring_cap, read when the kernel runs.
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
                              void *ring_k, void *ring_v, void *ring_gate,
-                             int64_t ring_cap, int64_t pos, hipStream_t stream);
+                             int64_t ring_cap, int64_t pos, hipStream_t stream,
+                             const int32_t *ctl = nullptr);
 
 int64_t decode_segments(int64_t rows_total);
 // Address of this device's library-owned decode scratch
@@ -150,7 +153,9 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
                          const void *ring_k, const void *ring_v,
                          int64_t ring_cap, int64_t ring_start,
                          int64_t recent_len, void *out, int64_t o_sb,
-                         int64_t o_sh, void *workspace, hipStream_t stream);
+                         int64_t o_sh, void *workspace, hipStream_t stream,
+                         const int32_t *ctl = nullptr, int pending = 0, int64_t max_rows = 0);
+hipError_t launch_decode_advance(int32_t *ctl, int64_t n, hipStream_t stream);
 
 // Per-launch table of the query chunks an attention launch covers.
 constexpr int kMaxChunksPerLaunch = 256;

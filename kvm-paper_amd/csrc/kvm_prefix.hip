@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, carry);
     }
 #pragma unroll 1
-    for (int ps = 0; ps < PASSES; ++ps) {
+    for (int ps = 0; ps < PASSES && t0 + ps * RPW < T; ++ps) {  // passes with a live token
       const int64_t t = t0 + ps * RPW + sub;
       const bool live = t < T;
       const int64_t r = bi * T + (live ? t : T - 1);
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     }
   }
 #pragma unroll 1
-  for (int ps = 0; ps < PASSES; ++ps) {
+  for (int ps = 0; ps < PASSES && t0 + ps * RPW < T; ++ps) {  // passes with a live token
     const int64_t t = t0 + ps * RPW + sub;
     const bool live = t < T;
     const int64_t tt = live ? t : T - 1;

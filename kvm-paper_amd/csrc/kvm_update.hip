@@ -554,7 +554,12 @@ __global__ __launch_bounds__(64) void k_ring_write(kvm_layer L, kvm_seq src,
                                                    uint16_t *rk, uint16_t *rv,
                                                    uint16_t *rg,
                                                    int64_t ring_cap,
-                                                   int64_t pos) {
+                                                   int64_t pos, const int32_t *ctl) {
+  if (ctl) {  // row after the window held in device counters (clamped to the ring)
+    const int64_t start = ((int64_t(ctl[1]) % ring_cap) + ring_cap) % ring_cap;
+    const int64_t len = min(max(int64_t(ctl[2]), int64_t(0)), ring_cap);
+    pos = (start + len) % ring_cap;
+  }
   const int row = blockIdx.x;
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int lane = threadIdx.x;
@@ -725,18 +730,18 @@ hipError_t launch_update(const kvm_layer &L, const kvm_seq &src,
 hipError_t launch_ring_write(const kvm_layer &L, const kvm_seq &src,
                              void *ring_k, void *ring_v, void *ring_gate,
                              int64_t ring_cap, int64_t pos,
-                             hipStream_t stream) {
+                             hipStream_t stream, const int32_t *ctl) {
   dim3 grid(unsigned(rows_of(L)));
   if (L.head_dim == 128)
     hipLaunchKernelGGL(k_ring_write<128>, grid, dim3(64), 0, stream, L, src,
                        static_cast<uint16_t *>(ring_k),
                        static_cast<uint16_t *>(ring_v),
-                       static_cast<uint16_t *>(ring_gate), ring_cap, pos);
+                       static_cast<uint16_t *>(ring_gate), ring_cap, pos, ctl);
   else
     hipLaunchKernelGGL(k_ring_write<64>, grid, dim3(64), 0, stream, L, src,
                        static_cast<uint16_t *>(ring_k),
                        static_cast<uint16_t *>(ring_v),
-                       static_cast<uint16_t *>(ring_gate), ring_cap, pos);
+                       static_cast<uint16_t *>(ring_gate), ring_cap, pos, ctl);
   return hipGetLastError();
 }
 

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -149,6 +149,10 @@ SIGNATURES = {
     "kvm_state_backward_workspace_bytes": (_i64, [_P(KvmStateBwdDesc)]),
     "kvm_state_backward": (ctypes.c_int, [_P(KvmStateBwdDesc), _vp]),
     "kvm_prefix": (ctypes.c_int, [_P(KvmPrefixDesc), _vp]),
+    "kvm_ring_write_dev": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _vp, _vp, _vp, _i64, _vp, _vp]),
+    "kvm_decode_attention_dev": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _vp, ctypes.c_int32,
+                                                _vp, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "kvm_decode_advance": (ctypes.c_int, [_vp, _i64, _vp]),
     "kvm_token_shift": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "kvm_state_append_direct": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _i64, _i64, _P(KvmState), _i64, _vp]),

@@ -39,7 +39,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .mixer import set_label
+from . import _lib
+from .mixer import SequenceMixer, set_label
 from .states_cache import StatesDictCache
 
 _KVM_PATH = "kvm_amd.mixer.SequenceMixer"
@@ -191,12 +192,19 @@ class MLP(nn.Module):
                 if prev is not None and prev.shape != (x.shape[0], 1, x.shape[2]):
                     raise AssertionError(f"cached MLP decode requires 'mlp_final_token' of shape "
                                          f"{(x.shape[0], 1, x.shape[2])}, got {tuple(prev.shape)}.")
-                # a copy, not a view: a view would keep the whole [B, T, d] input alive
-                past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:].clone()})
             if self._use_kernels(x):
                 xk = _kernel_token_shift(x, prev, self.x_k)
             else:
                 xk = x + self.x_k * token_shift_delta(x, prev, fallback="zero")
+            if past_key_values is not None:
+                # a copy, not a view: a view would keep the whole [B, T, d] input alive
+                # (written in place, after its last read, when the cache keeps fixed
+                # addresses for a captured decode step)
+                if (getattr(past_key_values, "static_states", False) and prev is not None
+                        and prev.shape == (x.shape[0], 1, x.shape[2]) and prev.dtype == x.dtype):
+                    prev.copy_(x[:, -1:])
+                else:
+                    past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:].clone()})
         else:
             xk = x
         h = self.c_fc(xk)
@@ -333,7 +341,13 @@ class RWKV7BackboneModel(nn.Module):
             raise ValueError("You must specify exactly one of input_ids or inputs_embeds")
         if inputs_embeds is None:
             inputs_embeds = self.embed(input_ids)
-        if cache_position is not None and cache_position.numel() > 0:
+        if (cache_position is not None and cache_position.numel() > 0 and cache_position.is_cuda
+                and isinstance(past_key_values, StatesDictCache)):
+            # The cache's own token count is what cache_position[0] must equal (each
+            # layer's cache asserts it); reading the GPU tensor back would stall the
+            # host on every decode step.
+            past_seen = past_key_values.get_seq_length(0)
+        elif cache_position is not None and cache_position.numel() > 0:
             past_seen = int(cache_position.reshape(-1)[0].item())
         elif position_ids is not None and position_ids.numel() > 0:
             past_seen = int(position_ids.reshape(-1)[0].item())
@@ -438,6 +452,125 @@ class RWKV7BackboneForCausalLM(nn.Module):
         return tokens
 
 
+class DecodeGraph:
+    """Cached single-token decode of ``model`` with the steady-state step
+    captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed.
+
+    A step that only appends the new token to every KVM layer's window ring
+    (the common case: no direct-state append, no state update, no window
+    slide) is replayed; the KVM kernels of the replay read their per-layer
+    counters {active state, ring start, window length} from device memory
+    (``kvm_ring_write_dev`` / ``kvm_decode_attention_dev``), one
+    ``kvm_decode_advance`` per step moves them on, and the host bookkeeping a
+    step does (cache token counts, window length) is mirrored in Python.
+    The other steps (one per chunk_len tokens) run eagerly and resynchronise
+    the device counters.  The layer cache keeps its per-token states at fixed
+    addresses (``static_states``) so that every replay reads the previous
+    step's.  No counterpart in the reference, which decodes eagerly
+    (model/kvm_triton_mixer.py:717-757): it removes the host cost of the
+    ~20 launches per layer of an eager step.  The graph is captured again
+    when a buffer it uses has been reallocated (a growing state budget)."""
+
+    def __init__(self, model: "RWKV7BackboneForCausalLM", cache: StatesDictCache):
+        self.model, self.cache = model, cache
+        cache.static_states = True
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.signature = None
+        self.ids = self.pos = self.ctl = self.logits = None
+        self.ctl_synced = False
+        self.replays = self.eager_steps = 0
+
+    def _kvm_caches(self):
+        from .decode_cache import KVMDecodeCache
+        out = []
+        for i in range(len(self.cache.layers)):
+            c = self.cache.layers[i].get(SequenceMixer._CACHE_TRITON_DECODE)
+            if isinstance(c, KVMDecodeCache):
+                out.append(c)
+        return out
+
+    def _sync_ctl(self, kv) -> None:
+        vals = torch.tensor([c.graph_counters() for c in kv], dtype=torch.int32)
+        self.ctl.copy_(vals)  # host to device, outside the graph
+        self.ctl_synced = True
+
+    @torch.no_grad()
+    def step(self, tok: torch.Tensor) -> torch.Tensor:
+        """Decode one token per sequence (``tok`` [B] ids on the GPU); returns
+        the fp32 logits [B, vocab] of the next position (for a replayed step, a
+        buffer the next step overwrites)."""
+        pos = self.cache.get_seq_length(0)
+        kv = self._kvm_caches()
+        plain = bool(kv) and len(kv) == len(self.cache.layers) and all(c.graph_step_is_plain() for c in kv)
+        if not plain:
+            self.ctl_synced = False
+            self.eager_steps += 1
+            out = self.model(input_ids=tok[:, None], past_key_values=self.cache, use_cache=True,
+                             cache_position=torch.tensor([pos]), logits_to_keep=1)
+            return out.logits[:, -1]
+        sig = tuple(c.graph_buffers() for c in kv)
+        if self.graph is None or sig != self.signature:
+            return self._capture(tok, pos, kv, sig)
+        if not self.ctl_synced:
+            self._sync_ctl(kv)
+        self.ids.copy_(tok[:, None])
+        self.pos.fill_(pos)
+        for i in range(len(self.cache.layers)):
+            self.cache.seen[i] += 1
+        for c in kv:
+            c.graph_advance_host_()
+        self.graph.replay()
+        self.replays += 1
+        return self.logits[:, -1]
+
+    def _capture(self, tok, pos, kv, sig):
+        dev = tok.device
+        if self.ids is None or self.ids.shape[0] != tok.shape[0]:
+            self.ids = torch.zeros(tok.shape[0], 1, dtype=torch.long, device=dev)
+            self.pos = torch.zeros(1, 1, dtype=torch.long, device=dev)
+        self.ctl = torch.zeros(len(kv), 4, dtype=torch.int32, device=dev)
+        self._sync_ctl(kv)
+        self.ids.copy_(tok[:, None])
+        self.pos.fill_(pos)
+        for i, c in enumerate(kv):
+            c.graph_ctl = self.ctl[i].data_ptr()
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        try:
+            # The step's host bookkeeping runs here, once; the capture records
+            # its device work, which the replay below then performs.
+            with torch.cuda.graph(graph):
+                out = self.model(input_ids=self.ids, past_key_values=self.cache, use_cache=True,
+                                 cache_position=torch.tensor([pos]), position_ids=self.pos, logits_to_keep=1)
+                self.logits = out.logits
+                _lib.check(_lib.load().kvm_decode_advance(self.ctl.data_ptr(), len(kv), _lib.stream_handle(dev)),
+                           "kvm_decode_advance")
+        finally:
+            for c in kv:
+                c.graph_ctl = None
+        self.graph, self.signature = graph, sig
+        graph.replay()
+        self.replays += 1
+        return self.logits[:, -1]
+
+    @torch.no_grad()
+    def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+        """``RWKV7BackboneForCausalLM.generate_greedy`` through this runner:
+        prefill eagerly, then decode step by step.  Returns [B, max_new_tokens]."""
+        B, T = input_ids.shape
+        out = self.model(input_ids=input_ids, past_key_values=self.cache, use_cache=True,
+                         cache_position=torch.arange(T, device=input_ids.device), logits_to_keep=1)
+        logits = out.logits[:, -1]
+        tokens = torch.empty(B, max_new_tokens, dtype=torch.long, device=input_ids.device)
+        for s in range(max_new_tokens):
+            tok = logits.argmax(-1)
+            tokens[:, s] = tok
+            if s + 1 == max_new_tokens:
+                break
+            logits = self.step(tok)
+        return tokens
+
+
 @torch.no_grad()
 def init_random_(model: nn.Module, seed: int = 0) -> nn.Module:
     """Seeded random weights for benchmarks and tests, generated on the
@@ -478,4 +611,4 @@ def init_random_(model: nn.Module, seed: int = 0) -> nn.Module:
 
 
 __all__ = ["MixerConfig", "RotaryEmbedding", "MLP", "Block", "RWKV7BackboneModel", "RWKV7BackboneForCausalLM",
-           "BaseModelOutput", "CausalLMOutput", "StatesDictCache", "init_random_", "token_shift_delta"]
+           "BaseModelOutput", "CausalLMOutput", "StatesDictCache", "DecodeGraph", "init_random_", "token_shift_delta"]

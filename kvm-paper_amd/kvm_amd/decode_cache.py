@@ -111,6 +111,7 @@ class KVMDecodeCache:
             int(lib.kvm_update_workspace_bytes(self.layer.ref(), self.chunk_len)), device=device, dtype=torch.uint8)
         self._alloc_decode_workspace()
         self._set_counters(total=0, state_len=0, coverage=0, begin=0, window=0)
+        self.graph_ctl: int | None = None  # device counter record while a decode step is captured
         if snapshot is not None:
             self.reset_(snapshot)
 
@@ -215,10 +216,49 @@ class KVMDecodeCache:
     def _write_window_row(self, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor, row: int) -> None:
         seq, keep = _lib.seq4(k, v, gate)
         lib = _lib.load()
-        _lib.check(lib.kvm_ring_write(self.layer.ref(), seq, self.recent_k.data_ptr(), self.recent_v.data_ptr(),
-                                      self.recent_gate.data_ptr(), self.ring_capacity, row,
-                                      _lib.stream_handle(self.device)), "kvm_ring_write")
+        if self.graph_ctl is not None:  # capture of a graph step: the row comes from the device counters
+            _lib.check(lib.kvm_ring_write_dev(self.layer.ref(), seq, self.recent_k.data_ptr(),
+                                              self.recent_v.data_ptr(), self.recent_gate.data_ptr(),
+                                              self.ring_capacity, self.graph_ctl,
+                                              _lib.stream_handle(self.device)), "kvm_ring_write_dev")
+        else:
+            _lib.check(lib.kvm_ring_write(self.layer.ref(), seq, self.recent_k.data_ptr(), self.recent_v.data_ptr(),
+                                          self.recent_gate.data_ptr(), self.ring_capacity, row,
+                                          _lib.stream_handle(self.device)), "kvm_ring_write")
         del keep
+
+    # -- graph-captured decode ------------------------------------------------
+    def graph_counters(self) -> list[int]:
+        """Device counter record {active_state_len, ring_start, recent_len, 0}
+        of the NEXT decode step (the values before its token is written)."""
+        active = self.state_len if self.total_len + 1 > self.ring_capacity else 0
+        return [active, self.recent_start, self.recent_len, 0]
+
+    def graph_step_is_plain(self) -> bool:
+        """Whether the next decode step only appends to the window ring (no
+        direct-state append, no state update, no slide, the same active state
+        length): the steps a captured graph replays."""
+        m = self.mixer
+        new_total = self.total_len + 1
+        if m._bswa_begin_for_total_len(new_total) != self.recent_begin:
+            return False
+        direct_target = min(new_total, self.chunk_len)
+        if max(direct_target, self.recent_begin) != self.state_coverage_len:
+            return False
+        if self.recent_len + 1 > self.ring_capacity:
+            return False
+        return self.total_len > self.ring_capacity  # active state length fixed (the whole state)
+
+    def graph_advance_host_(self) -> None:
+        """The host bookkeeping of one replayed plain step (append_recent_
+        without a slide)."""
+        self.recent_len += 1
+        self.total_len += 1
+
+    def graph_buffers(self) -> tuple:
+        """Device addresses a captured step depends on."""
+        return (self.state_k.data_ptr(), self.state_capacity, self.decode_workspace.data_ptr(),
+                self.recent_k.data_ptr(), self.recent_v.data_ptr(), self.recent_gate.data_ptr())
 
     # -- inspection -----------------------------------------------------------
     def _window(self, ring: torch.Tensor) -> torch.Tensor:

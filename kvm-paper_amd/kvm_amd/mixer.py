@@ -55,6 +55,25 @@ def set_label(label, module, mup_d_in_ratio=None):
     return module
 
 
+def _store_states(cache, layer_idx, states, new_states):
+    """Carry per-token states to the next step: copies (a view would keep
+    the whole [B, T, d] source alive), written in place into the previous
+    step's tensors when the cache asks for fixed addresses (a captured decode
+    step reads and writes the same buffers on every replay)."""
+    if getattr(cache, "static_states", False):
+        fresh = {}
+        for key, val in new_states.items():
+            old = states.get(key)
+            if old is not None and old.shape == val.shape and old.dtype == val.dtype:
+                old.copy_(val)
+            else:
+                fresh[key] = val.clone()
+        if fresh:
+            cache.update(layer_idx, offset=0, states_dict=fresh)
+        return
+    cache.update(layer_idx, offset=0, states_dict={key: val.clone() for key, val in new_states.items()})
+
+
 def apply_rotary_embeddings(x_BTHD, position_embeddings):
     """Interleaved-pair RoPE (model/rwkv7_backbone.py:76-88)."""
     cos, sin = position_embeddings
@@ -436,10 +455,9 @@ class SequenceMixer(nn.Module):
         _lib.check(lib.kvm_prefix(ctypes.byref(d), _lib.stream_handle(x.device)), "kvm_prefix")
         del keep
         if past_key_values is not None:
-            past_key_values.update(self.layer_idx, offset=0, states_dict={
-                self._CACHE_Q_FINAL: q_lin[:, -1:].clone(), self._CACHE_K_FINAL: k_lin[:, -1:].clone(),
-                self._CACHE_V_FINAL: v_last, self._CACHE_X_FINAL: x[:, -1:].detach().clone(),
-            })
+            new_states = {self._CACHE_Q_FINAL: q_lin[:, -1:], self._CACHE_K_FINAL: k_lin[:, -1:],
+                          self._CACHE_V_FINAL: v_last, self._CACHE_X_FINAL: x[:, -1:].detach()}
+            _store_states(past_key_values, self.layer_idx, states, new_states)
         if use_gate:
             merge_gate = gate.view(B, T, Hkv, 1).transpose(1, 2)
         else:
@@ -764,6 +782,13 @@ class SequenceMixer(nn.Module):
         active = c.state_len if c.total_len > c.ring_capacity else 0
         qv = _lib._bf16_view(q, "q")
         lib = _lib.load()
+        if c.graph_ctl is not None:  # capture of a graph step: counters from device memory
+            _lib.check(lib.kvm_decode_attention_dev(
+                c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), c.graph_ctl, 1,
+                c.recent_k.data_ptr(), c.recent_v.data_ptr(), c.ring_capacity, c.out.data_ptr(), c.out.stride(0),
+                c.out.stride(1), c.decode_workspace.data_ptr(), c.decode_workspace.numel(),
+                _lib.stream_handle(c.device)), "kvm_decode_attention_dev")
+            return c.out
         _lib.check(lib.kvm_decode_attention(
             c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), active,
             c.recent_k.data_ptr(), c.recent_v.data_ptr(), c.ring_capacity, c.recent_start, c.recent_len,
