@@ -299,6 +299,15 @@ int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out,
  * activation, F.relu(x).square() (model/rwkv7_backbone.py:174-175). */
 int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
 
+/* Y = X W^T for a few token rows: X bf16 [M, K] (row stride x_st), W bf16
+ * [N, K] (an nn.Linear weight, row stride w_st), Y bf16 [M, N] (row stride
+ * y_st), fp32 accumulation; 1 <= M <= 16, K a multiple of 32.  The linear
+ * layers of the decoder's single-token decode step (model/rwkv7_backbone.py
+ * MLP and attention projections, the LM head), which stream their weights
+ * once per step. */
+int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st, int64_t M,
+                   int64_t N, int64_t K, void *stream);
+
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
 int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc,

@@ -153,6 +153,17 @@ int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out,
   return KVM_OK;
 }
 
+int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st, int64_t M,
+                   int64_t N, int64_t K, void *stream) {
+  if (M < 1 || M > 16 || N < 1 || K < 32 || K % 32)
+    return fail(KVM_EINVAL, "gemm_small needs 1 <= M <= 16, N >= 1 and K a positive multiple of 32");
+  if (!x || !w || !y || !aligned16(x) || !aligned16(w) || x_st % 8 || w_st % 8 || x_st < K || w_st < K ||
+      y_st < N)
+    return fail(KVM_EINVAL, "gemm_small operands must be 16-byte aligned rows (strides multiples of 8)");
+  KVM_HIP(kvm::launch_gemm_small(x, x_st, w, w_st, y, y_st, M, N, K, as_stream(stream)), "gemm_small");
+  return KVM_OK;
+}
+
 int kvm_relu_square(const void *x, void *out, int64_t n, void *stream) {
   if (n < 8 || n % 8) return fail(KVM_EINVAL, "relu_square needs a positive element count that is a multiple of 8");
   if (!x || !out || !aligned16(x) || !aligned16(out))

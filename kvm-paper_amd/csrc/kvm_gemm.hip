@@ -1,0 +1,94 @@
+// Skinny GEMM of the decoder's decode step on gfx950: Y = X W^T for a few
+// rows of X (M <= 16 tokens) against a bf16 weight W [N, K] (nn.Linear
+// layout), fp32 accumulation, bf16 output.  The step is bound by streaming W
+// from HBM once (2.7 GB per config-5 decode step); a vendor GEMM tuned for
+// square shapes reads it at ~1.9 TB/s.
+//
+// A workgroup owns 16 rows of W (16 outputs per token) and its NW waves split
+// K evenly; NW (1 to 16) is the largest power of two leaving each wave at
+// least 256 of K.  A wave issues the loads of up to 16 k-steps (8 at 16 waves)
+// before their MFMAs: 16 bytes per lane, lanes 0-15 / 16-31 / ... covering 64
+// contiguous bytes of each row; v_mfma_f32_16x16x32_bf16 takes W rows as the A
+// operand and the tokens' X rows as the B operand (columns >= M read zero).
+// The per-wave partial tiles are summed in wave order through LDS, so the
+// result does not depend on timing.
+
+#include "kvm_device.hpp"
+#include "kvm_internal.hpp"
+
+namespace kvm {
+namespace {
+
+// k-steps of 32 whose loads are in flight together: 16, or 8 at 16 waves,
+// where 1024 threads leave a lane 128 registers.
+template <int NW>
+constexpr int kSteps = NW == 16 ? 8 : 16;
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restrict__ X, int64_t x_st,
+                                                        const uint16_t *__restrict__ W, int64_t w_st,
+                                                        uint16_t *__restrict__ Y, int64_t y_st, int M, int N,
+                                                        int K) {
+  __shared__ float red[NW][16][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kq = K / NW;  // a multiple of 32
+  const int kb = wave * kq, ke = kb + kq;
+  const bool row_ok = n0 + r < N, col_ok = r < M;
+  const uint16_t *wrow = W + int64_t(row_ok ? n0 + r : 0) * w_st + g * 8;
+  const uint16_t *xrow = X + int64_t(col_ok ? r : 0) * x_st + g * 8;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = kb; k0 < ke; k0 += 32 * kSteps<NW>) {
+    uint4 a[kSteps<NW>], b[kSteps<NW>];
+#pragma unroll
+    for (int c = 0; c < kSteps<NW>; ++c) {
+      const int k = k0 + 32 * c;
+      const bool in = k < ke;
+      a[c] = (in && row_ok) ? *reinterpret_cast<const uint4 *>(wrow + k) : make_uint4(0, 0, 0, 0);
+      b[c] = (in && col_ok) ? *reinterpret_cast<const uint4 *>(xrow + k) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < kSteps<NW>; ++c)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[c]), as_bf16x8(b[c]), acc, 0, 0, 0);
+  }
+  // C layout: lane holds rows n0 + 4g + i (outputs) of column r (token).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][4 * g + i][r] = acc[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < 256; i += NW * 64) {  // one (output, token) per thread
+    const int n = i / 16, m = i % 16;
+    if (m < M && n0 + n < N) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += red[w][n][m];
+      Y[int64_t(m) * y_st + n0 + n] = uint16_t(f2bf(s));
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
+                             int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  // Waves per workgroup: up to K / 256 (a power of two <= 16 dividing K / 32).
+  int nw = 1;
+  while (nw < 16 && K / (2 * nw) >= 256 && K % (32 * 2 * nw) == 0) nw *= 2;
+  const dim3 grid(unsigned((N + 15) / 16));
+  const uint16_t *xp = static_cast<const uint16_t *>(x), *wp = static_cast<const uint16_t *>(w);
+  uint16_t *yp = static_cast<uint16_t *>(y);
+#define KVM_GEMM(NWV)                                                                                      \
+  hipLaunchKernelGGL(k_gemm_small<NWV>, grid, dim3(NWV * 64), 0, stream, xp, x_st, wp, w_st, yp, y_st, int(M), \
+                     int(N), int(K))
+  switch (nw) {
+    case 1: KVM_GEMM(1); break;
+    case 2: KVM_GEMM(2); break;
+    case 4: KVM_GEMM(4); break;
+    case 8: KVM_GEMM(8); break;
+    default: KVM_GEMM(16); break;
+  }
+#undef KVM_GEMM
+  return hipGetLastError();
+}
+
+}  // namespace kvm

@@ -155,6 +155,7 @@ SIGNATURES = {
     "kvm_decode_advance": (ctypes.c_int, [_vp, _i64, _vp]),
     "kvm_token_shift": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "kvm_gemm_small": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kvm_state_append_direct": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _i64, _i64, _P(KvmState), _i64, _vp]),
     "kvm_state_refresh": (ctypes.c_int, [_P(KvmLayer), _P(KvmState), _i64, _i64, _vp]),
     "kvm_update_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),

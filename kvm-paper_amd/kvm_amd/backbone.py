@@ -40,6 +40,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _lib
+from .linear import linear, module_linear
 from .mixer import SequenceMixer, set_label
 from .states_cache import StatesDictCache
 
@@ -207,10 +208,10 @@ class MLP(nn.Module):
                     past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:].clone()})
         else:
             xk = x
-        h = self.c_fc(xk)
+        h = module_linear(self.c_fc, xk)
         if self._use_kernels(h):
-            return self.c_proj(_kernel_relu_square(h))
-        return self.c_proj(F.relu(h).square())
+            return module_linear(self.c_proj, _kernel_relu_square(h))
+        return module_linear(self.c_proj, F.relu(h).square())
 
     def _use_kernels(self, t: torch.Tensor) -> bool:
         """bf16 inference on the GPU takes the HIP elementwise kernels (same
@@ -421,7 +422,7 @@ class RWKV7BackboneForCausalLM(nn.Module):
                                 **kwargs)
         hidden, cache = base.last_hidden_state, base.past_key_values
         keep = slice(-logits_to_keep, None) if isinstance(logits_to_keep, int) else logits_to_keep
-        logits = self.lm_head(hidden[:, keep, :])
+        logits = module_linear(self.lm_head, hidden[:, keep, :])
         if self.config.logit_softcap != 0:
             logits = self.config.logit_softcap * torch.tanh(logits / self.config.logit_softcap)
         return CausalLMOutput(logits=logits.float(), past_key_values=cache)

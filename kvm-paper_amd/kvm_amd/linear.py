@@ -1,0 +1,53 @@
+"""Linear layers of the decoder's single-token decode step.
+
+A decode step multiplies a few token rows (M <= 16) by each weight matrix, so
+it is bound by reading the weights once; ``kvm_gemm_small`` streams them at
+HBM speed where a general GEMM does not.  Everything else (prefill, training,
+CPU tensors) goes to ``torch.nn.functional.linear``.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(x, weight, bias)``; bf16 inference on at most 16 rows runs
+    ``kvm_gemm_small`` (fp32 accumulation, one bf16 rounding)."""
+    K = int(weight.shape[-1])
+    if (bias is not None or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
+            or K % 32 or x.shape[-1] != K or (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad))):
+        return F.linear(x, weight, bias)
+    M = x.numel() // K
+    if M < 1 or M > 16:
+        return F.linear(x, weight, bias)
+    x2 = x.reshape(M, K)
+    # The stride of a single row is meaningless to torch (it may be anything);
+    # the kernel only needs K for it.
+    x_st = K if M == 1 else int(x2.stride(0))
+    if x2.stride(-1) != 1 or x_st % 8 or x_st < K or x2.data_ptr() % 16:
+        # clone, not contiguous(): a contiguous but misaligned view (a split
+        # of a wider row) would come back unchanged.
+        x2 = x2.clone(memory_format=torch.contiguous_format)
+        x_st = K
+    N = int(weight.shape[0])
+    w = weight
+    w_st = K if N == 1 else int(w.stride(0))
+    if w.stride(-1) != 1 or w_st % 8 or w_st < K or w.data_ptr() % 16:
+        w = weight.clone(memory_format=torch.contiguous_format)
+        w_st = K
+    y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    _lib.check(_lib.load().kvm_gemm_small(x2.data_ptr(), x_st, w.data_ptr(), w_st, y.data_ptr(), N,
+                                          M, N, K, _lib.stream_handle(x.device)), "kvm_gemm_small")
+    return y.view(*x.shape[:-1], N)
+
+
+def module_linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """``mod(x)`` through :func:`linear`."""
+    return linear(x, mod.weight, mod.bias)
+
+
+__all__ = ["linear", "module_linear"]

@@ -30,6 +30,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _lib
+from .linear import linear, module_linear
 from .decode_cache import DecodeCacheSnapshot, KVMDecodeCache
 from .schedule import (
     PrefillPlan,
@@ -296,7 +297,7 @@ class SequenceMixer(nn.Module):
         return {"v_first": self.c_v(x)}
 
     def _value_gate(self, x):
-        return torch.sigmoid(self.v_gate0 + self.v_gate2(self.v_gate1(x)))
+        return torch.sigmoid(self.v_gate0 + module_linear(self.v_gate2, module_linear(self.v_gate1, x)))
 
     def calc_qkv(self, x, v_first, past_key_values):
         """Projections, value residual, token shift, ln_q/ln_k (model/value_residual_mixin.py:173-237)."""
@@ -382,7 +383,7 @@ class SequenceMixer(nn.Module):
         if mode == 2:
             mods.append(self.v_gate1)
         if self._CONCAT_PROJ:
-            y = F.linear(x, self._projection_weight(mods))
+            y = linear(x, self._projection_weight(mods))
             sizes = [m.out_features for m in mods]
             parts = torch.split(y, sizes + [y.size(-1) - sum(sizes)], dim=-1)[:len(mods)]
         else:
@@ -393,10 +394,11 @@ class SequenceMixer(nn.Module):
         kw = parts[3] if use_gate else None
         gate_lin = None
         if mode == 2:
-            gate_lin = self.v_gate2(parts[-1])
+            gate_lin = module_linear(self.v_gate2, parts[-1])
         elif mode == 3:
             shift = self.x_v if self.value_projection_size == self.hidden_size else self.x_v_hidden
-            gate_lin = self.v_gate2(self.v_gate1(_token_shift(x, shift.view(1, 1, self.hidden_size), xp)))
+            gate_lin = module_linear(self.v_gate2, module_linear(
+                self.v_gate1, _token_shift(x, shift.view(1, 1, self.hidden_size), xp)))
         shift_on = self.tokenshift_mode == "rwkv"
         prev = [states.get(k) for k in (self._CACHE_Q_FINAL, self._CACHE_K_FINAL, self._CACHE_V_FINAL)]
         bf = dict(device=x.device, dtype=torch.bfloat16)
@@ -718,7 +720,7 @@ class SequenceMixer(nn.Module):
             raise AssertionError(f"HIP KVM decode cache length disagrees with the layer cache: {cache.total_len} != {past}")
         out = self._decode_one_token(q, k, v, merge_gate, cache)
         past_key_values.update(self.layer_idx, offset=1, states_dict={self._CACHE_TRITON_DECODE: cache})
-        return self.c_proj(out.transpose(1, 2).contiguous().view(int(q.size(0)), 1, -1))
+        return module_linear(self.c_proj, out.transpose(1, 2).contiguous().view(int(q.size(0)), 1, -1))
 
     def _decode_one_token(self, q, k, v, merge_gate, decode_cache: KVMDecodeCache) -> torch.Tensor:
         """Advance ``decode_cache`` by one post-QKV token and attend (model/kvm_triton_mixer.py:717-757)."""

@@ -1,0 +1,36 @@
+"""kvm_gemm_small (the decode step's linear layers) against an fp32 product.
+
+Y = X W^T with fp32 accumulation and one rounding to bf16: every output is
+within one bf16 ulp of the fp32 product of the same bf16 operands, plus the
+fp32 summation bound K 2^-24 sum_k |x_k w_k| (two fp32 sums of K terms in
+different orders; it dominates only where the result nearly cancels)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kvm_testlib as T
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 48, 128), (3, 100, 384), (8, 2048, 64), (8, 6160, 2048), (8, 2048, 2048),
+                                   (16, 2048, 8192), (8, 65536, 2048), (5, 300, 1152)])
+def test_gemm_small_matches_fp32(M, N, K):
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd.linear import linear
+
+    T.log(f"[gemm] M{M} N{N} K{K}")
+    gen = torch.Generator(device=DEV).manual_seed(M * 7 + N)
+    x = torch.randn(M, K, device=DEV, generator=gen).bfloat16()
+    w = (torch.randn(N, K, device=DEV, generator=gen) / K ** 0.5).bfloat16()
+    with torch.no_grad():
+        got = linear(x, w).float()
+    ref = x.float() @ w.float().t()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
+    bound = ulp + K * 2.0 ** -24 * (x.float().abs() @ w.float().abs().t())
+    excess = float(((got - ref).abs() / bound).max())
+    T.log(f"[gemm] max |err| / (1 ulp + fp32 sum bound) = {excess:.3f}")
+    assert excess <= 1.0, f"error {excess:.2f} x the bound"
