@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 8
+#define KVM_ABI_VERSION 9
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -266,7 +266,11 @@ int kvm_state_backward(const kvm_state_bwd_desc *d, void *stream);
  * parameters are bf16.  Outputs q_out [B,T,Hq,D], k_out [B,T,Hkv,D], v_out
  * [B,T,Hkv,Dv], gate_out [B,T,Hkv] (bf16, contiguous); v_last_out
  * (optional, [B,1,Hkv*Dv]) receives the last token's value after a value
- * residual applied before the shift (the decode cache's carried value). */
+ * residual applied before the shift (the decode cache's carried value);
+ * q_last_out / k_last_out (optional, [B,1,Hq*D] / [B,1,Hkv*D]) receive the
+ * last token's q_lin / k_lin rows (the carried rows of the next step's token
+ * shift).  With seq_len == 1 each of the three may be the corresponding
+ * q_prev / k_prev / v_prev itself (read before it is written). */
 typedef struct kvm_prefix_desc {
   int64_t batch, seq_len, q_heads, kv_heads, head_dim, value_dim;
   int64_t value_residual_mode; /* 0 none, 1 linear, 2 rwkv, 3 rwkv_post_tokenshift */
@@ -280,6 +284,7 @@ typedef struct kvm_prefix_desc {
   int64_t rope_sb, rope_st; /* element strides of cos/sin over batch and tokens */
   int64_t qkv_st, kw_st;     /* token strides (elements) of q/k/v_lin and key_weight */
   void *q_out, *k_out, *v_out, *gate_out, *v_last_out;
+  void *q_last_out, *k_last_out; /* optional [B, 1, width]: the last token's q_lin / k_lin rows */
 } kvm_prefix_desc;
 
 /* Run the pre-boundary elementwise work described above.  Replaces the
@@ -299,19 +304,47 @@ int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out,
  * activation, F.relu(x).square() (model/rwkv7_backbone.py:174-175). */
 int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
 
+/* Residual add, LayerNorm and token shift of the decoder block
+ * (model/rwkv7_backbone.py:180-235: x + s * f(ln(x)) around the mixer and
+ * the MLP, the final LayerNorm; :163-177 with model/tokenshift.py:11-37: the
+ * MLP's token shift, fallback "zero").  Over rows of x [batch, seq_len, width]
+ * (bf16, contiguous, width a multiple of 8 and at most 4096):
+ *   r = x + alpha * y   (y NULL: r = x; round_product != 0: bf16(y * alpha)
+ *                        is rounded before the add, as torch's x + y * s)
+ *   h = LayerNorm(r) * ln_w + ln_b   (eps; fp32, rounded once to bf16)
+ *   shifted = h + mix * (h_prev - h)  (h_prev: the previous token's h; for
+ *                        token 0 the carried row prev [batch, width], or
+ *                        zeros when prev is NULL)
+ * Every output is optional (NULL): out_x = r, out_h = h, out_shift = shifted
+ * (needs mix), state_out [batch, width] = h of the last token.  state_out may
+ * be prev itself only when seq_len == 1. */
+typedef struct kvm_add_norm_desc {
+  const void *x, *y;
+  double alpha;
+  int64_t round_product;
+  const void *ln_w, *ln_b; /* bf16 [width] */
+  double eps;
+  const void *mix, *prev; /* bf16 [width], bf16 [batch, width] */
+  void *out_x, *out_h, *out_shift, *state_out;
+  int64_t batch, seq_len, width;
+} kvm_add_norm_desc;
+
+int kvm_add_norm(const kvm_add_norm_desc *d, void *stream);
+
 /* Y = X W^T for a few token rows: X bf16 [M, K] (row stride x_st), W bf16
  * [N, K] (an nn.Linear weight, row stride w_st), Y bf16 [M, N] (row stride
  * y_st), fp32 accumulation; 1 <= M <= 16, K a multiple of 32.  The linear
  * layers of the decoder's single-token decode step (model/rwkv7_backbone.py
  * MLP and attention projections, the LM head), which stream their weights
- * once per step. */
+ * once per step.  epilogue 1 writes relu(y)^2 instead of y (the MLP's
+ * activation, rounded as kvm_relu_square of the bf16 product). */
 int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st, int64_t M,
-                   int64_t N, int64_t K, void *stream);
+                   int64_t N, int64_t K, int epilogue, void *stream);
 
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
 int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc,
-                                        5 prefill_bwd_desc, 6 state_bwd_desc */
+                                        5 prefill_bwd_desc, 6 state_bwd_desc, 7 add_norm_desc */
 const char *kvm_last_error(void);
 
 /* Workspace of kvm_prefill for the given descriptor (snapshot_ring and

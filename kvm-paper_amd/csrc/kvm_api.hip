@@ -136,6 +136,7 @@ int64_t kvm_struct_size(int which) {
     case 4: return sizeof(kvm_prefix_desc);
     case 5: return sizeof(kvm_prefill_bwd_desc);
     case 6: return sizeof(kvm_state_bwd_desc);
+    case 7: return sizeof(kvm_add_norm_desc);
     default: return -1;
   }
 }
@@ -153,14 +154,33 @@ int kvm_token_shift(const void *x, const void *prev, const void *mix, void *out,
   return KVM_OK;
 }
 
+int kvm_add_norm(const kvm_add_norm_desc *d, void *stream) {
+  if (!d) return fail(KVM_EINVAL, "add_norm: NULL descriptor");
+  const kvm_add_norm_desc &P = *d;
+  if (P.batch < 1 || P.seq_len < 1 || P.width < 8 || P.width % 8 || P.width > 4096)
+    return fail(KVM_EINVAL, "add_norm needs batch, seq_len >= 1 and width a multiple of 8 in [8, 4096]");
+  if (!P.x || !P.ln_w || !P.ln_b)
+    return fail(KVM_EINVAL, "add_norm needs x and the LayerNorm parameters");
+  if (P.out_shift && !P.mix) return fail(KVM_EINVAL, "add_norm: out_shift needs mix");
+  if (P.state_out && P.state_out == P.prev && P.seq_len != 1)
+    return fail(KVM_EINVAL, "add_norm: state_out may alias prev only when seq_len == 1");
+  const void *ptrs[] = {P.x, P.y, P.ln_w, P.ln_b, P.mix, P.prev, P.out_x, P.out_h, P.out_shift, P.state_out};
+  for (const void *p : ptrs)
+    if (p && !aligned16(p)) return fail(KVM_EINVAL, "add_norm pointers must be 16-byte aligned");
+  if (!(P.eps >= 0.0)) return fail(KVM_EINVAL, "add_norm: eps must be >= 0");
+  KVM_HIP(kvm::launch_add_norm(P, as_stream(stream)), "add_norm");
+  return KVM_OK;
+}
+
 int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st, int64_t M,
-                   int64_t N, int64_t K, void *stream) {
+                   int64_t N, int64_t K, int epilogue, void *stream) {
   if (M < 1 || M > 16 || N < 1 || K < 32 || K % 32)
     return fail(KVM_EINVAL, "gemm_small needs 1 <= M <= 16, N >= 1 and K a positive multiple of 32");
   if (!x || !w || !y || !aligned16(x) || !aligned16(w) || x_st % 8 || w_st % 8 || x_st < K || w_st < K ||
       y_st < N)
     return fail(KVM_EINVAL, "gemm_small operands must be 16-byte aligned rows (strides multiples of 8)");
-  KVM_HIP(kvm::launch_gemm_small(x, x_st, w, w_st, y, y_st, M, N, K, as_stream(stream)), "gemm_small");
+  if (epilogue != 0 && epilogue != 1) return fail(KVM_EINVAL, "gemm_small: epilogue must be 0 or 1");
+  KVM_HIP(kvm::launch_gemm_small(x, x_st, w, w_st, y, y_st, M, N, K, epilogue, as_stream(stream)), "gemm_small");
   return KVM_OK;
 }
 

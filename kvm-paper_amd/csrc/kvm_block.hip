@@ -1,0 +1,189 @@
+// The decoder block's elementwise work around its mixer and MLP on gfx950:
+// residual add, LayerNorm and the MLP's token shift in one pass.
+//
+// Reference: model/rwkv7_backbone.py:180-235 (Block.forward: x + s * f(ln(x))
+// for the mixer and the MLP, the final ln after the last block) and
+// :163-177 with model/tokenshift.py:11-37 (the MLP's token shift, fallback
+// "zero", and its carried last row).  In the reference these are separate
+// torch ops (add, layer_norm, sub / mul / add, copy), each reading and
+// writing the [B, T, W] tensor; here a row is read once (plus the first row
+// of a run once more, below) and each output written once.
+//
+// One wave per token row, kRun consecutive tokens of one sequence per wave:
+// lane l holds the 16-byte chunks l, l + 64, ... of the row (8 bf16 each).
+// The token shift takes the previous token's normalised row from registers;
+// the first row of a run recomputes its predecessor's (or, at t = 0, takes
+// the carried row, or zeros).
+//
+// Rounding follows the torch ops: the residual is bf16(x + s * y) when s is a
+// power of two (one fused add) and bf16(x + bf16(y * s)) otherwise; the
+// LayerNorm computes in fp32 (two-pass mean and biased variance) and rounds
+// once; the shift rounds after each of its three ops.  Only the LayerNorm's
+// fp32 reduction order differs from torch's, which can move a normalised
+// value by one bf16 ulp.
+
+#include "kvm_device.hpp"
+#include "kvm_internal.hpp"
+
+namespace kvm {
+namespace {
+
+constexpr int kRun = 4;  // tokens per wave for seq_len > 1
+
+template <int NC>
+struct Row {
+  float v[NC][8];
+};
+
+// Residual sum of row `r` (flat token index) into `out`; chunks past the
+// row's end hold zeros.
+template <int NC>
+__device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, int64_t r, int lane, Row<NC> &out) {
+  const int nch = int(P.width / 8);
+  const float s = float(P.alpha);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      const int64_t e = r * P.width + int64_t(c) * 8;
+      float x[8];
+      load8(static_cast<const uint16_t *>(P.x) + e, x);
+      if (P.y) {
+        float y[8];
+        load8(static_cast<const uint16_t *>(P.y) + e, y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = P.round_product ? rbf(x[i] + rbf(y[i] * s)) : rbf(x[i] + s * y[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out.v[j][i] = x[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out.v[j][i] = 0.f;
+    }
+  }
+}
+
+// bf16 LayerNorm of `x` into `h` (whole-wave reductions).
+template <int NC>
+__device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, const Row<NC> &x, Row<NC> &h) {
+  const int nch = int(P.width / 8);
+  const float inv_w = 1.0f / float(P.width);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += x.v[j][i];
+  const float mean = group_sum<64>(s) * inv_w;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    if (lane + 64 * j < nch) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = x.v[j][i] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float rstd = 1.0f / sqrtf(group_sum<64>(q) * inv_w + float(P.eps));
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float w[8], b[8];
+      load8(static_cast<const uint16_t *>(P.ln_w) + c * 8, w);
+      load8(static_cast<const uint16_t *>(P.ln_b) + c * 8, b);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h.v[j][i] = rbf((x.v[j][i] - mean) * rstd * w[i] + b[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h.v[j][i] = 0.f;
+    }
+  }
+}
+
+template <int NC>
+__device__ __forceinline__ void store_row(void *dst, int64_t r, int64_t width, int lane, const Row<NC> &x) {
+  const int nch = int(width / 8);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) store8(static_cast<uint16_t *>(dst) + r * width + int64_t(c) * 8, x.v[j]);
+  }
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) {
+  const int lane = threadIdx.x & 63;
+  const int64_t T = P.seq_len;
+  const int64_t runs = (T + run - 1) / run;
+  const int64_t wv = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (wv >= P.batch * runs) return;  // wave-uniform
+  const int64_t b = wv / runs, t0 = (wv % runs) * run;
+  const int nch = int(P.width / 8);
+  const bool shift = P.mix && P.out_shift;
+  Row<NC> carry;  // normalised row of the token before the current one
+  if (shift) {
+    if (t0 > 0) {
+      Row<NC> x;
+      residual_row<NC>(P, b * T + t0 - 1, lane, x);
+      norm_row<NC>(P, lane, x, carry);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (P.prev && c < nch) {
+          load8(static_cast<const uint16_t *>(P.prev) + b * P.width + int64_t(c) * 8, carry.v[j]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) carry.v[j][i] = 0.f;
+        }
+      }
+    }
+  }
+  const int64_t t_end = t0 + run < T ? t0 + run : T;
+#pragma unroll 1
+  for (int64_t t = t0; t < t_end; ++t) {
+    const int64_t r = b * T + t;
+    Row<NC> x, h;
+    residual_row<NC>(P, r, lane, x);
+    if (P.out_x) store_row<NC>(P.out_x, r, P.width, lane, x);
+    norm_row<NC>(P, lane, x, h);
+    if (P.out_h) store_row<NC>(P.out_h, r, P.width, lane, h);
+    if (P.state_out && t == T - 1) store_row<NC>(P.state_out, b, P.width, lane, h);
+    if (shift) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nch) {
+          float m[8], o[8];
+          load8(static_cast<const uint16_t *>(P.mix) + c * 8, m);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = rbf(h.v[j][i] + rbf(m[i] * rbf(carry.v[j][i] - h.v[j][i])));
+          store8(static_cast<uint16_t *>(P.out_shift) + r * P.width + int64_t(c) * 8, o);
+        }
+      }
+      carry = h;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_add_norm(const kvm_add_norm_desc &P, hipStream_t stream) {
+  const int run = P.seq_len > 1 ? kRun : 1;
+  const int64_t waves = P.batch * ((P.seq_len + run - 1) / run);
+  const dim3 grid(unsigned((waves + 3) / 4));
+  const int64_t nch = P.width / 8;
+  if (nch <= 64)
+    hipLaunchKernelGGL(k_add_norm<1>, grid, dim3(256), 0, stream, P, run);
+  else if (nch <= 128)
+    hipLaunchKernelGGL(k_add_norm<2>, grid, dim3(256), 0, stream, P, run);
+  else if (nch <= 256)
+    hipLaunchKernelGGL(k_add_norm<4>, grid, dim3(256), 0, stream, P, run);
+  else
+    hipLaunchKernelGGL(k_add_norm<8>, grid, dim3(256), 0, stream, P, run);
+  return hipGetLastError();
+}
+
+}  // namespace kvm

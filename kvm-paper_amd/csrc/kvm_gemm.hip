@@ -1,6 +1,6 @@
 // Skinny GEMM of the decoder's decode step on gfx950: Y = X W^T for a few
 // rows of X (M <= 16 tokens) against a bf16 weight W [N, K] (nn.Linear
-// layout), fp32 accumulation, bf16 output.  The step is bound by streaming W
+// layout), fp32 accumulation, bf16 output (or relu(Y)^2, the MLP's activation).  The step is bound by streaming W
 // from HBM once (2.7 GB per config-5 decode step); a vendor GEMM tuned for
 // square shapes reads it at ~1.9 TB/s.
 //
@@ -28,7 +28,7 @@ template <int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restrict__ X, int64_t x_st,
                                                         const uint16_t *__restrict__ W, int64_t w_st,
                                                         uint16_t *__restrict__ Y, int64_t y_st, int M, int N,
-                                                        int K) {
+                                                        int K, int epilogue) {
   __shared__ float red[NW][16][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
@@ -62,6 +62,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
       float s = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) s += red[w][n][m];
+      if (epilogue == 1) {  // relu(y)^2 of the bf16 product, rounded once more
+        const float r = fmaxf(rbf(s), 0.f);
+        s = r * r;
+      }
       Y[int64_t(m) * y_st + n0 + n] = uint16_t(f2bf(s));
     }
   }
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
 }  // namespace
 
 hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
-                             int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                             int64_t M, int64_t N, int64_t K, int epilogue, hipStream_t stream) {
   // Waves per workgroup: up to K / 256 (a power of two <= 16 dividing K / 32).
   int nw = 1;
   while (nw < 16 && K / (2 * nw) >= 256 && K % (32 * 2 * nw) == 0) nw *= 2;
@@ -79,7 +83,7 @@ hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t
   uint16_t *yp = static_cast<uint16_t *>(y);
 #define KVM_GEMM(NWV)                                                                                      \
   hipLaunchKernelGGL(k_gemm_small<NWV>, grid, dim3(NWV * 64), 0, stream, xp, x_st, wp, w_st, yp, y_st, int(M), \
-                     int(N), int(K))
+                     int(N), int(K), epilogue)
   switch (nw) {
     case 1: KVM_GEMM(1); break;
     case 2: KVM_GEMM(2); break;

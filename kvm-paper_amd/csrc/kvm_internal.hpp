@@ -230,9 +230,11 @@ int64_t state_bwd_max_chunk();
 hipError_t launch_state_backward(const StateBwdArgs &a, const UpdTable &sched, float *part,
                                  hipStream_t stream);
 
-// Y[M, N] = X[M, K] W[N, K]^T, bf16, M <= 16 (kvm_gemm.hip).
+// Y[M, N] = X[M, K] W[N, K]^T, bf16, M <= 16, epilogue 1 = relu^2 (kvm_gemm.hip).
 hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
-                             int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                             int64_t M, int64_t N, int64_t K, int epilogue, hipStream_t stream);
+// Residual add + LayerNorm + token shift of the decoder block (kvm_block.hip).
+hipError_t launch_add_norm(const kvm_add_norm_desc &P, hipStream_t stream);
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);
 hipError_t launch_token_shift(const void *x, const void *prev, const void *mix, void *out, int64_t B,
                               int64_t T, int64_t width, int zero_fallback, hipStream_t stream);

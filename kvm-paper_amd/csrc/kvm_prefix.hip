@@ -167,6 +167,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       const int64_t e = r * width + chan;
       float x[8];
       load_row8(P.q_lin, r * P.qkv_st + chan, x);
+      if (live && P.q_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.q_last_out) + bi * width + chan, x);
       if (shift) {
         float pv[8];
         if (ps == 0 && t0 == 0 && !P.q_prev)  // fallback "first": token 0 is its own predecessor
@@ -207,6 +208,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     // keys: token shift, ln_k, RoPE
     float x[8];
     load_row8(P.k_lin, ein, x);
+    if (live && P.k_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.k_last_out) + bi * width + chan, x);
     if (shift) {
       float pv[8];
       if (ps == 0 && t0 == 0 && !P.k_prev)

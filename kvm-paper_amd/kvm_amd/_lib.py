@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -133,6 +133,17 @@ class KvmPrefixDesc(ctypes.Structure):
         ("ln_q_w", _vp), ("ln_q_b", _vp), ("ln_k_w", _vp), ("ln_k_b", _vp),
         ("cos", _vp), ("sin", _vp), ("rope_sb", _i64), ("rope_st", _i64), ("qkv_st", _i64), ("kw_st", _i64),
         ("q_out", _vp), ("k_out", _vp), ("v_out", _vp), ("gate_out", _vp), ("v_last_out", _vp),
+        ("q_last_out", _vp), ("k_last_out", _vp),
+    ]
+
+
+class KvmAddNormDesc(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("y", _vp), ("alpha", ctypes.c_double), ("round_product", _i64),
+        ("ln_w", _vp), ("ln_b", _vp), ("eps", ctypes.c_double),
+        ("mix", _vp), ("prev", _vp),
+        ("out_x", _vp), ("out_h", _vp), ("out_shift", _vp), ("state_out", _vp),
+        ("batch", _i64), ("seq_len", _i64), ("width", _i64),
     ]
 
 
@@ -155,7 +166,8 @@ SIGNATURES = {
     "kvm_decode_advance": (ctypes.c_int, [_vp, _i64, _vp]),
     "kvm_token_shift": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
-    "kvm_gemm_small": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kvm_gemm_small": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
+    "kvm_add_norm": (ctypes.c_int, [_P(KvmAddNormDesc), _vp]),
     "kvm_state_append_direct": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _i64, _i64, _P(KvmState), _i64, _vp]),
     "kvm_state_refresh": (ctypes.c_int, [_P(KvmLayer), _P(KvmState), _i64, _i64, _vp]),
     "kvm_update_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),
@@ -197,7 +209,7 @@ def load(path: str | os.PathLike | None = None):
     if lib.kvm_abi_version() != ABI_VERSION:
         raise KvmLibraryError(f"{p}: ABI version {lib.kvm_abi_version()} != {ABI_VERSION}")
     for i, st in enumerate((KvmLayer, KvmSeq, KvmState, KvmPrefillDesc, KvmPrefixDesc, KvmPrefillBwdDesc,
-                              KvmStateBwdDesc)):
+                              KvmStateBwdDesc, KvmAddNormDesc)):
         if lib.kvm_struct_size(i) != ctypes.sizeof(st):
             raise KvmLibraryError(f"{p}: struct {st.__name__} size mismatch")
     if path is None:

@@ -30,6 +30,7 @@ as given.
 
 from __future__ import annotations
 
+import ctypes
 import importlib
 import math
 from dataclasses import dataclass
@@ -176,42 +177,59 @@ class MLP(nn.Module):
 
     def forward(self, x, past_key_values=None, **kwargs):
         if self.config.use_tokenshift_ffn:
-            prev = None
-            if past_key_values is not None:
-                layer_len = past_key_values.get_seq_length(self.layer_idx)
-                cur = int(x.size(1))
-                if layer_len < cur:
-                    raise AssertionError("MLP cache invariant violated: the layer cache must already include "
-                                         "the current attention pass before the MLP runs.")
-                prev = past_key_values.get_states(self.layer_idx).get(self._CACHE_FINAL)
-                prior = layer_len - cur
-                if prior > 0 and prev is None:
-                    raise AssertionError("cached MLP decode requires 'mlp_final_token' from a prior MLP pass.")
-                if prior == 0 and prev is not None:
-                    raise AssertionError("MLP cache invariant violated: found 'mlp_final_token' although no "
-                                         "prior MLP tokens exist for this layer.")
-                if prev is not None and prev.shape != (x.shape[0], 1, x.shape[2]):
-                    raise AssertionError(f"cached MLP decode requires 'mlp_final_token' of shape "
-                                         f"{(x.shape[0], 1, x.shape[2])}, got {tuple(prev.shape)}.")
+            prev = self.carried_row(x, past_key_values)
             if self._use_kernels(x):
                 xk = _kernel_token_shift(x, prev, self.x_k)
             else:
                 xk = x + self.x_k * token_shift_delta(x, prev, fallback="zero")
             if past_key_values is not None:
-                # a copy, not a view: a view would keep the whole [B, T, d] input alive
-                # (written in place, after its last read, when the cache keeps fixed
-                # addresses for a captured decode step)
-                if (getattr(past_key_values, "static_states", False) and prev is not None
-                        and prev.shape == (x.shape[0], 1, x.shape[2]) and prev.dtype == x.dtype):
-                    prev.copy_(x[:, -1:])
-                else:
-                    past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: x[:, -1:].clone()})
+                self.store_carried_row(x[:, -1:], prev, past_key_values)
         else:
             xk = x
-        h = module_linear(self.c_fc, xk)
-        if self._use_kernels(h):
-            return module_linear(self.c_proj, _kernel_relu_square(h))
-        return module_linear(self.c_proj, F.relu(h).square())
+        return self.ffn(xk)
+
+    def carried_row(self, x, past_key_values):
+        """The previous step's last input row [B, 1, d] from the cache (None
+        on an empty cache), with the cache invariants the reference asserts."""
+        if past_key_values is None:
+            return None
+        layer_len = past_key_values.get_seq_length(self.layer_idx)
+        cur = int(x.size(1))
+        if layer_len < cur:
+            raise AssertionError("MLP cache invariant violated: the layer cache must already include "
+                                 "the current attention pass before the MLP runs.")
+        prev = past_key_values.get_states(self.layer_idx).get(self._CACHE_FINAL)
+        prior = layer_len - cur
+        if prior > 0 and prev is None:
+            raise AssertionError("cached MLP decode requires 'mlp_final_token' from a prior MLP pass.")
+        if prior == 0 and prev is not None:
+            raise AssertionError("MLP cache invariant violated: found 'mlp_final_token' although no "
+                                 "prior MLP tokens exist for this layer.")
+        if prev is not None and prev.shape != (x.shape[0], 1, x.shape[2]):
+            raise AssertionError(f"cached MLP decode requires 'mlp_final_token' of shape "
+                                 f"{(x.shape[0], 1, x.shape[2])}, got {tuple(prev.shape)}.")
+        return prev
+
+    def store_carried_row(self, last, prev, past_key_values):
+        """Carry ``last`` [B, 1, d] to the next step: a copy, not a view (a
+        view would keep the whole [B, T, d] input alive), written in place,
+        after its last read, when the cache keeps fixed addresses for a
+        captured decode step."""
+        if self.in_place_carry(prev, last, past_key_values):
+            prev.copy_(last)
+        else:
+            past_key_values.update(self.layer_idx, offset=0, states_dict={self._CACHE_FINAL: last.clone()})
+
+    @staticmethod
+    def in_place_carry(prev, last, past_key_values) -> bool:
+        return (getattr(past_key_values, "static_states", False) and prev is not None
+                and prev.shape == last.shape and prev.dtype == last.dtype)
+
+    def ffn(self, xk):
+        """c_proj(relu(c_fc(xk))^2)."""
+        if self._use_kernels(xk):
+            return module_linear(self.c_proj, linear(xk, self.c_fc.weight, relu_square=True))
+        return module_linear(self.c_proj, F.relu(module_linear(self.c_fc, xk)).square())
 
     def _use_kernels(self, t: torch.Tensor) -> bool:
         """bf16 inference on the GPU takes the HIP elementwise kernels (same
@@ -237,17 +255,6 @@ def _kernel_token_shift(x: torch.Tensor, prev: torch.Tensor | None, mix: torch.T
     _lib.check(_lib.load().kvm_token_shift(x.data_ptr(), prev.data_ptr() if prev is not None else None,
                                            mix.data_ptr(), out.data_ptr(), B, T, d, 1,
                                            _lib.stream_handle(x.device)), "kvm_token_shift")
-    return out
-
-
-def _kernel_relu_square(h: torch.Tensor) -> torch.Tensor:
-    """relu(h)^2 in one HIP launch (kvm_relu_square)."""
-    from . import _lib
-
-    h = h.contiguous()
-    out = torch.empty_like(h)
-    _lib.check(_lib.load().kvm_relu_square(h.data_ptr(), out.data_ptr(), h.numel(), _lib.stream_handle(h.device)),
-               "kvm_relu_square")
     return out
 
 
@@ -380,6 +387,8 @@ class RWKV7BackboneModel(nn.Module):
         """model/rwkv7_backbone.py:585-685 (no alternating layers)."""
         x0 = x
         position_embeddings = self.rotary(position_ids)
+        if self._fused_blocks_ok(x):
+            return self._forward_fused(input_ids, x0, position_embeddings, kwargs)
         first = self.h[0]
         first_kwargs_fn = getattr(first.attn, "get_first_layer_kwargs", lambda x0, x, **kw: {})
         first_kwargs = first_kwargs_fn(x0=x0, x=first.ln_attn(x0), input_ids=input_ids, **kwargs)
@@ -394,6 +403,105 @@ class RWKV7BackboneModel(nn.Module):
             # An odd layer count pops an empty list, as the reference does.
             x = self.h[self.encoder_layers + i](x + self.skip_weights[i] * skips.pop(), **layer_kwargs)
         return self.ln_head(x)
+
+
+    def _fused_blocks_ok(self, x) -> bool:
+        """bf16 GPU inference of blocks without lambdas or U-net skips runs
+        each residual add with the LayerNorm after it (and the MLP's token
+        shift) in one kvm_add_norm launch."""
+        c = self.config
+        if (not x.is_cuda or x.dtype != torch.bfloat16 or c.use_block_lambdas or c.use_skip_connections
+                or x.size(-1) % 8 or x.size(-1) > 4096):
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        lns = [self.ln_head] + [ln for b in self.h for ln in (b.ln_attn, b.ln_mlp)]
+        if any(ln.weight is None or ln.bias is None or ln.weight.dtype != torch.bfloat16
+               or ln.bias.dtype != torch.bfloat16 for ln in lns):
+            return False
+        return not (c.use_tokenshift_ffn and any(b.mlp.x_k.dtype != torch.bfloat16 for b in self.h))
+
+    def _forward_fused(self, input_ids, x0, position_embeddings, kwargs):
+        """The block loop of _forward_model with each residual add fused to
+        the LayerNorm that reads its result (the next block's ln_attn, or
+        ln_head after the last block) and the MLP's token shift fused to
+        ln_mlp: x + s * f(h) and LN(x + s * f(h)) from one read of each."""
+        blocks = self.h
+        first = blocks[0]
+        _, h = _add_norm(x0, None, 1.0, first.ln_attn)
+        first_kwargs_fn = getattr(first.attn, "get_first_layer_kwargs", lambda x0, x, **kw: {})
+        first_kwargs = first_kwargs_fn(x0=x0, x=h, input_ids=input_ids, **kwargs)
+        layer_kwargs = dict(x0=x0, **first_kwargs, **kwargs)
+        layer_kwargs["position_embeddings"] = position_embeddings
+        pkv = layer_kwargs.get("past_key_values")
+        x = x0
+        for i, blk in enumerate(blocks):
+            attn_fn = (getattr(blk.attn, "forward_inference", blk.attn.forward)
+                       if not blk.training and pkv is not None else blk.attn.forward)
+            a = attn_fn(h, **layer_kwargs)
+            mlp = blk.mlp
+            if self.config.use_tokenshift_ffn:
+                prev = mlp.carried_row(a, pkv)
+                state = None
+                if pkv is not None:
+                    last_shape = (a.shape[0], 1, a.shape[2])
+                    in_place = a.size(1) == 1 and mlp.in_place_carry(prev, a[:, -1:], pkv) and prev.is_contiguous()
+                    state = prev if in_place else torch.empty(last_shape, device=a.device, dtype=a.dtype)
+                x, xk = _add_norm(x, a, blk.residual_scale, blk.ln_mlp, mix=mlp.x_k, prev=prev, state_out=state)
+                if pkv is not None and state is not prev:
+                    pkv.update(mlp.layer_idx, offset=0, states_dict={mlp._CACHE_FINAL: state})
+            else:
+                x, xk = _add_norm(x, a, blk.residual_scale, blk.ln_mlp)
+            m = mlp.ffn(xk)
+            last = i + 1 == len(blocks)
+            x, h = _add_norm(x, m, blk.residual_scale, self.ln_head if last else blocks[i + 1].ln_attn,
+                             want_x=not last)
+        return h
+
+
+def _add_norm(x, y, scale, ln, *, mix=None, prev=None, state_out=None, want_x=True):
+    """(x + scale * y, LN(x + scale * y)) in one kvm_add_norm launch; with
+    ``mix`` the second output is the token-shifted LN (fallback "zero", the
+    carried row ``prev`` before token 0) and ``state_out`` [B, 1, d] receives
+    the last token's LN row.  ``y`` None: (x, LN(x)).  The residual rounds as
+    Block._residual does."""
+    B, T, d = x.shape
+    x = x.contiguous()
+    desc = _lib.KvmAddNormDesc()
+    desc.x, desc.batch, desc.seq_len, desc.width = x.data_ptr(), B, T, d
+    out_x = x
+    keep = [x]
+    if y is not None:
+        y = y.contiguous()
+        keep.append(y)
+        sc = float(scale)
+        desc.y, desc.alpha = y.data_ptr(), sc
+        desc.round_product = 0 if sc > 0 and math.frexp(sc)[0] == 0.5 else 1
+        if want_x:
+            out_x = torch.empty_like(x)
+            desc.out_x = out_x.data_ptr()
+        else:
+            out_x = None
+    desc.ln_w, desc.ln_b, desc.eps = ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps)
+    out = torch.empty_like(x)
+    if mix is not None:
+        mix = mix.reshape(d).contiguous()
+        keep.append(mix)
+        desc.mix, desc.out_shift = mix.data_ptr(), out.data_ptr()
+        if prev is not None:
+            prev_c = prev.reshape(B, d)
+            if prev_c.data_ptr() != prev.data_ptr() or not prev.is_contiguous():
+                raise ValueError("add_norm: the carried row must be a contiguous [B, 1, d] tensor")
+            desc.prev = prev.data_ptr()
+    else:
+        desc.out_h = out.data_ptr()
+    if state_out is not None:
+        if not state_out.is_contiguous() or state_out.numel() != B * d:
+            raise ValueError("add_norm: state_out must be a contiguous [B, 1, d] tensor")
+        desc.state_out = state_out.data_ptr()
+    _lib.check(_lib.load().kvm_add_norm(ctypes.byref(desc), _lib.stream_handle(x.device)), "kvm_add_norm")
+    del keep
+    return out_x, out
 
 
 class RWKV7BackboneForCausalLM(nn.Module):

@@ -14,7 +14,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / "csrc"
 OUT = PKG / "libkvm_amd.so"
 SOURCES = ["kvm_api.hip", "kvm_update.hip", "kvm_chain.hip", "kvm_decode.hip", "kvm_attn.hip", "kvm_attn_bwd.hip",
-           "kvm_state_bwd.hip", "kvm_prefix.hip", "kvm_gemm.hip"]
+           "kvm_state_bwd.hip", "kvm_prefix.hip", "kvm_gemm.hip", "kvm_block.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -14,16 +14,21 @@ import torch.nn.functional as F
 from . import _lib
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+           relu_square: bool = False) -> torch.Tensor:
     """``F.linear(x, weight, bias)``; bf16 inference on at most 16 rows runs
-    ``kvm_gemm_small`` (fp32 accumulation, one bf16 rounding)."""
+    ``kvm_gemm_small`` (fp32 accumulation, one bf16 rounding).  With
+    ``relu_square`` the result is relu(y)^2 (the decoder MLP's activation),
+    computed in the GEMM's epilogue or by ``kvm_relu_square``; that flag is
+    for bf16 GPU inference only."""
     K = int(weight.shape[-1])
-    if (bias is not None or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
-            or K % 32 or x.shape[-1] != K or (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad))):
-        return F.linear(x, weight, bias)
-    M = x.numel() // K
-    if M < 1 or M > 16:
-        return F.linear(x, weight, bias)
+    small = not (bias is not None or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
+                 or K % 32 or x.shape[-1] != K
+                 or (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad)))
+    M = x.numel() // K if small else 0
+    if not small or M < 1 or M > 16:
+        y = F.linear(x, weight, bias)
+        return _relu_square(y) if relu_square else y
     x2 = x.reshape(M, K)
     # The stride of a single row is meaningless to torch (it may be anything);
     # the kernel only needs K for it.
@@ -41,8 +46,20 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         w_st = K
     y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
     _lib.check(_lib.load().kvm_gemm_small(x2.data_ptr(), x_st, w.data_ptr(), w_st, y.data_ptr(), N,
-                                          M, N, K, _lib.stream_handle(x.device)), "kvm_gemm_small")
+                                          M, N, K, int(relu_square), _lib.stream_handle(x.device)),
+               "kvm_gemm_small")
     return y.view(*x.shape[:-1], N)
+
+
+def _relu_square(h: torch.Tensor) -> torch.Tensor:
+    """relu(h)^2 in one HIP launch (kvm_relu_square): bf16 GPU tensors only."""
+    if not h.is_cuda or h.dtype != torch.bfloat16 or h.numel() % 8:
+        raise ValueError("relu_square runs on bf16 GPU tensors with a multiple of 8 elements")
+    h = h.contiguous()
+    out = torch.empty_like(h)
+    _lib.check(_lib.load().kvm_relu_square(h.data_ptr(), out.data_ptr(), h.numel(), _lib.stream_handle(h.device)),
+               "kvm_relu_square")
+    return out
 
 
 def module_linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:

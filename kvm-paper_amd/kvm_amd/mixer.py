@@ -406,7 +406,20 @@ class SequenceMixer(nn.Module):
         k = torch.empty(B, T, Hkv, D, **bf)
         v = torch.empty(B, T, Hkv, D, **bf)
         gate = torch.empty(B, T, Hkv, **bf) if use_gate else None
-        v_last = torch.empty(B, 1, Hkv * D, **bf) if past_key_values is not None else None
+        # The carried last rows (q_lin, k_lin, v after a pre-shift value
+        # residual) come from the kernel: into the previous step's tensors
+        # when the cache keeps fixed addresses (a single token reads them
+        # before it writes them), else into new ones.
+        last = [None, None, None]
+        if past_key_values is not None:
+            in_place = getattr(past_key_values, "static_states", False) and T == 1
+            for i, width in enumerate((Hq * D, Hkv * D, Hkv * D)):
+                p = prev[i]
+                if (in_place and p is not None and p.shape == (B, 1, width) and p.dtype == torch.bfloat16
+                        and p.is_contiguous()):
+                    last[i] = p
+                else:
+                    last[i] = torch.empty(B, 1, width, **bf)
         cos, sin = position_embeddings
         if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
             cos, sin = cos.bfloat16(), sin.bfloat16()
@@ -452,14 +465,16 @@ class SequenceMixer(nn.Module):
         d.rope_sb, d.rope_st = rope_sb, cos.stride(1)
         d.q_out, d.k_out, d.v_out = q.data_ptr(), k.data_ptr(), v.data_ptr()
         d.gate_out = gate.data_ptr() if gate is not None else None
-        d.v_last_out = v_last.data_ptr() if v_last is not None else None
+        d.q_last_out, d.k_last_out, d.v_last_out = (t.data_ptr() if t is not None else None for t in last)
         lib = _lib.load()
         _lib.check(lib.kvm_prefix(ctypes.byref(d), _lib.stream_handle(x.device)), "kvm_prefix")
         del keep
         if past_key_values is not None:
-            new_states = {self._CACHE_Q_FINAL: q_lin[:, -1:], self._CACHE_K_FINAL: k_lin[:, -1:],
-                          self._CACHE_V_FINAL: v_last, self._CACHE_X_FINAL: x[:, -1:].detach()}
-            _store_states(past_key_values, self.layer_idx, states, new_states)
+            fresh = {key: t for key, t, p in zip((self._CACHE_Q_FINAL, self._CACHE_K_FINAL, self._CACHE_V_FINAL),
+                                                 last, prev) if t is not p}
+            if fresh:
+                past_key_values.update(self.layer_idx, offset=0, states_dict=fresh)
+            _store_states(past_key_values, self.layer_idx, states, {self._CACHE_X_FINAL: x[:, -1:].detach()})
         if use_gate:
             merge_gate = gate.view(B, T, Hkv, 1).transpose(1, 2)
         else:

@@ -34,3 +34,23 @@ def test_gemm_small_matches_fp32(M, N, K):
     excess = float(((got - ref).abs() / bound).max())
     T.log(f"[gemm] max |err| / (1 ulp + fp32 sum bound) = {excess:.3f}")
     assert excess <= 1.0, f"error {excess:.2f} x the bound"
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 8192, 2048), (3, 100, 384)])
+def test_gemm_small_relu_square_epilogue(M, N, K):
+    """epilogue 1 writes relu(y)^2 of the same bf16 product: bit-identical to
+    the plain product followed by torch's relu().square() (which
+    kvm_relu_square matches bit for bit)."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd.linear import linear
+
+    T.log(f"[gemm] relu^2 epilogue M{M} N{N} K{K}")
+    gen = torch.Generator(device=DEV).manual_seed(N + K)
+    x = torch.randn(M, K, device=DEV, generator=gen).bfloat16()
+    w = (torch.randn(N, K, device=DEV, generator=gen) / K ** 0.5).bfloat16()
+    with torch.no_grad():
+        fused = linear(x, w, relu_square=True)
+        plain = torch.nn.functional.relu(linear(x, w)).square()
+    assert torch.equal(fused, plain)
+    assert bool((fused == 0).any()) and bool((fused > 0).any())

@@ -129,7 +129,8 @@ def test_mlp_kernels_match_torch_ops(lib, with_prev):
     """The decoder MLP's token shift (fallback "zero", or a carried previous
     token) and relu^2 kernels against the torch ops on the same GPU: bit-exact
     (elementwise, same bf16 rounding points)."""
-    from kvm_amd.backbone import _kernel_relu_square, _kernel_token_shift, token_shift_delta
+    from kvm_amd.backbone import _kernel_token_shift, token_shift_delta
+    from kvm_amd.linear import _relu_square
 
     gen = torch.Generator(device=DEV).manual_seed(8)
     B, Tn, d = 3, 77, 256
@@ -141,4 +142,4 @@ def test_mlp_kernels_match_torch_ops(lib, with_prev):
         ref = x + mix * token_shift_delta(x, prev, fallback="zero")
         assert torch.equal(got, ref), float((got.float() - ref.float()).abs().max())
         h = torch.randn(B, Tn, 4 * d, device=DEV, generator=gen).bfloat16()
-        assert torch.equal(_kernel_relu_square(h), torch.nn.functional.relu(h).square())
+        assert torch.equal(_relu_square(h), torch.nn.functional.relu(h).square())

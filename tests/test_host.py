@@ -49,7 +49,7 @@ def test_struct_layout_matches_binding():
 
     assert lib.kvm_abi_version() == L.ABI_VERSION
     for i, st in enumerate((L.KvmLayer, L.KvmSeq, L.KvmState, L.KvmPrefillDesc, L.KvmPrefixDesc, L.KvmPrefillBwdDesc,
-                              L.KvmStateBwdDesc)):
+                              L.KvmStateBwdDesc, L.KvmAddNormDesc)):
         assert lib.kvm_struct_size(i) == ctypes.sizeof(st)
     assert lib.kvm_struct_size(9) == -1
 
