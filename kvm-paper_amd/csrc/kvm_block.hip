@@ -28,44 +28,75 @@
 namespace kvm {
 namespace {
 
-constexpr int kRun = 4;  // tokens per wave for seq_len > 1
+constexpr int kRun = 8;  // tokens per wave for seq_len > 1
 
 template <int NC>
 struct Row {
   float v[NC][8];
 };
 
-// Residual sum of row `r` (flat token index) into `out`; chunks past the
-// row's end hold zeros.
+// The per-channel parameters of a lane's chunks (packed bf16), loaded once
+// per wave before the first row so that their latency overlaps the rows'.
 template <int NC>
-__device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, int64_t r, int lane, Row<NC> &out) {
+struct Params {
+  uint4 w[NC], b[NC], mix[NC];
+};
+
+template <int NC>
+__device__ __forceinline__ void load_params(const kvm_add_norm_desc &P, int lane, bool shift, Params<NC> &p) {
   const int nch = int(P.width / 8);
-  const float s = float(P.alpha);
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = lane + 64 * j;
-    if (c < nch) {
-      const int64_t e = r * P.width + int64_t(c) * 8;
-      float x[8];
-      load8(static_cast<const uint16_t *>(P.x) + e, x);
-      if (P.y) {
-        float y[8];
-        load8(static_cast<const uint16_t *>(P.y) + e, y);
+    const bool in = c < nch;
+    p.w[j] = in ? reinterpret_cast<const uint4 *>(P.ln_w)[c] : make_uint4(0, 0, 0, 0);
+    p.b[j] = in ? reinterpret_cast<const uint4 *>(P.ln_b)[c] : make_uint4(0, 0, 0, 0);
+    p.mix[j] = in && shift ? reinterpret_cast<const uint4 *>(P.mix)[c] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// The raw 16-byte chunks of row `r` (flat token index) of x and y; chunks
+// past the row's end read as zeros.
+template <int NC>
+struct Raw {
+  uint4 x[NC], y[NC];
+};
+
+template <int NC>
+__device__ __forceinline__ void fetch_row(const kvm_add_norm_desc &P, int64_t r, int lane, Raw<NC> &raw) {
+  const int nch = int(P.width / 8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = P.round_product ? rbf(x[i] + rbf(y[i] * s)) : rbf(x[i] + s * y[i]);
-      }
+  for (int j = 0; j < NC; ++j) {
+    const int c = lane + 64 * j;
+    const int64_t e = r * (P.width / 8) + c;
+    raw.x[j] = c < nch ? reinterpret_cast<const uint4 *>(P.x)[e] : make_uint4(0, 0, 0, 0);
+    raw.y[j] = c < nch && P.y ? reinterpret_cast<const uint4 *>(P.y)[e] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Residual sum x + s * y of a fetched row (zeros past the row's end).
+template <int NC>
+__device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, const Raw<NC> &raw, Row<NC> &out) {
+  const float s = float(P.alpha);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) out.v[j][i] = x[i];
-    } else {
+  for (int j = 0; j < NC; ++j) {
+    float x[8];
+    unpack8(raw.x[j], x);
+    if (P.y) {
+      float y[8];
+      unpack8(raw.y[j], y);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) out.v[j][i] = 0.f;
+      for (int i = 0; i < 8; ++i) x[i] = P.round_product ? rbf(x[i] + rbf(y[i] * s)) : rbf(x[i] + s * y[i]);
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out.v[j][i] = x[i];
   }
 }
 
 // bf16 LayerNorm of `x` into `h` (whole-wave reductions).
 template <int NC>
-__device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, const Row<NC> &x, Row<NC> &h) {
+__device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, const Params<NC> &p,
+                                         const Row<NC> &x, Row<NC> &h) {
   const int nch = int(P.width / 8);
   const float inv_w = 1.0f / float(P.width);
   float s = 0.f;
@@ -91,8 +122,8 @@ __device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, c
     const int c = lane + 64 * j;
     if (c < nch) {
       float w[8], b[8];
-      load8(static_cast<const uint16_t *>(P.ln_w) + c * 8, w);
-      load8(static_cast<const uint16_t *>(P.ln_b) + c * 8, b);
+      unpack8(p.w[j], w);
+      unpack8(p.b[j], b);
 #pragma unroll
       for (int i = 0; i < 8; ++i) h.v[j][i] = rbf((x.v[j][i] - mean) * rstd * w[i] + b[i]);
     } else {
@@ -122,12 +153,16 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
   const int64_t b = wv / runs, t0 = (wv % runs) * run;
   const int nch = int(P.width / 8);
   const bool shift = P.mix && P.out_shift;
+  Params<NC> prm;
+  load_params<NC>(P, lane, shift, prm);
   Row<NC> carry;  // normalised row of the token before the current one
   if (shift) {
     if (t0 > 0) {
+      Raw<NC> raw;
+      fetch_row<NC>(P, b * T + t0 - 1, lane, raw);
       Row<NC> x;
-      residual_row<NC>(P, b * T + t0 - 1, lane, x);
-      norm_row<NC>(P, lane, x, carry);
+      residual_row<NC>(P, raw, x);
+      norm_row<NC>(P, lane, prm, x, carry);
     } else {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
@@ -142,13 +177,17 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
     }
   }
   const int64_t t_end = t0 + run < T ? t0 + run : T;
+  Raw<NC> next;  // the next row's loads are in flight while a row is processed
+  fetch_row<NC>(P, b * T + t0, lane, next);
 #pragma unroll 1
   for (int64_t t = t0; t < t_end; ++t) {
     const int64_t r = b * T + t;
+    const Raw<NC> cur = next;
+    if (t + 1 < t_end) fetch_row<NC>(P, r + 1, lane, next);
     Row<NC> x, h;
-    residual_row<NC>(P, r, lane, x);
+    residual_row<NC>(P, cur, x);
     if (P.out_x) store_row<NC>(P.out_x, r, P.width, lane, x);
-    norm_row<NC>(P, lane, x, h);
+    norm_row<NC>(P, lane, prm, x, h);
     if (P.out_h) store_row<NC>(P.out_h, r, P.width, lane, h);
     if (P.state_out && t == T - 1) store_row<NC>(P.state_out, b, P.width, lane, h);
     if (shift) {
@@ -157,7 +196,7 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
         const int c = lane + 64 * j;
         if (c < nch) {
           float m[8], o[8];
-          load8(static_cast<const uint16_t *>(P.mix) + c * 8, m);
+          unpack8(prm.mix[j], m);
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = rbf(h.v[j][i] + rbf(m[i] * rbf(carry.v[j][i] - h.v[j][i])));
           store8(static_cast<uint16_t *>(P.out_shift) + r * P.width + int64_t(c) * 8, o);
