@@ -93,6 +93,19 @@ __device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, const R
   }
 }
 
+// Sum over the wave, the same value in every lane: DPP sums within each row
+// of 16 lanes, then the four row sums read from lanes 0, 16, 32, 48 and
+// added in a fixed order (no LDS round trips).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum<16>(v);
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // bf16 LayerNorm of `x` into `h` (whole-wave reductions).
 template <int NC>
 __device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, const Params<NC> &p,
@@ -104,7 +117,7 @@ __device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, c
   for (int j = 0; j < NC; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) s += x.v[j][i];
-  const float mean = group_sum<64>(s) * inv_w;
+  const float mean = wave_sum(s) * inv_w;
   float q = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
@@ -116,7 +129,7 @@ __device__ __forceinline__ void norm_row(const kvm_add_norm_desc &P, int lane, c
       }
     }
   }
-  const float rstd = 1.0f / sqrtf(group_sum<64>(q) * inv_w + float(P.eps));
+  const float rstd = 1.0f / sqrtf(wave_sum(q) * inv_w + float(P.eps));
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = lane + 64 * j;

@@ -38,7 +38,7 @@ __device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
 }
 
 template <int D, int GQ>
-__global__ __launch_bounds__(256) void k_decode_partial(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3 : 2))) void k_decode_partial(
     kvm_layer L, const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
     const uint16_t *__restrict__ sk, const uint16_t *__restrict__ sv,
     int64_t cap, int active, const uint16_t *__restrict__ rk,

@@ -39,27 +39,33 @@ __device__ __forceinline__ float param1(const void *p, int64_t elem) {
   return bf2f(static_cast<const uint16_t *>(p)[elem]);
 }
 
-// value residual applied to one row (v in place); row_elem indexes the
-// contiguous v_first / gate_lin rows
-__device__ __forceinline__ void value_residual(int mode, float (&v)[8], const kvm_prefix_desc &P,
-                                               int64_t row_elem, int64_t chan) {
+// The rows a value residual reads besides v: v_first and (modes 2 and 3)
+// gate_lin, both contiguous [B, T, width]; row_elem is the row's first
+// element of this lane's 8.
+struct VRes {
+  float vf[8], gl[8];
+};
+
+__device__ __forceinline__ void load_vres(int mode, const kvm_prefix_desc &P, int64_t row_elem, VRes &r) {
+  if (mode == 0) return;
+  load_row8(P.v_first, row_elem, r.vf);
+  if (mode >= 2) load_row8(P.gate_lin, row_elem, r.gl);
+}
+
+// value residual applied to one row (v in place).  g0: v_gate0 of the lane's
+// channels (modes 2, 3); lamb: the mixing weight (mode 1).
+__device__ __forceinline__ void value_residual(int mode, float (&v)[8], const VRes &r, const float (&g0)[8],
+                                               float lamb) {
   if (mode == 1) {  // (1 - lamb) * v + lamb * v_first
-    const float lamb = param1(P.lamb, 0);
     const float c1 = rbf(1.f - lamb);
-    float vf[8];
-    load_row8(P.v_first, row_elem, vf);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = rbf(rbf(c1 * v[i]) + rbf(lamb * vf[i]));
+    for (int i = 0; i < 8; ++i) v[i] = rbf(rbf(c1 * v[i]) + rbf(lamb * r.vf[i]));
   } else {  // v + (v_first - v) * sigmoid(v_gate0 + gate_lin)
-    float vf[8], gl[8], g0[8];
-    load_row8(P.v_first, row_elem, vf);
-    load_row8(P.gate_lin, row_elem, gl);
-    param8(P.v_gate0, chan, g0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float t = rbf(g0[i] + gl[i]);
+      const float t = rbf(g0[i] + r.gl[i]);
       const float g = rbf(1.f / (1.f + expf(-t)));
-      v[i] = rbf(v[i] + rbf(rbf(vf[i] - v[i]) * g));
+      v[i] = rbf(v[i] + rbf(rbf(r.vf[i] - v[i]) * g));
     }
   }
 }
@@ -70,14 +76,12 @@ __device__ __forceinline__ void token_shift(float (&x)[8], const float (&prev)[8
   for (int i = 0; i < 8; ++i) x[i] = rbf(x[i] + rbf(mix[i] * rbf(prev[i] - x[i])));
 }
 
-// LayerNorm over the row (bf16 output), then interleaved-pair RoPE:
+// LayerNorm over the row (bf16 output; w, b: the lane's 8 parameters),
+// then interleaved-pair RoPE with the row's cos / sin:
 // bf16(bf16(cos * x) + bf16(sin * x_pair)).
 template <int D>
-__device__ __forceinline__ void norm_rope(float (&x)[8], int part, const void *w, const void *b, float eps,
-                                          const kvm_prefix_desc &P, int64_t bi, int64_t t) {
-  float wf[8], bfv[8], c[8], s[8];
-  param8(w, part * 8, wf);
-  param8(b, part * 8, bfv);
+__device__ __forceinline__ void norm_rope(float (&x)[8], const float (&wf)[8], const float (&bfv)[8], float eps,
+                                          const float (&c)[8], const float (&s)[8]) {
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) sum += x[i];
@@ -93,9 +97,6 @@ __device__ __forceinline__ void norm_rope(float (&x)[8], int part, const void *w
   const float rstd = 1.0f / sqrtf(q / float(D) + eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i) x[i] = rbf((x[i] - mean) * rstd * wf[i] + bfv[i]);
-  const int64_t ro = bi * P.rope_sb + t * P.rope_st + part * 8;
-  load_row8(P.cos, ro, c);
-  load_row8(P.sin, ro, s);
   float y[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = rbf(rbf(c[i] * x[i]) + rbf(s[i] * x[i ^ 1]));
@@ -148,11 +149,16 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   const bool shift = P.token_shift != 0;
   const bool pre = mode == 1 || mode == 2;
   const int64_t t0 = tile * kTokWave;
+  const float eps = float(P.ln_eps);
+  // Every load of a pass is issued before its arithmetic (the outputs may
+  // alias nothing the kernel reads, but the compiler cannot know that).
 
   if (head < Hq) {
     const int64_t width = Hq * D;
     const int64_t chan = head * D + part * 8;
-    float mix[8], carry[8];
+    float mix[8], carry[8], wf[8], bfv[8];
+    param8(P.ln_q_w, part * 8, wf);
+    param8(P.ln_q_b, part * 8, bfv);
     if (shift) {
       param8(P.x_q, chan, mix);
       // predecessor of the tile's first token
@@ -163,10 +169,14 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     for (int ps = 0; ps < PASSES && t0 + ps * RPW < T; ++ps) {  // passes with a live token
       const int64_t t = t0 + ps * RPW + sub;
       const bool live = t < T;
-      const int64_t r = bi * T + (live ? t : T - 1);
+      const int64_t tt = live ? t : T - 1;
+      const int64_t r = bi * T + tt;
       const int64_t e = r * width + chan;
-      float x[8];
+      const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
+      float x[8], c[8], sn[8];
       load_row8(P.q_lin, r * P.qkv_st + chan, x);
+      load_row8(P.cos, ro, c);
+      load_row8(P.sin, ro, sn);
       if (live && P.q_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.q_last_out) + bi * width + chan, x);
       if (shift) {
         float pv[8];
@@ -176,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
         last_row<LPR>(x, part, carry);
         token_shift(x, pv, mix);
       }
-      norm_rope<D>(x, part, P.ln_q_w, P.ln_q_b, float(P.ln_eps), P, bi, live ? t : T - 1);
+      norm_rope<D>(x, wf, bfv, eps, c, sn);
       if (live) store8(static_cast<uint16_t *>(P.q_out) + e, x);
     }
     return;
@@ -184,15 +194,23 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   const int64_t hk = head - Hq;
   const int64_t width = Hkv * D;
   const int64_t chan = hk * D + part * 8;
-  float kmix[8], vmix[8], kcarry[8], vcarry[8];
+  float kmix[8], vmix[8], kcarry[8], vcarry[8], wf[8], bfv[8], g0[8];
+  param8(P.ln_k_w, part * 8, wf);
+  param8(P.ln_k_b, part * 8, bfv);
+  if (mode >= 2) param8(P.v_gate0, chan, g0);
+  const float lamb = mode == 1 ? param1(P.lamb, 0) : 0.f;
   if (shift) {
     param8(P.x_k, chan, kmix);
     param8(P.x_v, chan, vmix);
     if (t0 > 0) {
       const int64_t rp = bi * T + t0 - 1;
+      VRes vr;
       load_row8(P.k_lin, rp * P.qkv_st + chan, kcarry);
       load_row8(P.v_lin, rp * P.qkv_st + chan, vcarry);
-      if (pre) value_residual(mode, vcarry, P, rp * width + chan, chan);
+      if (pre) {
+        load_vres(mode, P, rp * width + chan, vr);
+        value_residual(mode, vcarry, vr, g0, lamb);
+      }
     } else {
       if (P.k_prev) load_row8(P.k_prev, bi * width + chan, kcarry);
       if (P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
@@ -205,9 +223,17 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     const int64_t tt = live ? t : T - 1;
     const int64_t r = bi * T + tt;
     const int64_t e = r * width + chan, ein = r * P.qkv_st + chan;
-    // keys: token shift, ln_k, RoPE
-    float x[8];
+    const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
+    float x[8], v[8], c[8], sn[8];
+    VRes vr;
     load_row8(P.k_lin, ein, x);
+    load_row8(P.v_lin, ein, v);
+    load_row8(P.cos, ro, c);
+    load_row8(P.sin, ro, sn);
+    load_vres(mode, P, e, vr);
+    const bool gate_lane = live && part == 0 && P.key_weight && P.gate_out;
+    const float kw = gate_lane ? bf2f(static_cast<const uint16_t *>(P.key_weight)[(bi * T + t) * P.kw_st + hk]) : 0.f;
+    // keys: token shift, ln_k, RoPE
     if (live && P.k_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.k_last_out) + bi * width + chan, x);
     if (shift) {
       float pv[8];
@@ -217,12 +243,10 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       last_row<LPR>(x, part, kcarry);
       token_shift(x, pv, kmix);
     }
-    norm_rope<D>(x, part, P.ln_k_w, P.ln_k_b, float(P.ln_eps), P, bi, tt);
+    norm_rope<D>(x, wf, bfv, eps, c, sn);
     if (live) store8(static_cast<uint16_t *>(P.k_out) + e, x);
     // values: value residual before / after the token shift
-    float v[8];
-    load_row8(P.v_lin, ein, v);
-    if (pre) value_residual(mode, v, P, e, chan);
+    if (pre) value_residual(mode, v, vr, g0, lamb);
     if (live && P.v_last_out && t == T - 1)
       store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
     if (shift) {
@@ -233,12 +257,11 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       last_row<LPR>(v, part, vcarry);
       token_shift(v, pv, vmix);
     }
-    if (mode == 3) value_residual(2, v, P, e, chan);
+    if (mode == 3) value_residual(2, v, vr, g0, lamb);
     if (live) store8(static_cast<uint16_t *>(P.v_out) + e, v);
     // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
-    if (live && part == 0 && P.key_weight && P.gate_out) {
+    if (gate_lane) {
       const int64_t ge = (bi * T + t) * Hkv + hk;
-      const float kw = bf2f(static_cast<const uint16_t *>(P.key_weight)[(bi * T + t) * P.kw_st + hk]);
       const float el = rbf(kw > 0.f ? kw : expm1f(kw));
       static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
     }
