@@ -286,15 +286,16 @@ def bench_e2e(args, torch, kvm_amd):
         torch.cuda.synchronize()
         return e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
 
+    n_eager = min(n_dec, args.e2e_eager_steps)
     with torch.no_grad():
         run(8, True)
         pre_ms, dec_ms = run(n_dec, True)
-        _, eager_ms = run(min(n_dec, 64), False)
+        eager_ms = run(n_eager, False)[1] if n_eager > 0 else None
     del model
     torch.cuda.empty_cache()
     return dict(prefill_ms=pre_ms, prefill_tok_s=B * T / (pre_ms * 1e-3), decode_ms_per_step=dec_ms / n_dec,
                 decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec, decode_path="hip_graph",
-                eager_decode_ms_per_step=eager_ms / min(n_dec, 64))
+                eager_decode_ms_per_step=eager_ms / n_eager if n_eager > 0 else None)
 
 
 def _cpu_prefill_inputs(torch, B, H, D, T, dtype, seed):
@@ -374,6 +375,9 @@ def main():
     ap.add_argument("--skip-backward", action="store_true")
     ap.add_argument("--e2e-decode", type=int, default=512,
                     help="greedy decode steps of the config-5 decoder run (default 512)")
+    ap.add_argument("--e2e-eager-steps", type=int, default=64,
+                    help="decode steps of the config-5 decoder also run without the HIP graph, "
+                         "for comparison (default 64; 0 skips)")
     ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e", "backward"], default=None,
                     help="run one workload (profiling); 'copy' streams a known number of bytes "
                          "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
@@ -488,10 +492,14 @@ def main():
         line["decoder_e2e"] = {
             "workload": "config 5: random-init 24-layer all-KVM decoder, d_model 2048, 16 heads of 128, vocab 65536, "
                         f"bf16, chunk 512, 512 fixed slots; prefill 16384 random token ids at batch 8, then "
-                        f"{e2e['decode_steps']} greedy decode steps (projections, MLP and LM head on torch/hipBLASLt)",
+                        f"{e2e['decode_steps']} greedy decode steps replayed from a HIP graph (projections, MLP "
+                        "and LM head: hipBLASLt in the prefill, kvm_gemm_small in decode)",
             "prefill_tokens_per_s": round(e2e["prefill_tok_s"], 1), "prefill_ms": round(e2e["prefill_ms"], 2),
             "decode_tokens_per_s": round(e2e["decode_tok_s"], 1),
             "decode_ms_per_step": round(e2e["decode_ms_per_step"], 3),
+            "decode_path": e2e["decode_path"],
+            "eager_decode_ms_per_step": (round(e2e["eager_decode_ms_per_step"], 3)
+                                         if e2e["eager_decode_ms_per_step"] is not None else None),
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

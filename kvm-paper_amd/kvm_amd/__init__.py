@@ -8,6 +8,7 @@ Public API:
                            (model.rwkv7_backbone.RWKV7BackboneForCausalLM)
   MixerConfig              its config (the reference's field names/defaults)
   StatesDictCache          per-layer carried-state cache of the decoder
+  DecodeGraph              the decoder's single-token step replayed from a HIP graph
   load_reference_checkpoint  the decoder from a reference checkpoint
                            (save_pretrained directory, trainer .pt, .safetensors)
   snapshot_from_states     DecodeCacheSnapshot from the eager mixer's state dict
@@ -15,7 +16,7 @@ Public API:
 """
 
 from ._lib import load as load_library
-from .backbone import MixerConfig, RWKV7BackboneForCausalLM, RWKV7BackboneModel, init_random_
+from .backbone import DecodeGraph, MixerConfig, RWKV7BackboneForCausalLM, RWKV7BackboneModel, init_random_
 from .checkpoint import load_reference_checkpoint, snapshot_from_states
 from .decode_cache import DecodeCacheSnapshot, KVMDecodeCache, TritonKVMDecodeCache
 from .mixer import SequenceMixer
@@ -23,4 +24,4 @@ from .states_cache import StatesDictCache
 
 __all__ = ["SequenceMixer", "KVMDecodeCache", "TritonKVMDecodeCache", "DecodeCacheSnapshot", "load_library",
            "MixerConfig", "RWKV7BackboneForCausalLM", "RWKV7BackboneModel", "StatesDictCache", "init_random_",
-           "load_reference_checkpoint", "snapshot_from_states"]
+           "load_reference_checkpoint", "snapshot_from_states", "DecodeGraph"]
