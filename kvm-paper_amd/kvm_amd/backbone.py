@@ -227,7 +227,7 @@ class MLP(nn.Module):
 
     def ffn(self, xk):
         """c_proj(relu(c_fc(xk))^2)."""
-        if self._use_kernels(xk):
+        if self._use_kernels(xk) and type(self.c_fc) is nn.Linear and self.c_fc.bias is None:
             return module_linear(self.c_proj, linear(xk, self.c_fc.weight, relu_square=True))
         return module_linear(self.c_proj, F.relu(module_linear(self.c_fc, xk)).square())
 

@@ -62,8 +62,12 @@ def _relu_square(h: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def module_linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    """``mod(x)`` through :func:`linear`."""
+def module_linear(mod: torch.nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """``mod(x)``, through :func:`linear` when ``mod`` is an ``nn.Linear``
+    (any other module, e.g. an ``nn.Identity`` a test puts in its place, is
+    called as it is)."""
+    if type(mod) is not torch.nn.Linear:
+        return mod(x)
     return linear(x, mod.weight, mod.bias)
 
 
