@@ -130,6 +130,17 @@ __device__ __forceinline__ void last_row(const float (&x)[8], int part, float (&
   for (int i = 0; i < 8; ++i) c[i] = __shfl(x[i], 64 - LPR + part);
 }
 
+// The raw rows one pass of a wave reads (packed bf16, 16 bytes per lane),
+// fetched a pass ahead so that their latency overlaps the previous pass.
+struct PassRaw {
+  uint4 x, v, c, s, vf, gl;
+  uint16_t kw;
+};
+
+__device__ __forceinline__ uint4 raw8(const void *base, int64_t elem) {
+  return *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + elem);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   constexpr int LPR = D / 8;          // lanes per row
@@ -150,102 +161,94 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   const bool pre = mode == 1 || mode == 2;
   const int64_t t0 = tile * kTokWave;
   const float eps = float(P.ln_eps);
-  // Every load of a pass is issued before its arithmetic (the outputs may
-  // alias nothing the kernel reads, but the compiler cannot know that).
-
-  if (head < Hq) {
-    const int64_t width = Hq * D;
-    const int64_t chan = head * D + part * 8;
-    float mix[8], carry[8], wf[8], bfv[8];
-    param8(P.ln_q_w, part * 8, wf);
-    param8(P.ln_q_b, part * 8, bfv);
-    if (shift) {
-      param8(P.x_q, chan, mix);
-      // predecessor of the tile's first token
-      if (t0 > 0) load_row8(P.q_lin, (bi * T + t0 - 1) * P.qkv_st + chan, carry);
-      else if (P.q_prev) load_row8(P.q_prev, bi * width + chan, carry);
-    }
-#pragma unroll 1
-    for (int ps = 0; ps < PASSES && t0 + ps * RPW < T; ++ps) {  // passes with a live token
-      const int64_t t = t0 + ps * RPW + sub;
-      const bool live = t < T;
-      const int64_t tt = live ? t : T - 1;
-      const int64_t r = bi * T + tt;
-      const int64_t e = r * width + chan;
-      const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
-      float x[8], c[8], sn[8];
-      load_row8(P.q_lin, r * P.qkv_st + chan, x);
-      load_row8(P.cos, ro, c);
-      load_row8(P.sin, ro, sn);
-      if (live && P.q_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.q_last_out) + bi * width + chan, x);
-      if (shift) {
-        float pv[8];
-        if (ps == 0 && t0 == 0 && !P.q_prev)  // fallback "first": token 0 is its own predecessor
-          for (int i = 0; i < 8; ++i) carry[i] = __shfl(x[i], part);
-        prev_rows<LPR>(x, carry, lane, pv);
-        last_row<LPR>(x, part, carry);
-        token_shift(x, pv, mix);
-      }
-      norm_rope<D>(x, wf, bfv, eps, c, sn);
-      if (live) store8(static_cast<uint16_t *>(P.q_out) + e, x);
-    }
-    return;
-  }
+  const bool is_q = head < Hq;
   const int64_t hk = head - Hq;
-  const int64_t width = Hkv * D;
-  const int64_t chan = hk * D + part * 8;
-  float kmix[8], vmix[8], kcarry[8], vcarry[8], wf[8], bfv[8], g0[8];
-  param8(P.ln_k_w, part * 8, wf);
-  param8(P.ln_k_b, part * 8, bfv);
-  if (mode >= 2) param8(P.v_gate0, chan, g0);
-  const float lamb = mode == 1 ? param1(P.lamb, 0) : 0.f;
+  const int64_t width = is_q ? Hq * D : Hkv * D;
+  const int64_t chan = (is_q ? head : hk) * D + part * 8;
+  const int npass = int(min(int64_t(PASSES), (T - t0 + RPW - 1) / RPW));  // passes with a live token
+  // Token of this lane in pass ps (clamped to T - 1 for the lanes past the end).
+  auto token = [&](int ps) {
+    const int64_t t = t0 + ps * RPW + sub;
+    return t < T ? t : T - 1;
+  };
+  auto fetch = [&](int ps, PassRaw &r) {
+    const int64_t tt = token(ps);
+    const int64_t row = bi * T + tt;
+    const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
+    r.x = raw8(is_q ? P.q_lin : P.k_lin, row * P.qkv_st + chan);
+    r.c = raw8(P.cos, ro);
+    r.s = raw8(P.sin, ro);
+    r.v = r.vf = r.gl = make_uint4(0, 0, 0, 0);
+    r.kw = 0;
+    if (!is_q) {
+      r.v = raw8(P.v_lin, row * P.qkv_st + chan);
+      if (mode != 0) r.vf = raw8(P.v_first, row * width + chan);
+      if (mode >= 2) r.gl = raw8(P.gate_lin, row * width + chan);
+      if (P.key_weight && part == 0) r.kw = static_cast<const uint16_t *>(P.key_weight)[row * P.kw_st + hk];
+    }
+  };
+
+  float wf[8], bfv[8], xmix[8], vmix[8], xcarry[8], vcarry[8], g0[8];
+  param8(is_q ? P.ln_q_w : P.ln_k_w, part * 8, wf);
+  param8(is_q ? P.ln_q_b : P.ln_k_b, part * 8, bfv);
+  if (!is_q && mode >= 2) param8(P.v_gate0, chan, g0);
+  const float lamb = !is_q && mode == 1 ? param1(P.lamb, 0) : 0.f;
+  const void *x_prev = is_q ? P.q_prev : P.k_prev;
   if (shift) {
-    param8(P.x_k, chan, kmix);
-    param8(P.x_v, chan, vmix);
+    param8(is_q ? P.x_q : P.x_k, chan, xmix);
+    if (!is_q) param8(P.x_v, chan, vmix);
+    // predecessor of the tile's first token
     if (t0 > 0) {
       const int64_t rp = bi * T + t0 - 1;
-      VRes vr;
-      load_row8(P.k_lin, rp * P.qkv_st + chan, kcarry);
-      load_row8(P.v_lin, rp * P.qkv_st + chan, vcarry);
-      if (pre) {
-        load_vres(mode, P, rp * width + chan, vr);
-        value_residual(mode, vcarry, vr, g0, lamb);
+      load_row8(is_q ? P.q_lin : P.k_lin, rp * P.qkv_st + chan, xcarry);
+      if (!is_q) {
+        load_row8(P.v_lin, rp * P.qkv_st + chan, vcarry);
+        if (pre) {
+          VRes vr;
+          load_vres(mode, P, rp * width + chan, vr);
+          value_residual(mode, vcarry, vr, g0, lamb);
+        }
       }
     } else {
-      if (P.k_prev) load_row8(P.k_prev, bi * width + chan, kcarry);
-      if (P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
+      if (x_prev) load_row8(x_prev, bi * width + chan, xcarry);
+      if (!is_q && P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
     }
   }
+  uint16_t *x_out = static_cast<uint16_t *>(is_q ? P.q_out : P.k_out);
+  uint16_t *x_last = static_cast<uint16_t *>(is_q ? P.q_last_out : P.k_last_out);
+
+  PassRaw next;
+  fetch(0, next);
 #pragma unroll 1
-  for (int ps = 0; ps < PASSES && t0 + ps * RPW < T; ++ps) {  // passes with a live token
+  for (int ps = 0; ps < npass; ++ps) {
+    const PassRaw cur = next;
+    if (ps + 1 < npass) fetch(ps + 1, next);
     const int64_t t = t0 + ps * RPW + sub;
     const bool live = t < T;
-    const int64_t tt = live ? t : T - 1;
-    const int64_t r = bi * T + tt;
-    const int64_t e = r * width + chan, ein = r * P.qkv_st + chan;
-    const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
-    float x[8], v[8], c[8], sn[8];
-    VRes vr;
-    load_row8(P.k_lin, ein, x);
-    load_row8(P.v_lin, ein, v);
-    load_row8(P.cos, ro, c);
-    load_row8(P.sin, ro, sn);
-    load_vres(mode, P, e, vr);
-    const bool gate_lane = live && part == 0 && P.key_weight && P.gate_out;
-    const float kw = gate_lane ? bf2f(static_cast<const uint16_t *>(P.key_weight)[(bi * T + t) * P.kw_st + hk]) : 0.f;
-    // keys: token shift, ln_k, RoPE
-    if (live && P.k_last_out && t == T - 1) store8(static_cast<uint16_t *>(P.k_last_out) + bi * width + chan, x);
+    const int64_t e = (bi * T + (live ? t : T - 1)) * width + chan;
+    float x[8], c[8], sn[8];
+    unpack8(cur.x, x);
+    unpack8(cur.c, c);
+    unpack8(cur.s, sn);
+    // q / k: carried raw row, token shift, LayerNorm, RoPE
+    if (live && x_last && t == T - 1) store8(x_last + bi * width + chan, x);
     if (shift) {
       float pv[8];
-      if (ps == 0 && t0 == 0 && !P.k_prev)
-        for (int i = 0; i < 8; ++i) kcarry[i] = __shfl(x[i], part);
-      prev_rows<LPR>(x, kcarry, lane, pv);
-      last_row<LPR>(x, part, kcarry);
-      token_shift(x, pv, kmix);
+      if (ps == 0 && t0 == 0 && !x_prev)  // fallback "first": token 0 is its own predecessor
+        for (int i = 0; i < 8; ++i) xcarry[i] = __shfl(x[i], part);
+      prev_rows<LPR>(x, xcarry, lane, pv);
+      last_row<LPR>(x, part, xcarry);
+      token_shift(x, pv, xmix);
     }
     norm_rope<D>(x, wf, bfv, eps, c, sn);
-    if (live) store8(static_cast<uint16_t *>(P.k_out) + e, x);
+    if (live) store8(x_out + e, x);
+    if (is_q) continue;  // wave-uniform
     // values: value residual before / after the token shift
+    float v[8];
+    VRes vr;
+    unpack8(cur.v, v);
+    unpack8(cur.vf, vr.vf);
+    unpack8(cur.gl, vr.gl);
     if (pre) value_residual(mode, v, vr, g0, lamb);
     if (live && P.v_last_out && t == T - 1)
       store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
@@ -260,8 +263,9 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     if (mode == 3) value_residual(2, v, vr, g0, lamb);
     if (live) store8(static_cast<uint16_t *>(P.v_out) + e, v);
     // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
-    if (gate_lane) {
+    if (live && part == 0 && P.key_weight && P.gate_out) {
       const int64_t ge = (bi * T + t) * Hkv + hk;
+      const float kw = bf2f(cur.kw);
       const float el = rbf(kw > 0.f ? kw : expm1f(kw));
       static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
     }
