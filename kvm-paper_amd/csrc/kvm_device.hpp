@@ -13,6 +13,17 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Workgroups of a 1-D grid are dispatched round-robin over the 8 XCDs (each
+// with its own L2).  This renumbering gives each XCD a contiguous range of
+// logical workgroup ids, so neighbouring logical ids (which share operands)
+// run on one XCD close together in time.
+__device__ __forceinline__ int xcd_contiguous(int bid, int n) {
+  constexpr int kXcd = 8;
+  const int x = bid % kXcd, jx = bid / kXcd;
+  const int q = n / kXcd, r = n % kXcd;
+  return x * q + min(x, r) + jx;
+}
+
 // bfloat16 <-> float.  float -> bfloat16 rounds to nearest even (the
 // rounding torch uses for every float -> bfloat16 conversion), done by the
 // gfx950 instruction v_cvt_pk_bf16_f32.

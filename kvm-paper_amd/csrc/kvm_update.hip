@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void k_prep(kvm_layer L, kvm_seq src, Pre
 // Token x slot similarity on MFMA 16x16x32 bf16.
 //
 // Workgroup: 64 overflow tokens x one split of at most kSplit slots of one
-// row (grid: rows x token tiles x slot splits).  The similarity is computed
+// row (1-D grid of rows x token tiles x slot splits).  The similarity is computed
 // transposed, D^T[slot][token] = S_attn . X^T, so the accumulator lane
 // layout (lane l holds slots 4*(l/16)+i of token l%16) reduces over slots
 // within a lane, then across the 4 lane groups and the 4 waves (LDS); one
@@ -192,7 +192,7 @@ constexpr int kSplit = 128;  // slots per workgroup
 template <int D, bool NOVELTY>
 __global__ __launch_bounds__(kThreads) void k_route(
     kvm_layer L, int n_tok, AttnRows sref, int s_lim, int protect, UpdateScratch sc,
-    int parity) {
+    int parity, int tiles, int splits) {
   constexpr int G = D / 8;
   constexpr int STR = D + 8;  // LDS row stride (elements), 16 B pad
   constexpr int KS = D / 32;
@@ -200,9 +200,12 @@ __global__ __launch_bounds__(kThreads) void k_route(
   __shared__ uint32_t hi_lds[4][64];
   __shared__ int idx_lds[4][64];
 
-  const int row = blockIdx.x;
-  const int tok0 = blockIdx.y * 64;
-  const int split = blockIdx.z;
+  // Logical order (row, token tile, slot split), contiguous per XCD: the
+  // workgroups of a row share its slot rows and tokens through one L2.
+  const int wg = xcd_contiguous(int(blockIdx.x), int(gridDim.x));
+  const int split = wg % splits;
+  const int tok0 = (wg / splits) % tiles * 64;
+  const int row = wg / (splits * tiles);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t rbase = int64_t(row) * n_tok;
 
@@ -687,9 +690,9 @@ static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
   const unsigned tiles = unsigned((n_tok + 63) / 64);
   hipError_t e;
   if (n_append > 0) {
-    const dim3 ngrid{rows, tiles, unsigned((state_before + kSplit - 1) / kSplit)};
-    hipLaunchKernelGGL((k_route<D, true>), ngrid, dim3(kThreads), 0, stream, L, int(n_tok),
-                       attn_in, int(state_before), 0, sc, parity);
+    const unsigned nsplit = unsigned((state_before + kSplit - 1) / kSplit);
+    hipLaunchKernelGGL((k_route<D, true>), dim3(rows * tiles * nsplit), dim3(kThreads), 0, stream, L,
+                       int(n_tok), attn_in, int(state_before), 0, sc, parity, int(tiles), int(nsplit));
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t lds = size_t(n_tok) * 12;
     hipLaunchKernelGGL(k_rank_append<D>, dim3(rows), dim3(512), lds, stream, L,
@@ -697,9 +700,9 @@ static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
                        int(state_before), st, attn_in, sc);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  const dim3 rgrid{rows, tiles, unsigned((s_after + kSplit - 1) / kSplit)};
-  hipLaunchKernelGGL((k_route<D, false>), rgrid, dim3(kThreads), 0, stream, L, int(n_tok),
-                     attn_in, s_after, protect, sc, parity);
+  const unsigned rsplit = unsigned((s_after + kSplit - 1) / kSplit);
+  hipLaunchKernelGGL((k_route<D, false>), dim3(rows * tiles * rsplit), dim3(kThreads), 0, stream, L,
+                     int(n_tok), attn_in, s_after, protect, sc, parity, int(tiles), int(rsplit));
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (route_out || append_out) {
     const int64_t n = int64_t(rows) * n_tok;
