@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void k_prep(kvm_layer L, kvm_seq src, Pre
 // ---------------------------------------------------------------------------
 // Token x slot similarity on MFMA 16x16x32 bf16.
 //
-// Workgroup: 64 overflow tokens x one split of at most kSplit slots of one
+// Workgroup: kRouteTok overflow tokens x one split of at most kSplit slots of one
 // row (1-D grid of rows x token tiles x slot splits).  The similarity is computed
 // transposed, D^T[slot][token] = S_attn . X^T, so the accumulator lane
 // layout (lane l holds slots 4*(l/16)+i of token l%16) reduces over slots
@@ -188,6 +188,7 @@ __global__ __launch_bounds__(kThreads) void k_prep(kvm_layer L, kvm_seq src, Pre
 //       argmax over slots [protect, s_lim) of the fp32 dot
 //       (model/kvm_fp32_routing_reference.py:30-34).
 constexpr int kSplit = 128;  // slots per workgroup
+constexpr int kRouteTok = 128;  // tokens per workgroup (8 tiles of 16)
 
 template <int D, bool NOVELTY>
 __global__ __launch_bounds__(kThreads) void k_route(
@@ -196,20 +197,21 @@ __global__ __launch_bounds__(kThreads) void k_route(
   constexpr int G = D / 8;
   constexpr int STR = D + 8;  // LDS row stride (elements), 16 B pad
   constexpr int KS = D / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t tok_lds[64 * STR];
-  __shared__ uint32_t hi_lds[4][64];
-  __shared__ int idx_lds[4][64];
+  constexpr int TT = kRouteTok / 16;  // token tiles
+  __shared__ __attribute__((aligned(16))) uint16_t tok_lds[kRouteTok * STR];
+  __shared__ uint32_t hi_lds[4][kRouteTok];
+  __shared__ int idx_lds[4][kRouteTok];
 
   // Logical order (row, token tile, slot split), contiguous per XCD: the
   // workgroups of a row share its slot rows and tokens through one L2.
   const int wg = xcd_contiguous(int(blockIdx.x), int(gridDim.x));
   const int split = wg % splits;
-  const int tok0 = (wg / splits) % tiles * 64;
+  const int tok0 = (wg / splits) % tiles * kRouteTok;
   const int row = wg / (splits * tiles);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t rbase = int64_t(row) * n_tok;
 
-  // Slot rows of this wave (two 16-slot tiles) and the 64 token operands,
+  // Slot rows of this wave (two 16-slot tiles) and the kRouteTok token operands,
   // all issued before any is used.
   const uint16_t *sbase = sref.k + int64_t(row) * sref.cap * D;
   const int jw = split * kSplit + wave * 32;
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(kThreads) void k_route(
                                                                    (lane >> 4) * 8)
                                 : make_uint4(0, 0, 0, 0);
   }
-  constexpr int IT = 64 * G / kThreads;
+  constexpr int IT = kRouteTok * G / kThreads;
   const uint16_t *opnd = NOVELTY ? sc.pk : sc.gk;
   uint4 xr[IT];
 #pragma unroll
@@ -240,11 +242,11 @@ __global__ __launch_bounds__(kThreads) void k_route(
   }
   __syncthreads();
 
-  // (2) similarity of the 4 token tiles against the wave's 32 slots.
-  float best[4];
-  int bidx[4];
+  // (2) similarity of the TT token tiles against the wave's 32 slots.
+  float best[TT];
+  int bidx[TT];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < TT; ++tt) {
     best[tt] = -INFINITY;
     bidx[tt] = -1;
     bf16x8 bx[KS];
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void k_route(
 
   // (3) lane groups, then waves (slot order: lower wave = lower slots).
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
     for (int o = 16; o <= 32; o <<= 1) {
       const float ob = __shfl_xor(best[tt], o);
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void k_route(
     }
   }
   __syncthreads();
-  if (tid < 64) {
+  if (tid < kRouteTok) {
     const int i_tok = tok0 + tid;
     if (i_tok < n_tok) {
       const int64_t o = rbase + i_tok;
@@ -687,7 +689,7 @@ static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
   const unsigned rows = unsigned(rows_of(L));
   const int s_after = int(state_before + n_append);
   const int protect = int(L.sink_len < s_after ? L.sink_len : s_after);
-  const unsigned tiles = unsigned((n_tok + 63) / 64);
+  const unsigned tiles = unsigned((n_tok + kRouteTok - 1) / kRouteTok);
   hipError_t e;
   if (n_append > 0) {
     const unsigned nsplit = unsigned((state_before + kSplit - 1) / kSplit);
