@@ -13,6 +13,10 @@ Workloads:
            a chunk boundary is crossed, split-K attention).  The timed
            region is `--decode-steps` consecutive tokens from a fresh
            snapshot, so the one update per 256 tokens is included.
+  config3  config 3: B2 H16 D128 T65536 chunk 512, ceil-sqrt slots capped
+           at 1024, clustered keys; the budget as written and a growth
+           variant (factor 16, 512 -> 1024 slots by appends); reported in the
+           "prefill_config3" object.
   decoder  config 5: random-init 24-layer all-KVM decoder (d_model 2048,
            16 heads of 128, vocab 65536, chunk 512, 512 fixed slots):
            prefill 16384 random token ids at batch 8, then greedy decode
@@ -60,13 +64,13 @@ def measured_traffic(kernel, workload):
     return None
 
 
-def _config(Hq, Hkv, D, C, n_bswa, min_len, n_max):
+def _config(Hq, Hkv, D, C, n_bswa, min_len, n_max, mode="fixed", factor=1.0):
     return SimpleNamespace(
         num_attention_heads=Hq, num_key_value_heads=Hkv, hidden_size=Hq * D, d_qk_head=D, d_v_head=D,
         d_head=None, num_hidden_layers=1, mup_base_dim=Hq * D, use_tokenshift_att=0, use_value_residual=0,
         kvm_value_residual_mode="rwkv", kvm_token_shift_mode="rwkv", rope_partial_dim=64, sink_len=1,
-        chunk_len=C, n_max_d_chunks=n_max, n_bswa_chunks=n_bswa, state_budget_mode="fixed",
-        state_growth_factor=1.0, state_growth_exponent=0.5, state_round_down=1, state_min_len=min_len,
+        chunk_len=C, n_max_d_chunks=n_max, n_bswa_chunks=n_bswa, state_budget_mode=mode,
+        state_growth_factor=factor, state_growth_exponent=0.5, state_round_down=1, state_min_len=min_len,
         state_saturation_n=None, kvm_use_merge_gate_keys=1, kvm_use_merge_gate_values=1,
         kvm_apply_merge_gate_to_appends=0, kvm_apply_merge_gate_to_initial_state=0, kvm_use_head_temps=1,
         kvm_use_vlens=1, kvm_aotriton_forward_attention=0,
@@ -138,6 +142,51 @@ def bench_prefill(args, torch, kvm_amd):
         ms=ms, wall_ms=wall * 1e3 / args.steps, tok_s=B * T / (ms * 1e-3), attn_ms=attn_ms, chain_ms=chain_ms,
         attn_flop=attn_flop, route_flop=route_flop, plan=plan, inputs=(q, k, v, g), mixer=mixer,
     )
+
+
+def bench_prefill_config3(args, torch, kvm_amd):
+    """B2 H16 D128 T65536 C512, slots ceil-sqrt(tokens seen) capped at 1024
+    (power-law budget, n_max_d_chunks 2), 10 % of the keys drawn from 8 shared centres.  As
+    written the budget never passes the 512 slots the first chunk fills ("literal": 125 updates,
+    no appends); the growth variant (factor 16) grows the state 512 -> 1024 through appends."""
+    B, H, D, T, C = 2, 16, 128, 65536, 512
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    q = (torch.randn(B, H, T, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16()
+    kf = torch.randn(B, H, T, D, generator=gen, device=dev)
+    centres = torch.randn(8, D, generator=gen, device=dev)
+    pick = torch.randint(0, 8, (B, H, T), generator=gen, device=dev)
+    sel = torch.rand(B, H, T, generator=gen, device=dev) < 0.1
+    kf = torch.where(sel.unsqueeze(-1), centres[pick] + 0.05 * torch.randn(B, H, T, D, generator=gen, device=dev),
+                     kf)
+    k = (kf / math.sqrt(D)).bfloat16()
+    del kf
+    v = (torch.randn(B, H, T, D, generator=gen, device=dev) / math.sqrt(D)).bfloat16()
+    g = (1 + torch.nn.functional.elu(torch.randn(B, H, T, 1, generator=gen, device=dev))).bfloat16()
+    out = {}
+    for name, factor in (("literal", 1.0), ("growth_f16", 16.0)):
+        mixer = kvm_amd.SequenceMixer(_config(H, H, D, C, 2, C, 2, "power_law", factor), 0).to(dev, torch.bfloat16)
+        mixer.eval()
+        plan = mixer.make_plan(T)
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                mixer.prefill_raw(q, k, v, g, plan=plan)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(args.steps):
+                mixer.prefill_raw(q, k, v, g, plan=plan, check_status=False)
+            end.record()
+            torch.cuda.synchronize()
+            mixer.check_prefill_status()
+        ms = start.elapsed_time(end) / args.steps
+        flop = 4 * D * H * B * attention_pairs(plan, 2) + 2 * D * H * B * routing_pairs(plan)
+        out[name] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+                     "updates": plan.n_updates, "final_slots": plan.final_state_len,
+                     "appended_per_row": int(sum(plan.upd_n_append)), "algorithmic_flop": flop,
+                     "frac_of_mfma_peak": round(flop / (ms * 1e-3) / 2.5e15, 4)}
+        del mixer
+    return out
 
 
 def bench_backward(args, torch, kvm_amd, pf):
@@ -373,12 +422,13 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--skip-e2e", action="store_true")
     ap.add_argument("--skip-backward", action="store_true")
+    ap.add_argument("--skip-config3", action="store_true")
     ap.add_argument("--e2e-decode", type=int, default=512,
                     help="greedy decode steps of the config-5 decoder run (default 512)")
     ap.add_argument("--e2e-eager-steps", type=int, default=64,
                     help="decode steps of the config-5 decoder also run without the HIP graph, "
                          "for comparison (default 64; 0 skips)")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e", "backward"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "copy", "e2e", "backward", "config3"], default=None,
                     help="run one workload (profiling); 'copy' streams a known number of bytes "
                          "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -403,6 +453,9 @@ def main():
     if args.only == "e2e":
         print(json.dumps(bench_e2e(args, torch, kvm_amd)))
         return
+    if args.only == "config3":
+        print(json.dumps(bench_prefill_config3(args, torch, kvm_amd)))
+        return
     if args.only == "decode":
         dec = bench_decode(args, torch, kvm_amd)
         print(json.dumps({k: v for k, v in dec.items()}))
@@ -422,6 +475,12 @@ def main():
         print("bench: config 2 training step (differentiable prefill + backward) ...", file=sys.stderr, flush=True)
         bwd = bench_backward(args, torch, kvm_amd, pf)
         print(f"bench: training step {bwd['step_ms']:.2f} ms (HIP attention backward {bwd['attn_bwd_ms']:.2f} ms)",
+              file=sys.stderr, flush=True)
+    pf3 = None
+    if not args.skip_config3:
+        print("bench: prefill config 3 (growable memory, two budgets) ...", file=sys.stderr, flush=True)
+        pf3 = bench_prefill_config3(args, torch, kvm_amd)
+        print("bench: config 3 " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in pf3.items()),
               file=sys.stderr, flush=True)
     dec = None
     if not args.skip_decode:
@@ -487,6 +546,13 @@ def main():
                         "head temperatures",
             "step_ms": round(bwd["step_ms"], 3), "attention_backward_ms": round(bwd["attn_bwd_ms"], 3),
             "tokens_per_s": round(32768 / (bwd["step_ms"] * 1e-3), 1),
+        }
+    if pf3 is not None:
+        line["prefill_config3"] = {
+            "workload": "config 3: KVM layer prefill B2 H16 D128 T65536 C512, ceil-sqrt slots capped at 1024, "
+                        "10% of keys from 8 shared centres; 'literal' is the budget as written (never passes the "
+                        "512 slots of the first chunk), 'growth_f16' grows 512 -> 1024 slots through appends",
+            **pf3,
         }
     if e2e is not None:
         line["decoder_e2e"] = {
