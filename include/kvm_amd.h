@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 9
+#define KVM_ABI_VERSION 10
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -270,7 +270,14 @@ int kvm_state_backward(const kvm_state_bwd_desc *d, void *stream);
  * q_last_out / k_last_out (optional, [B,1,Hq*D] / [B,1,Hkv*D]) receive the
  * last token's q_lin / k_lin rows (the carried rows of the next step's token
  * shift).  With seq_len == 1 each of the three may be the corresponding
- * q_prev / k_prev / v_prev itself (read before it is written). */
+ * q_prev / k_prev / v_prev itself (read before it is written).
+ * Optional window-ring write (seq_len == 1 only; model/kvm_triton_decode.py
+ * write_recent_ring, the row kvm_ring_write would write): with ring_k set,
+ * the token's k_out and v_out rows and its merge gate (1 when gate_out is
+ * NULL) of every (batch, kv head) row r = b * Hkv + h also go to ring_k /
+ * ring_v [r, ring_cap, D] and ring_gate [r, ring_cap] at position ring_pos,
+ * or, with ring_ctl (the int32[4] counters of kvm_ring_write_dev), at
+ * (ctl[1] + ctl[2]) mod ring_cap. */
 typedef struct kvm_prefix_desc {
   int64_t batch, seq_len, q_heads, kv_heads, head_dim, value_dim;
   int64_t value_residual_mode; /* 0 none, 1 linear, 2 rwkv, 3 rwkv_post_tokenshift */
@@ -285,6 +292,9 @@ typedef struct kvm_prefix_desc {
   int64_t qkv_st, kw_st;     /* token strides (elements) of q/k/v_lin and key_weight */
   void *q_out, *k_out, *v_out, *gate_out, *v_last_out;
   void *q_last_out, *k_last_out; /* optional [B, 1, width]: the last token's q_lin / k_lin rows */
+  void *ring_k, *ring_v, *ring_gate; /* optional window-ring write, above */
+  int64_t ring_cap, ring_pos;
+  const int32_t *ring_ctl;
 } kvm_prefix_desc;
 
 /* Run the pre-boundary elementwise work described above.  Replaces the

@@ -222,6 +222,16 @@ int kvm_prefix(const kvm_prefix_desc *d, void *stream) {
       if (p && !aligned16(p)) return fail(KVM_EINVAL, "previous-token rows must be 16-byte aligned");
   }
   if (d->v_last_out && !aligned16(d->v_last_out)) return fail(KVM_EINVAL, "v_last_out must be 16-byte aligned");
+  if ((d->q_last_out && !aligned16(d->q_last_out)) || (d->k_last_out && !aligned16(d->k_last_out)))
+    return fail(KVM_EINVAL, "q_last_out / k_last_out must be 16-byte aligned");
+  if (d->ring_k) {
+    if (d->seq_len != 1) return fail(KVM_EINVAL, "the prefix's ring write is for a single token (seq_len 1)");
+    if (!d->ring_v || !d->ring_gate || !aligned16(d->ring_k) || !aligned16(d->ring_v) || d->ring_cap < 1)
+      return fail(KVM_EINVAL, "ring write needs 16-byte aligned ring_k / ring_v, ring_gate and ring_cap >= 1");
+    if (!d->ring_ctl && (d->ring_pos < 0 || d->ring_pos >= d->ring_cap))
+      return fail(KVM_EINVAL, "ring_pos %lld outside the ring of %lld rows", (long long)d->ring_pos,
+                  (long long)d->ring_cap);
+  }
   if (d->rope_sb % 8 || d->rope_st % 8 || d->rope_st < d->head_dim)
     return fail(KVM_EINVAL, "cos/sin strides must be multiples of 8 elements covering head_dim");
   if (d->key_weight && !d->gate_out) return fail(KVM_EINVAL, "key_weight needs gate_out");

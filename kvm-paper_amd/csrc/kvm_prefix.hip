@@ -214,6 +214,19 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       if (!is_q && P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
     }
   }
+  // Window-ring row of a single decode token (kv heads).
+  const bool ring = !is_q && P.ring_k && T == 1;
+  int64_t ring_o = 0;
+  if (ring) {
+    int64_t pos = P.ring_pos;
+    if (P.ring_ctl) {
+      const int64_t cap = P.ring_cap;
+      const int64_t start = ((int64_t(P.ring_ctl[1]) % cap) + cap) % cap;
+      const int64_t len = min(max(int64_t(P.ring_ctl[2]), int64_t(0)), cap);
+      pos = (start + len) % cap;
+    }
+    ring_o = (bi * Hkv + hk) * P.ring_cap + pos;
+  }
   uint16_t *x_out = static_cast<uint16_t *>(is_q ? P.q_out : P.k_out);
   uint16_t *x_last = static_cast<uint16_t *>(is_q ? P.q_last_out : P.k_last_out);
 
@@ -243,6 +256,7 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     norm_rope<D>(x, wf, bfv, eps, c, sn);
     if (live) store8(x_out + e, x);
     if (is_q) continue;  // wave-uniform
+    if (ring && live) store8(static_cast<uint16_t *>(P.ring_k) + ring_o * D + part * 8, x);
     // values: value residual before / after the token shift
     float v[8];
     VRes vr;
@@ -262,13 +276,17 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     }
     if (mode == 3) value_residual(2, v, vr, g0, lamb);
     if (live) store8(static_cast<uint16_t *>(P.v_out) + e, v);
+    if (ring && live) store8(static_cast<uint16_t *>(P.ring_v) + ring_o * D + part * 8, v);
     // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
+    uint16_t gbits = 0x3f80;  // 1.0: no key weighting
     if (live && part == 0 && P.key_weight && P.gate_out) {
       const int64_t ge = (bi * T + t) * Hkv + hk;
       const float kw = bf2f(cur.kw);
       const float el = rbf(kw > 0.f ? kw : expm1f(kw));
-      static_cast<uint16_t *>(P.gate_out)[ge] = uint16_t(f2bf(1.f + el));
+      gbits = uint16_t(f2bf(1.f + el));
+      static_cast<uint16_t *>(P.gate_out)[ge] = gbits;
     }
+    if (ring && live && part == 0) static_cast<uint16_t *>(P.ring_gate)[ring_o] = gbits;
   }
 }
 

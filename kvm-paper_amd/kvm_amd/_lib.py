@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -134,6 +134,8 @@ class KvmPrefixDesc(ctypes.Structure):
         ("cos", _vp), ("sin", _vp), ("rope_sb", _i64), ("rope_st", _i64), ("qkv_st", _i64), ("kw_st", _i64),
         ("q_out", _vp), ("k_out", _vp), ("v_out", _vp), ("gate_out", _vp), ("v_last_out", _vp),
         ("q_last_out", _vp), ("k_last_out", _vp),
+        ("ring_k", _vp), ("ring_v", _vp), ("ring_gate", _vp), ("ring_cap", _i64), ("ring_pos", _i64),
+        ("ring_ctl", _vp),
     ]
 
 

@@ -428,17 +428,18 @@ class RWKV7BackboneModel(nn.Module):
         ln_mlp: x + s * f(h) and LN(x + s * f(h)) from one read of each."""
         blocks = self.h
         first = blocks[0]
-        _, h = _add_norm(x0, None, 1.0, first.ln_attn)
+        pkv = kwargs.get("past_key_values")
+        xf = self._carried_mixer_row(first, x0, pkv)
+        _, h = _add_norm(x0, None, 1.0, first.ln_attn, state_out=xf)
         first_kwargs_fn = getattr(first.attn, "get_first_layer_kwargs", lambda x0, x, **kw: {})
         first_kwargs = first_kwargs_fn(x0=x0, x=h, input_ids=input_ids, **kwargs)
         layer_kwargs = dict(x0=x0, **first_kwargs, **kwargs)
         layer_kwargs["position_embeddings"] = position_embeddings
-        pkv = layer_kwargs.get("past_key_values")
         x = x0
         for i, blk in enumerate(blocks):
             attn_fn = (getattr(blk.attn, "forward_inference", blk.attn.forward)
                        if not blk.training and pkv is not None else blk.attn.forward)
-            a = attn_fn(h, **layer_kwargs)
+            a = attn_fn(h, x_final_stored=xf is not None, **layer_kwargs)
             mlp = blk.mlp
             if self.config.use_tokenshift_ffn:
                 prev = mlp.carried_row(a, pkv)
@@ -454,9 +455,30 @@ class RWKV7BackboneModel(nn.Module):
                 x, xk = _add_norm(x, a, blk.residual_scale, blk.ln_mlp)
             m = mlp.ffn(xk)
             last = i + 1 == len(blocks)
+            xf = None if last else self._carried_mixer_row(blocks[i + 1], x, pkv)
             x, h = _add_norm(x, m, blk.residual_scale, self.ln_head if last else blocks[i + 1].ln_attn,
-                             want_x=not last)
+                             want_x=not last, state_out=xf)
         return h
+
+    @staticmethod
+    def _carried_mixer_row(blk, x, pkv):
+        """The mixer's carried input row (``att_x_final_token``) of ``blk``
+        when the block kernel can write the new one in place: a single token,
+        a cache with fixed addresses, an existing bf16 [B, 1, d] row, and a
+        mixer that does not read the old row during the step (every value
+        residual mode but rwkv_post_tokenshift, whose value-gate token shift
+        reads it)."""
+        if pkv is None or x.size(1) != 1 or not getattr(pkv, "static_states", False):
+            return None
+        mixer = blk.attn
+        key = getattr(mixer, "_CACHE_X_FINAL", None)
+        if key is None or getattr(mixer, "value_residual_mode", None) == "rwkv_post_tokenshift":
+            return None
+        prev = pkv.get_states(mixer.layer_idx).get(key)
+        if (prev is None or prev.shape != (x.shape[0], 1, x.shape[2]) or prev.dtype != torch.bfloat16
+                or not prev.is_contiguous()):
+            return None
+        return prev
 
 
 def _add_norm(x, y, scale, ln, *, mix=None, prev=None, state_out=None, want_x=True):
@@ -657,6 +679,7 @@ class DecodeGraph:
         finally:
             for c in kv:
                 c.graph_ctl = None
+                c.ring_row_written = False
         self.graph, self.signature = graph, sig
         graph.replay()
         self.replays += 1

@@ -112,6 +112,7 @@ class KVMDecodeCache:
         self._alloc_decode_workspace()
         self._set_counters(total=0, state_len=0, coverage=0, begin=0, window=0)
         self.graph_ctl: int | None = None  # device counter record while a decode step is captured
+        self.ring_row_written = False  # the prefix kernel wrote this step's ring row already
         if snapshot is not None:
             self.reset_(snapshot)
 
@@ -214,6 +215,9 @@ class KVMDecodeCache:
         self.total_len, self.recent_begin = int(total_len), int(recent_begin)
 
     def _write_window_row(self, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor, row: int) -> None:
+        if self.ring_row_written:  # written by the prefix kernel of this captured step
+            self.ring_row_written = False
+            return
         seq, keep = _lib.seq4(k, v, gate)
         lib = _lib.load()
         if self.graph_ctl is not None:  # capture of a graph step: the row comes from the device counters

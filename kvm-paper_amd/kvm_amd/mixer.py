@@ -342,7 +342,8 @@ class SequenceMixer(nn.Module):
         everything after them in one ``kvm_prefix`` launch; CPU tensors and
         autograd take the torch op sequence, which is the reference's."""
         if self._use_fused_prefix(x, position_embeddings):
-            return self._fused_prefix(x, v_first, position_embeddings, past_key_values)
+            return self._fused_prefix(x, v_first, position_embeddings, past_key_values,
+                                      x_final_stored=bool(kwargs.get("x_final_stored", False)))
         return self._torch_prefix(x, v_first, position_embeddings, past_key_values)
 
     _VR_MODES = {"none": 0, "linear": 1, "rwkv": 2, "rwkv_post_tokenshift": 3}
@@ -361,10 +362,12 @@ class SequenceMixer(nn.Module):
             return False
         return self.d_qk_head == self.d_v_head and self.d_qk_head in (64, 128)
 
-    def _fused_prefix(self, x, v_first, position_embeddings, past_key_values):
+    def _fused_prefix(self, x, v_first, position_embeddings, past_key_values, x_final_stored=False):
         """Projections (torch GEMMs), then value residual, token shift,
         ln_q/ln_k, RoPE and merge gate in one HIP launch (include/kvm_amd.h
-        kvm_prefix).  Same outputs and cache entries as ``_torch_prefix``."""
+        kvm_prefix).  Same outputs and cache entries as ``_torch_prefix``.
+        ``x_final_stored``: the caller already wrote x's last row over the
+        carried ``att_x_final_token`` (the block kernel that produced x)."""
         B, T, _ = x.size()
         states = past_key_values.get_states(self.layer_idx) if past_key_values is not None else {}
         past = past_key_values.get_seq_length(self.layer_idx) if past_key_values is not None else 0
@@ -466,6 +469,14 @@ class SequenceMixer(nn.Module):
         d.q_out, d.k_out, d.v_out = q.data_ptr(), k.data_ptr(), v.data_ptr()
         d.gate_out = gate.data_ptr() if gate is not None else None
         d.q_last_out, d.k_last_out, d.v_last_out = (t.data_ptr() if t is not None else None for t in last)
+        # A captured decode step (device ring counters) writes the token's
+        # window-ring row here instead of in a launch of its own.
+        dc = states.get(self._CACHE_TRITON_DECODE) if past_key_values is not None else None
+        if (T == 1 and isinstance(dc, KVMDecodeCache) and dc.graph_ctl is not None
+                and dc.recent_k.dtype == torch.bfloat16 and dc.recent_gate.dtype == torch.bfloat16):
+            d.ring_k, d.ring_v, d.ring_gate = dc.recent_k.data_ptr(), dc.recent_v.data_ptr(), dc.recent_gate.data_ptr()
+            d.ring_cap, d.ring_ctl = dc.ring_capacity, dc.graph_ctl
+            dc.ring_row_written = True
         lib = _lib.load()
         _lib.check(lib.kvm_prefix(ctypes.byref(d), _lib.stream_handle(x.device)), "kvm_prefix")
         del keep
@@ -474,7 +485,8 @@ class SequenceMixer(nn.Module):
                                                  last, prev) if t is not p}
             if fresh:
                 past_key_values.update(self.layer_idx, offset=0, states_dict=fresh)
-            _store_states(past_key_values, self.layer_idx, states, {self._CACHE_X_FINAL: x[:, -1:].detach()})
+            if not x_final_stored:
+                _store_states(past_key_values, self.layer_idx, states, {self._CACHE_X_FINAL: x[:, -1:].detach()})
         if use_gate:
             merge_gate = gate.view(B, T, Hkv, 1).transpose(1, 2)
         else:
