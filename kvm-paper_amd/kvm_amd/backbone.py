@@ -439,7 +439,7 @@ class RWKV7BackboneModel(nn.Module):
         for i, blk in enumerate(blocks):
             attn_fn = (getattr(blk.attn, "forward_inference", blk.attn.forward)
                        if not blk.training and pkv is not None else blk.attn.forward)
-            a = attn_fn(h, x_final_stored=xf is not None, **layer_kwargs)
+            a = attn_fn(h, **layer_kwargs) if xf is None else attn_fn(h, x_final_stored=True, **layer_kwargs)
             mlp = blk.mlp
             if self.config.use_tokenshift_ffn:
                 prev = mlp.carried_row(a, pkv)

@@ -294,7 +294,7 @@ class SequenceMixer(nn.Module):
         """model/value_residual_mixin.py:239-246."""
         if self.value_residual_mode == "none":
             return {"v_first": None}
-        return {"v_first": self.c_v(x)}
+        return {"v_first": module_linear(self.c_v, x)}
 
     def _value_gate(self, x):
         return torch.sigmoid(self.v_gate0 + module_linear(self.v_gate2, module_linear(self.v_gate1, x)))
