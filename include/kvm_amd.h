@@ -351,6 +351,23 @@ int kvm_add_norm(const kvm_add_norm_desc *d, void *stream);
 int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st, int64_t M,
                    int64_t N, int64_t K, int epilogue, void *stream);
 
+/* Rows of W per workgroup (8 or 16) kvm_gemm_small takes for M tokens and N
+ * outputs: the tile a packed W must be arranged for. */
+int kvm_gemm_small_tile_rows(int64_t M, int64_t N);
+
+/* kvm_gemm_small with W pre-arranged (once, by the caller) into 1 KiB chunks
+ * that each load instruction reads whole.  For tile_rows R = 16: chunk
+ * (b, s) = W rows 16b..16b+15, k 32s..32s+31, at element offset
+ * (b * K/32 + s) * 512, element (g * 16 + i) * 8 + e = W[16b + i][32s + 8g + e]
+ * (i < 16, g < 4, e < 8).  For R = 8 (K a multiple of 64): chunk (b, c) = rows
+ * 8b..8b+7, k 64c..64c+63, at (b * K/64 + c) * 512, element
+ * (g * 16 + h * 8 + j) * 8 + e = W[8b + j][64c + 32h + 8g + e] (j < 8, h < 2).
+ * Rows past N are zeros; wp holds ceil(N / R) * R * K elements.  tile_rows
+ * must be kvm_gemm_small_tile_rows(M, N).  Results are bit-identical to
+ * kvm_gemm_small's. */
+int kvm_gemm_small_packed(const void *x, int64_t x_st, const void *wp, void *y, int64_t y_st, int64_t M,
+                          int64_t N, int64_t K, int tile_rows, int epilogue, void *stream);
+
 /* ABI self-description, checked by the host binding at load time. */
 int kvm_abi_version(void);
 int64_t kvm_struct_size(int which); /* 0 layer, 1 seq, 2 state, 3 prefill_desc, 4 prefix_desc,

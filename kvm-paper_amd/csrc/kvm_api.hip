@@ -180,7 +180,31 @@ int kvm_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, voi
       y_st < N)
     return fail(KVM_EINVAL, "gemm_small operands must be 16-byte aligned rows (strides multiples of 8)");
   if (epilogue != 0 && epilogue != 1) return fail(KVM_EINVAL, "gemm_small: epilogue must be 0 or 1");
-  KVM_HIP(kvm::launch_gemm_small(x, x_st, w, w_st, y, y_st, M, N, K, epilogue, as_stream(stream)), "gemm_small");
+  KVM_HIP(kvm::launch_gemm_small(x, x_st, w, w_st, y, y_st, M, N, K, epilogue, false, as_stream(stream)),
+          "gemm_small");
+  return KVM_OK;
+}
+
+int kvm_gemm_small_tile_rows(int64_t M, int64_t N) {
+  if (M < 1 || M > 16 || N < 1) return fail(KVM_EINVAL, "gemm_small_tile_rows needs 1 <= M <= 16 and N >= 1");
+  return kvm::gemm_small_tile_rows(M, N);
+}
+
+int kvm_gemm_small_packed(const void *x, int64_t x_st, const void *wp, void *y, int64_t y_st, int64_t M,
+                          int64_t N, int64_t K, int tile_rows, int epilogue, void *stream) {
+  if (M < 1 || M > 16 || N < 1 || K < 32 || K % 32)
+    return fail(KVM_EINVAL, "gemm_small_packed needs 1 <= M <= 16, N >= 1 and K a positive multiple of 32");
+  const int rows = kvm::gemm_small_tile_rows(M, N);
+  if (tile_rows != rows)
+    return fail(KVM_EINVAL, "gemm_small_packed: W packed for %d-row tiles, this shape takes %d-row tiles",
+                tile_rows, rows);
+  if (rows == 8 && K % 64)
+    return fail(KVM_EINVAL, "gemm_small_packed: 8-row tiles need K a multiple of 64");
+  if (!x || !wp || !y || !aligned16(x) || !aligned16(wp) || x_st % 8 || x_st < K || y_st < N)
+    return fail(KVM_EINVAL, "gemm_small_packed operands must be 16-byte aligned rows (strides multiples of 8)");
+  if (epilogue != 0 && epilogue != 1) return fail(KVM_EINVAL, "gemm_small_packed: epilogue must be 0 or 1");
+  KVM_HIP(kvm::launch_gemm_small(x, x_st, wp, 0, y, y_st, M, N, K, epilogue, true, as_stream(stream)),
+          "gemm_small_packed");
   return KVM_OK;
 }
 

@@ -46,7 +46,11 @@ __device__ __forceinline__ uint4 swap_half_rows(uint4 u) {
 // after a swap of the two half rows.  Output rows and tokens 0-7 of the
 // 16 x 16 product then take only the wanted halves (rows >= 8 and columns
 // >= 8 hold cross terms and are not written).
-template <int NW, bool HALF>
+// PACKED: W comes pre-arranged in 1 KiB chunks, one per (tile of R rows,
+// load step of KC k), each holding the 64 lanes' 16-byte A-operand pieces in
+// lane order (see kvm_gemm_small_packed): every load instruction then reads
+// one contiguous KiB instead of 16 (or 8) row pieces 2*K bytes apart.
+template <int NW, bool HALF, bool PACKED>
 __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restrict__ X, int64_t x_st,
                                                         const uint16_t *__restrict__ W, int64_t w_st,
                                                         uint16_t *__restrict__ Y, int64_t y_st, int M, int N,
@@ -71,7 +75,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
     for (int c = 0; c < kSteps<NW>; ++c) {
       const int k = k0 + KC * c + kk;
       const bool in = k < ke;
-      a[c] = (in && row_ok) ? *reinterpret_cast<const uint4 *>(wrow + k) : make_uint4(0, 0, 0, 0);
+      if constexpr (PACKED) {
+        const int64_t chunk = int64_t(blockIdx.x) * (K / KC) + (k0 + KC * c) / KC;
+        a[c] = in ? *reinterpret_cast<const uint4 *>(W + (chunk * 64 + lane) * 8) : make_uint4(0, 0, 0, 0);
+      } else {
+        a[c] = (in && row_ok) ? *reinterpret_cast<const uint4 *>(wrow + k) : make_uint4(0, 0, 0, 0);
+      }
       b[c] = (in && col_ok) ? *reinterpret_cast<const uint4 *>(xrow + k) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
@@ -103,33 +112,47 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
 
 }  // namespace
 
-hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
-                             int64_t M, int64_t N, int64_t K, int epilogue, hipStream_t stream) {
-  // Waves per workgroup: up to K / 256 (a power of two <= 16 dividing K / 32).
-  int nw = 1;
-  while (nw < 16 && K / (2 * nw) >= 256 && K % (32 * 2 * nw) == 0) nw *= 2;
+int gemm_small_tile_rows(int64_t M, int64_t N) {
   // Half tiles where full ones would leave some of the GPU's 256 CUs idle
   // (measured: N = 2048 at K = 2048 / 8192 runs 1.2x / 1.6x faster in half
   // tiles, N = 6224 and 8192 at K = 2048 run slower).
-  const bool half = M <= 8 && (N + 15) / 16 < kGemmHalfBelow;
+  return M <= 8 && (N + 15) / 16 < kGemmHalfBelow ? 8 : 16;
+}
+
+hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
+                             int64_t M, int64_t N, int64_t K, int epilogue, bool packed, hipStream_t stream) {
+  const bool half = gemm_small_tile_rows(M, N) == 8;
+  // Waves per workgroup: up to K / 256 (a power of two <= 16 dividing K / 32;
+  // K / 64 for packed half tiles, whose chunks span 64 of K).
+  const int64_t kc = packed && half ? 64 : 32;
+  int nw = 1;
+  while (nw < 16 && K / (2 * nw) >= 256 && K % (kc * 2 * nw) == 0) nw *= 2;
   const dim3 grid(unsigned(half ? (N + 7) / 8 : (N + 15) / 16));
   const uint16_t *xp = static_cast<const uint16_t *>(x), *wp = static_cast<const uint16_t *>(w);
   uint16_t *yp = static_cast<uint16_t *>(y);
-#define KVM_GEMM(NWV, H)                                                                                 \
-  hipLaunchKernelGGL((k_gemm_small<NWV, H>), grid, dim3(NWV * 64), 0, stream, xp, x_st, wp, w_st, yp, y_st, \
+#define KVM_GEMM(NWV, H, P)                                                                                 \
+  hipLaunchKernelGGL((k_gemm_small<NWV, H, P>), grid, dim3(NWV * 64), 0, stream, xp, x_st, wp, w_st, yp, y_st, \
                      int(M), int(N), int(K), epilogue)
-#define KVM_GEMM_NW(H)            \
-  switch (nw) {                   \
-    case 1: KVM_GEMM(1, H); break;  \
-    case 2: KVM_GEMM(2, H); break;  \
-    case 4: KVM_GEMM(4, H); break;  \
-    case 8: KVM_GEMM(8, H); break;  \
-    default: KVM_GEMM(16, H); break; \
+#define KVM_GEMM_NW(H, P)            \
+  switch (nw) {                      \
+    case 1: KVM_GEMM(1, H, P); break;  \
+    case 2: KVM_GEMM(2, H, P); break;  \
+    case 4: KVM_GEMM(4, H, P); break;  \
+    case 8: KVM_GEMM(8, H, P); break;  \
+    default: KVM_GEMM(16, H, P); break; \
   }
   if (half) {
-    KVM_GEMM_NW(true)
+    if (packed) {
+      KVM_GEMM_NW(true, true)
+    } else {
+      KVM_GEMM_NW(true, false)
+    }
   } else {
-    KVM_GEMM_NW(false)
+    if (packed) {
+      KVM_GEMM_NW(false, true)
+    } else {
+      KVM_GEMM_NW(false, false)
+    }
   }
 #undef KVM_GEMM_NW
 #undef KVM_GEMM

@@ -231,8 +231,10 @@ hipError_t launch_state_backward(const StateBwdArgs &a, const UpdTable &sched, f
                                  hipStream_t stream);
 
 // Y[M, N] = X[M, K] W[N, K]^T, bf16, M <= 16, epilogue 1 = relu^2 (kvm_gemm.hip).
+// packed: w in the chunked layout of kvm_gemm_small_packed (w_st unused).
 hipError_t launch_gemm_small(const void *x, int64_t x_st, const void *w, int64_t w_st, void *y, int64_t y_st,
-                             int64_t M, int64_t N, int64_t K, int epilogue, hipStream_t stream);
+                             int64_t M, int64_t N, int64_t K, int epilogue, bool packed, hipStream_t stream);
+int gemm_small_tile_rows(int64_t M, int64_t N);
 // Residual add + LayerNorm + token shift of the decoder block (kvm_block.hip).
 hipError_t launch_add_norm(const kvm_add_norm_desc &P, hipStream_t stream);
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream);

@@ -170,6 +170,9 @@ SIGNATURES = {
     "kvm_relu_square": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "kvm_gemm_small": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "kvm_add_norm": (ctypes.c_int, [_P(KvmAddNormDesc), _vp]),
+    "kvm_gemm_small_tile_rows": (ctypes.c_int, [_i64, _i64]),
+    "kvm_gemm_small_packed": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
+                                             ctypes.c_int, _vp]),
     "kvm_state_append_direct": (ctypes.c_int, [_P(KvmLayer), _P(KvmSeq), _i64, _i64, _P(KvmState), _i64, _vp]),
     "kvm_state_refresh": (ctypes.c_int, [_P(KvmLayer), _P(KvmState), _i64, _i64, _vp]),
     "kvm_update_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),

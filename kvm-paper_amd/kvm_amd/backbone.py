@@ -610,6 +610,7 @@ class DecodeGraph:
         self.ids = self.pos = self.ctl = self.logits = None
         self.ctl_synced = False
         self.replays = self.eager_steps = 0
+        self.warmed = False  # the first plain step runs eagerly (lazy allocations, packed weights)
 
     def _kvm_caches(self):
         from .decode_cache import KVMDecodeCache
@@ -633,6 +634,9 @@ class DecodeGraph:
         pos = self.cache.get_seq_length(0)
         kv = self._kvm_caches()
         plain = bool(kv) and len(kv) == len(self.cache.layers) and all(c.graph_step_is_plain() for c in kv)
+        if plain and self.graph is None and not self.warmed:
+            self.warmed = True
+            plain = False
         if not plain:
             self.ctl_synced = False
             self.eager_steps += 1

@@ -8,6 +8,8 @@ CPU tensors) goes to ``torch.nn.functional.linear``.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 import torch.nn.functional as F
 
@@ -39,16 +41,67 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         x2 = x2.clone(memory_format=torch.contiguous_format)
         x_st = K
     N = int(weight.shape[0])
+    y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    lib = _lib.load()
+    rows = lib.kvm_gemm_small_tile_rows(M, N)
+    wp = _packed(weight, rows)
+    if wp is not None:
+        _lib.check(lib.kvm_gemm_small_packed(x2.data_ptr(), x_st, wp.data_ptr(), y.data_ptr(), N, M, N, K, rows,
+                                             int(relu_square), _lib.stream_handle(x.device)),
+                   "kvm_gemm_small_packed")
+        return y.view(*x.shape[:-1], N)
     w = weight
     w_st = K if N == 1 else int(w.stride(0))
     if w.stride(-1) != 1 or w_st % 8 or w_st < K or w.data_ptr() % 16:
         w = weight.clone(memory_format=torch.contiguous_format)
         w_st = K
-    y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
-    _lib.check(_lib.load().kvm_gemm_small(x2.data_ptr(), x_st, w.data_ptr(), w_st, y.data_ptr(), N,
-                                          M, N, K, int(relu_square), _lib.stream_handle(x.device)),
-               "kvm_gemm_small")
+    _lib.check(lib.kvm_gemm_small(x2.data_ptr(), x_st, w.data_ptr(), w_st, y.data_ptr(), N,
+                                  M, N, K, int(relu_square), _lib.stream_handle(x.device)), "kvm_gemm_small")
     return y.view(*x.shape[:-1], N)
+
+
+# Weights re-arranged for kvm_gemm_small_packed, per weight tensor (by id,
+# dropped when the tensor is freed) and tile height, rebuilt when the weight
+# changes (data pointer or version counter).
+_PACKS: dict[int, dict] = {}
+
+
+def _packed(weight: torch.Tensor, rows: int) -> torch.Tensor | None:
+    """``weight`` [N, K] in the chunk layout of kvm_gemm_small_packed for
+    ``rows``-row tiles (include/kvm_amd.h), made once per weight outside
+    graph capture; None where the layout does not apply (K not a multiple of
+    the chunk width), or while a graph is being captured and the weight has
+    no current pack (the plain kernel then runs)."""
+    N, K = (int(d) for d in weight.shape)
+    kc = 64 if rows == 8 else 32
+    if K % kc:
+        return None
+    entry = _PACKS.get(id(weight))
+    if entry is not None and entry["ref"]() is not weight:
+        entry = None
+    key = (weight.data_ptr(), weight._version)
+    if entry is not None and entry["key"] == key and rows in entry:
+        return entry[rows]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    if entry is None:
+        wid = id(weight)
+        entry = {"ref": weakref.ref(weight), "key": key}
+        _PACKS[wid] = entry
+        weakref.finalize(weight, _PACKS.pop, wid, None)
+    elif entry["key"] != key:
+        entry.clear()
+        entry.update(ref=weakref.ref(weight), key=key)
+    nb = -(-N // rows)
+    with torch.no_grad():
+        w = torch.zeros(nb * rows, K, device=weight.device, dtype=torch.bfloat16)
+        w[:N].copy_(weight)
+        if rows == 16:  # [b, i, s, g, e] -> [b, s, g, i, e]
+            p = w.view(nb, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4)
+        else:  # [b, j, c, h, g, e] -> [b, c, g, h, j, e]
+            p = w.view(nb, 8, K // 64, 2, 4, 8).permute(0, 2, 4, 3, 1, 5)
+        entry[rows] = p.contiguous().view(-1)
+    return entry[rows]
 
 
 def _relu_square(h: torch.Tensor) -> torch.Tensor:

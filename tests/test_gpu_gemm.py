@@ -54,3 +54,41 @@ def test_gemm_small_relu_square_epilogue(M, N, K):
         plain = torch.nn.functional.relu(linear(x, w)).square()
     assert torch.equal(fused, plain)
     assert bool((fused == 0).any()) and bool((fused > 0).any())
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 2048, 8192), (8, 6224, 2048), (3, 100, 384), (16, 300, 1152), (5, 2048, 64),
+                                   (8, 65536, 2048)])
+@pytest.mark.parametrize("epilogue", [0, 1])
+def test_gemm_small_packed_matches_plain(M, N, K, epilogue):
+    """kvm_gemm_small_packed (W re-arranged into per-load chunks) against
+    kvm_gemm_small on the same operands: bit-identical (same lanes, same
+    MFMA operands, same summation order)."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd import _lib
+    from kvm_amd.linear import _packed
+
+    T.log(f"[gemm] packed M{M} N{N} K{K} epilogue {epilogue}")
+    lib = _lib.load()
+    gen = torch.Generator(device=DEV).manual_seed(M + N + K)
+    x = torch.randn(M, K, device=DEV, generator=gen).bfloat16()
+    w = (torch.randn(N, K, device=DEV, generator=gen) / K ** 0.5).bfloat16()
+    rows = lib.kvm_gemm_small_tile_rows(M, N)
+    assert rows in (8, 16)
+    wp = _packed(w, rows)
+    if wp is None:
+        assert K % (64 if rows == 8 else 32)
+        pytest.skip("K does not fit the packed layout of this tile")
+    assert wp.numel() == -(-N // rows) * rows * K
+    st = _lib.stream_handle(x.device)
+    plain = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    packed = torch.empty_like(plain)
+    _lib.check(lib.kvm_gemm_small(x.data_ptr(), K, w.data_ptr(), K, plain.data_ptr(), N, M, N, K, epilogue, st),
+               "kvm_gemm_small")
+    _lib.check(lib.kvm_gemm_small_packed(x.data_ptr(), K, wp.data_ptr(), packed.data_ptr(), N, M, N, K, rows,
+                                         epilogue, st), "kvm_gemm_small_packed")
+    torch.cuda.synchronize()
+    assert torch.equal(plain, packed)
+    with pytest.raises(ValueError, match="packed for"):
+        _lib.check(lib.kvm_gemm_small_packed(x.data_ptr(), K, wp.data_ptr(), packed.data_ptr(), N, M, N, K,
+                                             24 - rows, epilogue, st), "kvm_gemm_small_packed")
