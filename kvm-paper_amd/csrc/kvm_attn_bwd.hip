@@ -486,6 +486,16 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
         }
         // P and dS (scaled by tau / sqrt(D)) in the B-operand layout of step hb:
         // lane holds queries qt*16 + 4*(lane/16) + i of key lane%16.
+        // Wave-uniform: every (query, key) pair of the step is visible (all 32
+        // queries valid, the wave's 16 keys valid and, in the window, at or
+        // before the first query and at or after the last query's window
+        // start), so no per-pair test is needed.
+        const int64_t kw = kb0 + wave * 16;
+        bool all_vis = 32 * hb + 32 <= nq && kw + 16 <= nkeys;
+        if (!SNAP) {
+          const int64_t qa = t0 + 32 * hb, qz = qa + 31;
+          all_vis = all_vis && kw + 15 <= qa && max(int64_t(0), (qz / C - n + 1) * int64_t(C)) <= kw;
+        }
         uint32_t pp[2][2], pd[2][2];
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2) {
@@ -496,11 +506,15 @@ void k_attn_bwd_dkdv(kvm_layer L, BwdArgs A, int kblocks, ChunkTable table) {
           float p[4], d[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int64_t t = t0 + qr + i;
-            bool vis = qr + i < nq && kp < nkeys;
-            if (!SNAP) {
-              const int64_t wbt = two_chunks ? (t < bnd ? wb0 : wb1) : max(int64_t(0), (t / C - n + 1) * int64_t(C));
-              vis = vis && kp <= t && wbt <= kp;
+            bool vis = true;
+            if (!all_vis) {
+              const int64_t t = t0 + qr + i;
+              vis = qr + i < nq && kp < nkeys;
+              if (!SNAP) {
+                const int64_t wbt =
+                    two_chunks ? (t < bnd ? wb0 : wb1) : max(int64_t(0), (t / C - n + 1) * int64_t(C));
+                vis = vis && kp <= t && wbt <= kp;
+              }
             }
             p[i] = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[q2][i], sc, -lv[i])) : 0.f;
             d[i] = p[i] * (dp[q2][i] - dv4[i]) * dsc;
