@@ -202,7 +202,11 @@ def bench_backward(args, torch, kvm_amd, pf):
     for p in mixer.parameters():
         p.requires_grad_(True)
 
+    params = [q, k, v, g, *mixer.parameters()]
+
     def step():
+        for t in params:  # zero_grad(set_to_none=True), as an optimizer step leaves them
+            t.grad = None
         y = training.prefill_with_grad(mixer, q, k, v, g)
         y.backward(dout)
 
