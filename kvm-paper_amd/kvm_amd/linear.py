@@ -8,6 +8,7 @@ CPU tensors) goes to ``torch.nn.functional.linear``.
 
 from __future__ import annotations
 
+import os
 import weakref
 
 import torch
@@ -69,12 +70,13 @@ _PACKS: dict[int, dict] = {}
 def _packed(weight: torch.Tensor, rows: int) -> torch.Tensor | None:
     """``weight`` [N, K] in the chunk layout of kvm_gemm_small_packed for
     ``rows``-row tiles (include/kvm_amd.h), made once per weight outside
-    graph capture; None where the layout does not apply (K not a multiple of
-    the chunk width), or while a graph is being captured and the weight has
-    no current pack (the plain kernel then runs)."""
+    graph capture (a second copy of every decode weight in HBM); None where
+    the layout does not apply (K not a multiple of the chunk width), while a
+    graph is being captured and the weight has no current pack, or with
+    KVM_AMD_PACK_WEIGHTS=0 (the plain kernel then runs)."""
     N, K = (int(d) for d in weight.shape)
     kc = 64 if rows == 8 else 32
-    if K % kc:
+    if K % kc or os.environ.get("KVM_AMD_PACK_WEIGHTS", "1") == "0":
         return None
     entry = _PACKS.get(id(weight))
     if entry is not None and entry["ref"]() is not weight:
