@@ -268,10 +268,25 @@ class SequenceMixer(nn.Module):
         ones = torch.ones(self.num_attention_heads, device=device, dtype=torch.float32)
         return ones, ones
 
+    def _fp32_params(self, device):
+        """fp32 copies of ln_s_k and the head temperatures (the kernels read
+        fp32), cached until one of the parameters is replaced or modified in
+        place (data pointer or version counter)."""
+        src = [self.ln_s_k.weight, self.ln_s_k.bias]
+        if self.config.kvm_use_head_temps:
+            src += [self.state_head_temp, self.front_head_temp]
+        key = tuple((p.data_ptr(), p._version, p.device) for p in src) + (str(device),)
+        cached = self.__dict__.get("_f32_cache")
+        if cached is None or cached[0] != key:
+            w = self.ln_s_k.weight.detach().float().contiguous()
+            b = self.ln_s_k.bias.detach().float().contiguous()
+            ts, tf = self._head_temperatures(device)
+            cached = (key, (w, b, ts, tf))
+            self.__dict__["_f32_cache"] = cached
+        return cached[1]
+
     def _layer_struct(self, batch: int, device, gate_initial: bool | None = None) -> _LayerHandle:
-        w = self.ln_s_k.weight.detach().float().contiguous()
-        b = self.ln_s_k.bias.detach().float().contiguous()
-        ts, tf = self._head_temperatures(device)
+        w, b, ts, tf = self._fp32_params(device)
         cfg = self.config
         gi = bool(cfg.kvm_apply_merge_gate_to_initial_state) if gate_initial is None else bool(gate_initial)
         s = _lib.KvmLayer(
