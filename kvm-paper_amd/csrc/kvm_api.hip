@@ -790,6 +790,7 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   };
 
   const size_t log_stride = size_t(L.batch * L.kv_heads) * size_t(C);
+  bool attn_rows_written = false;
   if (use_chain) {
     // Batches of consecutive updates, one persistent launch each.  A batch
     // [u, e) writes snapshots u+1..e into ring slots: every chunk reading a
@@ -821,6 +822,9 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
       }
       kvm::ChainPlan bp = cp;
       bp.fixed = !(fixed_env && fixed_env[0] == '0') && kvm::chain_fixed_ok(cp, cl, C);
+      // The fixed chain's last batch writes the final attention rows itself.
+      cl.final_rows = int32_t(bp.fixed && e == d->n_updates && d->state.s_k_attn && d->state.s_v_attn);
+      attn_rows_written = cl.final_rows != 0;
       KVM_HIP(kvm::launch_chain(L, d->kv, C, d->state, ring, cl, cs, bp, d->route_log,
                                 d->append_log, s),
               "state update chain");
@@ -855,8 +859,8 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   if ((rc = flush(d->n_updates + 1)) != KVM_OK) return rc;
   if ((rc = mark(3)) != KVM_OK) return rc;
 
-  // Final attention rows into the caller's state.
-  if (d->state.s_k_attn && d->state.s_v_attn) {
+  // Final attention rows into the caller's state (unless the chain wrote them).
+  if (d->state.s_k_attn && d->state.s_v_attn && !attn_rows_written) {
     const kvm::AttnRows last = snap_rows(d->n_updates);
     const size_t row_bytes = size_t(cur) * size_t(L.head_dim) * 2;
     const size_t dpitch = size_t(d->state.capacity) * size_t(L.head_dim) * 2;

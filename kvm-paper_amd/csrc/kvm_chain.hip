@@ -1118,7 +1118,11 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     }
   }
 
-  // ---- owned state back to the caller's arrays.
+  // ---- owned state back to the caller's arrays (and, after the last update
+  // of the prefill, its attention rows: the last snapshot's).
+  const bool attn_rows = list.final_rows != 0;
+  uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
+  uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
   for (int base = 0; base < nown; base += RPP) {
     const int l = base + tid / GL;
     if (l < nown) {
@@ -1127,6 +1131,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         const int64_t so = (srow + j) * D + part * 8;
         *reinterpret_cast<uint4 *>(s_k + so) = *reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]);
         *reinterpret_cast<uint4 *>(s_v + so) = *reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]);
+        if (attn_rows) {
+          *reinterpret_cast<uint4 *>(s_ka + so) = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
+          *reinterpret_cast<uint4 *>(s_va + so) = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
+        }
       }
     }
   }

@@ -88,6 +88,7 @@ constexpr int kChainMaxWorkgroups = 256;   // one 512-thread workgroup per CU
 struct ChainList {
   int32_t u0;     // update index of entry 0 (snapshot u0 -> u0 + 1, log offset)
   int32_t count;
+  int32_t final_rows;  // k_chain_fixed: also write the last snapshot's rows to the state's s_k_attn / s_v_attn
   int32_t tok_begin[kChainMax];
   int32_t state_before[kChainMax];
   int32_t n_append[kChainMax];
