@@ -35,8 +35,21 @@ struct Row {
   float v[NC][8];
 };
 
+// Every load of this file is issued without a branch around it (chunk
+// indices past the row's end are clamped, a NULL operand is replaced by a
+// valid one) and its value is selected where it is first used: a load whose
+// value is selected at a branch join makes the wave wait for it there, which
+// turns independent loads into one round trip each.
+__device__ __forceinline__ uint4 ld16(const void *base, int64_t chunk) {
+  return reinterpret_cast<const uint4 *>(base)[chunk];
+}
+__device__ __forceinline__ uint4 keep_if(bool in, uint4 v) {
+  return in ? v : make_uint4(0, 0, 0, 0);
+}
+
 // The per-channel parameters of a lane's chunks (packed bf16), loaded once
 // per wave before the first row so that their latency overlaps the rows'.
+// Chunks past the row's end hold a clamped chunk's values (never used).
 template <int NC>
 struct Params {
   uint4 w[NC], b[NC], mix[NC];
@@ -45,18 +58,18 @@ struct Params {
 template <int NC>
 __device__ __forceinline__ void load_params(const kvm_add_norm_desc &P, int lane, bool shift, Params<NC> &p) {
   const int nch = int(P.width / 8);
+  const void *mix = shift ? P.mix : P.ln_w;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    const int c = lane + 64 * j;
-    const bool in = c < nch;
-    p.w[j] = in ? reinterpret_cast<const uint4 *>(P.ln_w)[c] : make_uint4(0, 0, 0, 0);
-    p.b[j] = in ? reinterpret_cast<const uint4 *>(P.ln_b)[c] : make_uint4(0, 0, 0, 0);
-    p.mix[j] = in && shift ? reinterpret_cast<const uint4 *>(P.mix)[c] : make_uint4(0, 0, 0, 0);
+    const int c = min(lane + 64 * j, nch - 1);
+    p.w[j] = ld16(P.ln_w, c);
+    p.b[j] = ld16(P.ln_b, c);
+    p.mix[j] = ld16(mix, c);
   }
 }
 
-// The raw 16-byte chunks of row `r` (flat token index) of x and y; chunks
-// past the row's end read as zeros.
+// The raw 16-byte chunks of row `r` (flat token index) of x and y (y: x's
+// when there is none); chunks past the row's end hold a clamped chunk.
 template <int NC>
 struct Raw {
   uint4 x[NC], y[NC];
@@ -65,26 +78,29 @@ struct Raw {
 template <int NC>
 __device__ __forceinline__ void fetch_row(const kvm_add_norm_desc &P, int64_t r, int lane, Raw<NC> &raw) {
   const int nch = int(P.width / 8);
+  const void *y = P.y ? P.y : P.x;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    const int c = lane + 64 * j;
-    const int64_t e = r * (P.width / 8) + c;
-    raw.x[j] = c < nch ? reinterpret_cast<const uint4 *>(P.x)[e] : make_uint4(0, 0, 0, 0);
-    raw.y[j] = c < nch && P.y ? reinterpret_cast<const uint4 *>(P.y)[e] : make_uint4(0, 0, 0, 0);
+    const int64_t e = r * nch + min(lane + 64 * j, nch - 1);
+    raw.x[j] = ld16(P.x, e);
+    raw.y[j] = ld16(y, e);
   }
 }
 
 // Residual sum x + s * y of a fetched row (zeros past the row's end).
 template <int NC>
-__device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, const Raw<NC> &raw, Row<NC> &out) {
+__device__ __forceinline__ void residual_row(const kvm_add_norm_desc &P, int lane, const Raw<NC> &raw,
+                                             Row<NC> &out) {
   const float s = float(P.alpha);
+  const int nch = int(P.width / 8);
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
+    const bool in = lane + 64 * j < nch;
     float x[8];
-    unpack8(raw.x[j], x);
+    unpack8(keep_if(in, raw.x[j]), x);
     if (P.y) {
       float y[8];
-      unpack8(raw.y[j], y);
+      unpack8(keep_if(in, raw.y[j]), y);
 #pragma unroll
       for (int i = 0; i < 8; ++i) x[i] = P.round_product ? rbf(x[i] + rbf(y[i] * s)) : rbf(x[i] + s * y[i]);
     }
@@ -168,37 +184,33 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
   const bool shift = P.mix && P.out_shift;
   Params<NC> prm;
   load_params<NC>(P, lane, shift, prm);
+  const int64_t t_end = t0 + run < T ? t0 + run : T;
+  Raw<NC> next;  // the next row's loads are in flight while a row is processed
+  fetch_row<NC>(P, b * T + t0, lane, next);
   Row<NC> carry;  // normalised row of the token before the current one
   if (shift) {
     if (t0 > 0) {
       Raw<NC> raw;
       fetch_row<NC>(P, b * T + t0 - 1, lane, raw);
       Row<NC> x;
-      residual_row<NC>(P, raw, x);
+      residual_row<NC>(P, lane, raw, x);
       norm_row<NC>(P, lane, prm, x, carry);
     } else {
+      const void *prev = P.prev ? P.prev : P.x;
+      uint4 raw[NC];
 #pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const int c = lane + 64 * j;
-        if (P.prev && c < nch) {
-          load8(static_cast<const uint16_t *>(P.prev) + b * P.width + int64_t(c) * 8, carry.v[j]);
-        } else {
+      for (int j = 0; j < NC; ++j) raw[j] = ld16(prev, b * nch + min(lane + 64 * j, nch - 1));
 #pragma unroll
-          for (int i = 0; i < 8; ++i) carry.v[j][i] = 0.f;
-        }
-      }
+      for (int j = 0; j < NC; ++j) unpack8(keep_if(P.prev && lane + 64 * j < nch, raw[j]), carry.v[j]);
     }
   }
-  const int64_t t_end = t0 + run < T ? t0 + run : T;
-  Raw<NC> next;  // the next row's loads are in flight while a row is processed
-  fetch_row<NC>(P, b * T + t0, lane, next);
 #pragma unroll 1
   for (int64_t t = t0; t < t_end; ++t) {
     const int64_t r = b * T + t;
     const Raw<NC> cur = next;
     if (t + 1 < t_end) fetch_row<NC>(P, r + 1, lane, next);
     Row<NC> x, h;
-    residual_row<NC>(P, cur, x);
+    residual_row<NC>(P, lane, cur, x);
     if (P.out_x) store_row<NC>(P.out_x, r, P.width, lane, x);
     norm_row<NC>(P, lane, prm, x, h);
     if (P.out_h) store_row<NC>(P.out_h, r, P.width, lane, h);

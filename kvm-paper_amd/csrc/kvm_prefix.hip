@@ -27,30 +27,11 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ void load_row8(const void *base, int64_t elem, float (&x)[8]) {
-  load8(static_cast<const uint16_t *>(base) + elem, x);
-}
-
-__device__ __forceinline__ void param8(const void *p, int64_t elem, float (&x)[8]) {
-  load8(static_cast<const uint16_t *>(p) + elem, x);
-}
-
-__device__ __forceinline__ float param1(const void *p, int64_t elem) {
-  return bf2f(static_cast<const uint16_t *>(p)[elem]);
-}
-
 // The rows a value residual reads besides v: v_first and (modes 2 and 3)
-// gate_lin, both contiguous [B, T, width]; row_elem is the row's first
-// element of this lane's 8.
+// gate_lin, both contiguous [B, T, width].
 struct VRes {
   float vf[8], gl[8];
 };
-
-__device__ __forceinline__ void load_vres(int mode, const kvm_prefix_desc &P, int64_t row_elem, VRes &r) {
-  if (mode == 0) return;
-  load_row8(P.v_first, row_elem, r.vf);
-  if (mode >= 2) load_row8(P.gate_lin, row_elem, r.gl);
-}
 
 // value residual applied to one row (v in place).  g0: v_gate0 of the lane's
 // channels (modes 2, 3); lamb: the mixing weight (mode 1).
@@ -137,6 +118,15 @@ struct PassRaw {
   uint16_t kw;
 };
 
+// The value of a load, pinned where this is called: the compiler cannot sink
+// the load past this point (the wave waits here for it).
+__device__ __forceinline__ uint4 pinned(uint4 v) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t t = __builtin_bit_cast(u32x4_t, v);
+  asm volatile("" : "+v"(t));
+  return __builtin_bit_cast(uint4, t);
+}
+
 __device__ __forceinline__ uint4 raw8(const void *base, int64_t elem) {
   return *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + elem);
 }
@@ -184,34 +174,66 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
       r.v = raw8(P.v_lin, row * P.qkv_st + chan);
       if (mode != 0) r.vf = raw8(P.v_first, row * width + chan);
       if (mode >= 2) r.gl = raw8(P.gate_lin, row * width + chan);
-      if (P.key_weight && part == 0) r.kw = static_cast<const uint16_t *>(P.key_weight)[row * P.kw_st + hk];
+      // every lane loads the (b, t, kv head) weight; lane part 0 uses it
+      r.kw = static_cast<const uint16_t *>(P.key_weight ? P.key_weight : P.v_lin)[P.key_weight ? row * P.kw_st + hk : 0];
     }
   };
 
-  float wf[8], bfv[8], xmix[8], vmix[8], xcarry[8], vcarry[8], g0[8];
-  param8(is_q ? P.ln_q_w : P.ln_k_w, part * 8, wf);
-  param8(is_q ? P.ln_q_b : P.ln_k_b, part * 8, bfv);
-  if (!is_q && mode >= 2) param8(P.v_gate0, chan, g0);
-  const float lamb = !is_q && mode == 1 ? param1(P.lamb, 0) : 0.f;
+  // Prologue: the first pass's rows, then every parameter and predecessor
+  // row, all loaded before any of them is used and without branches around
+  // the loads (an unused or NULL operand reads a valid stand-in that is never
+  // used): a load whose value is consumed inside a branch makes the wave wait
+  // there, which would give every prologue load a round trip of its own.
+  PassRaw next;
+  fetch(0, next);
+  const void *ln_w = is_q ? P.ln_q_w : P.ln_k_w;
+  const int64_t own = part * 8;  // stand-in index: the lane's LayerNorm weights
+  const bool use_g0 = !is_q && mode >= 2, use_lamb = !is_q && mode == 1;
+  uint4 r_w = raw8(ln_w, own);
+  uint4 r_b = raw8(is_q ? P.ln_q_b : P.ln_k_b, own);
+  uint4 r_g0 = raw8(use_g0 ? P.v_gate0 : ln_w, use_g0 ? chan : own);
+  uint32_t r_lamb = static_cast<const uint16_t *>(use_lamb ? P.lamb : ln_w)[0];
   const void *x_prev = is_q ? P.q_prev : P.k_prev;
+  const bool vmix_on = shift && !is_q;
+  uint4 r_xmix = raw8(shift ? (is_q ? P.x_q : P.x_k) : ln_w, shift ? chan : own);
+  uint4 r_vmix = raw8(vmix_on ? P.x_v : ln_w, vmix_on ? chan : own);
+  // Predecessor of the tile's first token: the row before it (t0 > 0; for v
+  // with the inputs of a pre-shift value residual) or the carried rows.
+  const bool lin_pred = shift && t0 > 0;
+  const int64_t rp = bi * T + t0 - 1;
+  const bool xc_on = lin_pred || (shift && x_prev);
+  const bool vc_on = !is_q && (lin_pred || (shift && P.v_prev));
+  const bool vres_on = lin_pred && !is_q && pre;
+  uint4 r_xc = raw8(!xc_on ? ln_w : lin_pred ? (is_q ? P.q_lin : P.k_lin) : x_prev,
+                    !xc_on ? own : lin_pred ? rp * P.qkv_st + chan : bi * width + chan);
+  uint4 r_vc = raw8(!vc_on ? ln_w : lin_pred ? P.v_lin : P.v_prev,
+                    !vc_on ? own : lin_pred ? rp * P.qkv_st + chan : bi * width + chan);
+  uint4 r_vf = raw8(vres_on ? P.v_first : ln_w, vres_on ? rp * width + chan : own);
+  uint4 r_gl = raw8(vres_on && mode >= 2 ? P.gate_lin : ln_w, vres_on && mode >= 2 ? rp * width + chan : own);
+  // Every prologue value pinned here: the compiler cannot sink a load into
+  // the branch that uses its value, and the wave waits once for all of them.
+  // ring counters of a graph-replayed decode step (start, length)
+  const int32_t *ctl = P.ring_ctl ? P.ring_ctl : static_cast<const int32_t *>(ln_w);
+  int32_t ctl_start = ctl[1], ctl_len = ctl[2];
+  for (uint4 *r : {&r_w, &r_b, &r_g0, &r_xmix, &r_vmix, &r_xc, &r_vc, &r_vf, &r_gl}) *r = pinned(*r);
+  asm volatile("" : "+v"(r_lamb), "+v"(ctl_start), "+v"(ctl_len));
+
+  float wf[8], bfv[8], xmix[8], vmix[8], xcarry[8], vcarry[8], g0[8];
+  unpack8(r_w, wf);
+  unpack8(r_b, bfv);
+  unpack8(r_g0, g0);
+  const float lamb = use_lamb ? bf2f(r_lamb) : 0.f;
   if (shift) {
-    param8(is_q ? P.x_q : P.x_k, chan, xmix);
-    if (!is_q) param8(P.x_v, chan, vmix);
-    // predecessor of the tile's first token
-    if (t0 > 0) {
-      const int64_t rp = bi * T + t0 - 1;
-      load_row8(is_q ? P.q_lin : P.k_lin, rp * P.qkv_st + chan, xcarry);
-      if (!is_q) {
-        load_row8(P.v_lin, rp * P.qkv_st + chan, vcarry);
-        if (pre) {
-          VRes vr;
-          load_vres(mode, P, rp * width + chan, vr);
-          value_residual(mode, vcarry, vr, g0, lamb);
-        }
-      }
-    } else {
-      if (x_prev) load_row8(x_prev, bi * width + chan, xcarry);
-      if (!is_q && P.v_prev) load_row8(P.v_prev, bi * width + chan, vcarry);
+    unpack8(r_xmix, xmix);
+    unpack8(r_vmix, vmix);
+    // (no carried row at t0 == 0: the "first" fallback in the first pass)
+    unpack8(r_xc, xcarry);
+    unpack8(r_vc, vcarry);
+    if (vres_on) {
+      VRes vr;
+      unpack8(r_vf, vr.vf);
+      unpack8(r_gl, vr.gl);
+      value_residual(mode, vcarry, vr, g0, lamb);
     }
   }
   // Window-ring row of a single decode token (kv heads).
@@ -221,8 +243,8 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
     int64_t pos = P.ring_pos;
     if (P.ring_ctl) {
       const int64_t cap = P.ring_cap;
-      const int64_t start = ((int64_t(P.ring_ctl[1]) % cap) + cap) % cap;
-      const int64_t len = min(max(int64_t(P.ring_ctl[2]), int64_t(0)), cap);
+      const int64_t start = ((int64_t(ctl_start) % cap) + cap) % cap;
+      const int64_t len = min(max(int64_t(ctl_len), int64_t(0)), cap);
       pos = (start + len) % cap;
     }
     ring_o = (bi * Hkv + hk) * P.ring_cap + pos;
@@ -230,8 +252,6 @@ __global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
   uint16_t *x_out = static_cast<uint16_t *>(is_q ? P.q_out : P.k_out);
   uint16_t *x_last = static_cast<uint16_t *>(is_q ? P.q_last_out : P.k_last_out);
 
-  PassRaw next;
-  fetch(0, next);
 #pragma unroll 1
   for (int ps = 0; ps < npass; ++ps) {
     const PassRaw cur = next;
