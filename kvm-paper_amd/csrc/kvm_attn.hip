@@ -66,22 +66,27 @@ constexpr float kRescaleSlack = 8.0f;
 
 // S^T tiles of the 64 keys of a buffered block: s[kt][rt], kt = 16-key
 // tile, rt = 16-query tile.  kbuf + kb addresses key lane&15, dims
-// 8*(lane>>4).. of column group 0.
+// 8*(lane>>4).. of column group 0.  The k-step loop is outermost, so eight
+// independent accumulations are in flight between dependent MFMAs (each
+// tile still sums its k-steps in order 0, 1, ...).
 template <int D>
 __device__ __forceinline__ void score_block(const unsigned char *kbuf, const bf16x8 (&qf)[2][D / 32],
                                             f32x4 (&s)[4][2]) {
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
-    bf16x8 kf[D / 32];
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks)
-      kf[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(kbuf + ks * 4096 + kt * 1024));
     s[kt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-      s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[0][ks], s[kt][0], 0, 0, 0);
-      s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[1][ks], s[kt][1], 0, 0, 0);
+  for (int ks = 0; ks < D / 32; ++ks) {
+    bf16x8 kf[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+      kf[kt] = as_bf16x8(*reinterpret_cast<const uint4 *>(kbuf + ks * 4096 + kt * 1024));
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt], qf[0][ks], s[kt][0], 0, 0, 0);
+      s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt], qf[1][ks], s[kt][1], 0, 0, 0);
     }
   }
 }
