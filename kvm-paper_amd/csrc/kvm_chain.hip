@@ -1064,13 +1064,20 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
               &own_k[(lt + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]);
         // Only a block holding sink slots or slots >= S needs the mask.
         const bool masked = jb < protect || jb + 16 > S;
+        // k-steps outermost: the four token tiles' accumulations interleave
+        // (each still sums its k-steps in order).
+        f32x4 accs[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) accs[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            accs[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]),
+                                                               accs[tt], 0, 0, 0);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]), acc,
-                                                          0, 0, 0);
+          const f32x4 acc = accs[tt];
           if (masked) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {

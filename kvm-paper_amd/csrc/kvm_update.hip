@@ -254,12 +254,17 @@ __global__ __launch_bounds__(kThreads) void k_route(
     for (int ks = 0; ks < KS; ++ks)
       bx[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(
           &tok_lds[(tt * 16 + (lane & 15)) * STR + ks * 32 + (lane >> 4) * 8]));
+    // Both 16-slot tiles' accumulations interleave (each sums its k-steps
+    // in order); the tiles are then scanned in slot order.
+    f32x4 accs[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        accs[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a_reg[st][ks]), bx[ks], accs[st], 0, 0, 0);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a_reg[st][ks]), bx[ks], acc, 0, 0, 0);
+      const f32x4 acc = accs[st];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = jw + st * 16 + (lane >> 4) * 4 + i;
