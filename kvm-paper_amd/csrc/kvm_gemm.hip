@@ -8,9 +8,9 @@
 // A workgroup owns 16 rows of W (16 outputs per token; 8 in the half tiles
 // described below, for narrow W and M <= 8) and its NW waves split
 // K evenly; NW (1 to 16) is the largest power of two leaving each wave at
-// least 256 of K.  A wave issues the loads of up to 16 k-steps (8 at 16 waves)
-// before their MFMAs: 16 bytes per lane, lanes 0-15 / 16-31 / ... covering 64
-// contiguous bytes of each row; v_mfma_f32_16x16x32_bf16 takes W rows as the A
+// least 256 of K.  A wave issues the loads of 256 of K before their MFMAs:
+// 16 bytes per lane, lanes 0-15 / 16-31 / ... covering 64 contiguous bytes
+// of each row; v_mfma_f32_16x16x32_bf16 takes W rows as the A
 // operand and the tokens' X rows as the B operand (columns >= M read zero).
 // The per-wave partial tiles are summed in wave order through LDS, so the
 // result does not depend on timing.
@@ -21,10 +21,12 @@
 namespace kvm {
 namespace {
 
-// Loads per lane in flight together: 16, or 8 at 16 waves, where 1024
-// threads leave a lane 128 registers.
-template <int NW>
-constexpr int kSteps = NW == 16 ? 8 : 16;
+// Load steps per lane in flight together: 256 of K per wave (8 full-tile
+// steps of 32, 4 half-tile steps of 64), the share of K a wave gets in the
+// usual shapes (NW is chosen to leave each wave at least 256), so that no
+// MFMA of a dead step sits in the wave's dependent accumulation chain.
+template <bool HALF>
+constexpr int kSteps = HALF ? 4 : 8;
 
 constexpr int kGemmHalfBelow = 256;  // full 16-row tiles from this many on
 
@@ -69,10 +71,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
   const uint16_t *wrow = W + int64_t(row_ok ? n0 + jr : 0) * w_st + g * 8;
   const uint16_t *xrow = X + int64_t(col_ok ? jr : 0) * x_st + g * 8;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = kb; k0 < ke; k0 += KC * kSteps<NW>) {
-    uint4 a[kSteps<NW>], b[kSteps<NW>];
+  for (int k0 = kb; k0 < ke; k0 += KC * kSteps<HALF>) {
+    uint4 a[kSteps<HALF>], b[kSteps<HALF>];
 #pragma unroll
-    for (int c = 0; c < kSteps<NW>; ++c) {
+    for (int c = 0; c < kSteps<HALF>; ++c) {
       const int k = k0 + KC * c + kk;
       const bool in = k < ke;
       if constexpr (PACKED) {
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_small(const uint16_t *__restri
       b[c] = (in && col_ok) ? *reinterpret_cast<const uint4 *>(xrow + k) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int c = 0; c < kSteps<NW>; ++c) {
+    for (int c = 0; c < kSteps<HALF>; ++c) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[c]), as_bf16x8(b[c]), acc, 0, 0, 0);
       if constexpr (HALF)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(swap_half_rows(a[c])),
