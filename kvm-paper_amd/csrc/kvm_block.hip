@@ -187,21 +187,24 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
   const int64_t t_end = t0 + run < T ? t0 + run : T;
   Raw<NC> next;  // the next row's loads are in flight while a row is processed
   fetch_row<NC>(P, b * T + t0, lane, next);
-  Row<NC> carry;  // normalised row of the token before the current one
+  // Normalised row of the token before the current one, packed (its values
+  // are bf16 already): half the registers of the float row.
+  uint4 carry[NC];
   if (shift) {
     if (t0 > 0) {
       Raw<NC> raw;
       fetch_row<NC>(P, b * T + t0 - 1, lane, raw);
-      Row<NC> x;
+      Row<NC> x, h;
       residual_row<NC>(P, lane, raw, x);
-      norm_row<NC>(P, lane, prm, x, carry);
+      norm_row<NC>(P, lane, prm, x, h);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) carry[j] = pack8(h.v[j]);
     } else {
       const void *prev = P.prev ? P.prev : P.x;
-      uint4 raw[NC];
 #pragma unroll
-      for (int j = 0; j < NC; ++j) raw[j] = ld16(prev, b * nch + min(lane + 64 * j, nch - 1));
+      for (int j = 0; j < NC; ++j) carry[j] = ld16(prev, b * nch + min(lane + 64 * j, nch - 1));
 #pragma unroll
-      for (int j = 0; j < NC; ++j) unpack8(keep_if(P.prev && lane + 64 * j < nch, raw[j]), carry.v[j]);
+      for (int j = 0; j < NC; ++j) carry[j] = keep_if(P.prev && lane + 64 * j < nch, carry[j]);
     }
   }
 #pragma unroll 1
@@ -220,14 +223,15 @@ __global__ __launch_bounds__(256) void k_add_norm(kvm_add_norm_desc P, int run) 
       for (int j = 0; j < NC; ++j) {
         const int c = lane + 64 * j;
         if (c < nch) {
-          float m[8], o[8];
+          float m[8], cv[8], o[8];
           unpack8(prm.mix[j], m);
+          unpack8(carry[j], cv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = rbf(h.v[j][i] + rbf(m[i] * rbf(carry.v[j][i] - h.v[j][i])));
+          for (int i = 0; i < 8; ++i) o[i] = rbf(h.v[j][i] + rbf(m[i] * rbf(cv[i] - h.v[j][i])));
           store8(static_cast<uint16_t *>(P.out_shift) + r * P.width + int64_t(c) * 8, o);
         }
+        carry[j] = pack8(h.v[j]);
       }
-      carry = h;
     }
   }
 }
