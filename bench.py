@@ -417,7 +417,7 @@ def cpu_baseline(torch, sample_T):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--cpu-sample", type=int, default=32768,

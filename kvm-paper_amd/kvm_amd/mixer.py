@@ -24,6 +24,7 @@ import argparse
 import ctypes
 import math
 import os
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -101,6 +102,23 @@ class _LayerHandle:
 
     def ref(self):
         return ctypes.byref(self.struct)
+
+
+# The schedule's int32 arrays of a plan as ctypes arrays, made once per plan
+# object (a prefill loop that passes one plan pays the conversion once).
+_PLAN_ARRAYS: dict[int, tuple] = {}
+
+
+def _plan_arrays(plan: PrefillPlan) -> list:
+    hit = _PLAN_ARRAYS.get(id(plan))
+    if hit is not None and hit[0]() is plan:
+        return hit[1]
+    arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin,
+                                           plan.upd_state_before, plan.upd_n_append)]
+    pid = id(plan)
+    _PLAN_ARRAYS[pid] = (weakref.ref(plan), arrs)
+    weakref.finalize(plan, _PLAN_ARRAYS.pop, pid, None)
+    return arrs
 
 
 class SequenceMixer(nn.Module):
@@ -650,8 +668,7 @@ class SequenceMixer(nn.Module):
             extra["snap_v"] = torch.empty(shape, **bf)
         if want_lse:
             extra["lse"] = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
-        arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin,
-                                               plan.upd_state_before, plan.upd_n_append)]
+        arrs = _plan_arrays(plan)
         d = _lib.KvmPrefillDesc()
         d.layer = layer.struct
         d.q, d.q_sb, d.q_sh, d.q_st = qv.data_ptr(), qv.stride(0), qv.stride(1), qv.stride(2)
