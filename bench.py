@@ -268,10 +268,12 @@ def bench_decode(args, torch, kvm_amd):
         ea = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         for i in range(steps):
             ev[i][0].record()
-            mixer._decode_advance(ks[i], vs[i], gs[i], cache)
+            # The token's ring row is written by the attention launch
+            # (kvm_decode_step), as in the mixer's own decode step.
+            fresh = mixer._decode_advance(ks[i], vs[i], gs[i], cache, defer_ring_write=True)
             if inner:
                 ea[i][0].record()
-            mixer._decode_attention(qs[i], cache)
+            mixer._decode_attention(qs[i], cache, fresh)
             if inner:
                 ea[i][1].record()
             ev[i][1].record()
@@ -287,13 +289,14 @@ def bench_decode(args, torch, kvm_amd):
     attn_ms = [a.elapsed_time(b) for a, b in ea]
     total_ms = sum(step_ms)
     rows = B * H
-    # Algorithmic bytes per attention launch: each key and value row read once.
+    # Algorithmic bytes per attention launch: each key and value row read
+    # once, q read and out written, and the token's ring row (k, v, gate) written.
     active = S
     bytes_per = []
     for i in range(steps):
         t = total + 1 + i
         rb = max(0, (t + C - 1) // C * C - W)
-        bytes_per.append(rows * (active + (t - rb)) * (2 * D) * 2 + 2 * rows * D * 2)
+        bytes_per.append(rows * (active + (t - rb)) * (2 * D) * 2 + 2 * rows * D * 2 + rows * (2 * D + 1) * 2)
     return dict(
         ms_per_step=total_ms / steps, tok_s=B * steps / (total_ms * 1e-3), attn_ms=sum(attn_ms) / steps,
         bytes=sum(bytes_per) / steps, update_step_ms=step_ms[0], other_step_ms=sum(step_ms[1:]) / max(steps - 1, 1),

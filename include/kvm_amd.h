@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 10
+#define KVM_ABI_VERSION 11
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -446,6 +446,22 @@ int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
                          int64_t ring_start, int64_t recent_len, void *out,
                          int64_t o_sb, int64_t o_sh, void *workspace,
                          int64_t workspace_bytes, void *stream);
+
+/* One decode step's ring write and attention in the launches of
+ * kvm_decode_attention: the same result as kvm_ring_write(layer, src, ring_k,
+ * ring_v, ring_gate, ring_cap, (ring_start + recent_len - 1) % ring_cap)
+ * followed by kvm_decode_attention with these arguments.  recent_len counts
+ * the step's token (src, one token, not a ring) as the last window row; the
+ * attention reads it from src and the combine launch stores its k, v and
+ * merge gate in the ring.
+ * Replaces the ring write + attention of one decode token
+ * (write_recent_ring + kvm_decode_attention, model/kernels/kvm_triton_decode.py:18-70,
+ * 287-322, 175-284, 409-467). */
+int kvm_decode_step(const kvm_layer *layer, const void *q, int64_t q_sb, int64_t q_sh,
+                    const kvm_state *st, int64_t active_state_len, const kvm_seq *src,
+                    void *ring_k, void *ring_v, void *ring_gate, int64_t ring_cap,
+                    int64_t ring_start, int64_t recent_len, void *out, int64_t o_sb,
+                    int64_t o_sh, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Decode with the step counters in device memory, so that a decode step can
  * be captured once in a HIP graph and replayed (the kernels read the counters

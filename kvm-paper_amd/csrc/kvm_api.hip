@@ -626,6 +626,37 @@ int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
   return KVM_OK;
 }
 
+int kvm_decode_step(const kvm_layer *layer, const void *q, int64_t q_sb, int64_t q_sh,
+                    const kvm_state *st, int64_t active_state_len, const kvm_seq *src,
+                    void *ring_k, void *ring_v, void *ring_gate, int64_t ring_cap,
+                    int64_t ring_start, int64_t recent_len, void *out, int64_t o_sb,
+                    int64_t o_sh, void *workspace, int64_t workspace_bytes, void *stream) {
+  int rc;
+  if ((rc = check_seq(src, "src"))) return rc;
+  if (src->ring != 0) return fail(KVM_EINVAL, "the step's token cannot come from a ring");
+  if (!ring_gate) return fail(KVM_EINVAL, "ring_gate must be set");
+  if (recent_len < 1) return fail(KVM_EINVAL, "the step's token must be the last window row");
+  if ((rc = check_layer(layer)) || (rc = check_state(st, true))) return rc;
+  if (!q || !aligned16(q) || q_sb % 8 || q_sh % 8)
+    return fail(KVM_EINVAL, "q must be 16-byte aligned with strides multiple of 8");
+  if (!out) return fail(KVM_EINVAL, "out must be set");
+  if (!ring_k || !ring_v || !aligned16(ring_k) || !aligned16(ring_v) || ring_cap < 1)
+    return fail(KVM_EINVAL, "ring buffers must be set and 16-byte aligned");
+  if (active_state_len < 0 || active_state_len > st->capacity)
+    return fail(KVM_EINVAL, "active state length outside the state capacity");
+  if (recent_len > ring_cap || ring_start < 0 || ring_start >= ring_cap)
+    return fail(KVM_EINVAL, "recent window outside the ring");
+  const int64_t need = kvm::decode_workspace_bytes(*layer, active_state_len + recent_len);
+  if (!workspace || workspace_bytes < need)
+    return fail(KVM_ESPACE, "decode workspace of %lld bytes is smaller than %lld",
+                (long long)workspace_bytes, (long long)need);
+  KVM_HIP(kvm::launch_decode(*layer, q, q_sb, q_sh, *st, active_state_len, ring_k, ring_v,
+                             ring_cap, ring_start, recent_len, out, o_sb, o_sh, workspace,
+                             as_stream(stream), nullptr, 0, 0, src, ring_gate),
+          "kvm_decode_step");
+  return KVM_OK;
+}
+
 int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   if (!d) return fail(KVM_EINVAL, "prefill descriptor is NULL");
   int rc;

@@ -155,7 +155,8 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
                          int64_t ring_cap, int64_t ring_start,
                          int64_t recent_len, void *out, int64_t o_sb,
                          int64_t o_sh, void *workspace, hipStream_t stream,
-                         const int32_t *ctl = nullptr, int pending = 0, int64_t max_rows = 0);
+                         const int32_t *ctl = nullptr, int pending = 0, int64_t max_rows = 0,
+                         const kvm_seq *fresh = nullptr, void *ring_gate = nullptr);
 hipError_t launch_decode_advance(int32_t *ctl, int64_t n, hipStream_t stream);
 
 // Per-launch table of the query chunks an attention launch covers.

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -182,6 +182,8 @@ SIGNATURES = {
     "kvm_decode_workspace_bytes": (_i64, [_P(KvmLayer), _i64]),
     "kvm_decode_attention": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _i64, _vp, _vp,
                                             _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "kvm_decode_step": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _i64, _P(KvmSeq), _vp, _vp,
+                                       _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "kvm_decode_attention_noalloc": (ctypes.c_int, [_P(KvmLayer), _vp, _i64, _i64, _P(KvmState), _i64, _vp,
                                                     _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp]),
 }

@@ -199,9 +199,13 @@ class KVMDecodeCache:
         self.append_by_token.zero_()
 
     def append_recent_(self, new_k: torch.Tensor, new_v: torch.Tensor, new_gate: torch.Tensor, *,
-                       total_len: int, recent_begin: int) -> None:
+                       total_len: int, recent_begin: int, defer_write: bool = False) -> bool:
         """Slide the window to start at ``recent_begin`` and write the new
-        token (k, v, gate of one token) behind its last row."""
+        token (k, v, gate of one token) behind its last row.  With
+        ``defer_write`` the ring row is left unwritten where the next launch
+        can write it instead (host counters, row not written yet): the caller
+        must then pass the token to ``kvm_decode_step`` before anything else
+        reads the ring.  Returns whether the write was deferred."""
         slide = int(recent_begin) - self.recent_begin
         if not 0 <= slide <= self.recent_len:
             raise AssertionError("invalid recent-window transition")
@@ -210,9 +214,12 @@ class KVMDecodeCache:
             raise AssertionError("recent ring append would exceed capacity")
         W = self.ring_capacity
         head = (self.recent_start + slide) % W
-        self._write_window_row(new_k, new_v, new_gate, (head + kept) % W)
+        deferred = defer_write and self.graph_ctl is None and not self.ring_row_written
+        if not deferred:
+            self._write_window_row(new_k, new_v, new_gate, (head + kept) % W)
         self.recent_start, self.recent_len = head, kept + 1
         self.total_len, self.recent_begin = int(total_len), int(recent_begin)
+        return deferred
 
     def _write_window_row(self, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor, row: int) -> None:
         if self.ring_row_written:  # written by the prefix kernel of this captured step

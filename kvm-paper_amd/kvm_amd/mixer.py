@@ -783,13 +783,18 @@ class SequenceMixer(nn.Module):
 
     def _decode_one_token(self, q, k, v, merge_gate, decode_cache: KVMDecodeCache) -> torch.Tensor:
         """Advance ``decode_cache`` by one post-QKV token and attend (model/kvm_triton_mixer.py:717-757)."""
-        self._decode_advance(k, v, merge_gate, decode_cache)
-        return self._decode_attention(q, decode_cache)
+        fresh = self._decode_advance(k, v, merge_gate, decode_cache, defer_ring_write=True)
+        return self._decode_attention(q, decode_cache, fresh)
 
-    def _decode_advance(self, k, v, merge_gate, decode_cache: KVMDecodeCache) -> None:
+    def _decode_advance(self, k, v, merge_gate, decode_cache: KVMDecodeCache, *,
+                        defer_ring_write: bool = False):
         """Cache bookkeeping of one decode token: direct-state append while the
         prompt is shorter than a chunk, the state update when the window
-        crosses a chunk boundary, and the ring write."""
+        crosses a chunk boundary, and the ring write.  With
+        ``defer_ring_write`` (and KVM_AMD_FUSED_RING_WRITE not 0) the ring
+        write may be left to the attention launch: the return value is then
+        the token's (k, v, gate) to hand to :meth:`_decode_attention`, which
+        must come next; None when the row was written here."""
         if int(k.size(2)) != 1:
             raise ValueError("HIP KVM decode cache update accepts one token")
         c = decode_cache
@@ -817,7 +822,10 @@ class SequenceMixer(nn.Module):
                 raise AssertionError("decode crossed more than one state boundary")
             self._run_decode_state_update(c)
             c.state_coverage_len = new_cov
-        c.append_recent_(k, v, merge_gate, total_len=new_total, recent_begin=new_begin)
+        defer = defer_ring_write and os.environ.get("KVM_AMD_FUSED_RING_WRITE", "1") != "0"
+        if c.append_recent_(k, v, merge_gate, total_len=new_total, recent_begin=new_begin, defer_write=defer):
+            return (k, v, merge_gate)
+        return None
 
     def _run_decode_state_update(self, c: KVMDecodeCache) -> None:
         """Fold the oldest window chunk into the state (model/kvm_triton_mixer.py:759-864;
@@ -838,11 +846,25 @@ class SequenceMixer(nn.Module):
         c.state_len = cur + n_app
         c.update_count += 1
 
-    def _decode_attention(self, q: torch.Tensor, c: KVMDecodeCache) -> torch.Tensor:
-        """Attention of one query over the state and the window ring (model/kvm_triton_mixer.py:902-929)."""
+    def _decode_attention(self, q: torch.Tensor, c: KVMDecodeCache, fresh=None) -> torch.Tensor:
+        """Attention of one query over the state and the window ring
+        (model/kvm_triton_mixer.py:902-929); ``fresh`` is the deferred ring
+        row of :meth:`_decode_advance`, written by this launch (kvm_decode_step)."""
         active = c.state_len if c.total_len > c.ring_capacity else 0
         qv = _lib._bf16_view(q, "q")
         lib = _lib.load()
+        if fresh is not None:
+            if c.graph_ctl is not None:
+                raise AssertionError("a deferred ring row cannot be written under graph capture")
+            seq, keep = _lib.seq4(*fresh)
+            _lib.check(lib.kvm_decode_step(
+                c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), active, seq,
+                c.recent_k.data_ptr(), c.recent_v.data_ptr(), c.recent_gate.data_ptr(), c.ring_capacity,
+                c.recent_start, c.recent_len, c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+                c.decode_workspace.data_ptr(), c.decode_workspace.numel(), _lib.stream_handle(c.device)),
+                "kvm_decode_step")
+            del keep
+            return c.out
         if c.graph_ctl is not None:  # capture of a graph step: counters from device memory
             _lib.check(lib.kvm_decode_attention_dev(
                 c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), c.graph_ctl, 1,

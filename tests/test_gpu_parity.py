@@ -537,6 +537,79 @@ def test_decode_attention_exact(lib, B, Hq, Hkv, D, S, R, W, start):
     T.log(f"[decode-exact] max {mx:.2e} mean {mean:.2e}")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,D,S,R,W,start", [
+    (4, 8, 8, 128, 1000, 300, 512, 400),
+    (2, 8, 2, 64, 37, 120, 128, 100),
+    (3, 4, 4, 128, 0, 60, 64, 10),
+    (2, 16, 4, 128, 0, 1, 64, 63),
+])
+def test_decode_step_matches_write_then_attend(lib, B, Hq, Hkv, D, S, R, W, start):
+    """kvm_decode_step (ring write folded into the attention launches) gives
+    the output and ring contents of kvm_ring_write + kvm_decode_attention,
+    bit for bit; the token's row is the last of the R window rows."""
+    from kvm_amd import _lib
+
+    T.log(f"[decode-step] B{B} Hq{Hq} Hkv{Hkv} D{D} S{S} R{R} W{W} start{start}")
+    gen = torch.Generator().manual_seed(5)
+    rows = B * Hkv
+    cap = max(S, 1) + 5
+    t = dict(ka=torch.randn(rows, cap, D, generator=gen), va=0.5 * torch.randn(rows, cap, D, generator=gen),
+             rk=torch.randn(rows, W, D, generator=gen), rv=torch.randn(rows, W, D, generator=gen),
+             rg=1 + torch.rand(rows, W, generator=gen),
+             q=torch.randn(B, Hq, 1, D, generator=gen) / math.sqrt(D),
+             nk=torch.randn(B, Hkv, 1, D, generator=gen), nv=torch.randn(B, Hkv, 1, D, generator=gen),
+             ng=1 + torch.rand(B, Hkv, 1, 1, generator=gen))
+    dev = {n: x.bfloat16().to(DEV) for n, x in t.items()}
+    cfg = T.mixer_config(Hq, Hkv, D, 64)
+    m = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), 1 + 0.2 * torch.randn(Hq, generator=gen),
+                     1 + 0.2 * torch.randn(Hq, generator=gen))
+    layer = m._layer_struct(B, torch.device(DEV))
+    st = _lib.state_struct(dev["ka"], dev["va"], dev["va"][:, :, :1].contiguous(), dev["ka"], dev["va"], cap)
+    seq, keep = _lib.seq4(dev["nk"], dev["nv"], dev["ng"])
+    nws = int(lib.kvm_decode_workspace_bytes(layer.ref(), S + R))
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    q = dev["q"]
+    res = {}
+    for fused in (False, True):
+        rk, rv, rg = dev["rk"].clone(), dev["rv"].clone(), dev["rg"].clone()
+        out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=DEV)
+        if fused:
+            _lib.check(lib.kvm_decode_step(layer.ref(), q.data_ptr(), q.stride(0), q.stride(1), st, S, seq,
+                                           rk.data_ptr(), rv.data_ptr(), rg.data_ptr(), W, start, R, out.data_ptr(),
+                                           out.stride(0), out.stride(1), ws.data_ptr(), nws, 0), "decode step")
+        else:
+            _lib.check(lib.kvm_ring_write(layer.ref(), seq, rk.data_ptr(), rv.data_ptr(), rg.data_ptr(), W,
+                                          (start + R - 1) % W, 0), "ring write")
+            _lib.check(lib.kvm_decode_attention(layer.ref(), q.data_ptr(), q.stride(0), q.stride(1), st, S,
+                                                rk.data_ptr(), rv.data_ptr(), W, start, R, out.data_ptr(),
+                                                out.stride(0), out.stride(1), ws.data_ptr(), nws, 0), "decode")
+        torch.cuda.synchronize()
+        res[fused] = [x.cpu() for x in (out, rk, rv, rg)]
+    del keep
+    for name, a, b in zip(("out", "ring_k", "ring_v", "ring_gate"), res[False], res[True]):
+        assert torch.equal(a, b), f"decode step {name} differs from ring write + attention"
+    pos = (start + R - 1) % W
+    assert torch.equal(res[True][1][:, pos], t["nk"].bfloat16().reshape(rows, D))
+    T.log("[decode-step] output and ring bit-identical")
+
+
+def test_decode_step_rejects_bad_window(lib):
+    """kvm_decode_step refuses an empty window (the token must be its last row)."""
+    from kvm_amd import _lib
+
+    cfg = T.mixer_config(4, 4, 64, 64)
+    m = T.make_mixer(cfg, torch.ones(64), torch.zeros(64), torch.ones(4), torch.ones(4))
+    layer = m._layer_struct(1, torch.device(DEV))
+    x = torch.zeros(4, 8, 64, dtype=torch.bfloat16, device=DEV)
+    st = _lib.state_struct(x, x, x[:, :, :1].contiguous(), x, x, 8)
+    tok = torch.zeros(1, 4, 1, 64, dtype=torch.bfloat16, device=DEV)
+    seq, keep = _lib.seq4(tok, tok, tok[..., :1])
+    rc = lib.kvm_decode_step(layer.ref(), tok.data_ptr(), 256, 64, st, 4, seq, x.data_ptr(), x.data_ptr(),
+                             x.data_ptr(), 8, 0, 0, tok.data_ptr(), 256, 64, x.data_ptr(), x.numel() * 2, 0)
+    assert rc != 0 and b"last window row" in lib.kvm_last_error()
+    del keep
+
+
 def test_prefill_deterministic(lib):
     """Two prefills of the same input are bit-identical (no atomics anywhere)."""
     B, Hq, Hkv, Tn, D, C = 1, 8, 8, 4096, 128, 256
