@@ -452,8 +452,8 @@ int kvm_decode_attention(const kvm_layer *layer, const void *q, int64_t q_sb,
  * ring_v, ring_gate, ring_cap, (ring_start + recent_len - 1) % ring_cap)
  * followed by kvm_decode_attention with these arguments.  recent_len counts
  * the step's token (src, one token, not a ring) as the last window row; the
- * attention reads it from src and the combine launch stores its k, v and
- * merge gate in the ring.
+ * attention reads it from src and stores its k, v and merge gate in the ring
+ * slot, which no other read of the step touches.
  * Replaces the ring write + attention of one decode token
  * (write_recent_ring + kvm_decode_attention, model/kernels/kvm_triton_decode.py:18-70,
  * 287-322, 175-284, 409-467). */

@@ -45,7 +45,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
     int64_t cap, int active, const uint16_t *__restrict__ rk,
     const uint16_t *__restrict__ rv, int64_t ring_cap, int64_t ring_start,
     int recent_len, int nseg, float *__restrict__ part_acc,
-    float *__restrict__ part_ml, const int32_t *__restrict__ ctl, int pending, kvm_seq fresh) {
+    float *__restrict__ part_ml, const int32_t *__restrict__ ctl, int pending, kvm_seq fresh,
+    uint16_t *ring_k_out, uint16_t *ring_v_out, uint16_t *ring_g_out) {
   constexpr int G = D / 8;             // lanes per key row
   constexpr int RPS = 64 / G;          // rows per wave step
   constexpr int STEPS = kRowsPerWave / RPS;
@@ -81,12 +82,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
   const uint16_t *svrow = sv + int64_t(row) * cap * D;
   const uint16_t *rkrow = rk + int64_t(row) * ring_cap * D;
   const uint16_t *rvrow = rv + int64_t(row) * ring_cap * D;
-  // The newest window row straight from the step's token (its ring copy is
-  // written by the combine kernel, after every read of this launch).
+  // The newest window row straight from the step's token.  Its ring slot is
+  // read by no workgroup of this launch, so the first query-head group of
+  // the segment holding it stores the row there from the loaded registers.
   const bool from_fresh = fresh.k != nullptr;  // uniform
   const int fresh_row = active + recent_len - 1;
   const uint16_t *fkrow = from_fresh ? seq_k(fresh, b, hk, 0) : rkrow;
   const uint16_t *fvrow = from_fresh ? seq_v(fresh, b, hk, 0) : rvrow;
+  const bool store_fresh = from_fresh && blockIdx.z == 0 && seg == fresh_row / kSegRows;  // uniform
+  const int64_t fresh_slot = int64_t(row) * ring_cap + (ring_start + recent_len - 1) % ring_cap;
+  uint16_t gate_val = 0;
+  if (store_fresh && threadIdx.x == 0)
+    gate_val = *(static_cast<const uint16_t *>(fresh.gate) + b * fresh.g_sb + hk * fresh.g_sh);
 
   // Issue every K and V load of the wave first (2 x STEPS x 16 B per lane).
   uint4 kraw[STEPS], vraw[STEPS];
@@ -123,6 +130,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
     const int r = r0 + s * RPS + sub;
     float kx[8];
     unpack8(kraw[s], kx);
+    if (store_fresh && r == fresh_row)
+      *reinterpret_cast<uint4 *>(ring_k_out + fresh_slot * D + part * 8) = kraw[s];
 #pragma unroll
     for (int j = 0; j < GQ; ++j) {
       const float tau = r < active ? ts[j] : tf[j];
@@ -151,6 +160,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
   for (int s = 0; s < STEPS; ++s) {
     float vx[8];
     unpack8(vraw[s], vx);
+    if (store_fresh && r0 + s * RPS + sub == fresh_row)
+      *reinterpret_cast<uint4 *>(ring_v_out + fresh_slot * D + part * 8) = vraw[s];
 #pragma unroll
     for (int j = 0; j < GQ; ++j) {
       const float p = (m[j] == -INFINITY) ? 0.f : exp2f(sc[j][s] - m[j]);
@@ -181,6 +192,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
     }
   }
   __syncthreads();
+  if (store_fresh && threadIdx.x == 0) ring_g_out[fresh_slot] = gate_val;
   for (int e = threadIdx.x; e < GQ * D; e += 256) {
     const int j = e / D, d = e % D;
     float M = -INFINITY;
@@ -207,27 +219,10 @@ template <int D>
 __global__ __launch_bounds__(D) void k_decode_combine(
     int Hq, int nseg, const float *__restrict__ part_acc,
     const float *__restrict__ part_ml, uint16_t *__restrict__ out,
-    int64_t o_sb, int64_t o_sh, kvm_seq fresh, int Hkv, uint16_t *__restrict__ rk,
-    uint16_t *__restrict__ rv, uint16_t *__restrict__ rg, int64_t ring_cap, int64_t pos) {
+    int64_t o_sb, int64_t o_sh) {
   const int pid = blockIdx.x;
   const int b = pid / Hq, h = pid % Hq;
   const int d = threadIdx.x;
-  // The step's token into the window ring: the first query head of each kv
-  // head writes that kv head's row (k, v and the merge gate at pos).
-  if (fresh.k != nullptr && h % (Hq / Hkv) == 0) {
-    const int hk = h / (Hq / Hkv);
-    const int64_t o = (int64_t(b * Hkv + hk) * ring_cap + pos) * D;
-    constexpr int G = D / 8;
-    if (d < G) {
-      *reinterpret_cast<uint4 *>(rk + o + d * 8) = *reinterpret_cast<const uint4 *>(seq_k(fresh, b, hk, 0) + d * 8);
-    } else if (d < 2 * G) {
-      *reinterpret_cast<uint4 *>(rv + o + (d - G) * 8) =
-          *reinterpret_cast<const uint4 *>(seq_v(fresh, b, hk, 0) + (d - G) * 8);
-    } else if (d == 2 * G) {
-      rg[int64_t(b * Hkv + hk) * ring_cap + pos] =
-          *(static_cast<const uint16_t *>(fresh.gate) + b * fresh.g_sb + hk * fresh.g_sh);
-    }
-  }
   float M = -INFINITY;
   for (int s = 0; s < nseg; ++s)
     M = fmaxf(M, part_ml[(int64_t(pid) * nseg + s) * 2]);
@@ -248,7 +243,7 @@ hipError_t launch_partial(const kvm_layer &L, const void *q, int64_t q_sb,
                           int64_t ring_cap, int64_t ring_start,
                           int64_t recent_len, int nseg, float *pacc,
                           float *pml, const int32_t *ctl, int pending, const kvm_seq &fresh,
-                          hipStream_t stream) {
+                          uint16_t *rkw, uint16_t *rvw, uint16_t *rgw, hipStream_t stream) {
   const int group = int(L.q_heads / L.kv_heads);
   dim3 grid(unsigned(nseg), unsigned(L.batch * L.kv_heads),
             unsigned(group / GQ));
@@ -258,7 +253,8 @@ hipError_t launch_partial(const kvm_layer &L, const void *q, int64_t q_sb,
                      static_cast<const uint16_t *>(st.s_v_attn), st.capacity,
                      int(active), static_cast<const uint16_t *>(ring_k),
                      static_cast<const uint16_t *>(ring_v), ring_cap,
-                     ring_start, int(recent_len), nseg, pacc, pml, ctl, pending, fresh);
+                     ring_start, int(recent_len), nseg, pacc, pml, ctl, pending, fresh, rkw, rvw,
+                     rgw);
   return hipGetLastError();
 }
 
@@ -269,12 +265,12 @@ hipError_t launch_partial_d(const kvm_layer &L, const void *q, int64_t q_sb,
                             int64_t ring_cap, int64_t ring_start,
                             int64_t recent_len, int nseg, float *pacc,
                             float *pml, const int32_t *ctl, int pending, const kvm_seq &fresh,
-                            hipStream_t stream) {
+                            uint16_t *rkw, uint16_t *rvw, uint16_t *rgw, hipStream_t stream) {
   const int64_t group = L.q_heads / L.kv_heads;
 #define KVM_PARTIAL(GQ)                                                      \
   launch_partial<D, GQ>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,       \
                         ring_cap, ring_start, recent_len, nseg, pacc, pml, \
-                        ctl, pending, fresh, stream)
+                        ctl, pending, fresh, rkw, rvw, rgw, stream)
   if (group % 4 == 0) return KVM_PARTIAL(4);
   if (group % 2 == 0) return KVM_PARTIAL(2);
   return KVM_PARTIAL(1);
@@ -335,11 +331,10 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
   // Host counters: segments for the rows present; device counters: for
   // max_rows (segments past the live rows contribute nothing).
   // fresh (host counters only): the step's token, the last of the recent_len
-  // window rows, read from fresh by the partial kernel and copied into its
-  // ring slot (with its merge gate) by the combine kernel.
+  // window rows, read from fresh by the partial kernel, which also stores it
+  // (with its merge gate) in its ring slot.
   kvm_seq fr{};
   if (fresh && !ctl) fr = *fresh;
-  const int64_t pos = recent_len > 0 ? (ring_start + recent_len - 1) % ring_cap : 0;
   uint16_t *rk = static_cast<uint16_t *>(const_cast<void *>(ring_k));
   uint16_t *rv = static_cast<uint16_t *>(const_cast<void *>(ring_v));
   uint16_t *rg = static_cast<uint16_t *>(ring_gate);
@@ -351,22 +346,20 @@ hipError_t launch_decode(const kvm_layer &L, const void *q, int64_t q_sb,
   if (L.head_dim == 128)
     e = launch_partial_d<128>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
                               ring_cap, ring_start, recent_len, nseg, pacc,
-                              pml, ctl, pending, fr, stream);
+                              pml, ctl, pending, fr, rk, rv, rg, stream);
   else
     e = launch_partial_d<64>(L, q, q_sb, q_sh, st, active, ring_k, ring_v,
                              ring_cap, ring_start, recent_len, nseg, pacc, pml,
-                             ctl, pending, fr, stream);
+                             ctl, pending, fr, rk, rv, rg, stream);
   if (e != hipSuccess) return e;
   if (L.head_dim == 128)
     hipLaunchKernelGGL(k_decode_combine<128>, dim3(unsigned(npid)), dim3(128),
                        0, stream, int(L.q_heads), nseg, pacc, pml,
-                       static_cast<uint16_t *>(out), o_sb, o_sh, fr, int(L.kv_heads), rk, rv, rg,
-                       ring_cap, pos);
+                       static_cast<uint16_t *>(out), o_sb, o_sh);
   else
     hipLaunchKernelGGL(k_decode_combine<64>, dim3(unsigned(npid)), dim3(64), 0,
                        stream, int(L.q_heads), nseg, pacc, pml,
-                       static_cast<uint16_t *>(out), o_sb, o_sh, fr, int(L.kv_heads), rk, rv, rg,
-                       ring_cap, pos);
+                       static_cast<uint16_t *>(out), o_sb, o_sh);
   return hipGetLastError();
 }
 
