@@ -118,6 +118,27 @@ def test_invalid_layer_is_rejected_before_any_gpu_work(field, value, msg):
         L.check(rc, "refresh")
 
 
+def test_decode_step_argument_checks():
+    """kvm_decode_step refuses, before any GPU work, a token taken from a
+    ring, a missing gate ring and a window that does not hold the token."""
+    lib = _lib()
+    from kvm_amd import _lib as L
+
+    layer, keep = _layer()
+    st = L.KvmState(16, 16, 16, 16, 16, 8)
+
+    def call(seq, ring_gate=16, recent_len=1):
+        return lib.kvm_decode_step(ctypes.byref(layer), 16, 8, 8, ctypes.byref(st), 0, ctypes.byref(seq), 16, 16,
+                                   ring_gate, 8, 0, recent_len, 16, 8, 8, 16, 1 << 30, None)
+
+    plain = L.KvmSeq(16, 16, 16, 8, 8, 8, 8, 8, 8, 1, 1, 1, 0)
+    ringed = L.KvmSeq(16, 16, 16, 8, 8, 8, 8, 8, 8, 1, 1, 1, 4)
+    assert call(ringed) == L.KVM_EINVAL and "ring" in lib.kvm_last_error().decode()
+    assert call(plain, ring_gate=None) == L.KVM_EINVAL and "ring_gate" in lib.kvm_last_error().decode()
+    assert call(plain, recent_len=0) == L.KVM_EINVAL and "last window row" in lib.kvm_last_error().decode()
+    assert call(plain, recent_len=9) == L.KVM_EINVAL and "outside the ring" in lib.kvm_last_error().decode()
+
+
 def test_update_argument_checks():
     lib = _lib()
     from kvm_amd import _lib as L
