@@ -54,6 +54,25 @@
 #include <algorithm>
 
 namespace kvm {
+
+// Optional per-phase timestamps of k_chain_fixed (build with
+// -DKVM_CHAIN_TIMING): member 0 and member G-1 of group 0 record the wall
+// clock (100 MHz) at marks 0..15 of each of the first 128 phases; the host
+// reads them with kvm_chain_timing_read.  Without the define the marks
+// compile to nothing.
+#ifdef KVM_CHAIN_TIMING
+__device__ unsigned long long g_chain_ts[2][128][16];
+#define KVM_TS(k)                                                                        \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && p < 128) {                                                   \
+      if (blockIdx.x == 0) g_chain_ts[0][p][k] = wall_clock64();                         \
+      else if (blockIdx.x == 8 * (GM - 1)) g_chain_ts[1][p][k] = wall_clock64();          \
+    }                                                                                    \
+  } while (0)
+#else
+#define KVM_TS(k) ((void)0)
+#endif
+
 namespace {
 
 constexpr int kChainThreads = 512;
@@ -123,6 +142,23 @@ __device__ __forceinline__ uint4 l2_ld16(__amdgpu_buffer_rsrc_t r, int off) {
 }
 __device__ __forceinline__ uint32_t l2_ld4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScopeDevice);
+}
+__device__ __forceinline__ uint64_t l2_ld8(__amdgpu_buffer_rsrc_t r, int off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kScopeDevice);
+  return uint64_t(v[0]) | (uint64_t(v[1]) << 32);
+}
+
+// Route key of a (score, slot) candidate: the per-update routing kernel's
+// order-preserving encoding mono(fp32 score) << 32 | (0xffffffff - slot), so
+// an integer maximum picks the largest score and, among equal scores, the
+// lowest slot (torch.max returns the first maximum).  0 means no candidate.
+__device__ __forceinline__ uint64_t route_key(float score, int slot) {
+  const uint32_t u = __float_as_uint(score);
+  const uint32_t m = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (uint64_t(m) << 32) | uint64_t(0xffffffffu - uint32_t(slot));
+}
+__device__ __forceinline__ int route_key_slot(uint64_t key) {
+  return key ? int(0xffffffffu - uint32_t(key)) : -1;
 }
 
 // LDS byte address of a __shared__ object (wave-uniform).
@@ -669,21 +705,30 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 // Member m owns the 16-slot blocks m, m + G, m + 2G, ... of its row for the
 // whole launch: their sums (s_k, s_v, vlen) and attention key rows live in
 // the member's LDS.  Phase p of the launch:
-//   combine(p - 1)  every member reads the G partial maxima of every token
-//                   of update p - 1 and keeps the first argmax (largest
-//                   score, lowest slot);
+//   prep(p + 1)     merge keys / values of my share of update p + 1's tokens
+//                   (while the route keys of update p - 1 are in flight);
+//   combine(p - 1)  the route key of every token of update p - 1: each
+//                   member folded its own best slot into one 64-bit word
+//                   per token with atomicMax (largest score, lowest slot),
+//                   so one load per token gives the first argmax;
+//   lists(p - 1)    the tokens routed to each of my slots, in token order
+//                   (wave ballots: rank within the wave, per-wave counts);
 //   merge(p - 1)    sums of the tokens routed to my slots (token order),
-//                   refreshed attention rows into LDS and snapshot u0 + p;
+//                   refreshed attention rows into LDS and, straight from
+//                   registers, into snapshot u0 + p;
 //   route(p)        the merge keys of ALL tokens of update p against MY
 //                   slots (MFMA 16x16x32 bf16, the per-update kernel's
 //                   operand roles and k-step order, so the fp32 scores are
-//                   bit-identical) -> per-token maximum over my slots;
-//   prep(p + 1)     merge keys / values of my share of update p + 1's tokens;
+//                   bit-identical) -> per-token maximum over my slots,
+//                   folded into the route key of update p;
 //   one group barrier.
 // Merge keys / values rotate through three buffers (prepared one phase
-// ahead, read by route and, a phase later, by the merge); the partial
-// maxima alternate between two.  The raw tokens a prep needs are loaded
-// while the member waits at the previous barrier.
+// ahead, read by route and, a phase later, by the merge), and so do the
+// route keys (written in phase i, read in phase i + 1, cleared in phase
+// i + 2 by the member that preps those tokens).  The raw tokens a prep
+// needs are loaded while the member waits at the previous barrier; the
+// route operands of update p are loaded once the merge's gathered rows
+// have arrived, so they never queue in L2 ahead of the gathers.
 constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
 constexpr int kTokWave = 64;      // tokens per wave in route(p)
 constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
@@ -704,18 +749,16 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   constexpr int SP = kOwnMax / RPP;         // passes over the owned slots
   constexpr int RPI = 1024 / (2 * D);        // token rows per 1 KiB DMA instruction
   constexpr int KI = kStageRows / RPI;       // DMA instructions per staged chunk (keys or values)
-  constexpr int NBX = 4 * KS;               // route-operand loads per lane (load_bx)
   constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
   __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
-  __shared__ __attribute__((aligned(16))) uint16_t own_va[kOwnMax * D];   // attention values
   __shared__ __attribute__((aligned(16))) uint16_t own_sk[kOwnMax * D];   // key sums
   __shared__ __attribute__((aligned(16))) uint16_t own_sv[kOwnMax * D];   // value sums
   __shared__ __attribute__((aligned(16))) uint16_t stage_k[kStageRows * D];  // routed token rows
   __shared__ __attribute__((aligned(16))) uint16_t stage_v[kStageRows * D];
   __shared__ float own_vl[kOwnMax];
-  __shared__ int loc[kFixedMaxTok];      // local slot of each token's route, or -1
-  __shared__ int lst[kFixedMaxTok], sorted[kFixedMaxTok];
-  __shared__ int cnt[kOwnMax], off[kOwnMax], fill[kOwnMax];
+  __shared__ int sorted[kFixedMaxTok];
+  __shared__ int wsc[kChainWaves][kOwnMax];  // per-wave slot counts, then per-wave offsets
+  __shared__ int cnt[kOwnMax], off[kOwnMax];
   __shared__ int ok_lds;
   __shared__ float ln_w[D], ln_b[D];  // ln_s_k parameters (LDS: no wait on global loads)
 
@@ -728,6 +771,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int64_t rb = int64_t(row) * n_tok;
   const int64_t buf_stride = int64_t(rows) * n_tok * D;  // elements between merge buffers
+  const int64_t key_stride = int64_t(rows) * n_tok;      // words between route-key buffers
+  unsigned long long *rkeys = reinterpret_cast<unsigned long long *>(cs.part);
   const int tpm = (n_tok + G - 1) / G;                   // prep tokens per member (<= 64)
   const int pt0 = member * tpm;
   const int pnt = max(0, min(n_tok, pt0 + tpm) - pt0);
@@ -815,6 +860,11 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       }
     }
   };
+  // Route keys of my prep share of update i start at zero.
+  auto clear_keys = [&](int i) __attribute__((always_inline)) {
+    unsigned long long *kb = rkeys + (i % 3) * key_stride + rb + pt0;
+    if (tid < pnt) kb[tid] = 0ull;
+  };
 
   // Raw tokens of update i + 1 are loaded between arriving at the barrier
   // that ends phase i - 1 and waiting for it; phase i starts with their prep.
@@ -822,17 +872,16 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   load_raw(0, rt);
   __syncthreads();
   prep(0, rt);
+  clear_keys(0);
   arrive();
   if (list.count > 1) load_raw(1, rt);
   if (!wait()) return;
 
   for (int p = 0; p <= list.count; ++p) {
+    KVM_TS(0);
     const bool do_route = p < list.count;
     const bool do_prep = p + 1 < list.count;
-    // Loads are issued in the order they are needed (a wait for one load
-    // waits for every older one): the partial maxima first, the route
-    // operands of update p (my wave's 64 tokens; tokens >= n_tok read zero)
-    // behind the merge gathers.
+    // Route operands of update p: my wave's 64 tokens (tokens >= n_tok read zero).
     uint4 bx[4][KS];
     auto load_bx = [&]() __attribute__((always_inline)) {
       const __amdgpu_buffer_rsrc_t gr =
@@ -844,83 +893,66 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
                                     (lane >> 4) * 8) * 2);
     };
-    uint4 pw[GM / 2];
+    uint64_t my_key = 0;
     if (p >= 1) {
-      const __amdgpu_buffer_rsrc_t pr = l2_rsrc(
-          cs.part + (int64_t((p - 1) & 1) * rows * n_tok + rb) * G, int64_t(n_tok) * G * 8);
-#pragma unroll
-      for (int i = 0; i < GM / 2; ++i) pw[i] = l2_ld16(pr, (tid * GM + 2 * i) * 8);
+      const __amdgpu_buffer_rsrc_t kr =
+          l2_rsrc(rkeys + int64_t((p - 1) % 3) * key_stride + rb, int64_t(n_tok) * 8);
+      my_key = l2_ld8(kr, tid * 8);  // tokens >= n_tok read zero (no route)
     }
-    // The next update's prep while those loads are in flight.
+    // The next update's prep while that load is in flight.
     if (do_prep) prep(p + 1, rt);
+    if (do_route) clear_keys(p + 1);
     if (p == 0) load_bx();
+    KVM_TS(1);
 
     if (p >= 1) {
-      // ---- combine(p - 1): first argmax over the members' partial maxima.
+      // ---- combine(p - 1) and the lists of my slots.
       const int pi = p - 1;
       const int64_t u = int64_t(list.u0) + pi;
-      if (tid < kOwnMax) {
-        cnt[tid] = 0;
-        fill[tid] = 0;
+      const int bi = route_key_slot(my_key);
+      const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
+      const int my_loc = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
+      if (tid >= pt0 && tid < pt0 + pnt) {  // each member logs its prep share
+        if (route_log) route_log[u * log_stride + rb + tid] = bi;
+        if (append_log) append_log[u * log_stride + rb + tid] = 0;
       }
-      if (tid < n_tok) {
-        float bv = -INFINITY;
-        int bi = -1;
+      // Tokens of my wave with the same local slot (ballots over its bits):
+      // rank among them, and their count from the group's first lane.  A
+      // wave's LDS stores complete in order, so the clear of its own row of
+      // wsc precedes the counts it writes.
+      wsc[wave][lane] = 0;
+      uint64_t eq = __ballot(mine);
 #pragma unroll
-        for (int i = 0; i < GM / 2; ++i) {
-          const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
-          const int i0 = int(pw[i].y), i1 = int(pw[i].w);
-          if (i0 >= 0 && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
-            bv = v0;
-            bi = i0;
-          }
-          if (i1 >= 0 && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
-            bv = v1;
-            bi = i1;
-          }
-        }
-        const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
-        loc[tid] = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
-        if (tid >= pt0 && tid < pt0 + pnt) {  // each member logs its prep share
-          if (route_log) route_log[u * log_stride + rb + tid] = bi;
-          if (append_log) append_log[u * log_stride + rb + tid] = 0;
-        }
+      for (int bit = 0; bit < 6; ++bit) {
+        const uint64_t m = __ballot(mine && ((my_loc >> bit) & 1));
+        eq &= ((my_loc >> bit) & 1) ? m : ~m;
       }
+      const int rank = int(__builtin_amdgcn_mbcnt_hi(uint32_t(eq >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(uint32_t(eq), 0u)));
+      if (mine && rank == 0) wsc[wave][my_loc] = __popcll(eq);
       __syncthreads();
-      if (tid < n_tok && loc[tid] >= 0) atomicAdd(&cnt[loc[tid]], 1);
-      __syncthreads();
-      if (tid < 64) {  // exclusive prefix of the slot counts (kOwnMax == 64)
-        const int c = cnt[tid];
-        int incl = c;
+      if (tid < kOwnMax) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
+        int run = 0;
+#pragma unroll
+        for (int w = 0; w < kChainWaves; ++w) {
+          const int c = wsc[w][tid];
+          wsc[w][tid] = run;
+          run += c;
+        }
+        int incl = run;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
           const int y = __shfl_up(incl, o);
           if (tid >= o) incl += y;
         }
-        off[tid] = incl - c;
+        off[tid] = incl - run;
+        cnt[tid] = run;
       }
       __syncthreads();
+      if (mine) sorted[off[my_loc] + wsc[wave][my_loc] + rank] = tid;
       const int ntot = off[kOwnMax - 1] + cnt[kOwnMax - 1];  // tokens routed to my slots
-      if (tid < n_tok) {
-        const int l = loc[tid];
-        if (l >= 0) lst[off[l] + atomicAdd(&fill[l], 1)] = tid;
-      }
       __syncthreads();
-      // Each slot's tokens in token order (rank sort), so the fp32 sums run
-      // in token order whatever order the LDS atomics placed them in.
-      for (int base = 0; base < nown; base += RPP) {
-        const int l = base + tid / GL;
-        if (l < nown) {
-          const int n = cnt[l], o = off[l];
-          for (int e = part; e < n; e += GL) {
-            const int x = lst[o + e];
-            int r = 0;
-            for (int f = 0; f < n; ++f) r += lst[o + f] < x;
-            sorted[o + r] = x;
-          }
-        }
-      }
-      __syncthreads();
+      KVM_TS(2);
 
       // ---- merge(p - 1) (model/kvm_mixer.py:329-335).  The routed token
       // rows are staged in LDS (all loads of a chunk in flight together),
@@ -957,15 +989,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
             dma16_l2(gvr, vbase + uint32_t(ci * 1024), to);
         }
       };
-      // `outstanding`: vector loads issued after the gather that may stay in
-      // flight (loads return in order, so waiting for vmcnt <= outstanding
-      // waits for the gathered rows only).
-      auto stage_sum = [&](int c0, bool bx_behind) __attribute__((always_inline)) {
+      auto stage_sum = [&](int c0) __attribute__((always_inline)) {
         const int nrow = min(kStageRows, ntot - c0);
-        if (bx_behind)
-          asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NBX) : "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 #pragma unroll
         for (int sp = 0; sp < SP; ++sp) {
@@ -987,12 +1013,23 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         __syncthreads();
       };
       gather(0);
-      load_bx();
-      stage_sum(0, true);
+      KVM_TS(8);
+      stage_sum(0);
+      KVM_TS(9);
       for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
         gather(c0);
-        stage_sum(c0, false);
+        stage_sum(c0);
       }
+      if (do_route) load_bx();
+      KVM_TS(10);
+      // Refreshed attention rows: keys into LDS (route operands), keys and
+      // values into snapshot u0 + p straight from registers (non-temporal:
+      // the attention kernel reads them much later), and after the batch's
+      // last update also into the state's attention rows.
+      const AttnRows nxt = snap_at(snaps, int64_t(list.u0) + p);
+      const bool fin = !do_route && list.final_rows != 0;
+      uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
+      uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
         const int l = sp * RPP + tid / GL;
@@ -1013,36 +1050,22 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         float ka[8], va[8];
         attn_rows<D>(k, v, own_vl[l], part, L, ln_w, ln_b, ka, va);
         if (valid) {
-          *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = pack8(ka);
-          *reinterpret_cast<uint4 *>(&own_va[l * D + part * 8]) = pack8(va);
+          const uint4 kk = pack8(ka), vv = pack8(va);
+          *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
+          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
+          __builtin_nontemporal_store(u32x4{kk.x, kk.y, kk.z, kk.w}, reinterpret_cast<u32x4 *>(nxt.k + ao));
+          __builtin_nontemporal_store(u32x4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<u32x4 *>(nxt.v + ao));
+          if (fin) {
+            const int64_t so = (srow + j) * D + part * 8;
+            *reinterpret_cast<uint4 *>(s_ka + so) = kk;
+            *reinterpret_cast<uint4 *>(s_va + so) = vv;
+          }
         }
         __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
       }
       __syncthreads();
     }
-    // Refreshed rows of merge(p - 1) into snapshot u0 + p.  No other member
-    // reads them, so they are stored after arriving at the barrier (its
-    // s_waitcnt then waits only for what the other members need).
-    // Non-temporal stores: the attention kernel reads them much later, and
-    // keeping them out of L2 leaves room for the merge buffers the group
-    // reads back over the next two phases.
-    auto store_snapshot = [&]() __attribute__((always_inline)) {
-      if (p < 1) return;
-      const AttnRows nxt = snap_at(snaps, int64_t(list.u0) + p);
-#pragma unroll
-      for (int sp = 0; sp < SP; ++sp) {
-        const int l = sp * RPP + tid / GL;
-        const int j = own_local_to_slot(l, G, member);
-        if (l < nown && j < S) {
-          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
-          const uint4 kk = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
-          const uint4 vv = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
-          typedef unsigned u4 __attribute__((ext_vector_type(4)));
-          __builtin_nontemporal_store(u4{kk.x, kk.y, kk.z, kk.w}, reinterpret_cast<u4 *>(nxt.k + ao));
-          __builtin_nontemporal_store(u4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<u4 *>(nxt.v + ao));
-        }
-      }
-    };
+    KVM_TS(3);
 
     if (do_route) {
       // ---- route(p) (model/kvm_fp32_routing_reference.py:30-34) against my
@@ -1097,6 +1120,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
       }
+      unsigned long long *kb = rkeys + int64_t(p % 3) * key_stride + rb;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         float bv = best[tt];
@@ -1112,24 +1136,20 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
         const int t = wave * kTokWave + tt * 16 + lane;
-        if (lane < 16 && t < n_tok)
-          cs.part[(int64_t(p & 1) * rows * n_tok + rb + t) * G + member] =
-              make_uint2(__float_as_uint(bv), uint32_t(bi));
+        if (lane < 16 && t < n_tok && bi >= 0)
+          __hip_atomic_fetch_max(kb + t, (unsigned long long)route_key(bv, bi), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
       }
+      KVM_TS(4);
       arrive();
-      store_snapshot();
       if (p + 2 < list.count) load_raw(p + 2, rt);
+      KVM_TS(5);
       if (!wait()) return;
-    } else {
-      store_snapshot();
+      KVM_TS(6);
     }
   }
 
-  // ---- owned state back to the caller's arrays (and, after the last update
-  // of the prefill, its attention rows: the last snapshot's).
-  const bool attn_rows = list.final_rows != 0;
-  uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
-  uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
+  // ---- owned state back to the caller's arrays.
   for (int base = 0; base < nown; base += RPP) {
     const int l = base + tid / GL;
     if (l < nown) {
@@ -1138,10 +1158,6 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         const int64_t so = (srow + j) * D + part * 8;
         *reinterpret_cast<uint4 *>(s_k + so) = *reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]);
         *reinterpret_cast<uint4 *>(s_v + so) = *reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]);
-        if (attn_rows) {
-          *reinterpret_cast<uint4 *>(s_ka + so) = *reinterpret_cast<const uint4 *>(&own_k[l * STR + part * 8]);
-          *reinterpret_cast<uint4 *>(s_va + so) = *reinterpret_cast<const uint4 *>(&own_va[l * D + part * 8]);
-        }
       }
     }
   }
@@ -1261,3 +1277,10 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
 }
 
 }  // namespace kvm
+
+#ifdef KVM_CHAIN_TIMING
+// Copies the phase timestamps (2 x 128 x 16 words) of the last timed launch.
+extern "C" int kvm_chain_timing_read(void *dst, long words) {
+  return int(hipMemcpyFromSymbol(dst, HIP_SYMBOL(kvm::g_chain_ts), size_t(words) * 8));
+}
+#endif
