@@ -707,10 +707,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 // the member's LDS.  Phase p of the launch:
 //   prep(p + 1)     merge keys / values of my share of update p + 1's tokens
 //                   (while the route keys of update p - 1 are in flight);
-//   combine(p - 1)  the route key of every token of update p - 1: each
-//                   member folded its own best slot into one 64-bit word
-//                   per token with atomicMax (largest score, lowest slot),
-//                   so one load per token gives the first argmax;
+//   combine(p - 1)  every member's best slot for every token of update
+//                   p - 1 (largest score, then lowest slot);
 //   lists(p - 1)    the tokens routed to each of my slots, in token order
 //                   (wave ballots: rank within the wave, per-wave counts);
 //   merge(p - 1)    sums of the tokens routed to my slots (token order),
@@ -720,15 +718,20 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 //                   slots (MFMA 16x16x32 bf16, the per-update kernel's
 //                   operand roles and k-step order, so the fp32 scores are
 //                   bit-identical) -> per-token maximum over my slots,
-//                   folded into the route key of update p;
-//   one group barrier.
+//                   published as a tagged partial.
+// There is no group barrier per update.  A member publishes its partials
+// (score, slot, tag of the update) only after its earlier stores (the
+// merge keys / values it prepared) have reached L2 and every wave of the
+// workgroup has got there; a reader polls the tags of the partials it
+// needs.  Seeing member m's partials of update p therefore also shows that
+// m's prepared rows of update p + 1 are readable, and that m has finished
+// reading every buffer of update p - 1 (so they may be overwritten).
 // Merge keys / values rotate through three buffers (prepared one phase
-// ahead, read by route and, a phase later, by the merge), and so do the
-// route keys (written in phase i, read in phase i + 1, cleared in phase
-// i + 2 by the member that preps those tokens).  The raw tokens a prep
-// needs are loaded while the member waits at the previous barrier; the
-// route operands of update p are loaded once the merge's gathered rows
-// have arrived, so they never queue in L2 ahead of the gathers.
+// ahead, read by route and, a phase later, by the merge); partials
+// alternate between two.  The raw tokens a prep needs are loaded at the
+// end of the phase before; the route operands of update p are loaded once
+// the merge's gathered rows have arrived, so they never queue in L2 ahead
+// of the gathers.
 constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
 constexpr int kTokWave = 64;      // tokens per wave in route(p)
 constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
@@ -771,8 +774,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int64_t rb = int64_t(row) * n_tok;
   const int64_t buf_stride = int64_t(rows) * n_tok * D;  // elements between merge buffers
-  const int64_t key_stride = int64_t(rows) * n_tok;      // words between route-key buffers
-  unsigned long long *rkeys = reinterpret_cast<unsigned long long *>(cs.part);
+  const int64_t part_stride = int64_t(rows) * n_tok * G;  // partials between the two buffers
   const int tpm = (n_tok + G - 1) / G;                   // prep tokens per member (<= 64)
   const int pt0 = member * tpm;
   const int pnt = max(0, min(n_tok, pt0 + tpm) - pt0);
@@ -836,43 +838,58 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     }
   };
   // prep (model/kvm_mixer.py:120-129, model/kvm_triton_mixer.py:429-446):
-  // merge keys / values of my share of update i into merge buffer i % 3.
-  auto prep = [&](int i, const RawTok<D> &rt) __attribute__((always_inline)) {
-    uint16_t *gkb = cs.gk + (i % 3) * buf_stride + rb * D;
-    uint16_t *gvb = cs.gv + (i % 3) * buf_stride + rb * D;
+  // merge key / value rows of pass `it` over my share of an update's tokens
+  // (packed bf16), and their store into merge buffer i % 3.
+  auto prep_row = [&](const RawTok<D> &rt, int it, uint4 &pk, uint4 &pv) __attribute__((always_inline)) {
+    float k[8], v[8];
+    unpack8(rt.k[it], k);
+    unpack8(rt.v[it], v);
+    const float g = bf2f(rt.g[it]);
+    prep_key<D>(k, part, L, ln_w, ln_b);
+    float gk[8], gv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gk[e] = L.gate_keys ? k[e] * g : k[e];
+      gv[e] = L.gate_values ? v[e] * g : v[e];
+    }
+    pk = pack8(gk);
+    pv = pack8(gv);
+  };
+  auto prep_store = [&](int i, int it, const uint4 &pk, const uint4 &pv) __attribute__((always_inline)) {
+    const int lt = (tid + it * kChainThreads) / GL;
+    if (lt < pnt) {
+      const int64_t o = (i % 3) * buf_stride + (rb + pt0 + lt) * D + part * 8;
+      *reinterpret_cast<uint4 *>(cs.gk + o) = pk;
+      *reinterpret_cast<uint4 *>(cs.gv + o) = pv;
+    }
+  };
+  auto prep = [&](int i, const RawTok<D> &rt, int it0, int it1) __attribute__((always_inline)) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int lt = (tid + it * kChainThreads) / GL;
-      float k[8], v[8];
-      unpack8(rt.k[it], k);
-      unpack8(rt.v[it], v);
-      const float g = bf2f(rt.g[it]);
-      prep_key<D>(k, part, L, ln_w, ln_b);
-      float gk[8], gv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        gk[e] = L.gate_keys ? rbf(k[e] * g) : k[e];
-        gv[e] = L.gate_values ? rbf(v[e] * g) : v[e];
-      }
-      if (lt < pnt) {
-        store8(gkb + (pt0 + lt) * D + part * 8, gk);
-        store8(gvb + (pt0 + lt) * D + part * 8, gv);
+      if (it >= it0 && it < it1) {
+        uint4 pk, pv;
+        prep_row(rt, it, pk, pv);
+        prep_store(i, it, pk, pv);
       }
     }
   };
-  // Route keys of my prep share of update i start at zero.
-  auto clear_keys = [&](int i) __attribute__((always_inline)) {
-    unsigned long long *kb = rkeys + (i % 3) * key_stride + rb + pt0;
-    if (tid < pnt) kb[tid] = 0ull;
-  };
+  // Tag of the partials of update i (never 0: the entries are cleared to 0
+  // at the start of a launch, so a workspace's old contents never match).
+  auto tag_of = [](int i) __attribute__((always_inline)) { return uint32_t(0x8000u | uint32_t(i)); };
+  __shared__ int fail_lds;
 
   // Raw tokens of update i + 1 are loaded between arriving at the barrier
   // that ends phase i - 1 and waiting for it; phase i starts with their prep.
   RawTok<D> rt;
   load_raw(0, rt);
+  if (tid == 0) fail_lds = 0;
+  // My partials in both buffers start cleared.
+  for (int t = tid; t < n_tok; t += kChainThreads) {
+    cs.part[rb * G + int64_t(t) * G + member] = make_uint2(0u, 0u);
+    cs.part[part_stride + rb * G + int64_t(t) * G + member] = make_uint2(0u, 0u);
+  }
   __syncthreads();
-  prep(0, rt);
-  clear_keys(0);
+  prep(0, rt, 0, IT);
   arrive();
   if (list.count > 1) load_raw(1, rt);
   if (!wait()) return;
@@ -883,33 +900,87 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     const bool do_prep = p + 1 < list.count;
     // Route operands of update p: my wave's 64 tokens (tokens >= n_tok read zero).
     uint4 bx[4][KS];
-    auto load_bx = [&]() __attribute__((always_inline)) {
+    auto load_bx = [&](int tt0, int tt1, int ks0, int ks1) __attribute__((always_inline)) {
       const __amdgpu_buffer_rsrc_t gr =
           l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = tt0; tt < tt1; ++tt)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int ks = ks0; ks < ks1; ++ks)
           bx[tt][ks] = l2_ld16(gr, ((wave * kTokWave + tt * 16 + (lane & 15)) * D + ks * 32 +
                                     (lane >> 4) * 8) * 2);
     };
-    uint64_t my_key = 0;
+    // Partials of update p - 1 for my token (tokens >= n_tok read zero and
+    // are not waited for).
+    uint4 pw[GM / 2];
+    const __amdgpu_buffer_rsrc_t pr =
+        l2_rsrc(cs.part + int64_t((p - 1) & 1) * part_stride + rb * G, int64_t(n_tok) * G * 8);
     if (p >= 1) {
-      const __amdgpu_buffer_rsrc_t kr =
-          l2_rsrc(rkeys + int64_t((p - 1) % 3) * key_stride + rb, int64_t(n_tok) * 8);
-      my_key = l2_ld8(kr, tid * 8);  // tokens >= n_tok read zero (no route)
+#pragma unroll
+      for (int i = 0; i < GM / 2; ++i) pw[i] = l2_ld16(pr, (tid * GM + 2 * i) * 8);
     }
-    // The next update's prep while that load is in flight.
-    if (do_prep) prep(p + 1, rt);
-    if (do_route) clear_keys(p + 1);
-    if (p == 0) load_bx();
+    // The next update's prep while that load is in flight (from phase 1
+    // on, its second half waits for the merge's gathered rows instead).
+    constexpr int IT_LATE = IT / 2;
+    const int it_split = p >= 1 ? IT - IT_LATE : IT;
+    if (do_prep) prep(p + 1, rt, 0, it_split);
+    if (p == 0) load_bx(0, 4, 0, KS);
     KVM_TS(1);
 
     if (p >= 1) {
       // ---- combine(p - 1) and the lists of my slots.
       const int pi = p - 1;
       const int64_t u = int64_t(list.u0) + pi;
-      const int bi = route_key_slot(my_key);
+      // Wait (bounded) until every member's partial of my token carries the
+      // tag of update p - 1, then keep the first argmax: larger score, then
+      // lower slot (scores are MFMA sums started at +0, never -0 or NaN).
+      bool ok_tok = false;
+      {
+        const uint32_t want = tag_of(pi);
+        bool ok = tid >= n_tok;
+        unsigned polls = 0;
+        for (;;) {
+          bool fresh = true;
+#pragma unroll
+          for (int i = 0; i < GM / 2; ++i) fresh &= (pw[i].y >> 16) == want && (pw[i].w >> 16) == want;
+          ok |= fresh;
+          if (__all(ok) || polls >= cs.max_polls) break;
+          if ((polls & 255u) == 255u &&
+              __hip_atomic_load(cs.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            break;
+          __builtin_amdgcn_s_sleep(1);
+          ++polls;
+          if (!ok) {
+#pragma unroll
+            for (int i = 0; i < GM / 2; ++i) pw[i] = l2_ld16(pr, (tid * GM + 2 * i) * 8);
+          }
+        }
+        ok_tok = ok && tid < n_tok;
+        if (!__all(ok)) {
+          if ((tid & 63) == 0) {
+            __hip_atomic_store(cs.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_or(cs.status, unsigned(KVM_STATUS_CHAIN_TIMEOUT), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+            fail_lds = 1;
+          }
+        }
+      }
+      float bv = -INFINITY;
+      int bi = -1;
+#pragma unroll
+      for (int i = 0; i < GM / 2; ++i) {
+        const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
+        const int i0 = int(pw[i].y & 0xffffu), i1 = int(pw[i].w & 0xffffu);
+        if (i0 != 0xffff && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
+          bv = v0;
+          bi = i0;
+        }
+        if (i1 != 0xffff && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
+          bv = v1;
+          bi = i1;
+        }
+      }
+      if (!ok_tok) bi = -1;  // past n_tok, or a partial that never arrived
       const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
       const int my_loc = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
       if (tid >= pt0 && tid < pt0 + pnt) {  // each member logs its prep share
@@ -931,6 +1002,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
                                                      __builtin_amdgcn_mbcnt_lo(uint32_t(eq), 0u)));
       if (mine && rank == 0) wsc[wave][my_loc] = __popcll(eq);
       __syncthreads();
+      if (fail_lds) return;  // a partial never arrived: the launch is abandoned
       if (tid < kOwnMax) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
         int run = 0;
 #pragma unroll
@@ -980,13 +1052,15 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         for (int t = 0; t < 2 * KI / kChainWaves; ++t) {
           const int c = __builtin_amdgcn_readfirstlane(wave) + kChainWaves * t;
           const int ci = c < KI ? c : c - KI;
-          const int pos = c0 + ci * RPI + lane / GL;
-          const int tok = pos < ntot ? sorted[pos] : n_tok;  // n_tok: past the resource
-          const uint32_t to = uint32_t((tok * D + part * 8) * 2);
-          if (c < KI)
-            dma16_l2(gkr, kbase + uint32_t(ci * 1024), to);
-          else
-            dma16_l2(gvr, vbase + uint32_t(ci * 1024), to);
+          if (c0 + ci * RPI < ntot) {  // instructions wholly past ntot are not issued
+            const int pos = c0 + ci * RPI + lane / GL;
+            const int tok = pos < ntot ? sorted[pos] : n_tok;  // n_tok: past the resource
+            const uint32_t to = uint32_t((tok * D + part * 8) * 2);
+            if (c < KI)
+              dma16_l2(gkr, kbase + uint32_t(ci * 1024), to);
+            else
+              dma16_l2(gvr, vbase + uint32_t(ci * 1024), to);
+          }
         }
       };
       auto stage_sum = [&](int c0) __attribute__((always_inline)) {
@@ -1013,14 +1087,25 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         __syncthreads();
       };
       gather(0);
+      // Second half of the next update's prep while the rows are in flight;
+      // its stores wait until they have arrived (a store issued now would
+      // hold up the wait for the gathered rows).
+      uint4 lpk[IT_LATE > 0 ? IT_LATE : 1], lpv[IT_LATE > 0 ? IT_LATE : 1];
+      if (do_prep) {
+#pragma unroll
+        for (int x = 0; x < IT_LATE; ++x) prep_row(rt, IT - IT_LATE + x, lpk[x], lpv[x]);
+      }
       KVM_TS(8);
       stage_sum(0);
+      if (do_prep) {
+#pragma unroll
+        for (int x = 0; x < IT_LATE; ++x) prep_store(p + 1, IT - IT_LATE + x, lpk[x], lpv[x]);
+      }
       KVM_TS(9);
       for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
         gather(c0);
         stage_sum(c0);
       }
-      if (do_route) load_bx();
       KVM_TS(10);
       // Refreshed attention rows: keys into LDS (route operands), keys and
       // values into snapshot u0 + p straight from registers (non-temporal:
@@ -1030,11 +1115,26 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       const bool fin = !do_route && list.final_rows != 0;
       uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
       uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
+      // The route operands of update p are issued in small groups between
+      // the steps of the passes: the CU moves them from L2 at a fixed rate,
+      // and a wave that issues many at once waits until they are accepted.
+      constexpr int NBP = 4 * KS / SP;  // route-operand loads per pass
+      auto bx_group = [&](int sp, int g) __attribute__((always_inline)) {
+        if (do_route) {
+#pragma unroll
+          for (int x = g * NBP / 4; x < (g + 1) * NBP / 4; ++x) {
+            const int idx = sp * NBP + x;
+            load_bx(idx / KS, idx / KS + 1, idx % KS, idx % KS + 1);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
         const int l = sp * RPP + tid / GL;
         const int j = own_local_to_slot(l, G, member);
         const bool valid = l < nown && j < S;
+        bx_group(sp, 0);
         float k[8], v[8];
         unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
         unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
@@ -1047,8 +1147,20 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = pack8(k);
           *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = pack8(v);
         }
+        bx_group(sp, 1);
+        // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps).
         float ka[8], va[8];
-        attn_rows<D>(k, v, own_vl[l], part, L, ln_w, ln_b, ka, va);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ka[e] = k[e];
+          va[e] = v[e];
+        }
+        layer_norm8<D>(ka, part, ln_w, ln_b, float(L.ln_eps));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ka[e] = rbf(ka[e]);
+        bx_group(sp, 2);
+        attn_value8<D>(va, own_vl[l]);
+        bx_group(sp, 3);
         if (valid) {
           const uint4 kk = pack8(ka), vv = pack8(va);
           *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
@@ -1098,29 +1210,43 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           for (int tt = 0; tt < 4; ++tt)
             accs[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]),
                                                                accs[tt], 0, 0, 0);
+        const int j0 = jb + (lane >> 4) * 4;  // slot of acc[0]
+        if (masked) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const f32x4 acc = accs[tt];
-          if (masked) {
+          for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int j = jb + (lane >> 4) * 4 + i;
-              const float sc = ((j >= protect) && (j < S)) ? acc[i] : -INFINITY;
+              const int j = j0 + i;
+              const float sc = ((j >= protect) && (j < S)) ? accs[tt][i] : -INFINITY;
               const bool take = sc > best[tt];
               best[tt] = take ? sc : best[tt];
               bidx[tt] = take ? j : bidx[tt];
             }
-          } else {
+          }
+        } else {
+          // The lane's four slots as a tree (the earlier slot keeps ties),
+          // then against the running maximum: the same first maximum as a
+          // scan in slot order, with independent chains per token tile.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const bool take = acc[i] > best[tt];
-              best[tt] = take ? acc[i] : best[tt];
-              bidx[tt] = take ? jb + (lane >> 4) * 4 + i : bidx[tt];
-            }
+          for (int tt = 0; tt < 4; ++tt) {
+            const f32x4 acc = accs[tt];
+            const bool t1 = acc[1] > acc[0], t3 = acc[3] > acc[2];
+            const float v01 = t1 ? acc[1] : acc[0], v23 = t3 ? acc[3] : acc[2];
+            const int i01 = t1 ? 1 : 0, i23 = t3 ? 3 : 2;
+            const bool th = v23 > v01;
+            const float vh = th ? v23 : v01;
+            const int ih = th ? i23 : i01;
+            const bool take = vh > best[tt];
+            best[tt] = take ? vh : best[tt];
+            bidx[tt] = take ? j0 + ih : bidx[tt];
           }
         }
       }
-      unsigned long long *kb = rkeys + int64_t(p % 3) * key_stride + rb;
+      // Release: this member's earlier stores (its prepared rows of update
+      // p + 1) are in L2 before any of its partials of update p is.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      const uint32_t tg = tag_of(p) << 16;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         float bv = best[tt];
@@ -1136,15 +1262,13 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
         const int t = wave * kTokWave + tt * 16 + lane;
-        if (lane < 16 && t < n_tok && bi >= 0)
-          __hip_atomic_fetch_max(kb + t, (unsigned long long)route_key(bv, bi), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < 16 && t < n_tok)
+          cs.part[int64_t(p & 1) * part_stride + (rb + t) * G + member] =
+              make_uint2(__float_as_uint(bv), tg | (uint32_t(bi) & 0xffffu));
       }
       KVM_TS(4);
-      arrive();
       if (p + 2 < list.count) load_raw(p + 2, rt);
       KVM_TS(5);
-      if (!wait()) return;
       KVM_TS(6);
     }
   }
