@@ -1138,31 +1138,29 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         float k[8], v[8];
         unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
         unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
-        if (valid && cnt[l] > 0) {
+        if (valid && cnt[l] > 0) {  // state = bf16(state + bf16(sum))
+          round_pack8(sk[sp]);
+          round_pack8(sv[sp]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            k[e] = rbf(k[e] + rbf(sk[sp][e]));
-            v[e] = rbf(v[e] + rbf(sv[sp][e]));
+            k[e] += sk[sp][e];
+            v[e] += sv[sp][e];
           }
-          *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = pack8(k);
-          *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = pack8(v);
+          *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = round_pack8(k);
+          *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = round_pack8(v);
         }
         bx_group(sp, 1);
-        // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps).
-        float ka[8], va[8];
+        // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps;
+        // the rows are only stored, so they are rounded by the packing).
+        float ka[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ka[e] = k[e];
-          va[e] = v[e];
-        }
+        for (int e = 0; e < 8; ++e) ka[e] = k[e];
         layer_norm8<D>(ka, part, ln_w, ln_b, float(L.ln_eps));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ka[e] = rbf(ka[e]);
+        const uint4 kk = pack8(ka);
         bx_group(sp, 2);
-        attn_value8<D>(va, own_vl[l]);
+        const uint4 vv = attn_value8_packed<D>(v, own_vl[l]);
         bx_group(sp, 3);
         if (valid) {
-          const uint4 kk = pack8(ka), vv = pack8(va);
           *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
           const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
           __builtin_nontemporal_store(u32x4{kk.x, kk.y, kk.z, kk.w}, reinterpret_cast<u32x4 *>(nxt.k + ao));

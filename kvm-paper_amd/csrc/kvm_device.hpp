@@ -65,6 +65,13 @@ __device__ __forceinline__ void load8(const uint16_t *p, float (&x)[8]) {
 __device__ __forceinline__ void store8(uint16_t *p, const float (&x)[8]) {
   *reinterpret_cast<uint4 *>(p) = pack8(x);
 }
+// Rounds 8 floats to bfloat16 in place (rbf of each, two per conversion)
+// and returns them packed.
+__device__ __forceinline__ uint4 round_pack8(float (&x)[8]) {
+  const uint4 u = pack8(x);
+  unpack8(u, x);
+  return u;
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 u) {
   return __builtin_bit_cast(bf16x8, u);
@@ -153,16 +160,23 @@ __device__ __forceinline__ float row_norm8(const float (&x)[8]) {
 // q0 = v * r, then one correction q = q0 + r * fma(-q0, n, v) (Markstein's
 // method), which gives the correctly rounded v / n for normal operands; it
 // was checked bit-identical to v / n on gfx950 over 2^31 random operands.
+// attn_value8_packed returns the row packed; attn_value8 rounds in place.
 template <int D>
-__device__ __forceinline__ void attn_value8(float (&v)[8], float vlen) {
+__device__ __forceinline__ uint4 attn_value8_packed(const float (&v)[8], float vlen) {
   const float n = fmaxf(row_norm8<D>(v), 1e-12f);
   const float r = 1.0f / n;
+  float o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float q0 = v[i] * r;
     const float q = __builtin_fmaf(__builtin_fmaf(-q0, n, v[i]), r, q0);
-    v[i] = rbf(q * vlen);
+    o[i] = q * vlen;
   }
+  return pack8(o);
+}
+template <int D>
+__device__ __forceinline__ void attn_value8(float (&v)[8], float vlen) {
+  unpack8(attn_value8_packed<D>(v, vlen), v);
 }
 
 }  // namespace kvm

@@ -34,12 +34,18 @@ __device__ __forceinline__ float seq_g(const kvm_seq &s, int b, int h,
 template <int D>
 __device__ __forceinline__ void prep_key(float (&k)[8], int part, const kvm_layer &L,
                                          const float *w, const float *b) {
+  const int r = int(L.rope_partial_dim);
+  if ((r & 7) == 0) {  // a lane's 8 dims are zeroed together (one condition per lane)
+    const bool z = part * 8 < r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (part * 8 + i < L.rope_partial_dim) k[i] = 0.f;
+    for (int i = 0; i < 8; ++i) k[i] = z ? 0.f : k[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (part * 8 + i < r) k[i] = 0.f;
+  }
   layer_norm8<D>(k, part, w, b, float(L.ln_eps));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) k[i] = rbf(k[i]);
+  round_pack8(k);
 }
 template <int D>
 __device__ __forceinline__ void prep_key(float (&k)[8], int part, const kvm_layer &L) {
@@ -58,8 +64,7 @@ __device__ __forceinline__ void attn_rows(const float (&sk)[8], const float (&sv
     va[i] = sv[i];
   }
   layer_norm8<D>(ka, part, w, b, float(L.ln_eps));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ka[i] = rbf(ka[i]);
+  round_pack8(ka);
   attn_value8<D>(va, vlen);
 }
 template <int D>
