@@ -33,10 +33,13 @@
 // groups with a per-key swap of 32-byte halves, so that the K fragment reads
 // (ds_read_b128) and the V^T fragment reads (ds_read_b64_tr_b16, the gfx950
 // transposing LDS read) are free of bank conflicts while each 1 KiB DMA
-// instruction still reads whole 64-byte runs of 16 keys.  Two buffers; the
-// DMA of block j+1 runs while block j is consumed; one barrier per block.
-// A workgroup of 4 waves (one per SIMD) uses 64 KiB of LDS, so two
-// independent workgroups share a CU and fill each other's stalls.
+// instruction still reads whole 64-byte runs of 16 keys.  Key images are
+// triple-buffered and value images double-buffered: while block j is
+// consumed, the values of block j+1 and the keys of blocks j+1 and j+2 are in
+// flight (the loop is bound by how many bytes each CU has in flight from
+// L2).  One barrier per block.  A workgroup of 4 waves (one per SIMD) uses
+// 80 KiB of LDS (D = 128), so two independent workgroups share a CU (160 KiB)
+// and fill each other's stalls.
 // Workgroups are renumbered so that each XCD (dispatch is round-robin over
 // the 8 XCDs) runs a contiguous range of (head, chunk) tiles: the window keys
 // shared by neighbouring chunks stay in that XCD's L2.
@@ -201,8 +204,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles, int n_chunks,
                     ChunkTable table) {
   constexpr int NT = NW * 64, BM = NW * 32;
-  constexpr int BUF = Lay<D>::BUF;
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * BUF];
+  constexpr int BLK = Lay<D>::BLK;
+  constexpr int KBUFS = 3, VBUFS = 2;
+  constexpr int PER = Lay<D>::CHUNKS / NW;  // DMA instructions per wave and image
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[(KBUFS + VBUFS) * BLK];
   const int C = int(L.chunk_len), n = int(L.n_bswa_chunks);
   const int Hq = int(L.q_heads), Hkv = int(L.kv_heads);
   // XCD-contiguous renumbering of the 1-D grid: logical order (q row, chunk, q tile).
@@ -226,10 +231,9 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t qpos0 = q0 + wave * 32;
 
-  // Zero both buffers once: rows past a short block are then zeros or
-  // earlier keys, never uninitialised bytes.
-  for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT)
-    reinterpret_cast<uint4 *>(lds)[i] = make_uint4(0, 0, 0, 0);
+  // LDS is not cleared: key rows past a short block are masked (their
+  // scores are replaced, whatever the stale bytes), and the value rows past
+  // it are zeroed before each such block's DMA (zero_v_tail).
 
   // Q fragments (B operand of S^T): row rt*16 + lane%16, dims ks*32 + 8*(lane/16).
   bf16x8 qf[2][D / 32];
@@ -308,36 +312,48 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
       const int64_t q = causal ? qpos0 - (wb + int64_t(jj) * BN) : int64_t(BN);
       return int(min(max(q, int64_t(-64)), int64_t(BN)));
     };
-    auto issue = [&](int jj) {
+    // Keys of block jj into image jj % 3, values into image 3 + jj % 2.
+    auto issue_k = [&](int jj) {
       const int jn = jj * BN;
       const int nv = min(BN, nkeys - jn);
-      if (nv < BN) zero_v_tail<D, NT>(lds + (jj & 1) * BUF + Lay<D>::BLK, nv);
-      issue_block<D, NW>(lds_base + uint32_t((jj & 1) * BUF),
-                     key_rsrc(kp + int64_t(jn) * kstride, kstride, nv),
-                     key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), ko, vo, kstride_b,
-                     vstride_b, wave);
+      issue_image<D, NW>(lds_base + uint32_t((jj % KBUFS) * BLK),
+                         key_rsrc(kp + int64_t(jn) * kstride, kstride, nv), ko, kstride_b, wave);
     };
-    __syncthreads();  // both buffers are free (and zeroed, the first time)
-    issue(0);
-    // Block j is in buffer j & 1.  Step j: wait for this wave's DMA of block
-    // j, barrier (block j complete in LDS; every wave is past block j - 1),
-    // DMA of block j + 1 into the other buffer, then consume block j.
+    auto issue_v = [&](int jj) {
+      const int jn = jj * BN;
+      const int nv = min(BN, nkeys - jn);
+      if (nv < BN) zero_v_tail<D, NT>(lds + (KBUFS + (jj & 1)) * BLK, nv);
+      issue_image<D, NW>(lds_base + uint32_t((KBUFS + (jj & 1)) * BLK),
+                         key_rsrc(vp + int64_t(jn) * vstride, vstride, nv), vo, vstride_b, wave);
+    };
+    __syncthreads();  // every image is free
+    issue_k(0);
+    issue_v(0);
+    if (nb > 1) issue_k(1);
+    // Step j: this wave's DMAs were issued in the order ..., keys j, values
+    // j, keys j + 1; wait until only the keys of block j + 1 may be in
+    // flight, barrier (block j complete in LDS; every wave is past block
+    // j - 1, whose images are reused now), DMA of the values of block j + 1
+    // and the keys of block j + 2, then consume block j.
 #pragma unroll 1
     for (int j = 0; j < nb; ++j) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (j + 1 < nb)
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(PER) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (j + 1 < nb) issue(j + 1);
+      if (j + 1 < nb) issue_v(j + 1);
+      if (j + 2 < nb) issue_k(j + 2);
       const int qrel = qrel_of(j);
       if (qrel + 31 < 0) continue;  // wave-uniform: block above the wave's causal diagonal
       const int nvalid = min(BN, nkeys - j * BN);
       const bool masked = nvalid < BN || qrel < BN - 1;
-      const unsigned char *bc = lds + (j & 1) * BUF;
       f32x4 s[4][2];
-      score_block<D>(bc + kb, qf, s);
+      score_block<D>(lds + (j % KBUFS) * BLK + kb, qf, s);
       block_max<D>(s, as, masked, nvalid, causal, qrel, sc);
       bf16x8 pb[2][2];
       block_probs<D>(s, as, sc, pb);
-      block_pv<D>(bc + Lay<D>::BLK, vb0, vb1, pb, as);
+      block_pv<D>(lds + (KBUFS + (j & 1)) * BLK, vb0, vb1, pb, as);
     }
   }
 

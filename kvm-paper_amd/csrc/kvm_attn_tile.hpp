@@ -93,6 +93,21 @@ __device__ __forceinline__ void issue_block(uint32_t buf, __amdgpu_buffer_rsrc_t
   }
 }
 
+// DMA of one K (or V) block image (keys [0, nvalid) set by the resource) into
+// LDS byte address `img`: the instructions of issue_block for one half.
+template <int D, int NW>
+__device__ __forceinline__ void issue_image(uint32_t img, __amdgpu_buffer_rsrc_t r, uint32_t o,
+                                            uint32_t stride_b, int wave) {
+  constexpr int PER = Lay<D>::CHUNKS / NW;
+  static_assert(Lay<D>::CHUNKS % NW == 0, "DMA instructions split evenly over the waves");
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    const int c = wave + NW * t;
+    const int cg = c >> 2, rq = c & 3;
+    dma16(r, img + uint32_t(cg * 4096 + rq * 1024), o + uint32_t(16 * rq) * stride_b + uint32_t(cg * 64));
+  }
+}
+
 // Zero the rows [nv, 64) of one half of a buffer (a block shorter than 64
 // rows): the DMA leaves them untouched, and the weights that meet them are
 // zero, so stale bytes must not be Inf or NaN.  NT: threads of the workgroup.
