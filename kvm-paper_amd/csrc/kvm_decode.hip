@@ -123,7 +123,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
     }
   }
 
-  // Scores: bf16(key * temperature) . q (model/kernels/kvm_triton_decode.py:225-228).
+  // Scores: (key . q) * temperature * scale in fp32, the prefill kernel's form
+  // (k_attn_prefill multiplies the head temperature into the fp32 score), so
+  // that a decode step after a prefill of T tokens gives the prefill of T + 1
+  // tokens' last row.  The reference's Triton kernels round bf16(key *
+  // temperature) first (model/kernels/kvm_triton_decode.py:225-228); both
+  // forms are the same at temperature 1.
   float sc[GQ][STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
@@ -137,9 +142,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GQ == 1 ? 3
       const float tau = r < active ? ts[j] : tf[j];
       float d = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d += rbf(kx[i] * tau) * qv[j][i];
+      for (int i = 0; i < 8; ++i) d += kx[i] * qv[j][i];
       d = group_sum<G>(d);
-      sc[j][s] = r < total ? d * scale : -INFINITY;
+      sc[j][s] = r < total ? d * (scale * tau) : -INFINITY;
     }
   }
 

@@ -266,8 +266,8 @@ def test_full_size_decode_attention(lib):
     for bi in (0, 37, B - 1):
         for hq in (0, 13, Hq - 1):
             row = bi * Hkv + hq * Hkv // Hq
-            keys = torch.cat([(ka[row].cpu().float() * ts_b[hq]).bfloat16(),
-                              (rk[row].cpu()[idx].float() * tf_b[hq]).bfloat16()])
+            # head temperature on the exact score (the kernels' form)
+            keys = torch.cat([ka[row].cpu().double() * ts_b[hq], rk[row].cpu()[idx].double() * tf_b[hq]])
             vals = torch.cat([va[row].cpu(), rv[row].cpu()[idx]])
             ref = _fp64_attention(q[bi, hq].cpu(), keys, vals, torch.ones(1, S + R, dtype=torch.bool))
             mx, mean = T.assert_close_bf16(out[bi, hq].cpu().view(1, D), ref, f"decode b{bi} h{hq}",

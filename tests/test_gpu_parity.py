@@ -529,8 +529,10 @@ def test_decode_attention_exact(lib, B, Hq, Hkv, D, S, R, W, start):
     grp = Hq // Hkv
     idx = (start + torch.arange(R)) % W
     ts_b, tf_b = m.state_head_temp.float().cpu(), m.front_head_temp.float().cpu()
-    keys = torch.cat([(ka[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1).float() * ts_b.view(1, Hq, 1, 1)).bfloat16(),
-                      (rk[:, idx].view(B, Hkv, R, D).repeat_interleave(grp, 1).float() * tf_b.view(1, Hq, 1, 1)).bfloat16()], 2)
+    # The head temperature scales the exact score (the kernels' form; the same
+    # as scaling the unrounded keys).
+    keys = torch.cat([ka[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1).double() * ts_b.view(1, Hq, 1, 1),
+                      rk[:, idx].view(B, Hkv, R, D).repeat_interleave(grp, 1).double() * tf_b.view(1, Hq, 1, 1)], 2)
     vals = torch.cat([va[:, :S].view(B, Hkv, S, D).repeat_interleave(grp, 1), rv[:, idx].view(B, Hkv, R, D).repeat_interleave(grp, 1)], 2)
     ref = _fp64_attention(q, keys, vals, torch.ones(1, S + R, dtype=torch.bool)).squeeze(2)
     mx, mean = T.assert_close_bf16(out.cpu(), ref, "decode attention", max_abs=1e-2, mean_abs=1e-3)
@@ -748,6 +750,48 @@ def test_prefill_ragged_lengths_match_oracle(lib, Tn):
     scale = max(1.0, float(st[O.S_K].float().abs().max()))
     smx, _ = T.err_stats(got["kvm_s_k"][:, :, :S].cpu(), st[O.S_K])
     assert smx <= 2e-2 * scale, f"T={Tn}: state s_k after the decode step: max err {smx:.3e} (scale {scale:.2e})"
+
+
+@pytest.mark.parametrize("Tn", [100, 127, 191, 300])
+def test_decode_after_prefill_matches_longer_prefill(lib, Tn):
+    """One cached decode step after a prefill of T tokens gives the last row
+    of a prefill of T + 1 tokens (the oracle's invariant, decode after
+    prefill(T) = prefill(T + 1)), with head temperatures away from 1: the
+    prefill and decode kernels apply them the same way (on the fp32 score).
+    T = 127 and 191 put the decoded token at a chunk boundary (the decode
+    step runs a state update).  The two paths sum the softmax in different
+    orders and round the softmax weights differently, so the bar is a few
+    bf16 ulps of each output row."""
+    B, Hq, Hkv, D, C = 2, 4, 2, 128, 64
+    T.log(f"[decode-vs-prefill] B{B} Hq{Hq} Hkv{Hkv} T{Tn} D{D} C{C}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="fixed", min_len=C)
+    gen = torch.Generator().manual_seed(500 + Tn)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ft = (1 + 0.3 * torch.randn(Hq, generator=gen)).bfloat16()
+    stt = (1 + 0.3 * torch.randn(Hq, generator=gen)).bfloat16()
+    assert bool((ft != 1).all() and (stt != 1).all())
+    m = T.make_mixer(cfg, ln_w, ln_b, ft, stt)
+    q, k, v, g = (x.to(DEV) for x in _random_inputs(B, Hq, Hkv, Tn + 1, D, 600 + Tn))
+    cache = T.LayerStatesCache()
+    with torch.no_grad():
+        y_long = m.forward_prefill(q, k, v, g, None, None, None, T.LayerStatesCache())
+        m.forward_prefill(q[:, :, :Tn], k[:, :, :Tn], v[:, :, :Tn], g[:, :, :Tn], None, None, None, cache)
+        y_dec = m.forward_single(q[:, :, Tn:], k[:, :, Tn:], v[:, :, Tn:], g[:, :, Tn:], None, None, None, cache)
+    torch.cuda.synchronize()
+    last = y_long.view(B, Tn + 1, Hq * D)[:, Tn].float().cpu()
+    dec = y_dec.view(B, Hq * D).float().cpu()
+    diff = (last - dec).abs()
+    # One bf16 ulp of each head's output row, taken at the row's largest
+    # magnitude: the prefill rounds the softmax weights to bf16 for its PV
+    # product and the decode kernel keeps them in fp32, so elements near zero
+    # differ by an ulp of the row, not of themselves.
+    row_ulp = last.view(B, Hq, D).abs().amax(-1, keepdim=True).expand(B, Hq, D).reshape(B, Hq * D) * 2.0 ** -8
+    ratio = float((diff / row_ulp).max())
+    T.log(f"[decode-vs-prefill] max {float(diff.max()):.3e} mean {float(diff.mean()):.3e} "
+          f"max / row ulp {ratio:.2f}")
+    assert ratio <= 4.0, "decode step and the longer prefill's last row differ beyond 4 ulps of the row"
+    assert float(diff.mean()) <= 2e-5
 
 
 def test_prefill_saturation_budget_matches_oracle(lib):
