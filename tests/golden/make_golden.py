@@ -86,6 +86,49 @@ CASES = [
         sink=2, rope=16, mode="kvm_saturation", min_len=1, n_max=8, factor=1.0, expo=0.5,
         sat_n=500, round_down=16, decode_steps=70, temps=True, gate_appends=1, gate_initial=1,
     ),
+    # The paper's no-merge-gate ablation (configs/prolong/120M/ablation_kvm_no_merge_gate.yaml:
+    # kvm_use_merge_gate_keys / kvm_use_merge_gate_values 0): routes and slot
+    # sums use the ungated overflow streams (model/kvm_mixer.py:264-281).
+    dict(
+        name="no_merge_gate_bf16",
+        dtype="bf16", B=1, Hq=4, Hkv=2, D=64, T=700, C=64, n_bswa=2,
+        sink=1, rope=32, mode="fixed", min_len=64, n_max=1, factor=1.0, expo=0.5,
+        decode_steps=80, temps=True, gate_appends=0, gate_initial=0, gate_keys=0, gate_values=0,
+    ),
+    # Only the key gate, with growth (appends keep their ungated rows).
+    dict(
+        name="key_gate_only_growable_bf16",
+        dtype="bf16", B=1, Hq=2, Hkv=1, D=64, T=900, C=64, n_bswa=2,
+        sink=1, rope=16, mode="power_law", min_len=64, n_max=3, factor=5.0, expo=0.5,
+        decode_steps=0, temps=True, gate_appends=0, gate_initial=0, gate_keys=1, gate_values=0,
+    ),
+    # The no-head-temperature ablation (ablation_kvm_no_head_temps.yaml:
+    # kvm_use_head_temps 0), with two sink slots.
+    dict(
+        name="no_head_temps_bf16",
+        dtype="bf16", B=2, Hq=2, Hkv=2, D=64, T=600, C=64, n_bswa=2,
+        sink=2, rope=32, mode="fixed", min_len=64, n_max=1, factor=1.0, expo=0.5,
+        decode_steps=80, temps=False, gate_appends=0, gate_initial=0,
+    ),
+    # The historical golden's bf16 merge routing (model/kvm_mixer.py:321-331,
+    # the mixer without the FP32 cast): pins the oracle's bf16-routing branch.
+    # CPU oracle only: the HIP path always routes in fp32.
+    dict(
+        name="bf16_routing_bf16",
+        dtype="bf16", B=1, Hq=2, Hkv=2, D=64, T=640, C=64, n_bswa=2,
+        sink=1, rope=32, mode="fixed", min_len=64, n_max=1, factor=1.0, expo=0.5,
+        decode_steps=0, temps=True, gate_appends=0, gate_initial=0, routing="bf16",
+    ),
+    # kvm_use_vlens 0 (slot counts instead of value norms, model/kvm_mixer.py:
+    # 204-208, 337-338): pins the oracle's count branch.  CPU oracle only: the
+    # reference's Triton mixer rejects it (model/kvm_triton_mixer.py:218-219),
+    # and so does the HIP mixer.
+    dict(
+        name="no_vlens_bf16",
+        dtype="bf16", B=1, Hq=2, Hkv=2, D=64, T=640, C=64, n_bswa=2,
+        sink=1, rope=32, mode="fixed", min_len=64, n_max=1, factor=1.0, expo=0.5,
+        decode_steps=40, temps=True, gate_appends=0, gate_initial=0, vlens=0,
+    ),
 ]
 
 
@@ -138,10 +181,10 @@ def _config(case):
         state_budget_mode=case["mode"], state_growth_factor=case["factor"],
         state_growth_exponent=case["expo"], state_round_down=case.get("round_down", 1),
         state_min_len=case["min_len"], state_saturation_n=case.get("sat_n"),
-        kvm_use_merge_gate_keys=1, kvm_use_merge_gate_values=1,
+        kvm_use_merge_gate_keys=case.get("gate_keys", 1), kvm_use_merge_gate_values=case.get("gate_values", 1),
         kvm_apply_merge_gate_to_appends=case["gate_appends"],
         kvm_apply_merge_gate_to_initial_state=case["gate_initial"],
-        kvm_use_head_temps=int(case["temps"]), kvm_use_vlens=1,
+        kvm_use_head_temps=int(case["temps"]), kvm_use_vlens=case.get("vlens", 1),
         kvm_aotriton_forward_attention=0,
     )
 
@@ -171,7 +214,9 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
     gen = torch.Generator().manual_seed(1234 + len(case["name"]))
     inp = _inputs(case, gen)
     dt = inp["q"].dtype
-    mixer = fp32ref.SequenceMixer(_config(case), 0).to(dt).eval()
+    # The FP32-routing mixer, or the historical golden (bf16 routing) it derives from.
+    mixer_cls = eager.SequenceMixer if case.get("routing") == "bf16" else fp32ref.SequenceMixer
+    mixer = mixer_cls(_config(case), 0).to(dt).eval()
     with torch.no_grad():
         mixer.ln_s_k.weight.copy_(inp["ln_w"])
         mixer.ln_s_k.bias.copy_(inp["ln_b"])
@@ -183,7 +228,7 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
     records = []
     orig_split = eager._split_append_merge_idx_by_maxsim
     orig_scatter = torch.scatter
-    orig_merge = fp32ref.SequenceMixer._merge_into_state
+    orig_merge = mixer_cls._merge_into_state
 
     def split_wrapper(k_block, n_append, k_ref):
         app, mrg = orig_split(k_block, n_append, k_ref)
@@ -208,7 +253,7 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
         return out
 
     eager._split_append_merge_idx_by_maxsim = split_wrapper
-    fp32ref.SequenceMixer._merge_into_state = merge_wrapper
+    mixer_cls._merge_into_state = merge_wrapper
     try:
         T = case["T"]
         cache = StatesDictCache() if case["decode_steps"] else None
@@ -235,7 +280,7 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
             st = None
     finally:
         eager._split_append_merge_idx_by_maxsim = orig_split
-        fp32ref.SequenceMixer._merge_into_state = orig_merge
+        mixer_cls._merge_into_state = orig_merge
 
     out = {}
     for key, t in inp.items():
@@ -281,7 +326,9 @@ def _run_case(case, eager, fp32ref, StatesDictCache):
     meta.update(
         n_updates=len(upd), n_prefill_updates=n_prefill_updates,
         torch_version=torch.__version__, prefill_seconds=prefill_s,
-        reference="SmerkyG/KVM-paper eager model.kvm_fp32_routing_reference.SequenceMixer",
+        reference=("SmerkyG/KVM-paper eager model.kvm_mixer.SequenceMixer (bf16 routing)"
+                   if case.get("routing") == "bf16" else
+                   "SmerkyG/KVM-paper eager model.kvm_fp32_routing_reference.SequenceMixer"),
     )
     out["meta_json"] = np.array(json.dumps(meta))
     return out

@@ -15,6 +15,12 @@ def names():
     return sorted(p.stem for p in GOLDEN.glob("*.npz"))
 
 
+def product_names():
+    """Fixtures of configurations the HIP mixer implements (fp32 routing,
+    kvm_use_vlens 1); the others pin only the CPU oracle's branches."""
+    return [n for n in names() if meta(n).get("routing", "fp32") == "fp32" and meta(n).get("vlens", 1) == 1]
+
+
 def decode_names():
     """Fixtures that also hold cached single-token decode steps."""
     return [n for n in names() if meta(n).get("decode_steps", 0) > 0]
@@ -57,7 +63,9 @@ def oracle_setup(fx: dict):
         state_growth_exponent=m["expo"], state_round_down=m.get("round_down", 1), state_min_len=m["min_len"],
         state_saturation_n=m.get("sat_n"),
         gate_appends=bool(m["gate_appends"]), gate_initial=bool(m["gate_initial"]),
-        use_head_temps=bool(m["temps"]),
+        use_head_temps=bool(m["temps"]), gate_keys=bool(m.get("gate_keys", 1)),
+        gate_values=bool(m.get("gate_values", 1)), use_vlens=bool(m.get("vlens", 1)),
+        fp32_routing=m.get("routing", "fp32") == "fp32",
     )
     p = OracleParams(
         ln_weight=fx["in_ln_w"], ln_bias=fx["in_ln_b"],

@@ -41,6 +41,7 @@ def fixture_config(meta):
         factor=meta["factor"], expo=meta["expo"], temps=meta["temps"],
         gate_appends=meta["gate_appends"], gate_initial=meta["gate_initial"],
         sat_n=meta.get("sat_n"), round_down=meta.get("round_down", 1),
+        gate_keys=meta.get("gate_keys", 1), gate_values=meta.get("gate_values", 1),
     )
 
 

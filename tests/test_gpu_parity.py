@@ -27,7 +27,8 @@ from oracle import kvm_oracle as O
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-BF16_FIXTURES = [n for n in golden_io.names() if golden_io.load(n)["meta"]["dtype"] == "bf16"]
+# Fixtures of configurations the HIP mixer implements (the others pin only the CPU oracle).
+BF16_FIXTURES = [n for n in golden_io.product_names() if golden_io.load(n)["meta"]["dtype"] == "bf16"]
 
 
 @pytest.fixture(scope="module")

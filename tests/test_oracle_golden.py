@@ -116,3 +116,27 @@ def test_decode_matches_reference(name):
     assert len(rec.updates) == m["n_updates"]
     for i, u in enumerate(rec.updates):
         assert torch.equal(_route(u), fx[f"upd{i}_route"]), f"update {i} routes differ"
+
+
+@pytest.mark.parametrize("name,field", [
+    ("no_merge_gate_bf16", "gate_keys"), ("no_merge_gate_bf16", "gate_values"),
+    ("key_gate_only_growable_bf16", "gate_values"), ("no_head_temps_bf16", "use_head_temps"),
+    ("bf16_routing_bf16", "fp32_routing"), ("no_vlens_bf16", "use_vlens"),
+])
+def test_flag_fixtures_pin_their_branch(name, field):
+    """Each configuration-flag fixture decides its branch of the oracle: with
+    the flag the reference ran, the prefill is bit-exact; with it flipped
+    (the planted mistake), the output differs."""
+    import dataclasses
+
+    fx = golden_io.load(name)
+    if not _exact(fx):
+        pytest.skip("bit-exact comparison needs the torch build that wrote the fixture")
+    T = fx["meta"]["T"]
+    cfg, p = golden_io.oracle_setup(fx)
+    args = (fx["in_q"][:, :, :T], fx["in_k"][:, :, :T], fx["in_v"][:, :, :T], fx["in_gate"][:, :, :T], p)
+    y, _ = O.prefill(*args, cfg)
+    assert torch.equal(y, fx["y_prefill"])
+    flipped = dataclasses.replace(cfg, **{field: not getattr(cfg, field)})
+    y_bad, _ = O.prefill(*args, flipped)
+    assert not torch.equal(y_bad, fx["y_prefill"]), f"flipping {field} leaves the fixture's output unchanged"
