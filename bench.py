@@ -13,7 +13,7 @@ Workloads:
            a chunk boundary is crossed, split-K attention).  The timed
            region is `--decode-steps` consecutive tokens from a fresh
            snapshot, so the one update per 256 tokens is included.
-  config3  config 3: B2 H16 D128 T65536 chunk 512, ceil-sqrt slots capped
+  config3  config 3: B2 H16 D128 T65536 chunk 512, floor(sqrt(tokens seen)) slots capped
            at 1024, clustered keys; the budget as written and a growth
            variant (factor 16, 512 -> 1024 slots by appends); reported in the
            "prefill_config3" object.
@@ -145,7 +145,8 @@ def bench_prefill(args, torch, kvm_amd):
 
 
 def bench_prefill_config3(args, torch, kvm_amd):
-    """B2 H16 D128 T65536 C512, slots ceil-sqrt(tokens seen) capped at 1024
+    """B2 H16 D128 T65536 C512, slots floor(sqrt(tokens seen)) capped at 1024 (the reference's
+    power-law budget floors, model/kvm_mixer.py:141-147; BASELINE.json writes ceil)
     (power-law budget, n_max_d_chunks 2), 10 % of the keys drawn from 8 shared centres.  As
     written the budget never passes the 512 slots the first chunk fills ("literal": 125 updates,
     no appends); the growth variant (factor 16) grows the state 512 -> 1024 through appends."""
@@ -556,7 +557,7 @@ def main():
         }
     if pf3 is not None:
         line["prefill_config3"] = {
-            "workload": "config 3: KVM layer prefill B2 H16 D128 T65536 C512, ceil-sqrt slots capped at 1024, "
+            "workload": "config 3: KVM layer prefill B2 H16 D128 T65536 C512, floor(sqrt(tokens seen)) slots (the reference's power-law budget) capped at 1024, "
                         "10% of keys from 8 shared centres; 'literal' is the budget as written (never passes the "
                         "512 slots of the first chunk), 'growth_f16' grows 512 -> 1024 slots through appends",
             **pf3,

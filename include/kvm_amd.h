@@ -327,7 +327,9 @@ int kvm_relu_square(const void *x, void *out, int64_t n, void *stream);
  *                        zeros when prev is NULL)
  * Every output is optional (NULL): out_x = r, out_h = h, out_shift = shifted
  * (needs mix), state_out [batch, width] = h of the last token.  state_out may
- * be prev itself only when seq_len == 1. */
+ * be prev itself, and out_x / out_h / out_shift may be x or y, only when
+ * seq_len == 1 (KVM_EINVAL otherwise: the token shift reads the row before
+ * each run of rows, which another run may already have overwritten). */
 typedef struct kvm_add_norm_desc {
   const void *x, *y;
   double alpha;

@@ -164,6 +164,14 @@ int kvm_add_norm(const kvm_add_norm_desc *d, void *stream) {
   if (P.out_shift && !P.mix) return fail(KVM_EINVAL, "add_norm: out_shift needs mix");
   if (P.state_out && P.state_out == P.prev && P.seq_len != 1)
     return fail(KVM_EINVAL, "add_norm: state_out may alias prev only when seq_len == 1");
+  // With token shift, a run of rows starts from the previous run's last row
+  // of x and y, which that run's wave may already have overwritten through
+  // an aliased output.
+  if (P.seq_len != 1)
+    for (const void *o : {static_cast<const void *>(P.out_x), static_cast<const void *>(P.out_h),
+                          static_cast<const void *>(P.out_shift)})
+      if (o && (o == P.x || (P.y && o == P.y)))
+        return fail(KVM_EINVAL, "add_norm: an output may alias x or y only when seq_len == 1");
   const void *ptrs[] = {P.x, P.y, P.ln_w, P.ln_b, P.mix, P.prev, P.out_x, P.out_h, P.out_shift, P.state_out};
   for (const void *p : ptrs)
     if (p && !aligned16(p)) return fail(KVM_EINVAL, "add_norm pointers must be 16-byte aligned");

@@ -600,7 +600,10 @@ class DecodeGraph:
     step's.  No counterpart in the reference, which decodes eagerly
     (model/kvm_triton_mixer.py:717-757): it removes the host cost of the
     ~20 launches per layer of an eager step.  The graph is captured again
-    when a buffer it uses has been reallocated (a growing state budget)."""
+    when a buffer it uses has been reallocated (a growing state budget) or a
+    parameter has changed (new storage, or an in-place update seen by its
+    version counter): a replay would otherwise keep reading the weight copies
+    packed for kvm_gemm_small_packed at capture time."""
 
     def __init__(self, model: "RWKV7BackboneForCausalLM", cache: StatesDictCache):
         self.model, self.cache = model, cache
@@ -611,6 +614,10 @@ class DecodeGraph:
         self.ctl_synced = False
         self.replays = self.eager_steps = 0
         self.warmed = False  # the first plain step runs eagerly (lazy allocations, packed weights)
+        self._params = list(model.parameters())
+
+    def _weights_signature(self):
+        return tuple((p.data_ptr(), p._version) for p in self._params)
 
     def _kvm_caches(self):
         from .decode_cache import KVMDecodeCache
@@ -643,8 +650,12 @@ class DecodeGraph:
             out = self.model(input_ids=tok[:, None], past_key_values=self.cache, use_cache=True,
                              cache_position=torch.tensor([pos]), logits_to_keep=1)
             return out.logits[:, -1]
-        sig = tuple(c.graph_buffers() for c in kv)
+        sig = (tuple(c.graph_buffers() for c in kv), self._weights_signature())
         if self.graph is None or sig != self.signature:
+            if self.graph is not None and sig[1] != self.signature[1]:
+                self.warmed = False  # repack the changed weights in an eager step first
+                self.graph = None
+                return self.step(tok)
             return self._capture(tok, pos, kv, sig)
         if not self.ctl_synced:
             self._sync_ctl(kv)

@@ -14,8 +14,12 @@ and the carried-state cache entry follow the reference:
 Everything after the post-QKV boundary (window + memory attention, the
 block-boundary memory update, decode) runs in libkvm_amd.so through its C ABI
 (include/kvm_amd.h).  The projections before the boundary are plain torch
-modules, as in the reference.  Autograd (training) is not provided: a
-prefill that needs gradients raises ValueError.
+modules, as in the reference.  Training: a prefill that needs gradients runs
+through ``training.KVMPrefillFunction`` (the HIP forward keeping its
+snapshots, routes and log-sum-exp; the HIP attention and state backward),
+with the forward's routes as fixed metadata, as in the reference's training
+function (model/kvm_triton_mixer.py:24-195).  Only the cached decode path is
+inference-only.
 """
 
 from __future__ import annotations

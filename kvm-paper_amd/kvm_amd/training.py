@@ -23,8 +23,6 @@ Backward:
     pulls the snapshot-row gradients back through all of it to k, v (added
     to the window gradients), the gate and the ln_s_k parameters.
 
-``replay_snapshot_rows`` restates the snapshots in torch (fp32, differentiable)
-and serves as the reference the state kernel is tested against.
 """
 
 from __future__ import annotations
@@ -32,67 +30,8 @@ from __future__ import annotations
 import ctypes
 
 import torch
-import torch.nn.functional as F
 
 from . import _lib
-
-
-def replay_snapshot_rows(k, v, gate, ln_w, ln_b, plan, route_log, append_log, cfg):
-    """Attention rows of every snapshot, rebuilt in fp32 from the tokens and
-    the forward's routes (differentiable in k, v, gate, ln_w, ln_b).
-
-    k, v: [rows, T, D]; gate: [rows, T]; route_log / append_log:
-    [n_updates, rows, C] (slot of every overflow token; 1 if appended).
-    ``cfg`` carries eps, rope_partial_dim, gate_keys, gate_values,
-    gate_appends, gate_initial.  Returns a list of (k_rows, v_rows), one per
-    snapshot, each [rows, S_snapshot, D].  The state follows
-    model/kvm_mixer.py:434-447 (initial state), :231-248 (append) and
-    :321-340 (merge sums) with the routes given.
-    """
-    rows, T, D = k.shape
-    C = plan.chunk_len
-    r = int(cfg["rope_partial_dim"])
-    kz = torch.cat([torch.zeros_like(k[..., :r]), k[..., r:]], dim=-1)
-    prep = F.layer_norm(kz, (D,), ln_w, ln_b, cfg["eps"])
-    g = gate.unsqueeze(-1)
-    gk = prep * g if cfg["gate_keys"] else prep
-    gv = v * g if cfg["gate_values"] else v
-    ak, av = (gk, gv) if cfg["gate_appends"] else (prep, v)
-
-    def attn_rows(s_k, s_v, vlen):
-        return (F.layer_norm(s_k, (D,), ln_w, ln_b, cfg["eps"]),
-                F.normalize(s_v, dim=-1) * vlen.unsqueeze(-1))
-
-    L0 = plan.initial_state_len
-    s_k = (prep * g if cfg["gate_initial"] else prep)[:, :L0]
-    s_v = (v * g if cfg["gate_initial"] else v)[:, :L0]
-    vlen = v[:, :L0].norm(dim=-1)
-    snaps = [attn_rows(s_k, s_v, vlen)]
-    ridx = torch.arange(rows, device=k.device).unsqueeze(1)
-    for u in range(plan.n_updates):
-        tb, before, n_app = plan.upd_token_begin[u], plan.upd_state_before[u], plan.upd_n_append[u]
-        route = route_log[u].long()                 # [rows, C]
-        app = append_log[u].bool()
-        after = before + n_app
-        if n_app:
-            # Appended tokens take slots before .. after - 1 in token order.
-            tok = app.nonzero()[:, 1].view(rows, n_app) + tb
-            new_k = ak[ridx, tok]
-            new_v = av[ridx, tok]
-            s_k = torch.cat([s_k, new_k], dim=1)
-            s_v = torch.cat([s_v, new_v], dim=1)
-            vlen = torch.cat([vlen, new_v.norm(dim=-1)], dim=1)
-        merged = ~app
-        flat = (ridx * after + route).masked_select(merged)
-        tok_rows = (ridx * T + tb + torch.arange(C, device=k.device)).masked_select(merged)
-        dk = torch.zeros(rows * after, D, device=k.device, dtype=k.dtype).index_add(
-            0, flat, gk.reshape(rows * T, D).index_select(0, tok_rows))
-        dv = torch.zeros(rows * after, D, device=k.device, dtype=k.dtype).index_add(
-            0, flat, gv.reshape(rows * T, D).index_select(0, tok_rows))
-        s_k = s_k + dk.view(rows, after, D)
-        s_v = s_v + dv.view(rows, after, D)
-        snaps.append(attn_rows(s_k, s_v, vlen))
-    return snaps
 
 
 def attention_backward(mixer, q, k, v, gate, res, dout):
@@ -156,7 +95,11 @@ class KVMPrefillFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, mixer, q, k, v, gate, ln_w, ln_b, state_temp, front_temp):
         with torch.no_grad():
-            res = mixer.prefill_raw(q, k, v, gate, route_log=True, keep_snapshots=True, want_lse=True)
+            # No status read here (a host synchronisation per layer and step):
+            # the word is sticky, and the backward reads it once before using
+            # anything the forward produced.
+            res = mixer.prefill_raw(q, k, v, gate, route_log=True, keep_snapshots=True, want_lse=True,
+                                    check_status=False)
         ctx.mixer = mixer
         ctx.res = res
         ctx.save_for_backward(q, k, v, gate, ln_w, ln_b, state_temp, front_temp)
@@ -166,6 +109,7 @@ class KVMPrefillFunction(torch.autograd.Function):
     def backward(ctx, dout):
         q, k, v, gate, ln_w, ln_b, state_temp, front_temp = ctx.saved_tensors
         mixer, res = ctx.mixer, ctx.res
+        mixer.check_prefill_status()  # a timed-out update chain raises here, before its results are used
         plan = res["plan"]
         dq, dk_w, dv_w, d_snap_k, d_snap_v, d_ts, d_tf = attention_backward(mixer, q, k, v, gate, res, dout)
         if plan.n_chunks > mixer.config.n_bswa_chunks:  # some query chunk read the memory state
@@ -234,5 +178,5 @@ def prefill_with_grad(mixer, q, k, v, gate):
     return KVMPrefillFunction.apply(mixer, q, k, v, gate, mixer.ln_s_k.weight, mixer.ln_s_k.bias, ts, tf)
 
 
-__all__ = ["KVMPrefillFunction", "prefill_with_grad", "replay_snapshot_rows", "attention_backward",
+__all__ = ["KVMPrefillFunction", "prefill_with_grad", "attention_backward",
            "state_backward"]

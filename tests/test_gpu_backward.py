@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 import kvm_testlib as T
+from snapshot_replay import replay_snapshot_rows
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -117,20 +118,28 @@ def test_mixer_forward_trains_through_the_hip_prefill():
         assert float(p.grad.float().abs().max()) > 0, f"{name}: zero gradient"
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,C,Tn,mode,factor,gates", [
-    (1, 4, 2, 64, 64, 300, "fixed", 1.0, (1, 1, 0, 0)),
-    (2, 4, 2, 64, 64, 450, "power_law", 8.0, (1, 1, 0, 0)),
-    (1, 2, 1, 128, 128, 700, "power_law", 8.0, (1, 0, 1, 1)),
-    (1, 2, 2, 64, 32, 230, "fixed", 1.0, (1, 1, 0, 0)),  # chunks shorter than a 64-row block
+@pytest.mark.parametrize("B,Hq,Hkv,D,C,Tn,mode,factor,gates,extra", [
+    (1, 4, 2, 64, 64, 300, "fixed", 1.0, (1, 1, 0, 0), {}),
+    (2, 4, 2, 64, 64, 450, "power_law", 8.0, (1, 1, 0, 0), {}),
+    (1, 2, 1, 128, 128, 700, "power_law", 8.0, (1, 0, 1, 1), {}),
+    (1, 2, 2, 64, 32, 230, "fixed", 1.0, (1, 1, 0, 0), {}),  # chunks shorter than a 64-row block
+    # the saturation budget with state_round_down 16, GQA and two sinks
+    (2, 4, 2, 64, 64, 600, "kvm_saturation", 1.0, (1, 1, 1, 0),
+     {"sat_n": 500, "round_down": 16, "min_len": 1, "n_max": 8, "sink": 2}),
+    # kvm_use_head_temps 0 (no temperature parameters), two sinks, no merge gates
+    (2, 2, 2, 64, 64, 400, "fixed", 1.0, (0, 0, 0, 0), {"temps": False, "sink": 2}),
 ])
-def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gates):
+def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gates, extra):
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
     from kvm_amd import training
 
     gk_, gv_, ga_, gi_ = gates
-    T.log(f"[backward] B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn} {mode} gates {gates}")
-    cfg = T.mixer_config(Hq, Hkv, D, C, rope=16, mode=mode, min_len=C, n_max=4, factor=factor, expo=0.5,
+    temps = extra.get("temps", True)
+    T.log(f"[backward] B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn} {mode} gates {gates} {extra}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, rope=16, mode=mode, min_len=extra.get("min_len", C),
+                         n_max=extra.get("n_max", 4), factor=factor, expo=0.5, sat_n=extra.get("sat_n"),
+                         round_down=extra.get("round_down", 1), sink=extra.get("sink", 1), temps=temps,
                          gate_keys=gk_, gate_values=gv_, gate_appends=ga_, gate_initial=gi_)
     gen = torch.Generator().manual_seed(11)
     lnw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
@@ -150,24 +159,36 @@ def test_backward_matches_fp32_autograd(B, Hq, Hkv, D, C, Tn, mode, factor, gate
     y.backward(dout.to(DEV))
     torch.cuda.synchronize()
     hip = {"q": xs[0].grad, "k": xs[1].grad, "v": xs[2].grad, "gate": xs[3].grad,
-           "ln_w": m.ln_s_k.weight.grad, "ln_b": m.ln_s_k.bias.grad,
-           "tau_state": m.state_head_temp.grad, "tau_front": m.front_head_temp.grad}
+           "ln_w": m.ln_s_k.weight.grad, "ln_b": m.ln_s_k.bias.grad}
+    if temps:
+        hip.update(tau_state=m.state_head_temp.grad, tau_front=m.front_head_temp.grad)
+    else:
+        assert not hasattr(m, "state_head_temp") and not hasattr(m, "front_head_temp")
     # Routes of the HIP forward (deterministic: the same call again).
     with torch.no_grad():
         res = m.prefill_raw(*(t.to(DEV) for t in (q, k, v, g)), route_log=True)
     plan = res["plan"]
     if mode != "fixed":
         assert sum(plan.upd_n_append) > 0
-    # fp32 reference with the same routes
+    # Sinks are never merge targets.
+    merged = res["append_log"] == 0
+    assert bool((res["route_log"][merged] >= cfg.sink_len).all())
+    # fp32 reference with the same routes (temperatures 1, without gradient, when the mixer has none)
     f32 = [t.to(DEV).float().requires_grad_(True) for t in (q, k, v, g, lnw, lnb, tsh, tfh)]
+    if not temps:
+        f32[6], f32[7] = torch.ones(Hq, device=DEV), torch.ones(Hq, device=DEV)
     rcfg = {"rope": 16, "gate_keys": gk_, "gate_values": gv_, "gate_appends": ga_, "gate_initial": gi_}
     yr = fixed_route_forward(*f32, plan, res["route_log"], res["append_log"], rcfg, cfg.n_bswa_chunks)
     T.assert_close_bf16(y.detach().float().transpose(1, 2), yr.detach(), "forward vs fp32 fixed-route forward")
-    grads = torch.autograd.grad(yr.transpose(1, 2), f32, dout.to(DEV).float())
-    names = ["q", "k", "v", "gate", "ln_w", "ln_b", "tau_state", "tau_front"]
+    names = ["q", "k", "v", "gate", "ln_w", "ln_b"] + (["tau_state", "tau_front"] if temps else [])
+    grads = torch.autograd.grad(yr.transpose(1, 2), f32[:len(names)], dout.to(DEV).float(), allow_unused=True)
     worst = []
     for name, ref in zip(names, grads):
         got = hip[name].float()
+        if ref is None:  # an input the configuration does not use (the gate with every gate off)
+            assert float(got.abs().max()) == 0.0, f"d{name} should be zero"
+            worst.append(f"{name} unused (0)")
+            continue
         assert got.shape == ref.shape, f"{name}: {tuple(got.shape)} vs {tuple(ref.shape)}"
         err = (got - ref).abs()
         rmax = float(err.max() / ref.abs().max().clamp_min(1e-12))
@@ -226,7 +247,7 @@ def test_state_backward_matches_replay_autograd(B, Hkv, D, C, Tn, mode, gates):
     got = (dk.view(rows, Tn, D), dv.view(rows, Tn, D), dgate.view(rows, Tn), d_ln[0], d_ln[1])
     leaves = [x.float().requires_grad_(True) for x in (kd.reshape(rows, Tn, D), vd.reshape(rows, Tn, D),
                                                          gd.reshape(rows, Tn), lnw.to(DEV), lnb.to(DEV))]
-    snaps = training.replay_snapshot_rows(*leaves, plan, res["route_log"], res["append_log"], lcfg)
+    snaps = replay_snapshot_rows(*leaves, plan, res["route_log"], res["append_log"], lcfg)
     total = sum((ka * dsk[s, :, :ka.size(1)]).sum() + (va * dsv[s, :, :va.size(1)]).sum()
                 for s, (ka, va) in enumerate(snaps))
     ref = torch.autograd.grad(total, leaves)

@@ -144,3 +144,40 @@ def test_graph_decode_matches_eager_growing_state():
                 assert torch.equal(va, vb), f"layer {layer} {key} differs"
             else:
                 assert va == vb, f"layer {layer} {key}: {va} != {vb}"
+
+
+def test_graph_follows_weight_updates():
+    """A parameter updated in place between replays (its version counter
+    moves) makes DecodeGraph repack and recapture: every step's logits equal
+    an eager step's with the same weights, before and after the update."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd.backbone import DecodeGraph, StatesDictCache
+
+    B, Tp, n, s_upd = 2, 140, 40, 15
+    model = _model(11)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    prompt = torch.randint(0, 512, (B, Tp), device=DEV, generator=gen)
+    toks = torch.randint(0, 512, (n, B), device=DEV, generator=gen)
+    T.log(f"[decode-graph-weights] B{B} prompt {Tp}, {n} steps, weights updated in place at step {s_upd}")
+    with torch.no_grad():
+        caches = [StatesDictCache(), StatesDictCache()]
+        for c in caches:
+            model(input_ids=prompt, past_key_values=c, use_cache=True,
+                  cache_position=torch.arange(Tp, device=DEV), logits_to_keep=1)
+        runner = DecodeGraph(model, caches[1])
+        replays_before = 0
+        for s in range(n):
+            if s == s_upd:
+                replays_before = runner.replays
+                model.transformer.h[0].mlp.c_fc.weight.mul_(1.25)
+                model.lm_head.weight.mul_(0.75)
+            ref = model(input_ids=toks[s][:, None], past_key_values=caches[0], use_cache=True,
+                        cache_position=torch.tensor([Tp + s]), logits_to_keep=1).logits[:, -1].clone()
+            got = runner.step(toks[s]).clone()
+            d = float((got - ref).abs().max())
+            assert d == 0.0, f"step {s}: logits differ by {d:.3e} (replays {runner.replays})"
+        torch.cuda.synchronize()
+    T.log(f"[decode-graph-weights] {runner.replays} replays ({replays_before} before the update), "
+          f"{runner.eager_steps} eager steps")
+    assert replays_before >= 5 and runner.replays > replays_before + 5

@@ -139,6 +139,30 @@ def test_decode_step_argument_checks():
     assert call(plain, recent_len=9) == L.KVM_EINVAL and "outside the ring" in lib.kvm_last_error().decode()
 
 
+def test_add_norm_rejects_aliased_outputs():
+    """kvm_add_norm refuses, before any GPU work, an output that is x or y
+    when seq_len > 1 (the token shift reads the previous run's last row,
+    which an aliased output may already have overwritten); one token may be
+    updated in place."""
+    lib = _lib()
+    from kvm_amd import _lib as L
+
+    def call(seq_len, **out):
+        d = L.KvmAddNormDesc()
+        d.x, d.y, d.alpha, d.ln_w, d.ln_b, d.eps = 16, 32, 1.0, 48, 64, 1e-5
+        d.mix, d.prev = 80, 96
+        d.batch, d.seq_len, d.width = 2, seq_len, 128
+        for k, v in out.items():
+            setattr(d, k, v)
+        return lib.kvm_add_norm(ctypes.byref(d), None)
+
+    for field, ptr in (("out_x", 16), ("out_h", 32), ("out_shift", 16)):
+        assert call(8, **{field: ptr}) == L.KVM_EINVAL, field
+        assert "alias x or y" in lib.kvm_last_error().decode()
+    assert call(8, out_x=112, out_h=128, out_shift=144, state_out=96) == L.KVM_EINVAL
+    assert "state_out may alias prev" in lib.kvm_last_error().decode()
+
+
 def test_update_argument_checks():
     lib = _lib()
     from kvm_amd import _lib as L

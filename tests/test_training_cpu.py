@@ -1,6 +1,6 @@
 """CPU checks of the training path's host side.
 
-``kvm_amd.training.replay_snapshot_rows`` rebuilds the memory snapshots from
+``snapshot_replay.replay_snapshot_rows`` rebuilds the memory snapshots from
 the tokens and a forward's routes; the backward pulls the snapshot-row
 gradients through it.  Here it is fed the routes the CPU oracle chose and
 must reproduce the oracle's own state trajectory (fp32, every snapshot),
@@ -41,7 +41,7 @@ def _routes_from_oracle(rec, plan, rows, C):
 ])
 def test_replay_reproduces_the_oracle_state(mode, factor, gates):
     from kvm_amd.schedule import StateBudget, prefill_plan
-    from kvm_amd.training import replay_snapshot_rows
+    from snapshot_replay import replay_snapshot_rows
 
     B, Hq, Hkv, D, C, T = 2, 4, 2, 64, 32, 300
     gk, gv, ga, gi = gates
