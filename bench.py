@@ -23,9 +23,13 @@ Workloads:
            (`--e2e-decode` steps); reported in the "decoder_e2e" object.
 
 Prints ONE JSON line: value = prefill tokens/s; the decode figures are in
-the "decode" object.  roofline: achieved algorithmic FLOP/s (prefill
-attention kernel, bf16 MFMA) and bytes/s (decode attention), both timed with
-HIP events on the launch stream.  cpu_baseline: the CPU oracle (an eager
+the "decode" object.  roofline: achieved algorithmic FLOP/s of the prefill's
+dominant kernel (by event time: the update chain or the attention; both, and
+the whole path, are in roofline.per_kernel / roofline.whole_path) against
+the bf16 MFMA peak, and bytes/s of the decode attention against HBM, all
+timed with HIP events on the launch stream.  --evict also times every
+prefill after streaming 512 MiB (the reference's cache-eviction protocol).
+cpu_baseline: the CPU oracle (an eager
 restatement of the reference, pinned to it by golden fixtures) on a bounded
 sample of the prefill workload.
 """
@@ -133,6 +137,24 @@ def bench_prefill(args, torch, kvm_amd):
             mixer.prefill_raw(q, k, v, g, plan=plan, events=evs[i], check_status=False)
         torch.cuda.synchronize()
         mixer.check_prefill_status()
+        # Optional cache-evicting timing (the reference's protocol,
+        # scripts/kvm_benchmark/common.py:283-295): a 512 MiB buffer is
+        # streamed before every timed prefill, outside its event pair.
+        evict_ms = None
+        if getattr(args, "evict", False):
+            flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+            pairs = []
+            for i in range(args.steps):
+                flush.add_(1)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                mixer.prefill_raw(q, k, v, g, plan=plan, check_status=False)
+                b.record()
+                pairs.append((a, b))
+            torch.cuda.synchronize()
+            mixer.check_prefill_status()
+            evict_ms = sum(a.elapsed_time(b) for a, b in pairs) / args.steps
+            del flush
     ms = start.elapsed_time(end) / args.steps
     attn_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
     chain_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
@@ -140,6 +162,7 @@ def bench_prefill(args, torch, kvm_amd):
     route_flop = 2 * D * H * B * routing_pairs(plan)
     return dict(
         ms=ms, wall_ms=wall * 1e3 / args.steps, tok_s=B * T / (ms * 1e-3), attn_ms=attn_ms, chain_ms=chain_ms,
+        evict_ms=evict_ms,
         attn_flop=attn_flop, route_flop=route_flop, plan=plan, inputs=(q, k, v, g), mixer=mixer,
     )
 
@@ -440,6 +463,9 @@ def main():
                     help="run one workload (profiling); 'copy' streams a known number of bytes "
                          "through a plain device copy to calibrate the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--evict", action="store_true",
+                    help="also time every prefill after streaming 512 MiB through the caches (the reference's "
+                         "protocol); reported as prefill.evicted_ms_per_step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -471,7 +497,8 @@ def main():
     print("bench: prefill config 2 ...", file=sys.stderr, flush=True)
     pf = bench_prefill(args, torch, kvm_amd)
     if args.only == "prefill":
-        print(json.dumps({"ms": pf["ms"], "attention_ms": pf["attn_ms"], "chain_ms": pf["chain_ms"]}))
+        print(json.dumps({"ms": pf["ms"], "attention_ms": pf["attn_ms"], "chain_ms": pf["chain_ms"],
+                          "evicted_ms": pf["evict_ms"]}))
         return
     if args.only == "backward":
         print(json.dumps(bench_backward(args, torch, kvm_amd, pf)))
@@ -506,7 +533,23 @@ def main():
     if not args.skip_cpu:
         print("bench: cpu baseline ...", file=sys.stderr, flush=True)
         cpu = cpu_baseline(torch, args.cpu_sample)
+    # Per-kernel rooflines of the prefill (algorithmic FLOP of the launch over
+    # its event time), the dominant kernel's as the line's `roofline`, and
+    # the whole path's.
     attn_achieved = pf["attn_flop"] / (pf["attn_ms"] * 1e-3)
+    chain_achieved = pf["route_flop"] / (pf["chain_ms"] * 1e-3)
+    path_achieved = (pf["attn_flop"] + pf["route_flop"]) / (pf["ms"] * 1e-3)
+    per_kernel = {
+        "k_attn_prefill": {"bound": "mfma", "ms": round(pf["attn_ms"], 4), "flop": pf["attn_flop"],
+                           "achieved": round(attn_achieved / 1e12, 2), "frac": round(attn_achieved / PEAK_BF16_FLOPS, 4),
+                           "traffic": measured_traffic("k_attn_prefill", "config2")},
+        "k_chain_fixed": {"bound": "mfma (latency of the update recurrence in practice)", "ms": round(pf["chain_ms"], 4),
+                          "flop": pf["route_flop"], "achieved": round(chain_achieved / 1e12, 2),
+                          "frac": round(chain_achieved / PEAK_BF16_FLOPS, 4),
+                          "traffic": measured_traffic("k_chain_fixed", "config2")},
+    }
+    dominant = max(per_kernel, key=lambda n: per_kernel[n]["ms"])
+    dk = per_kernel[dominant]
     line = {
         "metric": "KVM prefill tokens/s @32K and decode tokens/s @128K; % MFMA/HBM roofline",
         "value": round(pf["tok_s"], 1),
@@ -529,11 +572,16 @@ def main():
             "whole_path_frac_of_mfma_peak": round((pf["attn_flop"] + pf["route_flop"]) / (pf["ms"] * 1e-3) / PEAK_BF16_FLOPS, 4),
         },
         "roofline": {
-            "bound": "mfma", "kernel": "k_attn_prefill", "achieved": round(attn_achieved / 1e12, 2),
-            "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s", "frac": round(attn_achieved / PEAK_BF16_FLOPS, 4),
-            "traffic": measured_traffic("k_attn_prefill", "config2"),
+            "bound": "mfma", "kernel": dominant, "achieved": dk["achieved"],
+            "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s", "frac": dk["frac"], "traffic": dk["traffic"],
+            "per_kernel": per_kernel,
+            "whole_path": {"achieved": round(path_achieved / 1e12, 2), "frac": round(path_achieved / PEAK_BF16_FLOPS, 4),
+                           "ms": round(pf["ms"], 4), "flop": pf["attn_flop"] + pf["route_flop"]},
         },
     }
+    if pf["evict_ms"] is not None:
+        line["prefill"]["evicted_ms_per_step"] = round(pf["evict_ms"], 4)
+        line["prefill"]["evicted_tokens_per_s"] = round(32768 / (pf["evict_ms"] * 1e-3), 1)
     if dec is not None:
         bw = dec["bytes"] / (dec["attn_ms"] * 1e-3)
         line["decode"] = {

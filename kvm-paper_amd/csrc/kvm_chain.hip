@@ -344,7 +344,7 @@ struct RawTok {
 template <int D>
 __global__ __launch_bounds__(kChainThreads) void k_chain(
     kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
-    ChainScratch cs, int rows, int G, int tpw, int spm_max, int32_t *route_log,
+    ChainScratch cs, int rows, int row0, int nrows, int G, int tpw, int spm_max, int32_t *route_log,
     int32_t *append_log, int64_t log_stride) {
   constexpr int GL = D / 8;                 // lanes per D-wide row
   constexpr int STR = D + 8;                // LDS row stride (elements)
@@ -372,13 +372,13 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
   const int tid = threadIdx.x, part = tid % GL;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int member = q % G, group = (q / G) * 8 + xcd;
-  if (group >= rows) return;
+  if (group >= nrows) return;
   for (int d = tid; d < D; d += kChainThreads) {
     ln_w[d] = static_cast<const float *>(L.ln_weight)[d];
     ln_b[d] = static_cast<const float *>(L.ln_bias)[d];
   }
   __syncthreads();
-  const int row = group;
+  const int row = row0 + group;  // this launch serves rows row0 .. row0 + nrows - 1
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int t0 = member * tpw;
   const int ntk = max(0, min(n_tok, t0 + tpw) - t0);
@@ -744,7 +744,8 @@ __device__ __forceinline__ int own_local_to_slot(int l, int G, int m) {
 template <int D, int GM>  // GM: the group size G (8 or 16)
 __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
-    ChainScratch cs, int rows, int32_t *route_log, int32_t *append_log, int64_t log_stride) {
+    ChainScratch cs, int rows, int row0, int nrows, int32_t *route_log, int32_t *append_log,
+    int64_t log_stride) {
   constexpr int GL = D / 8;                 // lanes per D-wide row
   constexpr int STR = D + 8;                // LDS row stride of key rows (elements)
   constexpr int KS = D / 32;
@@ -769,8 +770,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = tid % GL;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int member = q % G, group = (q / G) * 8 + xcd;
-  if (group >= rows) return;
-  const int row = group;
+  if (group >= nrows) return;
+  const int row = row0 + group;  // this launch serves rows row0 .. row0 + nrows - 1
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int64_t rb = int64_t(row) * n_tok;
   const int64_t buf_stride = int64_t(rows) * n_tok * D;  // elements between merge buffers
@@ -1303,13 +1304,17 @@ bool chain_plan(const kvm_layer &L, int64_t n_tok, int64_t max_slots, ChainPlan 
   const int64_t rows = L.batch * L.kv_heads;
   const int64_t groups = (rows + 7) / 8 * 8;
   int G = groups * 16 <= limit ? 16 : 8;
+  // More rows than one launch keeps resident: consecutive launches over
+  // batches of rows (a multiple of 8, one group per XCD each).
+  const int64_t batch_groups = std::min<int64_t>(groups, limit / G / 8 * 8);
   const int64_t tpw = ((n_tok + G - 1) / G + 15) / 16 * 16;
-  if (tpw > kChainTok || groups * G > limit || n_tok < 1) return false;
+  if (tpw > kChainTok || batch_groups < 8 || n_tok < 1) return false;
   p->fixed = false;
   p->G = G;
   p->tpw = int(tpw);
   p->spm_max = int((max_slots + G - 1) / G);
-  p->workgroups = int(groups * G);
+  p->row_batch = int(batch_groups);
+  p->workgroups = int(batch_groups * G);
   const int64_t dyn = (4 * n_tok + 3 * int64_t(p->spm_max)) * 4;
   if (dyn > 48 * 1024) return false;
   p->dyn_lds = size_t(dyn);
@@ -1365,37 +1370,40 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
                         const ChainScratch &cs, const ChainPlan &p, int32_t *route_log,
                         int32_t *append_log, hipStream_t stream) {
   if (list.count <= 0) return hipSuccess;
-  // Barrier counters and the abort flag start at zero in every launch.
-  hipError_t e = launch_fill_u32(cs.bar, kChainMaxWorkgroups * kCounterStride + 64, 0u, stream);
-  if (e != hipSuccess) return e;
   const int rows = int(L.batch * L.kv_heads);
   const int64_t log_stride = int64_t(rows) * n_tok;
-  if (p.fixed && chain_fixed_ok(p, list, n_tok)) {
-    const dim3 grid(p.workgroups), blk(kChainThreads);
-    const int nt = int(n_tok);
-    if (L.head_dim == 128 && p.G == 8)
-      hipLaunchKernelGGL((k_chain_fixed<128, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
-                         cs, rows, route_log, append_log, log_stride);
-    else if (L.head_dim == 128)
-      hipLaunchKernelGGL((k_chain_fixed<128, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
-                         cs, rows, route_log, append_log, log_stride);
-    else if (p.G == 8)
-      hipLaunchKernelGGL((k_chain_fixed<64, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
-                         cs, rows, route_log, append_log, log_stride);
-    else
-      hipLaunchKernelGGL((k_chain_fixed<64, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list,
-                         cs, rows, route_log, append_log, log_stride);
-    return hipGetLastError();
+  const bool fixed = p.fixed && chain_fixed_ok(p, list, n_tok);
+  for (int row0 = 0; row0 < rows; row0 += p.row_batch) {
+    const int nrows = std::min(p.row_batch, rows - row0);
+    // Barrier counters and the abort flag start at zero in every launch.
+    hipError_t e = launch_fill_u32(cs.bar, kChainMaxWorkgroups * kCounterStride + 64, 0u, stream);
+    if (e != hipSuccess) return e;
+    const dim3 grid(unsigned((nrows + 7) / 8 * 8 * p.G)), blk(kChainThreads);
+    if (fixed) {
+      const int nt = int(n_tok);
+      if (L.head_dim == 128 && p.G == 8)
+        hipLaunchKernelGGL((k_chain_fixed<128, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
+                           row0, nrows, route_log, append_log, log_stride);
+      else if (L.head_dim == 128)
+        hipLaunchKernelGGL((k_chain_fixed<128, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
+                           row0, nrows, route_log, append_log, log_stride);
+      else if (p.G == 8)
+        hipLaunchKernelGGL((k_chain_fixed<64, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
+                           row0, nrows, route_log, append_log, log_stride);
+      else
+        hipLaunchKernelGGL((k_chain_fixed<64, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
+                           row0, nrows, route_log, append_log, log_stride);
+    } else if (L.head_dim == 128) {
+      hipLaunchKernelGGL(k_chain<128>, grid, blk, p.dyn_lds, stream, L, src, int(n_tok), st, snaps, list, cs,
+                         rows, row0, nrows, p.G, p.tpw, p.spm_max, route_log, append_log, log_stride);
+    } else {
+      hipLaunchKernelGGL(k_chain<64>, grid, blk, p.dyn_lds, stream, L, src, int(n_tok), st, snaps, list, cs,
+                         rows, row0, nrows, p.G, p.tpw, p.spm_max, route_log, append_log, log_stride);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
-  if (L.head_dim == 128)
-    hipLaunchKernelGGL(k_chain<128>, dim3(p.workgroups), dim3(kChainThreads), p.dyn_lds, stream, L,
-                       src, int(n_tok), st, snaps, list, cs, rows, p.G, p.tpw, p.spm_max,
-                       route_log, append_log, log_stride);
-  else
-    hipLaunchKernelGGL(k_chain<64>, dim3(p.workgroups), dim3(kChainThreads), p.dyn_lds, stream, L,
-                       src, int(n_tok), st, snaps, list, cs, rows, p.G, p.tpw, p.spm_max,
-                       route_log, append_log, log_stride);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 }  // namespace kvm

@@ -117,7 +117,8 @@ struct ChainPlan {
   int G;          // workgroups per row
   int tpw;        // tokens per workgroup (multiple of 16, <= 64)
   int spm_max;    // slots per workgroup at max_slots
-  int workgroups;
+  int row_batch;  // rows per launch (all rows, or batches of them when they do not fit at once)
+  int workgroups; // per launch
   size_t dyn_lds;
 };
 // False when the shape does not fit the chain (the per-update kernels then run).

@@ -673,6 +673,9 @@ def test_prefill_wide_chunks_match_oracle(lib, B, Hq, Hkv, Tn, D, C, mode):
     (1, 4, 2, 2000, 128, 100, "power_law", 3, 1, None),
     (1, 32, 32, 8192, 128, 512, "fixed", 1, 0, None),
     (1, 4, 4, 6000, 64, 256, "power_law", 2, 0, 3),
+    # more rows than one launch keeps resident (45 rows: launches over rows 0-31 and 32-44)
+    (9, 10, 5, 2600, 128, 512, "fixed", 1, 0, None),
+    (9, 5, 5, 1500, 64, 128, "power_law", 2, 0, None),
 ])
 def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C, mode, sink, gate_app,
                                           budget):
