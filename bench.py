@@ -366,16 +366,83 @@ def bench_e2e(args, torch, kvm_amd):
         torch.cuda.synchronize()
         return e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
 
+    def breakdown():
+        """One more prefill with HIP events around each stage of every layer
+        (separate from the timed run): the mixer's projections + fused
+        prefix, its KVM prefill (update chain / per-update kernels, then the
+        attention launches, from kvm_prefill's own event marks), its output
+        projection (the rest of the mixer), the MLP (hipBLASLt GEMMs +
+        relu^2) and the fused residual-add + LayerNorm launches; "other" is
+        the rest of the prefill (embedding, LM head on the last token)."""
+        import kvm_amd.backbone as bb
+
+        rec = {k: [] for k in ("mixer", "prefix", "kvm", "mlp", "add_norm")}
+        ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+        def timed(fn, key):
+            def w(*a, **kw):
+                e0, e1 = ev(), ev()
+                e0.record()
+                r = fn(*a, **kw)
+                e1.record()
+                rec[key].append((e0, e1))
+                return r
+            return w
+
+        def kvm_timed(fn):
+            def w(*a, **kw):
+                es = [ev() for _ in range(4)]
+                for e in es:  # every event recorded once, whatever the call marks
+                    e.record()
+                kw["events"] = es
+                r = fn(*a, **kw)
+                rec["kvm"].append(es)
+                return r
+            return w
+
+        saved_add_norm = bb._add_norm
+        for blk in model.transformer.h:
+            m = blk.attn
+            m.forward_inference = timed(m.forward_inference, "mixer")
+            m.forward_prefix = timed(m.forward_prefix, "prefix")
+            m.prefill_raw = kvm_timed(m.prefill_raw)
+            blk.mlp.ffn = timed(blk.mlp.ffn, "mlp")
+        bb._add_norm = timed(saved_add_norm, "add_norm")
+        try:
+            cache = StatesDictCache()
+            e0, e1 = ev(), ev()
+            torch.cuda.synchronize()
+            e0.record()
+            model(input_ids=ids, past_key_values=cache, use_cache=True,
+                  cache_position=torch.arange(T, device="cuda"), logits_to_keep=1)
+            e1.record()
+            torch.cuda.synchronize()
+        finally:
+            bb._add_norm = saved_add_norm
+            for blk in model.transformer.h:
+                for name in ("forward_inference", "forward_prefix", "prefill_raw"):
+                    blk.attn.__dict__.pop(name, None)
+                blk.mlp.__dict__.pop("ffn", None)
+        tot = lambda key: sum(a.elapsed_time(b) for a, b in rec[key])  # noqa: E731
+        upd = sum(es[0].elapsed_time(es[1]) for es in rec["kvm"])
+        att = sum(es[2].elapsed_time(es[3]) for es in rec["kvm"])
+        total = e0.elapsed_time(e1)
+        mixer, prefix, mlp, an = tot("mixer"), tot("prefix"), tot("mlp"), tot("add_norm")
+        return {"total": total, "mixer_projections_and_prefix": prefix, "kvm_updates": upd,
+                "kvm_attention": att, "mixer_output_projection_and_rest": mixer - prefix - upd - att,
+                "mlp": mlp, "add_norm": an, "other": total - mixer - mlp - an}
+
     n_eager = min(n_dec, args.e2e_eager_steps)
     with torch.no_grad():
         run(8, True)
         pre_ms, dec_ms = run(n_dec, True)
         eager_ms = run(n_eager, False)[1] if n_eager > 0 else None
+        stages = breakdown()
     del model
     torch.cuda.empty_cache()
     return dict(prefill_ms=pre_ms, prefill_tok_s=B * T / (pre_ms * 1e-3), decode_ms_per_step=dec_ms / n_dec,
                 decode_tok_s=B * n_dec / (dec_ms * 1e-3), decode_steps=n_dec, decode_path="hip_graph",
-                eager_decode_ms_per_step=eager_ms / n_eager if n_eager > 0 else None)
+                eager_decode_ms_per_step=eager_ms / n_eager if n_eager > 0 else None, prefill_stages_ms=stages)
 
 
 def _cpu_prefill_inputs(torch, B, H, D, T, dtype, seed):
@@ -622,6 +689,7 @@ def main():
             "decode_path": e2e["decode_path"],
             "eager_decode_ms_per_step": (round(e2e["eager_decode_ms_per_step"], 3)
                                          if e2e["eager_decode_ms_per_step"] is not None else None),
+            "prefill_stages_ms": {k: round(v, 2) for k, v in e2e["prefill_stages_ms"].items()},
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
