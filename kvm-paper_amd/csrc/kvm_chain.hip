@@ -726,9 +726,17 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 // needs.  Seeing member m's partials of update p therefore also shows that
 // m's prepared rows of update p + 1 are readable, and that m has finished
 // reading every buffer of update p - 1 (so they may be overwritten).
-// Merge keys / values rotate through three buffers (prepared one phase
+// Merge keys / values rotate through four buffers (prepared one phase
 // ahead, read by route and, a phase later, by the merge); partials
-// alternate between two.  The raw tokens a prep needs are loaded at the
+// alternate between two.  Four, not three: a member starts the prep of
+// update p + 1 (into buffer (p + 1) % 4) before it has seen the partials of
+// update p - 1, so another member may still be in phase p - 1, gathering
+// the rows of update p - 2 and loading route operands of update p - 1,
+// while a member already in phase p + 1 may be preparing update p + 2; with
+// three buffers update p + 1 would share the buffer of update p - 2.  The
+// two partial buffers suffice: a member publishes update p only after it
+// has seen every member's partials of update p - 1, by which time every
+// member has stopped polling those of update p - 2.  The raw tokens a prep needs are loaded at the
 // end of the phase before; the route operands of update p are loaded once
 // the merge's gathered rows have arrived, so they never queue in L2 ahead
 // of the gathers.
@@ -840,7 +848,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   };
   // prep (model/kvm_mixer.py:120-129, model/kvm_triton_mixer.py:429-446):
   // merge key / value rows of pass `it` over my share of an update's tokens
-  // (packed bf16), and their store into merge buffer i % 3.
+  // (packed bf16), and their store into merge buffer i % 4.
   auto prep_row = [&](const RawTok<D> &rt, int it, uint4 &pk, uint4 &pv) __attribute__((always_inline)) {
     float k[8], v[8];
     unpack8(rt.k[it], k);
@@ -859,7 +867,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   auto prep_store = [&](int i, int it, const uint4 &pk, const uint4 &pv) __attribute__((always_inline)) {
     const int lt = (tid + it * kChainThreads) / GL;
     if (lt < pnt) {
-      const int64_t o = (i % 3) * buf_stride + (rb + pt0 + lt) * D + part * 8;
+      const int64_t o = (i % 4) * buf_stride + (rb + pt0 + lt) * D + part * 8;
       *reinterpret_cast<uint4 *>(cs.gk + o) = pk;
       *reinterpret_cast<uint4 *>(cs.gv + o) = pv;
     }
@@ -903,7 +911,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     uint4 bx[4][KS];
     auto load_bx = [&](int tt0, int tt1, int ks0, int ks1) __attribute__((always_inline)) {
       const __amdgpu_buffer_rsrc_t gr =
-          l2_rsrc(cs.gk + (p % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(cs.gk + (p % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
 #pragma unroll
       for (int tt = tt0; tt < tt1; ++tt)
 #pragma unroll
@@ -1031,9 +1039,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // rows are staged in LDS (all loads of a chunk in flight together),
       // then each slot sums its rows in token order.
       const __amdgpu_buffer_rsrc_t gkr =
-          l2_rsrc(cs.gk + (pi % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(cs.gk + (pi % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
       const __amdgpu_buffer_rsrc_t gvr =
-          l2_rsrc(cs.gv + (pi % 3) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(cs.gv + (pi % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
       float sk[SP][8], sv[SP][8];
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp)
@@ -1333,9 +1341,9 @@ bool chain_fixed_ok(const ChainPlan &p, const ChainList &list, int64_t n_tok) {
 int64_t chain_scratch_bytes(const kvm_layer &L, int64_t n_tok) {
   const size_t tok = size_t(L.batch * L.kv_heads) * size_t(n_tok);
   auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
-  // three merge buffers of keys, three of values (buffer b at gk + b * rows * n_tok * D),
+  // four merge buffers of keys, four of values (buffer b at gk + b * rows * n_tok * D),
   // routes, novelty, two sets of per-member maxima (up to 16 members), counters
-  return int64_t(2 * a256(3 * tok * size_t(L.head_dim) * 2) + 2 * a256(tok * 4) +
+  return int64_t(2 * a256(4 * tok * size_t(L.head_dim) * 2) + 2 * a256(tok * 4) +
                  a256(2 * tok * 16 * 8) +
                  a256(size_t(kChainMaxWorkgroups) * kCounterStride * 4 + 256));
 }
@@ -1346,13 +1354,13 @@ ChainScratch carve_chain_scratch(void *base, const kvm_layer &L, int64_t n_tok) 
   unsigned char *p = static_cast<unsigned char *>(base);
   ChainScratch c;
   const size_t kb = tok * size_t(L.head_dim) * 2, ib = a256(tok * 4);
-  const size_t kb3 = a256(3 * kb), pb = a256(2 * tok * 16 * 8);
+  const size_t kb4 = a256(4 * kb), pb = a256(2 * tok * 16 * 8);
   c.gk = reinterpret_cast<uint16_t *>(p);
-  c.gv = reinterpret_cast<uint16_t *>(p + kb3);
-  c.route = reinterpret_cast<int32_t *>(p + 2 * kb3);
-  c.nov = reinterpret_cast<float *>(p + 2 * kb3 + ib);
-  c.part = reinterpret_cast<uint2 *>(p + 2 * kb3 + 2 * ib);
-  c.bar = reinterpret_cast<unsigned *>(p + 2 * kb3 + 2 * ib + pb);
+  c.gv = reinterpret_cast<uint16_t *>(p + kb4);
+  c.route = reinterpret_cast<int32_t *>(p + 2 * kb4);
+  c.nov = reinterpret_cast<float *>(p + 2 * kb4 + ib);
+  c.part = reinterpret_cast<uint2 *>(p + 2 * kb4 + 2 * ib);
+  c.bar = reinterpret_cast<unsigned *>(p + 2 * kb4 + 2 * ib + pb);
   c.abort_flag = c.bar + size_t(kChainMaxWorkgroups) * kCounterStride;
   c.status = nullptr;  // set by the caller
   c.max_polls = kChainDefaultPolls;

@@ -716,6 +716,56 @@ def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C
     T.log(f"[chain] {plan.n_updates} updates, S={S}, {n_app} appended tokens: identical")
 
 
+@pytest.mark.parametrize("B,Hkv,Tn,D,C", [
+    (4, 8, 8192, 128, 512),  # 32 rows: one launch
+    (9, 5, 4096, 64, 256),   # 45 rows: two row batches
+])
+def test_chain_skewed_routes_match_per_update_kernels(lib, monkeypatch, B, Hkv, Tn, D, C):
+    """Keys close to one shared direction send most of a chunk's tokens to
+    the slots of one or two members of the slot-owner chain (which member
+    changes from update to update), so members run far apart in time; the
+    chain must still equal the barrier-synchronised per-update kernels
+    bit for bit, on every one of three runs.  (A merge buffer reused one
+    update too early showed up only under such skew.)"""
+    Hq = Hkv
+    T.log(f"[chain-skew] B{B} Hkv{Hkv} T{Tn} D{D} C{C}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="fixed", sink=1, min_len=C, n_max=4, factor=6.0)
+    gen = torch.Generator().manual_seed(3)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, torch.ones(Hq), torch.ones(Hq))
+    q, _, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 29)
+    d = torch.randn(D, generator=gen)
+    k = (d / d.norm() + 0.02 * torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16()
+    q, k, v, g = (t.to(DEV) for t in (q, k, v, g))
+    plan = m.make_plan(Tn)
+    S = plan.final_state_len
+    keys = ("route_log", "out", "state_k", "state_v", "state_vlen", "state_k_attn", "state_v_attn")
+    monkeypatch.setenv("KVM_AMD_CHAIN", "0")
+    with torch.no_grad():
+        ref = m.prefill_raw(q, k, v, g, route_log=True)
+    torch.cuda.synchronize()
+    # the skew this test depends on: the busiest member's share of a row's chunk, averaged
+    G = 8
+    r = ref["route_log"][: plan.n_updates].long()
+    mem = torch.where(r >= 0, (r // 16) % G, G).flatten(0, 1)  # [update * row, token]
+    counts = torch.stack([torch.bincount(x, minlength=G + 1)[:G] for x in mem.cpu()])
+    busiest = float(counts.max(dim=1).values.float().mean()) / C
+    T.log(f"[chain-skew] {plan.n_updates} updates, S={S}; the busiest member takes {busiest:.0%} of a chunk on average")
+    assert busiest >= 0.4, f"inputs did not skew the routes (busiest member {busiest:.0%})"
+    monkeypatch.setenv("KVM_AMD_CHAIN", "1")
+    monkeypatch.setenv("KVM_AMD_CHAIN_FIXED", "1")
+    for run in range(3):
+        with torch.no_grad():
+            a = m.prefill_raw(q, k, v, g, route_log=True)
+        torch.cuda.synchronize()
+        for key in keys:
+            x, y = a[key], ref[key]
+            if key.startswith("state"):
+                x, y = x[:, :S], y[:, :S]
+            assert torch.equal(x, y), f"run {run}: {key}"
+
+
 @pytest.mark.parametrize("Tn", [1, 5, 63, 64, 65, 128, 129, 191, 300])
 def test_prefill_ragged_lengths_match_oracle(lib, Tn):
     """Prompt lengths around the chunk and window boundaries (C = 64, window
