@@ -224,6 +224,38 @@ def load(path: str | os.PathLike | None = None):
     return lib
 
 
+OPS_PATH = Path(__file__).resolve().parent / "libkvm_amd_torch.so"
+_OPS = None
+
+
+def ops():
+    """``torch.ops.kvm_amd``: the torch operators (``prefill``,
+    ``decode_step``) over libkvm_amd.so (csrc/kvm_torch_ops.cpp); loaded
+    once, after the C library's ABI check.  Raises if it is not built."""
+    global _OPS
+    if _OPS is None:
+        load()
+        if not OPS_PATH.exists():
+            raise KvmLibraryError(
+                f"{OPS_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`; "
+                "there is no CPU fallback")
+        torch.ops.load_library(str(OPS_PATH))
+        _OPS = torch.ops.kvm_amd
+    return _OPS
+
+
+def call_op(op, *args):
+    """Call a torch operator of the library: invalid arguments stay
+    ValueError, any other failure it reports becomes KvmLibraryError (a
+    RuntimeError, the reference's type for device-level errors)."""
+    try:
+        return op(*args)
+    except ValueError:
+        raise
+    except RuntimeError as e:
+        raise KvmLibraryError(str(e)) from e
+
+
 def check(rc: int, what: str):
     """Raise the reference's exception type for a failed call."""
     if rc == KVM_OK:

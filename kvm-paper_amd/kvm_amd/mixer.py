@@ -107,9 +107,18 @@ class _LayerHandle:
     def ref(self):
         return ctypes.byref(self.struct)
 
+    def op_args(self):
+        """(cfg integers, ln_eps, ln_w, ln_b, state_temp, front_temp): the
+        layer as the torch operators take it (csrc/kvm_torch_ops.cpp)."""
+        s = self.struct
+        cfg = [s.batch, s.q_heads, s.kv_heads, s.head_dim, s.value_dim, s.chunk_len, s.n_bswa_chunks,
+               s.sink_len, s.rope_partial_dim, s.gate_keys, s.gate_values, s.gate_appends, s.gate_initial]
+        return (cfg, float(s.ln_eps), *self.keep)
 
-# The schedule's int32 arrays of a plan as ctypes arrays, made once per plan
-# object (a prefill loop that passes one plan pays the conversion once).
+
+# The schedule's int32 arrays of a plan as ctypes arrays (and as one host
+# int32 tensor for the torch operator), made once per plan object (a
+# prefill loop that passes one plan pays the conversion once).
 _PLAN_ARRAYS: dict[int, tuple] = {}
 
 
@@ -117,8 +126,10 @@ def _plan_arrays(plan: PrefillPlan) -> list:
     hit = _PLAN_ARRAYS.get(id(plan))
     if hit is not None and hit[0]() is plan:
         return hit[1]
-    arrs = [_lib.int32_array(a) for a in (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin,
-                                           plan.upd_state_before, plan.upd_n_append)]
+    parts = (plan.chunk_state_len, plan.chunk_snapshot, plan.upd_token_begin, plan.upd_state_before,
+             plan.upd_n_append)
+    arrs = [_lib.int32_array(a) for a in parts]
+    arrs.append(torch.tensor([int(x) for a in parts for x in a], dtype=torch.int32))
     pid = id(plan)
     _PLAN_ARRAYS[pid] = (weakref.ref(plan), arrs)
     weakref.finalize(plan, _PLAN_ARRAYS.pop, pid, None)
@@ -657,9 +668,9 @@ class SequenceMixer(nn.Module):
             "state_k_attn": torch.empty(rows, cap, D, **bf), "state_v_attn": torch.empty(rows, cap, D, **bf),
         }
         qv = _lib._bf16_view(q, "q")
-        seq, keep = _lib.seq4(k, v, merge_gate)
-        layer = self._layer_struct(B, dev)
-        lib = _lib.load()
+        kv, vv = _lib._bf16_view(k, "k"), _lib._bf16_view(v, "v")
+        gv = merge_gate if merge_gate.dtype == torch.bfloat16 else merge_gate.to(torch.bfloat16)
+        cfg, eps, w, b, ts, tf = self._layer_struct(B, dev).op_args()
         n_snaps = plan.n_updates + 1
         per_snap = 2 * rows * plan.max_state_len * D * 2
         budget = _SNAPSHOT_BUDGET if snapshot_budget is None else int(snapshot_budget)
@@ -672,43 +683,19 @@ class SequenceMixer(nn.Module):
             extra["snap_v"] = torch.empty(shape, **bf)
         if want_lse:
             extra["lse"] = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
-        arrs = _plan_arrays(plan)
-        d = _lib.KvmPrefillDesc()
-        d.layer = layer.struct
-        d.q, d.q_sb, d.q_sh, d.q_st = qv.data_ptr(), qv.stride(0), qv.stride(1), qv.stride(2)
-        d.kv = seq
-        d.seq_len = int(T)
-        d.out, d.o_sb, d.o_st, d.o_sh = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
-        d.state = _lib.state_struct(st["state_k"], st["state_v"], st["state_vlen"], st["state_k_attn"],
-                                    st["state_v_attn"], cap)
-        d.n_chunks = plan.n_chunks
-        d.chunk_state_len, d.chunk_snapshot = arrs[0], arrs[1]
-        d.n_updates = plan.n_updates
-        d.upd_token_begin, d.upd_state_before, d.upd_n_append = arrs[2], arrs[3], arrs[4]
-        d.max_state_len = plan.max_state_len
-        d.snapshot_ring = ring
-        if keep_snapshots:
-            d.snap_k, d.snap_v = extra["snap_k"].data_ptr(), extra["snap_v"].data_ptr()
-        if want_lse:
-            d.lse = extra["lse"].data_ptr()
-        nbytes = int(lib.kvm_prefill_workspace_bytes(ctypes.byref(d)))
-        if nbytes < 0:
-            raise ValueError("invalid prefill descriptor: " + lib.kvm_last_error().decode())
-        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
-        d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
         logs = {}
         if route_log:
             n = max(plan.n_updates, 1)
             logs["route_log"] = torch.full((n, rows, self.chunk_len), -1, device=dev, dtype=torch.int32)
             logs["append_log"] = torch.zeros((n, rows, self.chunk_len), device=dev, dtype=torch.int32)
-            d.route_log, d.append_log = logs["route_log"].data_ptr(), logs["append_log"].data_ptr()
-        ev_arr = None
-        if events is not None:
-            ev_arr = (ctypes.c_void_p * 4)(*[e.cuda_event if e is not None else None for e in events])
-            d.events = ctypes.cast(ev_arr, ctypes.c_void_p)
-        d.status = None if check_status is None else self._status_word(dev).data_ptr()
-        _lib.check(lib.kvm_prefill(ctypes.byref(d), _lib.stream_handle(dev)), "kvm_prefill")
-        del keep, ws
+        ev = [] if events is None else [int(e.cuda_event) if e is not None else 0 for e in events]
+        status = None if check_status is None else self._status_word(dev)
+        # One torch operator (csrc/kvm_torch_ops.cpp) over kvm_prefill, on the
+        # current stream; it sizes and allocates the workspace itself.
+        _lib.call_op(_lib.ops().prefill, qv, kv, vv, gv, w, b, ts, tf, cfg, eps, _plan_arrays(plan)[5],
+                     plan.n_chunks, plan.n_updates, plan.max_state_len, ring, out, st["state_k"], st["state_v"],
+                     st["state_vlen"], st["state_k_attn"], st["state_v_attn"], status, logs.get("route_log"),
+                     logs.get("append_log"), extra.get("snap_k"), extra.get("snap_v"), extra.get("lse"), ev)
         if check_status:
             self.check_prefill_status(dev)
         res = {"out": out, "plan": plan, "capacity": cap, **st, **logs, **extra}
@@ -860,14 +847,14 @@ class SequenceMixer(nn.Module):
         if fresh is not None:
             if c.graph_ctl is not None:
                 raise AssertionError("a deferred ring row cannot be written under graph capture")
-            seq, keep = _lib.seq4(*fresh)
-            _lib.check(lib.kvm_decode_step(
-                c.layer.ref(), qv.data_ptr(), qv.stride(0), qv.stride(1), c.state_struct(), active, seq,
-                c.recent_k.data_ptr(), c.recent_v.data_ptr(), c.recent_gate.data_ptr(), c.ring_capacity,
-                c.recent_start, c.recent_len, c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
-                c.decode_workspace.data_ptr(), c.decode_workspace.numel(), _lib.stream_handle(c.device)),
-                "kvm_decode_step")
-            del keep
+            k1, v1, g1 = fresh
+            g1 = g1 if g1.dtype == torch.bfloat16 else g1.to(torch.bfloat16)
+            cfg, eps, w, b, ts, tf = c.layer.op_args()
+            # The torch operator over kvm_decode_step (csrc/kvm_torch_ops.cpp), on the current stream.
+            _lib.call_op(_lib.ops().decode_step, qv, _lib._bf16_view(k1, "k"), _lib._bf16_view(v1, "v"), g1, w, b,
+                         ts, tf, cfg, eps, c.state_k, c.state_v, c.state_vlen, c.state_k_attn, c.state_v_attn,
+                         active, c.recent_k, c.recent_v, c.recent_gate, c.recent_start, c.recent_len, c.out,
+                         c.decode_workspace)
             return c.out
         if c.graph_ctl is not None:  # capture of a graph step: counters from device memory
             _lib.check(lib.kvm_decode_attention_dev(

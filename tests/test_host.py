@@ -356,3 +356,19 @@ def test_m0_only_written_by_the_lds_dma_helpers(src, tmp_path):
             assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith(" lds"), (src, ln, nxt)
             writes += 1
     assert writes > 0
+
+
+def test_torch_operator_library_registers_the_ops():
+    """libkvm_amd_torch.so (csrc/kvm_torch_ops.cpp) loads over the C library
+    and registers torch.ops.kvm_amd.prefill / decode_step with schemas that
+    mark their outputs as written."""
+    _lib()
+    import torch
+    from kvm_amd import _lib as L
+
+    ops = L.ops()
+    prefill = str(ops.prefill.default._schema)
+    decode = str(ops.decode_step.default._schema)
+    assert prefill.startswith("kvm_amd::prefill(") and "Tensor(a!) out" in prefill and "int[] cfg" in prefill
+    assert decode.startswith("kvm_amd::decode_step(") and "Tensor(d!) out" in decode
+    assert torch.ops.kvm_amd.prefill is ops.prefill
