@@ -179,6 +179,28 @@ __device__ __forceinline__ void dma16_l2(__amdgpu_buffer_rsrc_t r, uint32_t lds,
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r) : "memory");
 }
 
+// The same from device memory with the non-temporal policy: raw token rows
+// are read once, and streaming them keeps them from evicting the merge
+// buffers the group reads back from L2 one and two updates later.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r) : "memory");
+}
+
+// 16-byte buffer store at a 32-bit byte offset from the resource's base
+// (aux: cache policy bits; kPolicyNT streams the line to memory).
+constexpr int kPolicyNT = 2;
+template <int AUX>
+__device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, const uint4 &v) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, r, int(off), 0, AUX);
+}
+
+// Waits until at most N vector memory operations of the wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 // Raw token rows are read once: non-temporal loads keep them from evicting
 // the merge buffers the group reads back from L2 one and two updates later.
 __device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
@@ -762,12 +784,17 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   constexpr int RPI = 1024 / (2 * D);        // token rows per 1 KiB DMA instruction
   constexpr int KI = kStageRows / RPI;       // DMA instructions per staged chunk (keys or values)
   constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
+  constexpr int NRAW = 2 * (kChainTok / RPI) / kChainWaves;  // raw-row DMA instructions per wave
+  static_assert(NRAW * kChainWaves == 2 * (kChainTok / RPI), "raw DMA split");
   __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
   __shared__ __attribute__((aligned(16))) uint16_t own_sk[kOwnMax * D];   // key sums
   __shared__ __attribute__((aligned(16))) uint16_t own_sv[kOwnMax * D];   // value sums
   __shared__ __attribute__((aligned(16))) uint16_t stage_k[kStageRows * D];  // routed token rows
   __shared__ __attribute__((aligned(16))) uint16_t stage_v[kStageRows * D];
+  __shared__ __attribute__((aligned(16))) uint16_t raw_k[kChainTok * D];  // raw rows of my prep share
+  __shared__ __attribute__((aligned(16))) uint16_t raw_v[kChainTok * D];
   __shared__ float own_vl[kOwnMax];
+  __shared__ int tok_lds[kChainMax];  // first token of each update (list.tok_begin)
   __shared__ int sorted[kFixedMaxTok];
   __shared__ int wsc[kChainWaves][kOwnMax];  // per-wave slot counts, then per-wave offsets
   __shared__ int cnt[kOwnMax], off[kOwnMax];
@@ -782,8 +809,18 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   const int row = row0 + group;  // this launch serves rows row0 .. row0 + nrows - 1
   const int b = row / int(L.kv_heads), h = row % int(L.kv_heads);
   const int64_t rb = int64_t(row) * n_tok;
-  const int64_t buf_stride = int64_t(rows) * n_tok * D;  // elements between merge buffers
-  const int64_t part_stride = int64_t(rows) * n_tok * G;  // partials between the two buffers
+  // Per-row bases; the buffers of one kind lie a 32-bit stride apart (the host
+  // launches the chain only when they fit).
+  const int buf_stride = rows * n_tok * D;   // elements between merge buffers
+  const int part_stride = rows * n_tok * G;  // partials between the two buffers
+  uint16_t *const gk_row = cs.gk + rb * D;
+  uint16_t *const gv_row = cs.gv + rb * D;
+  uint2 *const part_row = cs.part + rb * G;
+  uint16_t *const snk_row = snaps.k + int64_t(row) * snaps.cap * D;
+  uint16_t *const snv_row = snaps.v + int64_t(row) * snaps.cap * D;
+  const int snap_stride = int(snaps.stride);
+  const int snap_bytes = int(snaps.cap) * D * 2;
+  const int k_st = int(src.k_st), v_st = int(src.v_st), g_st = int(src.g_st);
   const int tpm = (n_tok + G - 1) / G;                   // prep tokens per member (<= 64)
   const int pt0 = member * tpm;
   const int pnt = max(0, min(n_tok, pt0 + tpm) - pt0);
@@ -813,6 +850,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     ln_w[d] = static_cast<const float *>(L.ln_weight)[d];
     ln_b[d] = static_cast<const float *>(L.ln_bias)[d];
   }
+  // The first token of every update, read from LDS where the raw rows are
+  // fetched (a scalar load of the kernel argument would wait for memory).
+  for (int i = tid; i < list.count; i += kChainThreads) tok_lds[i] = list.tok_begin[i];
   // ---- owned state and attention keys into LDS (slots >= S stay zero).
   {
     const AttnRows a0 = snap_at(snaps, list.u0);
@@ -833,52 +873,60 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     }
   }
 
-  // Raw tokens of my prep share of update i (token 0 of the chunk for idle
-  // lanes; prefill tokens never come from a ring).
-  auto load_raw = [&](int i, RawTok<D> &rt) __attribute__((always_inline)) {
-    const int64_t tb = list.tok_begin[i];
+  // Raw key / value rows of my prep share of update i go from device memory
+  // straight into LDS (non-temporal DMA, no registers): wave w issues
+  // instructions w, w + 8, ... of the keys, then of the values, each filling
+  // RPI consecutive rows; rows past my share lie past the resource and read
+  // zero.  The gates go into registers.  Issued a whole phase before the prep
+  // that reads them, so the prep never waits for device memory.  Prefill
+  // tokens never come from a ring (src.ring == 0, checked by the host).
+  uint16_t rg[IT];
+  auto raw_dma = [&](int i) __attribute__((always_inline)) {
+    const int64_t tb = int64_t(__builtin_amdgcn_readfirstlane(tok_lds[i])) + pt0;
+    const int kb = pnt > 0 ? ((pnt - 1) * k_st + D) * 2 : 0;
+    const int vb = pnt > 0 ? ((pnt - 1) * v_st + D) * 2 : 0;
+    const __amdgpu_buffer_rsrc_t kr = l2_rsrc(k_row + tb * k_st, kb);
+    const __amdgpu_buffer_rsrc_t vr = l2_rsrc(v_row + tb * v_st, vb);
+    const uint32_t kbase = lds_addr(raw_k), vbase = lds_addr(raw_v);
+#pragma unroll
+    for (int t = 0; t < NRAW; ++t) {
+      const int c = __builtin_amdgcn_readfirstlane(wave) + kChainWaves * t;
+      constexpr int KIR = kChainTok / RPI;
+      const int ci = c < KIR ? c : c - KIR;
+      const int r = ci * RPI + lane / GL;
+      if (c < KIR)
+        dma16_nt(kr, kbase + uint32_t(ci * 1024), uint32_t((r * k_st + part * 8) * 2));
+      else
+        dma16_nt(vr, vbase + uint32_t(ci * 1024), uint32_t((r * v_st + part * 8) * 2));
+    }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int lt = (tid + it * kChainThreads) / GL;
-      const int64_t t = tb + (lt < pnt ? pt0 + lt : 0);
-      rt.k[it] = ld_stream16(k_row + t * src.k_st + part * 8);
-      rt.v[it] = ld_stream16(v_row + t * src.v_st + part * 8);
-      rt.g[it] = g_row[t * src.g_st];
+      rg[it] = g_row[tb * g_st + (lt < pnt ? lt : 0) * g_st];
     }
   };
   // prep (model/kvm_mixer.py:120-129, model/kvm_triton_mixer.py:429-446):
-  // merge key / value rows of pass `it` over my share of an update's tokens
-  // (packed bf16), and their store into merge buffer i % 4.
-  auto prep_row = [&](const RawTok<D> &rt, int it, uint4 &pk, uint4 &pv) __attribute__((always_inline)) {
-    float k[8], v[8];
-    unpack8(rt.k[it], k);
-    unpack8(rt.v[it], v);
-    const float g = bf2f(rt.g[it]);
-    prep_key<D>(k, part, L, ln_w, ln_b);
-    float gk[8], gv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      gk[e] = L.gate_keys ? k[e] * g : k[e];
-      gv[e] = L.gate_values ? v[e] * g : v[e];
-    }
-    pk = pack8(gk);
-    pv = pack8(gv);
-  };
-  auto prep_store = [&](int i, int it, const uint4 &pk, const uint4 &pv) __attribute__((always_inline)) {
-    const int lt = (tid + it * kChainThreads) / GL;
-    if (lt < pnt) {
-      const int64_t o = (i % 4) * buf_stride + (rb + pt0 + lt) * D + part * 8;
-      *reinterpret_cast<uint4 *>(cs.gk + o) = pk;
-      *reinterpret_cast<uint4 *>(cs.gv + o) = pv;
-    }
-  };
-  auto prep = [&](int i, const RawTok<D> &rt, int it0, int it1) __attribute__((always_inline)) {
+  // merge key / value rows of my share of update i (from the raw rows in
+  // LDS), packed bf16, stored into merge buffer i % 4.
+  auto prep = [&](int i) __attribute__((always_inline)) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      if (it >= it0 && it < it1) {
-        uint4 pk, pv;
-        prep_row(rt, it, pk, pv);
-        prep_store(i, it, pk, pv);
+      const int lt = (tid + it * kChainThreads) / GL;
+      float k[8], v[8];
+      unpack8(*reinterpret_cast<const uint4 *>(&raw_k[lt * D + part * 8]), k);
+      unpack8(*reinterpret_cast<const uint4 *>(&raw_v[lt * D + part * 8]), v);
+      const float g = bf2f(rg[it]);
+      prep_key<D>(k, part, L, ln_w, ln_b);
+      float gk[8], gv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gk[e] = L.gate_keys ? k[e] * g : k[e];
+        gv[e] = L.gate_values ? v[e] * g : v[e];
+      }
+      if (lt < pnt) {
+        const uint32_t o = uint32_t(((pt0 + lt) * D + part * 8) * 2);
+        st16<0>(l2_rsrc(gk_row + (i % 4) * buf_stride, n_tok * D * 2), o, pack8(gk));
+        st16<0>(l2_rsrc(gv_row + (i % 4) * buf_stride, n_tok * D * 2), o, pack8(gv));
       }
     }
   };
@@ -887,22 +935,26 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   auto tag_of = [](int i) __attribute__((always_inline)) { return uint32_t(0x8000u | uint32_t(i)); };
   __shared__ int fail_lds;
 
-  // Raw tokens of update i + 1 are loaded between arriving at the barrier
-  // that ends phase i - 1 and waiting for it; phase i starts with their prep.
-  RawTok<D> rt;
-  load_raw(0, rt);
+  // Prologue: prep(0), then the raw rows of update 1; the group barrier's
+  // store wait (vmcnt(0)) also completes that DMA, and its workgroup barrier
+  // makes the rows visible to every wave.
+  __syncthreads();  // tok_lds, ln_w / ln_b and the owned rows are in LDS
+  raw_dma(0);
   if (tid == 0) fail_lds = 0;
   // My partials in both buffers start cleared.
   for (int t = tid; t < n_tok; t += kChainThreads) {
     cs.part[rb * G + int64_t(t) * G + member] = make_uint2(0u, 0u);
     cs.part[part_stride + rb * G + int64_t(t) * G + member] = make_uint2(0u, 0u);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  prep(0, rt, 0, IT);
+  prep(0);
+  __syncthreads();  // every wave has read the raw rows of update 0
+  if (list.count > 1) raw_dma(1);
   arrive();
-  if (list.count > 1) load_raw(1, rt);
   if (!wait()) return;
 
+  int snap_i = int(int64_t(list.u0) % snaps.ring);  // ring entry of snapshot u0 + p
   for (int p = 0; p <= list.count; ++p) {
     KVM_TS(0);
     const bool do_route = p < list.count;
@@ -911,7 +963,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     uint4 bx[4][KS];
     auto load_bx = [&](int tt0, int tt1, int ks0, int ks1) __attribute__((always_inline)) {
       const __amdgpu_buffer_rsrc_t gr =
-          l2_rsrc(cs.gk + (p % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(gk_row + (p % 4) * buf_stride, n_tok * D * 2);
 #pragma unroll
       for (int tt = tt0; tt < tt1; ++tt)
 #pragma unroll
@@ -923,17 +975,18 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     // are not waited for).
     uint4 pw[GM / 2];
     const __amdgpu_buffer_rsrc_t pr =
-        l2_rsrc(cs.part + int64_t((p - 1) & 1) * part_stride + rb * G, int64_t(n_tok) * G * 8);
+        l2_rsrc(part_row + ((p - 1) & 1) * part_stride, n_tok * G * 8);
     if (p >= 1) {
 #pragma unroll
       for (int i = 0; i < GM / 2; ++i) pw[i] = l2_ld16(pr, (tid * GM + 2 * i) * 8);
     }
-    // The next update's prep while that load is in flight (from phase 1
-    // on, its second half waits for the merge's gathered rows instead).
-    constexpr int IT_LATE = IT / 2;
-    const int it_split = p >= 1 ? IT - IT_LATE : IT;
-    if (do_prep) prep(p + 1, rt, 0, it_split);
-    if (p == 0) load_bx(0, 4, 0, KS);
+    // The next update's prep (raw rows already in LDS) while that load is
+    // in flight.
+    if (do_prep) prep(p + 1);
+    if (p == 0) {
+      load_bx(0, 4, 0, KS);
+      __syncthreads();  // every wave has read the raw rows of update 1
+    }
     KVM_TS(1);
 
     if (p >= 1) {
@@ -965,6 +1018,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
         ok_tok = ok && tid < n_tok;
+        KVM_TS(7);
         if (!__all(ok)) {
           if ((tid & 63) == 0) {
             __hip_atomic_store(cs.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -974,21 +1028,26 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
       }
-      float bv = -INFINITY;
-      int bi = -1;
+      // The route operands of update p: every member stores its prepared
+      // rows of update p before it publishes any partial of update p - 1,
+      // so they are in L2 now.  Issued here, while the memory pipeline is
+      // otherwise idle during the lists, they have landed long before the
+      // gathers behind them are waited for.
+      // The first half of the k-steps here, the rest in two quarters at the
+      // refresh passes: a CU's vector memory pipeline moves about 64 bytes
+      // per clock, so a burst of all of them would stall the issuing waves
+      // and delay the gathers queued behind them.
+      if (do_route) load_bx(0, 4, 0, KS / 2);
+      // Partials are route keys (see route(p)): the largest wins.
+      uint64_t best = 0;
 #pragma unroll
       for (int i = 0; i < GM / 2; ++i) {
-        const float v0 = __uint_as_float(pw[i].x), v1 = __uint_as_float(pw[i].z);
-        const int i0 = int(pw[i].y & 0xffffu), i1 = int(pw[i].w & 0xffffu);
-        if (i0 != 0xffff && (bi < 0 || v0 > bv || (v0 == bv && i0 < bi))) {
-          bv = v0;
-          bi = i0;
-        }
-        if (i1 != 0xffff && (bi < 0 || v1 > bv || (v1 == bv && i1 < bi))) {
-          bv = v1;
-          bi = i1;
-        }
+        const uint64_t k0 = (uint64_t(pw[i].x) << 32) | (pw[i].y & 0xffffu);
+        const uint64_t k1 = (uint64_t(pw[i].z) << 32) | (pw[i].w & 0xffffu);
+        best = k0 > best ? k0 : best;
+        best = k1 > best ? k1 : best;
       }
+      int bi = (best >> 32) != 0 ? int(0xffffu - uint32_t(best & 0xffffu)) : -1;
       if (!ok_tok) bi = -1;  // past n_tok, or a partial that never arrived
       const bool mine = bi >= 0 && ((bi >> 4) % G) == member;
       const int my_loc = mine ? ((((bi >> 4) / G) << 4) | (bi & 15)) : -1;
@@ -1039,9 +1098,9 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // rows are staged in LDS (all loads of a chunk in flight together),
       // then each slot sums its rows in token order.
       const __amdgpu_buffer_rsrc_t gkr =
-          l2_rsrc(cs.gk + (pi % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(gk_row + (pi % 4) * buf_stride, n_tok * D * 2);
       const __amdgpu_buffer_rsrc_t gvr =
-          l2_rsrc(cs.gv + (pi % 4) * buf_stride + rb * D, int64_t(n_tok) * D * 2);
+          l2_rsrc(gv_row + (pi % 4) * buf_stride, n_tok * D * 2);
       float sk[SP][8], sv[SP][8];
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp)
@@ -1055,26 +1114,34 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // chunk fills staged rows RPI*c .. RPI*c + RPI - 1; wave w issues
       // c = w, w + 8, ... of the keys, then of the values.  Rows past ntot
       // point past the resource and are not written.
+      // Wave w fills staged rows RPI*ci .. RPI*ci + RPI - 1 for ci = w, w + 8,
+      // ...: the token indices of all its instructions are read from LDS
+      // first (one wait), then the key and the value row of each are issued.
       auto gather = [&](int c0) __attribute__((always_inline)) {
         const uint32_t kbase = lds_addr(stage_k), vbase = lds_addr(stage_v);
+        const int w0 = __builtin_amdgcn_readfirstlane(wave);
+        constexpr int NG = KI / kChainWaves;
+        static_assert(NG * kChainWaves == KI, "gather split");
+        uint32_t to[NG];
 #pragma unroll
-        for (int t = 0; t < 2 * KI / kChainWaves; ++t) {
-          const int c = __builtin_amdgcn_readfirstlane(wave) + kChainWaves * t;
-          const int ci = c < KI ? c : c - KI;
+        for (int t = 0; t < NG; ++t) {
+          const int pos = c0 + (w0 + kChainWaves * t) * RPI + lane / GL;
+          const int tok = sorted[min(pos, kFixedMaxTok - 1)];
+          // Rows past ntot point past the resource (n_tok) and are not written.
+          to[t] = uint32_t(((pos < ntot ? tok : n_tok) * D + part * 8) * 2);
+        }
+#pragma unroll
+        for (int t = 0; t < NG; ++t) {
+          const int ci = w0 + kChainWaves * t;
           if (c0 + ci * RPI < ntot) {  // instructions wholly past ntot are not issued
-            const int pos = c0 + ci * RPI + lane / GL;
-            const int tok = pos < ntot ? sorted[pos] : n_tok;  // n_tok: past the resource
-            const uint32_t to = uint32_t((tok * D + part * 8) * 2);
-            if (c < KI)
-              dma16_l2(gkr, kbase + uint32_t(ci * 1024), to);
-            else
-              dma16_l2(gvr, vbase + uint32_t(ci * 1024), to);
+            dma16_l2(gkr, kbase + uint32_t(ci * 1024), to[t]);
+            dma16_l2(gvr, vbase + uint32_t(ci * 1024), to[t]);
           }
         }
       };
       auto stage_sum = [&](int c0) __attribute__((always_inline)) {
         const int nrow = min(kStageRows, ntot - c0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_vm<0>();
         __syncthreads();
 #pragma unroll
         for (int sp = 0; sp < SP; ++sp) {
@@ -1096,20 +1163,8 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         __syncthreads();
       };
       gather(0);
-      // Second half of the next update's prep while the rows are in flight;
-      // its stores wait until they have arrived (a store issued now would
-      // hold up the wait for the gathered rows).
-      uint4 lpk[IT_LATE > 0 ? IT_LATE : 1], lpv[IT_LATE > 0 ? IT_LATE : 1];
-      if (do_prep) {
-#pragma unroll
-        for (int x = 0; x < IT_LATE; ++x) prep_row(rt, IT - IT_LATE + x, lpk[x], lpv[x]);
-      }
       KVM_TS(8);
       stage_sum(0);
-      if (do_prep) {
-#pragma unroll
-        for (int x = 0; x < IT_LATE; ++x) prep_store(p + 1, IT - IT_LATE + x, lpk[x], lpv[x]);
-      }
       KVM_TS(9);
       for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
         gather(c0);
@@ -1120,30 +1175,20 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // values into snapshot u0 + p straight from registers (non-temporal:
       // the attention kernel reads them much later), and after the batch's
       // last update also into the state's attention rows.
-      const AttnRows nxt = snap_at(snaps, int64_t(list.u0) + p);
+      // Snapshot u0 + p: ring entry snap_i (advanced by one per phase).
+      const __amdgpu_buffer_rsrc_t nk =
+          l2_rsrc(snk_row + int64_t(snap_i) * snap_stride, snap_bytes);
+      const __amdgpu_buffer_rsrc_t nv =
+          l2_rsrc(snv_row + int64_t(snap_i) * snap_stride, snap_bytes);
       const bool fin = !do_route && list.final_rows != 0;
       uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
       uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
-      // The route operands of update p are issued in small groups between
-      // the steps of the passes: the CU moves them from L2 at a fixed rate,
-      // and a wave that issues many at once waits until they are accepted.
-      constexpr int NBP = 4 * KS / SP;  // route-operand loads per pass
-      auto bx_group = [&](int sp, int g) __attribute__((always_inline)) {
-        if (do_route) {
-#pragma unroll
-          for (int x = g * NBP / 4; x < (g + 1) * NBP / 4; ++x) {
-            const int idx = sp * NBP + x;
-            load_bx(idx / KS, idx / KS + 1, idx % KS, idx % KS + 1);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      };
+      if (do_route) load_bx(0, 4, KS / 2, KS * 3 / 4);  // the third quarter of the route operands
 #pragma unroll
       for (int sp = 0; sp < SP; ++sp) {
         const int l = sp * RPP + tid / GL;
         const int j = own_local_to_slot(l, G, member);
         const bool valid = l < nown && j < S;
-        bx_group(sp, 0);
         float k[8], v[8];
         unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
         unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
@@ -1158,7 +1203,6 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = round_pack8(k);
           *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = round_pack8(v);
         }
-        bx_group(sp, 1);
         // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps;
         // the rows are only stored, so they are rounded by the packing).
         float ka[8];
@@ -1166,14 +1210,12 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         for (int e = 0; e < 8; ++e) ka[e] = k[e];
         layer_norm8<D>(ka, part, ln_w, ln_b, float(L.ln_eps));
         const uint4 kk = pack8(ka);
-        bx_group(sp, 2);
         const uint4 vv = attn_value8_packed<D>(v, own_vl[l]);
-        bx_group(sp, 3);
         if (valid) {
           *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
-          const int64_t ao = (int64_t(row) * nxt.cap + j) * D + part * 8;
-          __builtin_nontemporal_store(u32x4{kk.x, kk.y, kk.z, kk.w}, reinterpret_cast<u32x4 *>(nxt.k + ao));
-          __builtin_nontemporal_store(u32x4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<u32x4 *>(nxt.v + ao));
+          const uint32_t ao = uint32_t((j * D + part * 8) * 2);
+          st16<kPolicyNT>(nk, ao, kk);
+          st16<kPolicyNT>(nv, ao, vv);
           if (fin) {
             const int64_t so = (srow + j) * D + part * 8;
             *reinterpret_cast<uint4 *>(s_ka + so) = kk;
@@ -1181,6 +1223,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
         __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
+        if (sp == 0) {
+          KVM_TS(11);
+          if (do_route) load_bx(0, 4, KS * 3 / 4, KS);  // the last quarter of the route operands
+        }
       }
       __syncthreads();
     }
@@ -1217,6 +1263,16 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           for (int tt = 0; tt < 4; ++tt)
             accs[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), as_bf16x8(bx[tt][ks]),
                                                                accs[tt], 0, 0, 0);
+        // The raw rows of update p + 2 once the first block's products have
+        // been issued: every route operand has arrived by then, so the DMA
+        // queues behind nothing the route waits for, and the release wait
+        // below completes it (every wave read the raw rows of update p + 1
+        // at the start of this phase, before the lists' barriers).
+        if (lt == 0 && p + 2 < list.count) {
+          __builtin_amdgcn_sched_barrier(0);
+          raw_dma(p + 2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         const int j0 = jb + (lane >> 4) * 4;  // slot of acc[0]
         if (masked) {
 #pragma unroll
@@ -1249,35 +1305,43 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
       }
+      KVM_TS(12);
+      if (nown == 0 && p + 2 < list.count) raw_dma(p + 2);  // a member without slots
       // Release: this member's earlier stores (its prepared rows of update
       // p + 1) are in L2 before any of its partials of update p is.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      KVM_TS(13);
+      // Partials are route keys: {mono(score), tag << 16 | (0xffff - slot)},
+      // compared as 64-bit integers (the tags are equal), so the maximum is
+      // the largest score and, among equal scores, the lowest slot; no
+      // candidate is {0, tag << 16}, below every real key.
       const uint32_t tg = tag_of(p) << 16;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        float bv = best[tt];
-        int bi = bidx[tt];
+        const uint32_t bu = __float_as_uint(best[tt]);
+        uint32_t khi = bidx[tt] >= 0 ? ((bu & 0x80000000u) ? ~bu : (bu | 0x80000000u)) : 0u;
+        uint32_t klo = bidx[tt] >= 0 ? 0xffffu - uint32_t(bidx[tt]) : 0u;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-          const uint32_t vb = __float_as_uint(bv), ib = uint32_t(bi);
-          const float ob = __uint_as_float(r == 0 ? xor16_lane(vb, lane) : xor32_lane(vb, lane));
-          const int oi = int(r == 0 ? xor16_lane(ib, lane) : xor32_lane(ib, lane));
-          if (oi >= 0 && (bi < 0 || ob > bv || (ob == bv && oi < bi))) {
-            bv = ob;
-            bi = oi;
-          }
+          const uint32_t ohi = r == 0 ? xor16_lane(khi, lane) : xor32_lane(khi, lane);
+          const uint32_t olo = r == 0 ? xor16_lane(klo, lane) : xor32_lane(klo, lane);
+          const uint64_t mine = (uint64_t(khi) << 32) | klo, other = (uint64_t(ohi) << 32) | olo;
+          const bool take = other > mine;
+          khi = take ? ohi : khi;
+          klo = take ? olo : klo;
         }
         const int t = wave * kTokWave + tt * 16 + lane;
         if (lane < 16 && t < n_tok)
-          cs.part[int64_t(p & 1) * part_stride + (rb + t) * G + member] =
-              make_uint2(__float_as_uint(bv), tg | (uint32_t(bi) & 0xffffu));
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, make_uint2(khi, tg | klo)),
+              l2_rsrc(part_row + (p & 1) * part_stride, n_tok * G * 8), (t * G + member) * 8, 0, 0);
       }
       KVM_TS(4);
-      if (p + 2 < list.count) load_raw(p + 2, rt);
       KVM_TS(5);
       KVM_TS(6);
     }
+    snap_i = snap_i + 1 == int(snaps.ring) ? 0 : snap_i + 1;
   }
 
   // ---- owned state back to the caller's arrays.

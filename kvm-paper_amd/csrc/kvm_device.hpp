@@ -77,10 +77,14 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 u) {
   return __builtin_bit_cast(bf16x8, u);
 }
 
-// DPP lane moves within rows of 16 lanes (VALU, no LDS round trip).
+// DPP lane moves within rows of 16 lanes (VALU, no LDS round trip).  Every
+// pattern below reads a valid lane, so the `old` operand (0) is never used;
+// being the identity of addition, it lets the compiler fold the move into
+// the consuming v_add_f32 (v_add_f32_dpp: one instruction per step).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]

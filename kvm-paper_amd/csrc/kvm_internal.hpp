@@ -106,7 +106,7 @@ struct ChainScratch {
   uint16_t *gv;          // merge values bf16 [3][rows, n_tok, D]
   int32_t *route;        // merge slot of each token, -1 if appended [rows, n_tok]
   float *nov;            // novelty of each token [rows, n_tok]
-  uint2 *part;           // per-member route maxima (score bits, slot) [2][rows, n_tok, G]
+  uint2 *part;           // per-member route maxima as route keys {mono(score), tag << 16 | (0xffff - slot)} [2][rows, n_tok, G]
   unsigned *bar;         // group barrier counters
   unsigned *abort_flag;  // set when a group wait timed out (cleared per launch)
   unsigned *status;      // sticky: KVM_STATUS_CHAIN_TIMEOUT is ORed in on a time-out
