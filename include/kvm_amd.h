@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 11
+#define KVM_ABI_VERSION 12
 
 #define KVM_OK 0
 #define KVM_EINVAL (-1)
@@ -65,6 +65,12 @@ extern "C" {
 #define KVM_STATUS_CHAIN_TIMEOUT 1 /* a persistent update chain gave up waiting for its
                                       row group: state, snapshots and outputs of that
                                       prefill are incomplete */
+
+/* Bits of kvm_prefill_desc.flags. */
+#define KVM_PREFILL_NO_CHAIN 1 /* run the memory updates as per-update kernels instead of a
+                                  persistent chain (bit-identical results; no requirement
+                                  that every workgroup of the chain be resident at once, so
+                                  it completes on a GPU shared with other work) */
 
 /* Static description of one KVM layer (the mixer attributes the forward
  * path reads: model/kvm_mixer.py:79-118, model/rwkv7_backbone.py:319-373).
@@ -163,6 +169,7 @@ typedef struct kvm_prefill_desc {
                                     replace the workspace's snapshot ring (snapshot_ring must be
                                     n_updates + 1) and keep every snapshot for the backward */
   void *snap_v;
+  int64_t flags;                 /* KVM_PREFILL_* bits (0: defaults) */
 } kvm_prefill_desc;
 
 /* One prefill's attention backward (the gradient of

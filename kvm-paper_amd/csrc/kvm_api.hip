@@ -767,11 +767,11 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
   };
 
   // Updates run as persistent chains when the shape fits (one launch per
-  // batch of updates), else as per-update kernels.  KVM_AMD_CHAIN=0 forces
-  // the per-update kernels.
+  // batch of updates), else as per-update kernels.  KVM_PREFILL_NO_CHAIN in
+  // the call's flags, or KVM_AMD_CHAIN=0, forces the per-update kernels.
   kvm::ChainPlan cp;
   const char *chain_env = getenv("KVM_AMD_CHAIN");
-  const bool use_chain = !(chain_env && chain_env[0] == '0') &&
+  const bool use_chain = !(d->flags & KVM_PREFILL_NO_CHAIN) && !(chain_env && chain_env[0] == '0') &&
                          kvm::chain_plan(L, C, d->max_state_len, &cp);
 
   // Status word of the chain: the caller's (sticky, never cleared here), or

@@ -67,6 +67,21 @@ struct AttnState {
 // multiplies per lane) is skipped in almost every block.
 constexpr float kRescaleSlack = 8.0f;
 
+// Maxima of scores without the quieting copies (v_max_f32 x, x) the compiler
+// adds around fmaxf in IEEE mode: scores are MFMA sums of finite products or
+// the -inf of a mask, never NaN, so the plain instructions give the same
+// result.
+__device__ __forceinline__ float max2_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // S^T tiles of the 64 keys of a buffered block: s[kt][rt], kt = 16-key
 // tile, rt = 16-query tile.  kbuf + kb addresses key lane&15, dims
 // 8*(lane>>4).. of column group 0.  The k-step loop is outermost, so eight
@@ -119,19 +134,19 @@ __device__ __forceinline__ void block_max(f32x4 (&s)[4][2], AttnState<D> &as, bo
   float m_new[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    float mx = fmaxf(fmaxf(s[0][rt][0], s[0][rt][1]), s[0][rt][2]);
-    mx = fmaxf(fmaxf(mx, s[0][rt][3]), s[1][rt][0]);
-    mx = fmaxf(fmaxf(mx, s[1][rt][1]), s[1][rt][2]);
-    mx = fmaxf(fmaxf(mx, s[1][rt][3]), s[2][rt][0]);
-    mx = fmaxf(fmaxf(mx, s[2][rt][1]), s[2][rt][2]);
-    mx = fmaxf(fmaxf(mx, s[2][rt][3]), s[3][rt][0]);
-    mx = fmaxf(fmaxf(mx, s[3][rt][1]), s[3][rt][2]);
-    mx = fmaxf(mx, s[3][rt][3]);
+    float mx = max3_raw(s[0][rt][0], s[0][rt][1], s[0][rt][2]);
+    mx = max3_raw(mx, s[0][rt][3], s[1][rt][0]);
+    mx = max3_raw(mx, s[1][rt][1], s[1][rt][2]);
+    mx = max3_raw(mx, s[1][rt][3], s[2][rt][0]);
+    mx = max3_raw(mx, s[2][rt][1], s[2][rt][2]);
+    mx = max3_raw(mx, s[2][rt][3], s[3][rt][0]);
+    mx = max3_raw(mx, s[3][rt][1], s[3][rt][2]);
+    mx = max2_raw(mx, s[3][rt][3]);
     // max with lane ^ 16, then lane ^ 32 (each swap returns both values)
     const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    mx = max2_raw(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
     const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    mx = max2_raw(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     m_new[rt] = mx * scale;
     need |= m_new[rt] > as.m[rt] + kRescaleSlack;
   }
@@ -156,7 +171,7 @@ __device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], AttnState<D>
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const float base = as.m[rt] == -INFINITY ? 0.f : as.m[rt];
-    float psum = 0.f;
+    float psum;
     uint32_t pk[4][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -164,7 +179,8 @@ __device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], AttnState<D>
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][rt][i], scale, -base));
-        psum += p[i];
+        // The block's sum starts at its first weight (p >= +0, so 0 + p == p).
+        psum = (kt == 0 && i == 0) ? p[i] : psum + p[i];
       }
       pk[kt][0] = pack_bf16x2(p[0], p[1]);
       pk[kt][1] = pack_bf16x2(p[2], p[3]);

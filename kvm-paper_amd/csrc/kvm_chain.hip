@@ -1038,6 +1038,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // per clock, so a burst of all of them would stall the issuing waves
       // and delay the gathers queued behind them.
       if (do_route) load_bx(0, 4, 0, KS / 2);
+      KVM_TS(14);
       // Partials are route keys (see route(p)): the largest wins.
       uint64_t best = 0;
 #pragma unroll
@@ -1071,6 +1072,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       if (mine && rank == 0) wsc[wave][my_loc] = __popcll(eq);
       __syncthreads();
       if (fail_lds) return;  // a partial never arrived: the launch is abandoned
+      KVM_TS(15);
       if (tid < kOwnMax) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
         int run = 0;
 #pragma unroll

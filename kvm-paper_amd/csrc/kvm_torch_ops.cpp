@@ -130,7 +130,7 @@ void prefill(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v, cons
              const c10::optional<at::Tensor> &status, const c10::optional<at::Tensor> &route_log,
              const c10::optional<at::Tensor> &append_log, const c10::optional<at::Tensor> &snap_k,
              const c10::optional<at::Tensor> &snap_v, const c10::optional<at::Tensor> &lse,
-             std::vector<int64_t> events) {
+             std::vector<int64_t> events, int64_t flags) {
   check_bf16_rows(q, "q");
   TORCH_CHECK_VALUE(plan.device().is_cpu() && plan.scalar_type() == at::kInt && plan.is_contiguous() &&
                         plan.numel() == 2 * n_chunks + 3 * n_updates,
@@ -166,6 +166,7 @@ void prefill(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v, cons
   d.lse = static_cast<float *>(const_cast<void *>(ptr(lse)));
   d.snap_k = const_cast<void *>(ptr(snap_k));
   d.snap_v = const_cast<void *>(ptr(snap_v));
+  d.flags = flags;
   void *ev[4] = {nullptr, nullptr, nullptr, nullptr};
   for (size_t i = 0; i < events.size(); ++i) ev[i] = reinterpret_cast<void *>(events[i]);
   if (!events.empty()) d.events = ev;
@@ -207,7 +208,7 @@ TORCH_LIBRARY(kvm_amd, m) {
       "int max_state_len, int snapshot_ring, Tensor(a!) out, Tensor(b!) state_k, Tensor(c!) state_v, "
       "Tensor(d!) state_vlen, Tensor(e!) state_k_attn, Tensor(f!) state_v_attn, Tensor(g!)? status, "
       "Tensor(h!)? route_log, Tensor(i!)? append_log, Tensor(j!)? snap_k, Tensor(k!)? snap_v, "
-      "Tensor(l!)? lse, int[] events) -> ()",
+      "Tensor(l!)? lse, int[] events, int flags) -> ()",
       prefill);
   m.def(
       "decode_step(Tensor q, Tensor k_new, Tensor v_new, Tensor gate_new, Tensor ln_w, Tensor ln_b, "

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libkvm_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 KVM_OK = 0
 KVM_EINVAL = -1
@@ -24,6 +24,7 @@ KVM_EHIP = -2
 KVM_ESPACE = -3
 KVM_EABORT = -4
 KVM_STATUS_CHAIN_TIMEOUT = 1
+KVM_PREFILL_NO_CHAIN = 1
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -80,6 +81,7 @@ class KvmPrefillDesc(ctypes.Structure):
         ("status", _vp),
         ("lse", _vp),
         ("snap_k", _vp), ("snap_v", _vp),
+        ("flags", _i64),
     ]
 
 

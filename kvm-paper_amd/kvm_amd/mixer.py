@@ -24,6 +24,8 @@ inference-only.
 
 from __future__ import annotations
 
+import warnings
+
 import argparse
 import ctypes
 import math
@@ -608,22 +610,34 @@ class SequenceMixer(nn.Module):
         None) reported a device-side failure since the last check.  Waits for
         the work already queued, so call it where a synchronisation is
         acceptable."""
-        for key, word in list(self.__dict__.get("_status_words", {}).items()):
+        for key in list(self.__dict__.get("_status_words", {})):
             if device is not None and key != str(device):
                 continue
-            bits = int(word.item())
-            if bits:
-                word.zero_()
-                if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT:
-                    raise _lib.KvmLibraryError(
-                        "kvm_prefill: the persistent update chain timed out waiting for its row group "
-                        "(another workload held compute units); the prefill's outputs and state are incomplete")
-                raise _lib.KvmLibraryError(f"kvm_prefill: device status word {bits:#x}")
+            self._raise_status(self._take_status(key))
+
+    def _take_status(self, device) -> int:
+        """The status word's bits for ``device`` (one synchronisation), cleared."""
+        word = self.__dict__.get("_status_words", {}).get(str(device))
+        if word is None:
+            return 0
+        bits = int(word.item())
+        if bits:
+            word.zero_()
+        return bits
+
+    @staticmethod
+    def _raise_status(bits: int) -> None:
+        if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT:
+            raise _lib.KvmLibraryError(
+                "kvm_prefill: the persistent update chain timed out waiting for its row group "
+                "(another workload held compute units); the prefill's outputs and state are incomplete")
+        if bits:
+            raise _lib.KvmLibraryError(f"kvm_prefill: device status word {bits:#x}")
 
     def prefill_raw(self, q, k, v, merge_gate, *, plan: PrefillPlan | None = None, state_capacity: int | None = None,
                     route_log: bool = False, snapshot_budget: int | None = None,
                     events=None, check_status: bool | None = True, keep_snapshots: bool = False,
-                    want_lse: bool = False) -> dict:
+                    want_lse: bool = False, chain: bool = True) -> dict:
         """Post-QKV prefill on the HIP library; returns the raw outputs.
 
         q [B,Hq,T,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] bf16 (any strides with a
@@ -636,12 +650,19 @@ class SequenceMixer(nn.Module):
         attention launches (timing).
 
         ``check_status``: read the device status word after the call (one
-        synchronisation) and raise RuntimeError if the update chain gave up.
+        synchronisation).  If the persistent update chain gave up (another
+        workload held compute units, so its row groups could not all be
+        resident), the call is repeated on the per-update kernels, which give
+        bit-identical results without that requirement, and a RuntimeWarning
+        is issued; a failure there raises RuntimeError.
         Callers that issue many prefills back to back pass False and call
         ``check_prefill_status()`` once afterwards; the word is sticky.
         With ``check_status=None`` no status word is passed: the library then
         waits for the stream itself and reports a failure as its return code
         (the C ABI's synchronous mode).
+
+        ``chain=False`` runs the memory updates as per-update kernels from the
+        start (``KVM_PREFILL_NO_CHAIN``).
 
         Training (``kvm_amd.training``): ``keep_snapshots`` returns every
         memory snapshot the query chunks read (``snap_k`` / ``snap_v``, bf16
@@ -692,12 +713,26 @@ class SequenceMixer(nn.Module):
         status = None if check_status is None else self._status_word(dev)
         # One torch operator (csrc/kvm_torch_ops.cpp) over kvm_prefill, on the
         # current stream; it sizes and allocates the workspace itself.
-        _lib.call_op(_lib.ops().prefill, qv, kv, vv, gv, w, b, ts, tf, cfg, eps, _plan_arrays(plan)[5],
-                     plan.n_chunks, plan.n_updates, plan.max_state_len, ring, out, st["state_k"], st["state_v"],
-                     st["state_vlen"], st["state_k_attn"], st["state_v_attn"], status, logs.get("route_log"),
-                     logs.get("append_log"), extra.get("snap_k"), extra.get("snap_v"), extra.get("lse"), ev)
+        def call(flags):
+            _lib.call_op(_lib.ops().prefill, qv, kv, vv, gv, w, b, ts, tf, cfg, eps, _plan_arrays(plan)[5],
+                         plan.n_chunks, plan.n_updates, plan.max_state_len, ring, out, st["state_k"],
+                         st["state_v"], st["state_vlen"], st["state_k_attn"], st["state_v_attn"], status,
+                         logs.get("route_log"), logs.get("append_log"), extra.get("snap_k"), extra.get("snap_v"),
+                         extra.get("lse"), ev, flags)
+
+        call(0 if chain else _lib.KVM_PREFILL_NO_CHAIN)
         if check_status:
-            self.check_prefill_status(dev)
+            bits = self._take_status(dev)
+            if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT and chain:
+                warnings.warn("kvm_prefill: the persistent update chain timed out waiting for its row group "
+                              "(another workload held compute units); repeating the prefill on the per-update "
+                              "kernels", RuntimeWarning, stacklevel=2)
+                if "route_log" in logs:
+                    logs["route_log"].fill_(-1)
+                    logs["append_log"].zero_()
+                call(_lib.KVM_PREFILL_NO_CHAIN)
+                bits = self._take_status(dev)
+            self._raise_status(bits)
         res = {"out": out, "plan": plan, "capacity": cap, **st, **logs, **extra}
         return res
 
