@@ -845,7 +845,19 @@ int kvm_prefill(const kvm_prefill_desc *d, void *stream) {
     const char *fixed_env = getenv("KVM_AMD_CHAIN_FIXED");
     const kvm::SnapRing ring{snap_k, snap_v, snap_stride, R, d->max_state_len};
     for (int64_t u = 0; u < d->n_updates;) {
-      const int64_t e = std::min({d->n_updates, u + int64_t(kvm::kChainMax), u + R});
+      int64_t e = std::min({d->n_updates, u + int64_t(kvm::kChainMax), u + R});
+      // A batch whose updates stop appending part-way (a growing budget that
+      // reaches its cap) ends where they stop: the tail, whose state length
+      // no longer changes, runs on the slot-owner kernel in the next launch.
+      {
+        int64_t tail = e;
+        while (tail > u + 1 && d->upd_n_append[tail - 1] == 0 &&
+               d->upd_state_before[tail - 1] == d->upd_state_before[e - 1])
+          --tail;
+        if (tail > u && tail < e && (d->upd_n_append[tail - 1] != 0 ||
+                                     d->upd_state_before[tail - 1] != d->upd_state_before[e - 1]))
+          e = tail;
+      }
       if (e - R >= 0) {
         if ((rc = flush(u + 1)) != KVM_OK) return rc;
         if (next_chunk < n_chunks && next_chunk >= n && d->chunk_snapshot[next_chunk] <= e - R)

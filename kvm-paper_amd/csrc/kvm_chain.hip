@@ -69,8 +69,14 @@ __device__ unsigned long long g_chain_ts[2][128][16];
       else if (blockIdx.x == 8 * (GM - 1)) g_chain_ts[1][p][k] = wall_clock64();          \
     }                                                                                    \
   } while (0)
+// The appending chain's marks: member 0 of group 0, update i of the launch.
+#define KVM_TS_A(k)                                                                      \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && i < 128) g_chain_ts[0][i][k] = wall_clock64(); \
+  } while (0)
 #else
 #define KVM_TS(k) ((void)0)
+#define KVM_TS_A(k) ((void)0)
 #endif
 
 namespace {
@@ -486,14 +492,17 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
     int32_t *rlog = route_log ? route_log + u * log_stride + rb : nullptr;
     int32_t *alog = append_log ? append_log + u * log_stride + rb : nullptr;
     const uint16_t *cur_k = cur.k + int64_t(row) * cur.cap * D;
+    KVM_TS_A(0);
 
     // ---- append (model/kvm_mixer.py:44-75, 231-248): the n_append least
     // novel tokens, ties to the lower index, become slots sb.. in token order.
     if (na > 0) {
       scan_slots<D, true>(op_n, cur_k, 0, sb, ntk, red_v, red_i, res_v, nullptr, [] {});
       if (tid < ntk) cs.nov[rb + t0 + tid] = res_v[tid];
+      KVM_TS_A(1);
       arrive();
       if (!wait()) return;
+      KVM_TS_A(2);
       const __amdgpu_buffer_rsrc_t nr = l2_rsrc(cs.nov + rb, int64_t(n_tok) * 4);
       for (int t = tid; t < n_tok; t += kChainThreads) novl[t] = __uint_as_float(l2_ld4(nr, t * 4));
       __syncthreads();
@@ -507,6 +516,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
         tok_a[t] = r < na ? 1 : 0;
       }
       __syncthreads();
+      KVM_TS_A(3);
       // Positions of my appended tokens (tokens before them that append).
       if (tid < ntk) {
         const int t = t0 + tid;
@@ -542,8 +552,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
           store8(cur.v + ao, va);
         }
       }
+      KVM_TS_A(4);
       arrive();
       if (!wait()) return;
+      KVM_TS_A(5);
     }
 
     // ---- route (model/kvm_fp32_routing_reference.py:30-34); the next
@@ -553,6 +565,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
                          [&]() __attribute__((always_inline)) {
                            if (more) load_raw(i + 1, rt);
                          });
+    KVM_TS_A(6);
     if (tid < ntk) {
       const int t = t0 + tid;
       const bool app = na > 0 && tok_a[t] != 0;
@@ -568,8 +581,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
         rlog[t] = r;
       }
     }
+    KVM_TS_A(7);
     arrive();
     if (!wait()) return;
+    KVM_TS_A(8);
 
     // ---- merge + refresh (model/kvm_mixer.py:329-335) of my slots
     const int spm = (s_after + G - 1) / G;
@@ -647,6 +662,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
       }
     }
     __syncthreads();
+    KVM_TS_A(9);
     auto merge_slot = [&](int local, const uint4 &k_raw, const uint4 &v_raw,
                           float vlen) __attribute__((always_inline)) {
       const bool valid = local < nsl;
@@ -710,12 +726,15 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
       merge_slot(base + tid / GL, k0, v0, l0);
       if (base + RPP < nsl) merge_slot(base + RPP + tid / GL, k1, v1, l1);
     }
+    KVM_TS_A(10);
 
     // ---- next update's prep while the other members finish this merge.
     if (more) {
       arrive();
       prep(i + 1, rt);
+      KVM_TS_A(11);
       if (!wait()) return;
+      KVM_TS_A(12);
     }
   }
 }
@@ -762,16 +781,17 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
 // end of the phase before; the route operands of update p are loaded once
 // the merge's gathered rows have arrived, so they never queue in L2 ahead
 // of the gathers.
-constexpr int kOwnMax = 64;       // owned slots per member (4 blocks of 16)
+constexpr int kOwnMax = 128;      // owned slots per member at most (8 blocks of 16)
 constexpr int kTokWave = 64;      // tokens per wave in route(p)
 constexpr int kFixedMaxTok = kChainWaves * kTokWave;  // == kChainThreads: one token per thread
-constexpr int kStageRows = 128;   // routed token rows staged in LDS at once
 
 __device__ __forceinline__ int own_local_to_slot(int l, int G, int m) {
   return (((l >> 4) * G + m) << 4) | (l & 15);
 }
 
-template <int D, int GM>  // GM: the group size G (8 or 16)
+// GM: the group size G (8 or 16); OWN: owned slots per member the LDS holds
+// (64, or 128 for states of up to 1024 slots at G = 8).
+template <int D, int GM, int OWN>
 __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
     kvm_layer L, kvm_seq src, int n_tok, kvm_state st, SnapRing snaps, ChainList list,
     ChainScratch cs, int rows, int row0, int nrows, int32_t *route_log, int32_t *append_log,
@@ -780,24 +800,37 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   constexpr int STR = D + 8;                // LDS row stride of key rows (elements)
   constexpr int KS = D / 32;
   constexpr int RPP = kChainThreads / GL;   // rows per pass
-  constexpr int SP = kOwnMax / RPP;         // passes over the owned slots
+  constexpr int SP = OWN / RPP;             // passes over the owned slots
+  constexpr int HP = SP < 2 ? SP : 2;       // passes per half (the sums of one half live in registers)
+  constexpr int NH = SP / HP;               // halves of the owned slots
+  // Routed token rows staged in LDS at once (96 at OWN 128 and D 128, where
+  // the owned rows need the room).
+  constexpr int STAGE = (OWN == 128 && D == 128) ? 96 : 128;
   constexpr int RPI = 1024 / (2 * D);        // token rows per 1 KiB DMA instruction
-  constexpr int KI = kStageRows / RPI;       // DMA instructions per staged chunk (keys or values)
+  constexpr int KI = STAGE / RPI;            // DMA instructions per staged chunk (keys or values)
+  constexpr int LOG2_OWN = OWN == 128 ? 7 : 6;
+  static_assert(OWN == 64 || OWN == 128, "owned slots");
+  static_assert(SP == NH * HP, "refresh halves");
+  static_assert(kChainTok <= STAGE, "raw rows alias the staging buffers");
   constexpr int IT = RawTok<D>::IT;         // passes over the member's prep tokens
   constexpr int NRAW = 2 * (kChainTok / RPI) / kChainWaves;  // raw-row DMA instructions per wave
   static_assert(NRAW * kChainWaves == 2 * (kChainTok / RPI), "raw DMA split");
-  __shared__ __attribute__((aligned(16))) uint16_t own_k[kOwnMax * STR];  // attention keys
-  __shared__ __attribute__((aligned(16))) uint16_t own_sk[kOwnMax * D];   // key sums
-  __shared__ __attribute__((aligned(16))) uint16_t own_sv[kOwnMax * D];   // value sums
-  __shared__ __attribute__((aligned(16))) uint16_t stage_k[kStageRows * D];  // routed token rows
-  __shared__ __attribute__((aligned(16))) uint16_t stage_v[kStageRows * D];
-  __shared__ __attribute__((aligned(16))) uint16_t raw_k[kChainTok * D];  // raw rows of my prep share
-  __shared__ __attribute__((aligned(16))) uint16_t raw_v[kChainTok * D];
-  __shared__ float own_vl[kOwnMax];
+  __shared__ __attribute__((aligned(16))) uint16_t own_k[OWN * STR];  // attention keys
+  __shared__ __attribute__((aligned(16))) uint16_t own_sk[OWN * D];   // key sums
+  __shared__ __attribute__((aligned(16))) uint16_t own_sv[OWN * D];   // value sums
+  // Routed token rows of the merge.  The raw key / value rows of my prep
+  // share of an update share these buffers: they are DMA'd during a phase's
+  // route, after that phase's sums have read the staged rows, and read by
+  // the next phase's prep, before that phase's gathers are issued.
+  __shared__ __attribute__((aligned(16))) uint16_t stage_k[STAGE * D];
+  __shared__ __attribute__((aligned(16))) uint16_t stage_v[STAGE * D];
+  uint16_t *const raw_k = stage_k;
+  uint16_t *const raw_v = stage_v;
+  __shared__ float own_vl[OWN];
   __shared__ int tok_lds[kChainMax];  // first token of each update (list.tok_begin)
   __shared__ int sorted[kFixedMaxTok];
-  __shared__ int wsc[kChainWaves][kOwnMax];  // per-wave slot counts, then per-wave offsets
-  __shared__ int cnt[kOwnMax], off[kOwnMax];
+  __shared__ int wsc[kChainWaves][OWN];  // per-wave slot counts, then per-wave offsets
+  __shared__ int cnt[OWN], off[OWN];
   __shared__ int ok_lds;
   __shared__ float ln_w[D], ln_b[D];  // ln_s_k parameters (LDS: no wait on global loads)
 
@@ -856,7 +889,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   // ---- owned state and attention keys into LDS (slots >= S stay zero).
   {
     const AttnRows a0 = snap_at(snaps, list.u0);
-    for (int base = 0; base < kOwnMax; base += RPP) {
+    for (int base = 0; base < OWN; base += RPP) {
       const int l = base + tid / GL;
       const int j = own_local_to_slot(l, G, member);
       const bool valid = l < nown && j < S;
@@ -1060,10 +1093,11 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       // rank among them, and their count from the group's first lane.  A
       // wave's LDS stores complete in order, so the clear of its own row of
       // wsc precedes the counts it writes.
-      wsc[wave][lane] = 0;
+#pragma unroll
+      for (int c = 0; c < OWN; c += 64) wsc[wave][c + lane] = 0;
       uint64_t eq = __ballot(mine);
 #pragma unroll
-      for (int bit = 0; bit < 6; ++bit) {
+      for (int bit = 0; bit < LOG2_OWN; ++bit) {
         const uint64_t m = __ballot(mine && ((my_loc >> bit) & 1));
         eq &= ((my_loc >> bit) & 1) ? m : ~m;
       }
@@ -1073,26 +1107,38 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       __syncthreads();
       if (fail_lds) return;  // a partial never arrived: the launch is abandoned
       KVM_TS(15);
-      if (tid < kOwnMax) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
-        int run = 0;
+      if (tid < 64) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
+        constexpr int PER = OWN / 64;  // consecutive slots per lane
+        int run[PER], tot = 0;
 #pragma unroll
-        for (int w = 0; w < kChainWaves; ++w) {
-          const int c = wsc[w][tid];
-          wsc[w][tid] = run;
-          run += c;
+        for (int x = 0; x < PER; ++x) {
+          const int e = tid * PER + x;
+          run[x] = 0;
+#pragma unroll
+          for (int w = 0; w < kChainWaves; ++w) {
+            const int c = wsc[w][e];
+            wsc[w][e] = run[x];
+            run[x] += c;
+          }
+          tot += run[x];
         }
-        int incl = run;
+        int incl = tot;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
           const int y = __shfl_up(incl, o);
           if (tid >= o) incl += y;
         }
-        off[tid] = incl - run;
-        cnt[tid] = run;
+        int base = incl - tot;
+#pragma unroll
+        for (int x = 0; x < PER; ++x) {
+          off[tid * PER + x] = base;
+          cnt[tid * PER + x] = run[x];
+          base += run[x];
+        }
       }
       __syncthreads();
       if (mine) sorted[off[my_loc] + wsc[wave][my_loc] + rank] = tid;
-      const int ntot = off[kOwnMax - 1] + cnt[kOwnMax - 1];  // tokens routed to my slots
+      const int ntot = off[OWN - 1] + cnt[OWN - 1];  // tokens routed to my slots
       __syncthreads();
       KVM_TS(2);
 
@@ -1103,22 +1149,14 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           l2_rsrc(gk_row + (pi % 4) * buf_stride, n_tok * D * 2);
       const __amdgpu_buffer_rsrc_t gvr =
           l2_rsrc(gv_row + (pi % 4) * buf_stride, n_tok * D * 2);
-      float sk[SP][8], sv[SP][8];
-#pragma unroll
-      for (int sp = 0; sp < SP; ++sp)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          sk[sp][e] = 0.f;
-          sv[sp][e] = 0.f;
-        }
-      // Routed rows are staged kStageRows at a time, straight from L2 into
-      // LDS (device-scope LDS-DMA loads, no registers): instruction c of a
-      // chunk fills staged rows RPI*c .. RPI*c + RPI - 1; wave w issues
-      // c = w, w + 8, ... of the keys, then of the values.  Rows past ntot
-      // point past the resource and are not written.
-      // Wave w fills staged rows RPI*ci .. RPI*ci + RPI - 1 for ci = w, w + 8,
-      // ...: the token indices of all its instructions are read from LDS
-      // first (one wait), then the key and the value row of each are issued.
+      // Sums of the half of my slots being merged (registers for HP passes).
+      float sk[HP][8], sv[HP][8];
+      // Routed rows are staged STAGE at a time, straight from L2 into LDS
+      // (device-scope LDS-DMA loads, no registers).  Wave w fills staged rows
+      // RPI*ci .. RPI*ci + RPI - 1 for ci = w, w + 8, ...: the token indices
+      // of all its instructions are read from LDS first (one wait), then the
+      // key and the value row of each are issued.  Rows past ntot point past
+      // the resource and are not written.
       auto gather = [&](int c0) __attribute__((always_inline)) {
         const uint32_t kbase = lds_addr(stage_k), vbase = lds_addr(stage_v);
         const int w0 = __builtin_amdgcn_readfirstlane(wave);
@@ -1141,13 +1179,18 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           }
         }
       };
-      auto stage_sum = [&](int c0) __attribute__((always_inline)) {
-        const int nrow = min(kStageRows, ntot - c0);
-        wait_vm<0>();
-        __syncthreads();
+      // Adds the staged rows c0 .. of the slots of half h to the sums, in
+      // token order; `arrived`: wait for this wave's gathers, then for every
+      // wave's (not needed when the rows were staged for an earlier half).
+      auto stage_sum = [&](int c0, int h, bool arrived) __attribute__((always_inline)) {
+        const int nrow = min(STAGE, ntot - c0);
+        if (arrived) {
+          wait_vm<0>();
+          __syncthreads();
+        }
 #pragma unroll
-        for (int sp = 0; sp < SP; ++sp) {
-          const int l = sp * RPP + tid / GL;
+        for (int sp = 0; sp < HP; ++sp) {
+          const int l = (h * HP + sp) * RPP + tid / GL;
           if (l < nown) {
             const int e0 = max(off[l], c0), e1 = min(off[l] + cnt[l], c0 + nrow);
             for (int e = e0; e < e1; ++e) {
@@ -1164,15 +1207,6 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
         }
         __syncthreads();
       };
-      gather(0);
-      KVM_TS(8);
-      stage_sum(0);
-      KVM_TS(9);
-      for (int c0 = kStageRows; c0 < ntot; c0 += kStageRows) {
-        gather(c0);
-        stage_sum(c0);
-      }
-      KVM_TS(10);
       // Refreshed attention rows: keys into LDS (route operands), keys and
       // values into snapshot u0 + p straight from registers (non-temporal:
       // the attention kernel reads them much later), and after the batch's
@@ -1185,49 +1219,88 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       const bool fin = !do_route && list.final_rows != 0;
       uint16_t *s_ka = static_cast<uint16_t *>(st.s_k_attn);
       uint16_t *s_va = static_cast<uint16_t *>(st.s_v_attn);
-      if (do_route) load_bx(0, 4, KS / 2, KS * 3 / 4);  // the third quarter of the route operands
+      auto refresh = [&](int h) __attribute__((always_inline)) {
 #pragma unroll
-      for (int sp = 0; sp < SP; ++sp) {
-        const int l = sp * RPP + tid / GL;
-        const int j = own_local_to_slot(l, G, member);
-        const bool valid = l < nown && j < S;
-        float k[8], v[8];
-        unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
-        unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
-        if (valid && cnt[l] > 0) {  // state = bf16(state + bf16(sum))
-          round_pack8(sk[sp]);
-          round_pack8(sv[sp]);
+        for (int sp = 0; sp < HP; ++sp) {
+          const int l = (h * HP + sp) * RPP + tid / GL;
+          const int j = own_local_to_slot(l, G, member);
+          const bool valid = l < nown && j < S;
+          float k[8], v[8];
+          unpack8(*reinterpret_cast<const uint4 *>(&own_sk[l * D + part * 8]), k);
+          unpack8(*reinterpret_cast<const uint4 *>(&own_sv[l * D + part * 8]), v);
+          if (valid && cnt[l] > 0) {  // state = bf16(state + bf16(sum))
+            round_pack8(sk[sp]);
+            round_pack8(sv[sp]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              k[e] += sk[sp][e];
+              v[e] += sv[sp][e];
+            }
+            *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = round_pack8(k);
+            *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = round_pack8(v);
+          }
+          // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps;
+          // the rows are only stored, so they are rounded by the packing).
+          float ka[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ka[e] = k[e];
+          layer_norm8<D>(ka, part, ln_w, ln_b, float(L.ln_eps));
+          const uint4 kk = pack8(ka);
+          const uint4 vv = attn_value8_packed<D>(v, own_vl[l]);
+          if (valid) {
+            *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
+            const uint32_t ao = uint32_t((j * D + part * 8) * 2);
+            st16<kPolicyNT>(nk, ao, kk);
+            st16<kPolicyNT>(nv, ao, vv);
+            if (fin) {
+              const int64_t so = (srow + j) * D + part * 8;
+              *reinterpret_cast<uint4 *>(s_ka + so) = kk;
+              *reinterpret_cast<uint4 *>(s_va + so) = vv;
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
+          if (h == NH - 1 && sp == 0) {
+            KVM_TS(11);
+            if (do_route) load_bx(0, 4, KS * 3 / 4, KS);  // the last quarter of the route operands
+          }
+        }
+      };
+      auto zero_sums = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int sp = 0; sp < HP; ++sp)
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            k[e] += sk[sp][e];
-            v[e] += sv[sp][e];
+            sk[sp][e] = 0.f;
+            sv[sp][e] = 0.f;
           }
-          *reinterpret_cast<uint4 *>(&own_sk[l * D + part * 8]) = round_pack8(k);
-          *reinterpret_cast<uint4 *>(&own_sv[l * D + part * 8]) = round_pack8(v);
-        }
-        // Attention rows of the slot (kvm_seq.hpp attn_rows, in two steps;
-        // the rows are only stored, so they are rounded by the packing).
-        float ka[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ka[e] = k[e];
-        layer_norm8<D>(ka, part, ln_w, ln_b, float(L.ln_eps));
-        const uint4 kk = pack8(ka);
-        const uint4 vv = attn_value8_packed<D>(v, own_vl[l]);
-        if (valid) {
-          *reinterpret_cast<uint4 *>(&own_k[l * STR + part * 8]) = kk;
-          const uint32_t ao = uint32_t((j * D + part * 8) * 2);
-          st16<kPolicyNT>(nk, ao, kk);
-          st16<kPolicyNT>(nv, ao, vv);
-          if (fin) {
-            const int64_t so = (srow + j) * D + part * 8;
-            *reinterpret_cast<uint4 *>(s_ka + so) = kk;
-            *reinterpret_cast<uint4 *>(s_va + so) = vv;
+      };
+      gather(0);
+      KVM_TS(8);
+      if (ntot <= STAGE) {  // one staged round serves every half
+#pragma unroll 1
+        for (int h = 0; h < NH; ++h) {
+          zero_sums();
+          stage_sum(0, h, h == 0);
+          if (h == 0) {
+            KVM_TS(9);
+            KVM_TS(10);
           }
+          // The third quarter of the route operands with the last half (not
+          // earlier: with them resident the earlier halves' sums would spill).
+          if (h == NH - 1 && do_route) load_bx(0, 4, KS / 2, KS * 3 / 4);
+          refresh(h);
         }
-        __builtin_amdgcn_sched_barrier(0);  // one slot pass at a time (register pressure)
-        if (sp == 0) {
-          KVM_TS(11);
-          if (do_route) load_bx(0, 4, KS * 3 / 4, KS);  // the last quarter of the route operands
+      } else {  // several rounds: each half gathers them again
+#pragma unroll 1
+        for (int h = 0; h < NH; ++h) {
+          zero_sums();
+          for (int c0 = 0; c0 < ntot; c0 += STAGE) {
+            if (h > 0 || c0 > 0) gather(c0);
+            stage_sum(c0, h, true);
+          }
+          if (h == NH - 1 && do_route) load_bx(0, 4, KS / 2, KS * 3 / 4);
+          refresh(h);
+          __syncthreads();  // every wave has read the staged rows before the next gather
         }
       }
       __syncthreads();
@@ -1400,8 +1473,9 @@ bool chain_fixed_ok(const ChainPlan &p, const ChainList &list, int64_t n_tok) {
   const int S = list.state_before[0];
   for (int i = 0; i < list.count; ++i)
     if (list.n_append[i] != 0 || list.state_before[i] != S) return false;
+  // Owned slots per member: up to 64 at G = 16, up to 128 at G = 8.
   const int nblk = (S + 15) / 16;
-  return (nblk + p.G - 1) / p.G * 16 <= kOwnMax;
+  return (nblk + p.G - 1) / p.G * 16 <= (p.G == 8 ? kOwnMax : 64);
 }
 
 int64_t chain_scratch_bytes(const kvm_layer &L, int64_t n_tok) {
@@ -1455,18 +1529,23 @@ hipError_t launch_chain(const kvm_layer &L, const kvm_seq &src, int64_t n_tok,
     const dim3 grid(unsigned((nrows + 7) / 8 * 8 * p.G)), blk(kChainThreads);
     if (fixed) {
       const int nt = int(n_tok);
-      if (L.head_dim == 128 && p.G == 8)
-        hipLaunchKernelGGL((k_chain_fixed<128, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
-                           row0, nrows, route_log, append_log, log_stride);
+      const bool own128 = ((list.state_before[0] + 15) / 16 + p.G - 1) / p.G * 16 > 64;  // G == 8 then
+#define KVM_FIXED(DD, GG, OO)                                                                               \
+  hipLaunchKernelGGL((k_chain_fixed<DD, GG, OO>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows, \
+                     row0, nrows, route_log, append_log, log_stride)
+      if (L.head_dim == 128 && p.G == 8 && own128)
+        KVM_FIXED(128, 8, 128);
+      else if (L.head_dim == 128 && p.G == 8)
+        KVM_FIXED(128, 8, 64);
       else if (L.head_dim == 128)
-        hipLaunchKernelGGL((k_chain_fixed<128, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
-                           row0, nrows, route_log, append_log, log_stride);
+        KVM_FIXED(128, 16, 64);
+      else if (p.G == 8 && own128)
+        KVM_FIXED(64, 8, 128);
       else if (p.G == 8)
-        hipLaunchKernelGGL((k_chain_fixed<64, 8>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
-                           row0, nrows, route_log, append_log, log_stride);
+        KVM_FIXED(64, 8, 64);
       else
-        hipLaunchKernelGGL((k_chain_fixed<64, 16>), grid, blk, 0, stream, L, src, nt, st, snaps, list, cs, rows,
-                           row0, nrows, route_log, append_log, log_stride);
+        KVM_FIXED(64, 16, 64);
+#undef KVM_FIXED
     } else if (L.head_dim == 128) {
       hipLaunchKernelGGL(k_chain<128>, grid, blk, p.dyn_lds, stream, L, src, int(n_tok), st, snaps, list, cs,
                          rows, row0, nrows, p.G, p.tpw, p.spm_max, route_log, append_log, log_stride);

@@ -716,6 +716,54 @@ def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C
     T.log(f"[chain] {plan.n_updates} updates, S={S}, {n_app} appended tokens: identical")
 
 
+@pytest.mark.parametrize("B,Hkv,Tn,D,min_len,skew", [
+    (1, 32, 8192, 128, 768, False),   # 96 owned slots per member
+    (1, 32, 8192, 128, 1024, False),  # 128 owned slots per member
+    (2, 16, 6144, 64, 1024, False),
+    (4, 8, 8192, 128, 1024, True),    # most tokens to a few slots: several staged rounds per half
+])
+def test_chain_wide_state_matches_per_update_kernels(lib, monkeypatch, B, Hkv, Tn, D, min_len, skew):
+    """A fixed budget above the first chunk: the first update appends up to
+    `min_len` slots (appending chain), every later one appends nothing, so
+    the launch is split there and the rest runs on the slot-owner chain with
+    more than 64 slots per member (up to 128 at 8 members).  Routes, state
+    and outputs must equal the per-update kernels bit for bit."""
+    C, Hq = 512, Hkv
+    T.log(f"[chain-wide] B{B} Hkv{Hkv} T{Tn} D{D} C{C} min_len {min_len} skew {skew}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="fixed", sink=1, min_len=min_len, n_max=4, factor=6.0)
+    gen = torch.Generator().manual_seed(5)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 23)
+    if skew:
+        d = torch.randn(D, generator=gen)
+        k = (d / d.norm() + 0.02 * torch.randn(B, Hkv, Tn, D, generator=gen) / math.sqrt(D)).bfloat16()
+    q, k, v, g = (t.to(DEV) for t in (q, k, v, g))
+    plan = m.make_plan(Tn)
+    S = plan.final_state_len
+    assert S == min_len and plan.upd_n_append[0] > 0 and not any(plan.upd_n_append[1:])
+    res = {}
+    for name, chain, fixed in (("owner", "1", "1"), ("per-update", "0", "1")):
+        monkeypatch.setenv("KVM_AMD_CHAIN", chain)
+        monkeypatch.setenv("KVM_AMD_CHAIN_FIXED", fixed)
+        with torch.no_grad():
+            res[name] = m.prefill_raw(q, k, v, g, route_log=True)
+        torch.cuda.synchronize()
+    a, b = res["owner"], res["per-update"]
+    for key in ("route_log", "append_log", "out"):
+        assert torch.equal(a[key], b[key]), f"{key}"
+    for key in ("state_k", "state_v", "state_vlen", "state_k_attn", "state_v_attn"):
+        assert torch.equal(a[key][:, :S], b[key][:, :S]), f"{key}"
+    r = b["route_log"][1: plan.n_updates].long()
+    mem = torch.where(r >= 0, (r // 16) % 8, 8).flatten(0, 1)
+    busiest = float(torch.stack([torch.bincount(x, minlength=9)[:8] for x in mem.cpu()]).max(dim=1).values
+                    .float().mean())
+    T.log(f"[chain-wide] {plan.n_updates} updates, S={S}: identical; busiest member takes {busiest:.0f} tokens")
+    if skew:
+        assert busiest > 96, "inputs did not skew the routes past one staged round"
+
+
 @pytest.mark.parametrize("B,Hkv,Tn,D,C", [
     (4, 8, 8192, 128, 512),  # 32 rows: one launch
     (9, 5, 4096, 64, 256),   # 45 rows: two row batches
