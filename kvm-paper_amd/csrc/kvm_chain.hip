@@ -395,7 +395,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
   int *cnt = sorted + n_tok;      // [spm_max]
   int *off = cnt + spm_max;       // [spm_max]
   int *fill = off + spm_max;      // [spm_max]
-  float *novl = reinterpret_cast<float *>(lst);  // [n_tok] novelty of all tokens (rank phase)
+  int *apos = sorted;             // [n_tok] append position of each token (append phase)
+  // [npow] sort keys of the append selection, 8-byte aligned after fill
+  const int npow = n_tok <= 1 ? 1 : 1 << (32 - __builtin_clz(unsigned(n_tok - 1)));
+  uint64_t *skey = reinterpret_cast<uint64_t *>(fill + spm_max + (spm_max & 1));
 
   const int tid = threadIdx.x, part = tid % GL;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
@@ -503,27 +506,61 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
       arrive();
       if (!wait()) return;
       KVM_TS_A(2);
+      // The na smallest (novelty, token) pairs: a bitonic sort of the unique
+      // keys mono(novelty) << 32 | token (the same order as comparing the
+      // novelty, then the index; -0 is read as +0 so that it ties with it),
+      // padded with the largest key to a power of two.
       const __amdgpu_buffer_rsrc_t nr = l2_rsrc(cs.nov + rb, int64_t(n_tok) * 4);
-      for (int t = tid; t < n_tok; t += kChainThreads) novl[t] = __uint_as_float(l2_ld4(nr, t * 4));
-      __syncthreads();
-      for (int t = tid; t < n_tok; t += kChainThreads) {
-        const float x = novl[t];
-        int r = 0;
-        for (int w = 0; w < n_tok; ++w) {
-          const float y = novl[w];
-          r += (y < x) || (y == x && w < t);
+      for (int t = tid; t < npow; t += kChainThreads) {
+        uint64_t key = ~uint64_t(0);
+        if (t < n_tok) {
+          const float x = __uint_as_float(l2_ld4(nr, t * 4)) + 0.0f;
+          const uint32_t bits = __float_as_uint(x);
+          const uint32_t m = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+          key = (uint64_t(m) << 32) | uint32_t(t);
         }
-        tok_a[t] = r < na ? 1 : 0;
+        skey[t] = key;
+        if (t < n_tok) tok_a[t] = 0;
       }
+      __syncthreads();
+      for (int k2 = 2; k2 <= npow; k2 <<= 1) {
+        for (int j = k2 >> 1; j > 0; j >>= 1) {
+          for (int e = tid; e < npow; e += kChainThreads) {
+            const int f = e ^ j;
+            if (f > e) {
+              const uint64_t a = skey[e], c = skey[f];
+              if ((a > c) == ((e & k2) == 0)) {
+                skey[e] = c;
+                skey[f] = a;
+              }
+            }
+          }
+          __syncthreads();
+        }
+      }
+      for (int r = tid; r < na; r += kChainThreads) tok_a[int(uint32_t(skey[r]))] = 1;
       __syncthreads();
       KVM_TS_A(3);
-      // Positions of my appended tokens (tokens before them that append).
-      if (tid < ntk) {
-        const int t = t0 + tid;
-        int p = 0;
-        for (int w = 0; w < t; ++w) p += tok_a[w];
-        res_i[tid] = tok_a[t] ? p : -1;
+      // Append position of every appended token: the appended tokens before
+      // it, by wave ballots in token order (wave totals in res_v).
+      {
+        int base = 0;
+        for (int c0 = 0; c0 < n_tok; c0 += kChainThreads) {
+          const int t = c0 + tid;
+          const bool ap = t < n_tok && tok_a[t] != 0;
+          const uint64_t bal = __ballot(ap);
+          const int before = int(__builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)));
+          if ((tid & 63) == 0) res_v[tid >> 6] = __int_as_float(__popcll(bal));
+          __syncthreads();
+          int wb = base;
+          for (int w = 0; w < (tid >> 6); ++w) wb += __float_as_int(res_v[w]);
+          if (t < n_tok) apos[t] = ap ? wb + before : -1;
+          for (int w = 0; w < kChainWaves; ++w) base += __float_as_int(res_v[w]);
+          __syncthreads();
+        }
       }
+      if (tid < ntk) res_i[tid] = apos[t0 + tid];
       __syncthreads();
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
@@ -571,15 +608,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
       const bool app = na > 0 && tok_a[t] != 0;
       cs.route[rb + t] = app ? -1 : res_i[tid];
       if (alog) alog[t] = app ? 1 : 0;
-      if (rlog) {
-        int r = res_i[tid];
-        if (app) {
-          int p = 0;
-          for (int w = 0; w < t; ++w) p += tok_a[w];
-          r = sb + p;
-        }
-        rlog[t] = r;
-      }
+      if (rlog) rlog[t] = app ? sb + apos[t] : res_i[tid];
     }
     KVM_TS_A(7);
     arrive();
@@ -1462,7 +1491,11 @@ bool chain_plan(const kvm_layer &L, int64_t n_tok, int64_t max_slots, ChainPlan 
   p->spm_max = int((max_slots + G - 1) / G);
   p->row_batch = int(batch_groups);
   p->workgroups = int(batch_groups * G);
-  const int64_t dyn = (4 * n_tok + 3 * int64_t(p->spm_max)) * 4;
+  // ints of the lists, then the append selection's 8-byte keys (a power of
+  // two of them) after one int of alignment padding.
+  int64_t npow = 1;
+  while (npow < n_tok) npow <<= 1;
+  const int64_t dyn = (4 * n_tok + 3 * int64_t(p->spm_max) + 1) * 4 + npow * 8;
   if (dyn > 48 * 1024) return false;
   p->dyn_lds = size_t(dyn);
   return true;
