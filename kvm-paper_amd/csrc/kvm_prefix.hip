@@ -7,8 +7,8 @@
 // (about twenty launches per layer, each reading and writing the tensor);
 // here every element is read once and written once.
 //
-// Work split: a wave covers 32 consecutive tokens of one (batch, head), q
-// heads first, then kv heads.  A row of D features is held by D/8
+// Work split: a wave covers 32 consecutive tokens of one (batch, head) and
+// one row kind: q, k or v.  A row of D features is held by D/8
 // consecutive lanes, 8 features per lane (one 16-byte access), so a pass
 // works on 64/(D/8) tokens.  The token shift takes the previous token's row
 // from the neighbouring lane group (or the pass before): every input row is
@@ -33,28 +33,66 @@ struct VRes {
   float vf[8], gl[8];
 };
 
+// rbf of 8 values, two per conversion instruction.
+__device__ __forceinline__ void rbf8(float (&x)[8]) { (void)round_pack8(x); }
+
+// 1 / (1 + exp(-t)) in fp32: the reciprocal from v_rcp_f32 refined by one
+// Newton step, which gives the correctly rounded quotient of the division
+// except in rare cases one ulp off (and 0 where exp(-t) overflows).
+__device__ __forceinline__ float sigmoid_f32(float t) {
+  const float d = 1.f + expf(-t);
+  const float r = __builtin_amdgcn_rcpf(d);
+  return d == INFINITY ? 0.f : __builtin_fmaf(__builtin_fmaf(-d, r, 1.f), r, r);
+}
+
 // value residual applied to one row (v in place).  g0: v_gate0 of the lane's
 // channels (modes 2, 3); lamb: the mixing weight (mode 1).
 __device__ __forceinline__ void value_residual(int mode, float (&v)[8], const VRes &r, const float (&g0)[8],
                                                float lamb) {
+  float a[8], b[8];
   if (mode == 1) {  // (1 - lamb) * v + lamb * v_first
     const float c1 = rbf(1.f - lamb);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = rbf(rbf(c1 * v[i]) + rbf(lamb * r.vf[i]));
+    for (int i = 0; i < 8; ++i) {
+      a[i] = c1 * v[i];
+      b[i] = lamb * r.vf[i];
+    }
+    rbf8(a);
+    rbf8(b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = a[i] + b[i];
   } else {  // v + (v_first - v) * sigmoid(v_gate0 + gate_lin)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float t = rbf(g0[i] + r.gl[i]);
-      const float g = rbf(1.f / (1.f + expf(-t)));
-      v[i] = rbf(v[i] + rbf(rbf(r.vf[i] - v[i]) * g));
+      a[i] = g0[i] + r.gl[i];
+      b[i] = r.vf[i] - v[i];
     }
+    rbf8(a);
+    rbf8(b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = sigmoid_f32(a[i]);
+    rbf8(a);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] *= a[i];
+    rbf8(b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] += b[i];
   }
+  rbf8(v);
 }
 
 // x + x_mix * (prev - x)
 __device__ __forceinline__ void token_shift(float (&x)[8], const float (&prev)[8], const float (&mix)[8]) {
+  float d[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = rbf(x[i] + rbf(mix[i] * rbf(prev[i] - x[i])));
+  for (int i = 0; i < 8; ++i) d[i] = prev[i] - x[i];
+  rbf8(d);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) d[i] *= mix[i];
+  rbf8(d);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] += d[i];
+  rbf8(x);
 }
 
 // LayerNorm over the row (bf16 output; w, b: the lane's 8 parameters),
@@ -77,12 +115,19 @@ __device__ __forceinline__ void norm_rope(float (&x)[8], const float (&wf)[8], c
   q = group_sum<D / 8>(q);
   const float rstd = 1.0f / sqrtf(q / float(D) + eps);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = rbf((x[i] - mean) * rstd * wf[i] + bfv[i]);
-  float y[8];
+  for (int i = 0; i < 8; ++i) x[i] = (x[i] - mean) * rstd * wf[i] + bfv[i];
+  rbf8(x);
+  float a[8], b[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) y[i] = rbf(rbf(c[i] * x[i]) + rbf(s[i] * x[i ^ 1]));
+  for (int i = 0; i < 8; ++i) {
+    a[i] = c[i] * x[i];
+    b[i] = s[i] * x[i ^ 1];
+  }
+  rbf8(a);
+  rbf8(b);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = y[i];
+  for (int i = 0; i < 8; ++i) x[i] = a[i] + b[i];
+  rbf8(x);
 }
 
 // One wave covers kTokWave consecutive tokens of one (batch, head), RPW rows
@@ -112,9 +157,11 @@ __device__ __forceinline__ void last_row(const float (&x)[8], int part, float (&
 }
 
 // The raw rows one pass of a wave reads (packed bf16, 16 bytes per lane),
-// fetched a pass ahead so that their latency overlaps the previous pass.
+// fetched a pass ahead so that their latency overlaps the previous pass: x,
+// cos and sin for a q or k row; v, v_first, gate_lin and the key weight for
+// a v row.
 struct PassRaw {
-  uint4 x, v, c, s, vf, gl;
+  uint4 a, b, c;
   uint16_t kw;
 };
 
@@ -131,190 +178,236 @@ __device__ __forceinline__ uint4 raw8(const void *base, int64_t elem) {
   return *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + elem);
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
-  constexpr int LPR = D / 8;          // lanes per row
-  constexpr int RPW = 64 / LPR;       // rows per pass
-  constexpr int PASSES = kTokWave / RPW;
-  const int lane = threadIdx.x & 63;
-  const int part = lane % LPR, sub = lane / LPR;
-  const int64_t T = P.seq_len, Hq = P.q_heads, Hkv = P.kv_heads;
-  const int64_t tiles = (T + kTokWave - 1) / kTokWave;
-  const int64_t wv = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-  const int64_t tile = wv % tiles;
-  const int64_t bh = wv / tiles;
-  const int64_t head = bh % (Hq + Hkv);
-  const int64_t bi = bh / (Hq + Hkv);
-  if (bi >= P.batch) return;  // wave-uniform
-  const int mode = int(P.value_residual_mode);
-  const bool shift = P.token_shift != 0;
-  const bool pre = mode == 1 || mode == 2;
-  const int64_t t0 = tile * kTokWave;
-  const float eps = float(P.ln_eps);
-  const bool is_q = head < Hq;
-  const int64_t hk = head - Hq;
-  const int64_t width = is_q ? Hq * D : Hkv * D;
-  const int64_t chan = (is_q ? head : hk) * D + part * 8;
-  const int npass = int(min(int64_t(PASSES), (T - t0 + RPW - 1) / RPW));  // passes with a live token
-  // Token of this lane in pass ps (clamped to T - 1 for the lanes past the end).
-  auto token = [&](int ps) {
-    const int64_t t = t0 + ps * RPW + sub;
-    return t < T ? t : T - 1;
-  };
-  auto fetch = [&](int ps, PassRaw &r) {
-    const int64_t tt = token(ps);
-    const int64_t row = bi * T + tt;
-    const int64_t ro = bi * P.rope_sb + tt * P.rope_st + part * 8;
-    r.x = raw8(is_q ? P.q_lin : P.k_lin, row * P.qkv_st + chan);
-    r.c = raw8(P.cos, ro);
-    r.s = raw8(P.sin, ro);
-    r.v = r.vf = r.gl = make_uint4(0, 0, 0, 0);
-    r.kw = 0;
-    if (!is_q) {
-      r.v = raw8(P.v_lin, row * P.qkv_st + chan);
-      if (mode != 0) r.vf = raw8(P.v_first, row * width + chan);
-      if (mode >= 2) r.gl = raw8(P.gate_lin, row * width + chan);
-      // every lane loads the (b, t, kv head) weight; lane part 0 uses it
-      r.kw = static_cast<const uint16_t *>(P.key_weight ? P.key_weight : P.v_lin)[P.key_weight ? row * P.kw_st + hk : 0];
-    }
-  };
+// What one wave works on: kTokWave tokens from t0 of one (batch, head) row
+// kind, channels chan.. of a row of `width` elements.
+struct PrefixTile {
+  int64_t bi, t0, hk, chan, width;
+  int npass, lane, part, sub;
+};
 
-  // Prologue: the first pass's rows, then every parameter and predecessor
-  // row, all loaded before any of them is used and without branches around
-  // the loads (an unused or NULL operand reads a valid stand-in that is never
-  // used): a load whose value is consumed inside a branch makes the wave wait
-  // there, which would give every prologue load a round trip of its own.
+// Window-ring row of a single decode token (kv heads): ring_pos, or with
+// device counters (start, length) the row after the live ones.
+__device__ __forceinline__ int64_t ring_row(const kvm_prefix_desc &P, const PrefixTile &w, int32_t ctl_start,
+                                            int32_t ctl_len) {
+  int64_t pos = P.ring_pos;
+  if (P.ring_ctl) {
+    const int64_t cap = P.ring_cap;
+    const int64_t start = ((int64_t(ctl_start) % cap) + cap) % cap;
+    const int64_t len = min(max(int64_t(ctl_len), int64_t(0)), cap);
+    pos = (start + len) % cap;
+  }
+  return (w.bi * P.kv_heads + w.hk) * P.ring_cap + pos;
+}
+
+// q or k rows: carried raw row, token shift, LayerNorm, RoPE.
+//
+// Prologue (both row kinds): the first pass's rows, then every parameter and
+// predecessor row, all loaded before any of them is used and without
+// branches around the loads (an unused or NULL operand reads a valid
+// stand-in that is never used): a load whose value is consumed inside a
+// branch makes the wave wait there, which would give every prologue load a
+// round trip of its own.
+template <int D>
+__device__ __forceinline__ void qk_rows(const kvm_prefix_desc &P, const PrefixTile &w, bool is_q) {
+  constexpr int LPR = D / 8, RPW = 64 / LPR;
+  const int64_t T = P.seq_len;
+  const bool shift = P.token_shift != 0;
+  const void *src = is_q ? P.q_lin : P.k_lin;
+  auto fetch = [&](int ps, PassRaw &r) {
+    const int64_t t = w.t0 + ps * RPW + w.sub;
+    const int64_t tt = t < T ? t : T - 1;  // lanes past the end read the last token
+    const int64_t ro = w.bi * P.rope_sb + tt * P.rope_st + w.part * 8;
+    r.a = raw8(src, (w.bi * T + tt) * P.qkv_st + w.chan);
+    r.b = raw8(P.cos, ro);
+    r.c = raw8(P.sin, ro);
+  };
   PassRaw next;
   fetch(0, next);
   const void *ln_w = is_q ? P.ln_q_w : P.ln_k_w;
-  const int64_t own = part * 8;  // stand-in index: the lane's LayerNorm weights
-  const bool use_g0 = !is_q && mode >= 2, use_lamb = !is_q && mode == 1;
+  const int64_t own = w.part * 8;  // stand-in index: the lane's LayerNorm weights
   uint4 r_w = raw8(ln_w, own);
   uint4 r_b = raw8(is_q ? P.ln_q_b : P.ln_k_b, own);
-  uint4 r_g0 = raw8(use_g0 ? P.v_gate0 : ln_w, use_g0 ? chan : own);
-  uint32_t r_lamb = static_cast<const uint16_t *>(use_lamb ? P.lamb : ln_w)[0];
+  uint4 r_mix = raw8(shift ? (is_q ? P.x_q : P.x_k) : ln_w, shift ? w.chan : own);
+  // Predecessor of the tile's first token: the row before it (t0 > 0) or
+  // the carried row.
   const void *x_prev = is_q ? P.q_prev : P.k_prev;
-  const bool vmix_on = shift && !is_q;
-  uint4 r_xmix = raw8(shift ? (is_q ? P.x_q : P.x_k) : ln_w, shift ? chan : own);
-  uint4 r_vmix = raw8(vmix_on ? P.x_v : ln_w, vmix_on ? chan : own);
-  // Predecessor of the tile's first token: the row before it (t0 > 0; for v
-  // with the inputs of a pre-shift value residual) or the carried rows.
-  const bool lin_pred = shift && t0 > 0;
-  const int64_t rp = bi * T + t0 - 1;
-  const bool xc_on = lin_pred || (shift && x_prev);
-  const bool vc_on = !is_q && (lin_pred || (shift && P.v_prev));
-  const bool vres_on = lin_pred && !is_q && pre;
-  uint4 r_xc = raw8(!xc_on ? ln_w : lin_pred ? (is_q ? P.q_lin : P.k_lin) : x_prev,
-                    !xc_on ? own : lin_pred ? rp * P.qkv_st + chan : bi * width + chan);
-  uint4 r_vc = raw8(!vc_on ? ln_w : lin_pred ? P.v_lin : P.v_prev,
-                    !vc_on ? own : lin_pred ? rp * P.qkv_st + chan : bi * width + chan);
-  uint4 r_vf = raw8(vres_on ? P.v_first : ln_w, vres_on ? rp * width + chan : own);
-  uint4 r_gl = raw8(vres_on && mode >= 2 ? P.gate_lin : ln_w, vres_on && mode >= 2 ? rp * width + chan : own);
-  // Every prologue value pinned here: the compiler cannot sink a load into
-  // the branch that uses its value, and the wave waits once for all of them.
+  const bool lin_pred = shift && w.t0 > 0;
+  const bool c_on = lin_pred || (shift && x_prev);
+  uint4 r_c = raw8(!c_on ? ln_w : lin_pred ? src : x_prev,
+                   !c_on ? own : lin_pred ? (w.bi * T + w.t0 - 1) * P.qkv_st + w.chan : w.bi * w.width + w.chan);
   // ring counters of a graph-replayed decode step (start, length)
   const int32_t *ctl = P.ring_ctl ? P.ring_ctl : static_cast<const int32_t *>(ln_w);
   int32_t ctl_start = ctl[1], ctl_len = ctl[2];
-  for (uint4 *r : {&r_w, &r_b, &r_g0, &r_xmix, &r_vmix, &r_xc, &r_vc, &r_vf, &r_gl}) *r = pinned(*r);
-  asm volatile("" : "+v"(r_lamb), "+v"(ctl_start), "+v"(ctl_len));
+  for (uint4 *r : {&r_w, &r_b, &r_mix, &r_c}) *r = pinned(*r);
+  asm volatile("" : "+v"(ctl_start), "+v"(ctl_len));
 
-  float wf[8], bfv[8], xmix[8], vmix[8], xcarry[8], vcarry[8], g0[8];
+  float wf[8], bfv[8], mix[8], carry[8];
   unpack8(r_w, wf);
   unpack8(r_b, bfv);
+  if (shift) {
+    unpack8(r_mix, mix);
+    unpack8(r_c, carry);  // (no carried row at t0 == 0: the "first" fallback in the first pass)
+  }
+  const bool ring = !is_q && P.ring_k && T == 1;
+  const int64_t ring_o = ring ? ring_row(P, w, ctl_start, ctl_len) : 0;
+  uint16_t *x_out = static_cast<uint16_t *>(is_q ? P.q_out : P.k_out);
+  uint16_t *x_last = static_cast<uint16_t *>(is_q ? P.q_last_out : P.k_last_out);
+  const float eps = float(P.ln_eps);
+#pragma unroll 1
+  for (int ps = 0; ps < w.npass; ++ps) {
+    const PassRaw cur = next;
+    if (ps + 1 < w.npass) fetch(ps + 1, next);
+    const int64_t t = w.t0 + ps * RPW + w.sub;
+    const bool live = t < T;
+    const int64_t e = (w.bi * T + (live ? t : T - 1)) * w.width + w.chan;
+    float x[8], c[8], sn[8];
+    unpack8(cur.a, x);
+    unpack8(cur.b, c);
+    unpack8(cur.c, sn);
+    if (live && x_last && t == T - 1) store8(x_last + w.bi * w.width + w.chan, x);
+    if (shift) {
+      float pv[8];
+      if (ps == 0 && w.t0 == 0 && !x_prev)  // fallback "first": token 0 is its own predecessor
+        for (int i = 0; i < 8; ++i) carry[i] = __shfl(x[i], w.part);
+      prev_rows<LPR>(x, carry, w.lane, pv);
+      last_row<LPR>(x, w.part, carry);
+      token_shift(x, pv, mix);
+    }
+    norm_rope<D>(x, wf, bfv, eps, c, sn);
+    if (live) store8(x_out + e, x);
+    if (ring && live) store8(static_cast<uint16_t *>(P.ring_k) + ring_o * D + w.part * 8, x);
+  }
+}
+
+// v rows: value residual before / after the token shift, and the merge gate
+// 1 + elu(key_weight), one value per (b, t, kv head).
+template <int D>
+__device__ __forceinline__ void v_rows(const kvm_prefix_desc &P, const PrefixTile &w) {
+  constexpr int LPR = D / 8, RPW = 64 / LPR;
+  const int64_t T = P.seq_len;
+  const int mode = int(P.value_residual_mode);
+  const bool shift = P.token_shift != 0;
+  const bool pre = mode == 1 || mode == 2;
+  auto fetch = [&](int ps, PassRaw &r) {
+    const int64_t t = w.t0 + ps * RPW + w.sub;
+    const int64_t row = w.bi * T + (t < T ? t : T - 1);
+    r.a = raw8(P.v_lin, row * P.qkv_st + w.chan);
+    r.b = r.c = make_uint4(0, 0, 0, 0);
+    if (mode != 0) r.b = raw8(P.v_first, row * w.width + w.chan);
+    if (mode >= 2) r.c = raw8(P.gate_lin, row * w.width + w.chan);
+    // every lane loads the (b, t, kv head) weight; lane part 0 uses it
+    r.kw = static_cast<const uint16_t *>(P.key_weight ? P.key_weight : P.v_lin)[P.key_weight ? row * P.kw_st + w.hk : 0];
+  };
+  PassRaw next;
+  fetch(0, next);
+  const void *stand = P.ln_k_w;  // a valid operand for the loads a mode does not use
+  const int64_t own = w.part * 8;
+  const bool use_g0 = mode >= 2, use_lamb = mode == 1;
+  uint4 r_g0 = raw8(use_g0 ? P.v_gate0 : stand, use_g0 ? w.chan : own);
+  uint32_t r_lamb = static_cast<const uint16_t *>(use_lamb ? P.lamb : stand)[0];
+  uint4 r_mix = raw8(shift ? P.x_v : stand, shift ? w.chan : own);
+  // Predecessor of the tile's first token: the row before it (with the
+  // inputs of a pre-shift value residual) or the carried row.
+  const bool lin_pred = shift && w.t0 > 0;
+  const int64_t rp = w.bi * T + w.t0 - 1;
+  const bool c_on = lin_pred || (shift && P.v_prev);
+  const bool vres_on = lin_pred && pre;
+  uint4 r_c = raw8(!c_on ? stand : lin_pred ? P.v_lin : P.v_prev,
+                   !c_on ? own : lin_pred ? rp * P.qkv_st + w.chan : w.bi * w.width + w.chan);
+  uint4 r_vf = raw8(vres_on ? P.v_first : stand, vres_on ? rp * w.width + w.chan : own);
+  uint4 r_gl = raw8(vres_on && mode >= 2 ? P.gate_lin : stand, vres_on && mode >= 2 ? rp * w.width + w.chan : own);
+  const int32_t *ctl = P.ring_ctl ? P.ring_ctl : static_cast<const int32_t *>(stand);
+  int32_t ctl_start = ctl[1], ctl_len = ctl[2];
+  for (uint4 *r : {&r_g0, &r_mix, &r_c, &r_vf, &r_gl}) *r = pinned(*r);
+  asm volatile("" : "+v"(r_lamb), "+v"(ctl_start), "+v"(ctl_len));
+
+  float g0[8], mix[8], carry[8];
   unpack8(r_g0, g0);
   const float lamb = use_lamb ? bf2f(r_lamb) : 0.f;
   if (shift) {
-    unpack8(r_xmix, xmix);
-    unpack8(r_vmix, vmix);
-    // (no carried row at t0 == 0: the "first" fallback in the first pass)
-    unpack8(r_xc, xcarry);
-    unpack8(r_vc, vcarry);
+    unpack8(r_mix, mix);
+    unpack8(r_c, carry);
     if (vres_on) {
       VRes vr;
       unpack8(r_vf, vr.vf);
       unpack8(r_gl, vr.gl);
-      value_residual(mode, vcarry, vr, g0, lamb);
+      value_residual(mode, carry, vr, g0, lamb);
     }
   }
-  // Window-ring row of a single decode token (kv heads).
-  const bool ring = !is_q && P.ring_k && T == 1;
-  int64_t ring_o = 0;
-  if (ring) {
-    int64_t pos = P.ring_pos;
-    if (P.ring_ctl) {
-      const int64_t cap = P.ring_cap;
-      const int64_t start = ((int64_t(ctl_start) % cap) + cap) % cap;
-      const int64_t len = min(max(int64_t(ctl_len), int64_t(0)), cap);
-      pos = (start + len) % cap;
-    }
-    ring_o = (bi * Hkv + hk) * P.ring_cap + pos;
-  }
-  uint16_t *x_out = static_cast<uint16_t *>(is_q ? P.q_out : P.k_out);
-  uint16_t *x_last = static_cast<uint16_t *>(is_q ? P.q_last_out : P.k_last_out);
-
+  const bool ring = P.ring_k && T == 1;
+  const int64_t ring_o = ring ? ring_row(P, w, ctl_start, ctl_len) : 0;
 #pragma unroll 1
-  for (int ps = 0; ps < npass; ++ps) {
+  for (int ps = 0; ps < w.npass; ++ps) {
     const PassRaw cur = next;
-    if (ps + 1 < npass) fetch(ps + 1, next);
-    const int64_t t = t0 + ps * RPW + sub;
+    if (ps + 1 < w.npass) fetch(ps + 1, next);
+    const int64_t t = w.t0 + ps * RPW + w.sub;
     const bool live = t < T;
-    const int64_t e = (bi * T + (live ? t : T - 1)) * width + chan;
-    float x[8], c[8], sn[8];
-    unpack8(cur.x, x);
-    unpack8(cur.c, c);
-    unpack8(cur.s, sn);
-    // q / k: carried raw row, token shift, LayerNorm, RoPE
-    if (live && x_last && t == T - 1) store8(x_last + bi * width + chan, x);
-    if (shift) {
-      float pv[8];
-      if (ps == 0 && t0 == 0 && !x_prev)  // fallback "first": token 0 is its own predecessor
-        for (int i = 0; i < 8; ++i) xcarry[i] = __shfl(x[i], part);
-      prev_rows<LPR>(x, xcarry, lane, pv);
-      last_row<LPR>(x, part, xcarry);
-      token_shift(x, pv, xmix);
-    }
-    norm_rope<D>(x, wf, bfv, eps, c, sn);
-    if (live) store8(x_out + e, x);
-    if (is_q) continue;  // wave-uniform
-    if (ring && live) store8(static_cast<uint16_t *>(P.ring_k) + ring_o * D + part * 8, x);
-    // values: value residual before / after the token shift
+    const int64_t e = (w.bi * T + (live ? t : T - 1)) * w.width + w.chan;
     float v[8];
     VRes vr;
-    unpack8(cur.v, v);
-    unpack8(cur.vf, vr.vf);
-    unpack8(cur.gl, vr.gl);
+    unpack8(cur.a, v);
+    unpack8(cur.b, vr.vf);
+    unpack8(cur.c, vr.gl);
     if (pre) value_residual(mode, v, vr, g0, lamb);
     if (live && P.v_last_out && t == T - 1)
-      store8(static_cast<uint16_t *>(P.v_last_out) + bi * width + chan, v);
+      store8(static_cast<uint16_t *>(P.v_last_out) + w.bi * w.width + w.chan, v);
     if (shift) {
       float pv[8];
-      if (ps == 0 && t0 == 0 && !P.v_prev)
-        for (int i = 0; i < 8; ++i) vcarry[i] = __shfl(v[i], part);
-      prev_rows<LPR>(v, vcarry, lane, pv);
-      last_row<LPR>(v, part, vcarry);
-      token_shift(v, pv, vmix);
+      if (ps == 0 && w.t0 == 0 && !P.v_prev)
+        for (int i = 0; i < 8; ++i) carry[i] = __shfl(v[i], w.part);
+      prev_rows<LPR>(v, carry, w.lane, pv);
+      last_row<LPR>(v, w.part, carry);
+      token_shift(v, pv, mix);
     }
     if (mode == 3) value_residual(2, v, vr, g0, lamb);
     if (live) store8(static_cast<uint16_t *>(P.v_out) + e, v);
-    if (ring && live) store8(static_cast<uint16_t *>(P.ring_v) + ring_o * D + part * 8, v);
-    // merge gate 1 + elu(key_weight), one value per (b, t, kv head)
+    if (ring && live) store8(static_cast<uint16_t *>(P.ring_v) + ring_o * D + w.part * 8, v);
     uint16_t gbits = 0x3f80;  // 1.0: no key weighting
-    if (live && part == 0 && P.key_weight && P.gate_out) {
-      const int64_t ge = (bi * T + t) * Hkv + hk;
+    if (live && w.part == 0 && P.key_weight && P.gate_out) {
+      const int64_t ge = (w.bi * T + t) * P.kv_heads + w.hk;
       const float kw = bf2f(cur.kw);
       const float el = rbf(kw > 0.f ? kw : expm1f(kw));
       gbits = uint16_t(f2bf(1.f + el));
       static_cast<uint16_t *>(P.gate_out)[ge] = gbits;
     }
-    if (ring && live && part == 0) static_cast<uint16_t *>(P.ring_gate)[ring_o] = gbits;
+    if (ring && live && w.part == 0) static_cast<uint16_t *>(P.ring_gate)[ring_o] = gbits;
   }
+}
+
+// One wave per (batch, row kind, token tile); row kinds: the q heads, the k
+// heads, then the v heads.  A wave holds only its own kind's parameters and
+// rows, so the kernel keeps few enough registers for four waves per SIMD.
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_prefix(kvm_prefix_desc P) {
+  constexpr int LPR = D / 8, RPW = 64 / LPR, PASSES = kTokWave / RPW;
+  const int64_t T = P.seq_len, Hq = P.q_heads, Hkv = P.kv_heads;
+  const int64_t tiles = (T + kTokWave - 1) / kTokWave;
+  const int64_t wv = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t tile = wv % tiles;
+  const int64_t kind = (wv / tiles) % (Hq + 2 * Hkv);
+  PrefixTile w;
+  w.bi = wv / tiles / (Hq + 2 * Hkv);
+  if (w.bi >= P.batch) return;  // wave-uniform
+  w.lane = threadIdx.x & 63;
+  w.part = w.lane % LPR;
+  w.sub = w.lane / LPR;
+  w.t0 = tile * kTokWave;
+  w.npass = int(min(int64_t(PASSES), (T - w.t0 + RPW - 1) / RPW));  // passes with a live token
+  const bool is_q = kind < Hq;
+  w.hk = is_q ? 0 : (kind - Hq) % Hkv;
+  w.width = is_q ? Hq * D : Hkv * D;
+  w.chan = (is_q ? kind : w.hk) * D + w.part * 8;
+  if (kind < Hq + Hkv)
+    qk_rows<D>(P, w, is_q);
+  else
+    v_rows<D>(P, w);
 }
 
 }  // namespace
 
 hipError_t launch_prefix(const kvm_prefix_desc &P, hipStream_t stream) {
   const int64_t tiles = (P.seq_len + kTokWave - 1) / kTokWave;
-  const int64_t waves = P.batch * (P.q_heads + P.kv_heads) * tiles;
+  const int64_t waves = P.batch * (P.q_heads + 2 * P.kv_heads) * tiles;
   const dim3 grid{unsigned((waves + kThreads / 64 - 1) / (kThreads / 64)), 1u, 1u};
   if (P.head_dim == 128)
     hipLaunchKernelGGL(k_prefix<128>, grid, dim3(kThreads), 0, stream, P);

@@ -31,7 +31,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     M = x.numel() // K if small else 0
     if not small or M < 1 or M > 16:
         y = F.linear(x, weight, bias)
-        return _relu_square(y) if relu_square else y
+        return _relu_square(y, out=y) if relu_square else y
     x2 = x.reshape(M, K)
     # The stride of a single row is meaningless to torch (it may be anything);
     # the kernel only needs K for it.
@@ -106,12 +106,14 @@ def _packed(weight: torch.Tensor, rows: int) -> torch.Tensor | None:
     return entry[rows]
 
 
-def _relu_square(h: torch.Tensor) -> torch.Tensor:
-    """relu(h)^2 in one HIP launch (kvm_relu_square): bf16 GPU tensors only."""
+def _relu_square(h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """relu(h)^2 in one HIP launch (kvm_relu_square): bf16 GPU tensors only.
+    ``out`` may be ``h`` itself (each element is read before it is written)."""
     if not h.is_cuda or h.dtype != torch.bfloat16 or h.numel() % 8:
         raise ValueError("relu_square runs on bf16 GPU tensors with a multiple of 8 elements")
     h = h.contiguous()
-    out = torch.empty_like(h)
+    if out is None or not out.is_contiguous() or out.shape != h.shape or out.dtype != h.dtype:
+        out = torch.empty_like(h)
     _lib.check(_lib.load().kvm_relu_square(h.data_ptr(), out.data_ptr(), h.numel(), _lib.stream_handle(h.device)),
                "kvm_relu_square")
     return out

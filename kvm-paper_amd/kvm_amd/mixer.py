@@ -549,14 +549,15 @@ class SequenceMixer(nn.Module):
 
     def _projection_weight(self, mods):
         """torch.cat of the modules' weights, padded with zero rows to a
-        multiple of 8 outputs (16-byte aligned output rows), rebuilt whenever
-        one of them is replaced or modified in place (data pointer or version
-        counter)."""
+        multiple of 64 outputs (128-byte aligned output rows, so that each
+        head's piece of a row is whole cache lines for the prefix kernel),
+        rebuilt whenever one of them is replaced or modified in place (data
+        pointer or version counter)."""
         key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.device) for m in mods)
         cached = self.__dict__.get("_proj_cat")
         if cached is None or cached[0] != key:
             w0 = mods[0].weight
-            pad = -sum(m.out_features for m in mods) % 8
+            pad = -sum(m.out_features for m in mods) % 64
             with torch.no_grad():
                 cached = (key, torch.cat([m.weight for m in mods] + [w0.new_zeros(pad, w0.size(1))], dim=0))
             self.__dict__["_proj_cat"] = cached
