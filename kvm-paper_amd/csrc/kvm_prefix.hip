@@ -17,7 +17,8 @@
 // Rounding: each reference op computes in fp32 and rounds to bf16 (torch's
 // opmath for bf16 tensors); the same rounding points are kept here, so the
 // outputs match the torch sequence except where an fp32 result of a
-// transcendental or of the LayerNorm's reductions differs in its last bit.
+// transcendental, of the sigmoid's quotient or of the LayerNorm's reductions
+// differs in its last bit.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
