@@ -66,6 +66,11 @@ struct AttnState {
 // representable range for fp32 sums and bf16 P, and the O rescale (64
 // multiplies per lane) is skipped in almost every block.
 constexpr float kRescaleSlack = 8.0f;
+// A block's weights are first computed against the current reference
+// maxima; the block maxima are needed only when some lane's sum of its
+// weights of a row exceeds 2^kRescaleSlack (no weight exceeds that when no
+// sum does) or a row has no reference yet.
+constexpr float kSumLimit = 256.0f;
 
 // Maxima of scores without the quieting copies (v_max_f32 x, x) the compiler
 // adds around fmaxf in IEEE mode: scores are MFMA sums of finite products or
@@ -109,27 +114,27 @@ __device__ __forceinline__ void score_block(const unsigned char *kbuf, const bf1
   }
 }
 
-// Masking (keys >= nvalid, or causal keys > qrel + row, where qrel is the
-// wave's first query minus the position of the block's first key), row
-// maxima (v_permlane swaps across the 16-lane groups) and the lazy move of
-// the reference maximum with its O rescale.
-template <int D>
-__device__ __forceinline__ void block_max(f32x4 (&s)[4][2], AttnState<D> &as, bool masked,
-                                          int nvalid, bool causal, int qrel, float scale) {
+// Masking: keys >= nvalid, or causal keys > qrel + row, where qrel is the
+// wave's first query minus the position of the block's first key.
+__device__ __forceinline__ void block_mask(f32x4 (&s)[4][2], int nvalid, bool causal, int qrel) {
   const int lane = threadIdx.x & 63;
-  if (masked) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int lim = qrel + rt * 16 + (lane & 15);
+  for (int rt = 0; rt < 2; ++rt) {
+    const int lim = qrel + rt * 16 + (lane & 15);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kt * 16 + (lane >> 4) * 4 + i;
-          if (key >= nvalid || (causal && key > lim)) s[kt][rt][i] = -INFINITY;
-        }
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int key = kt * 16 + (lane >> 4) * 4 + i;
+        if (key >= nvalid || (causal && key > lim)) s[kt][rt][i] = -INFINITY;
+      }
   }
+}
+
+// Row maxima (v_permlane swaps across the 16-lane groups) and the lazy move
+// of the reference maximum with its O rescale.
+template <int D>
+__device__ __forceinline__ void block_max(const f32x4 (&s)[4][2], AttnState<D> &as, float scale) {
   bool need = false;
   float m_new[2];
 #pragma unroll
@@ -164,10 +169,10 @@ __device__ __forceinline__ void block_max(f32x4 (&s)[4][2], AttnState<D> &as, bo
 }
 
 // P^T = exp2(S^T * scale - m) in the B-operand layout (two 32-key steps,
-// each lane 8 keys, 4 per kt) and the lane-partial row sums.
+// each lane 8 keys, 4 per kt) and the lane-partial row sums of the block.
 template <int D>
-__device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], AttnState<D> &as,
-                                            float scale, bf16x8 (&pb)[2][2]) {
+__device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], const AttnState<D> &as,
+                                            float scale, bf16x8 (&pb)[2][2], float (&bsum)[2]) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const float base = as.m[rt] == -INFINITY ? 0.f : as.m[rt];
@@ -185,7 +190,7 @@ __device__ __forceinline__ void block_probs(const f32x4 (&s)[4][2], AttnState<D>
       pk[kt][0] = pack_bf16x2(p[0], p[1]);
       pk[kt][1] = pack_bf16x2(p[2], p[3]);
     }
-    as.l[rt] += psum;
+    bsum[rt] = psum;
     pb[0][rt] = as_bf16x8(make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]));
     pb[1][rt] = as_bf16x8(make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]));
   }
@@ -366,9 +371,26 @@ void k_attn_prefill(kvm_layer L, PrefillAttnArgs A, int chunk_begin, int qtiles,
       const bool masked = nvalid < BN || qrel < BN - 1;
       f32x4 s[4][2];
       score_block<D>(lds + (j % KBUFS) * BLK + kb, qf, s);
-      block_max<D>(s, as, masked, nvalid, causal, qrel, sc);
+      if (masked) block_mask(s, nvalid, causal, qrel);
+      // Weights against the current references; the maxima (and a second
+      // pass over the weights) only where a reference must be set or may
+      // move (a weight above 2^kRescaleSlack: the block maximum exceeds the
+      // reference by more than the slack).  Outside rounding ties at that
+      // boundary the references move in the same blocks as when the maxima
+      // come first.
       bf16x8 pb[2][2];
-      block_probs<D>(s, as, sc, pb);
+      float bsum[2];
+      bool slow = __ballot(as.m[0] == -INFINITY || as.m[1] == -INFINITY) != 0;
+      if (!slow) {
+        block_probs<D>(s, as, sc, pb, bsum);
+        slow = __ballot(bsum[0] > kSumLimit || bsum[1] > kSumLimit) != 0;
+      }
+      if (slow) {
+        block_max<D>(s, as, sc);
+        block_probs<D>(s, as, sc, pb, bsum);
+      }
+      as.l[0] += bsum[0];
+      as.l[1] += bsum[1];
       block_pv<D>(lds + (KBUFS + (j & 1)) * BLK, vb0, vb1, pb, as);
     }
   }
