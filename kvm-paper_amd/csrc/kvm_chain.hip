@@ -1222,16 +1222,35 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           const int l = (h * HP + sp) * RPP + tid / GL;
           if (l < nown) {
             const int e0 = max(off[l], c0), e1 = min(off[l] + cnt[l], c0 + nrow);
-            for (int e = e0; e < e1; ++e) {
+            auto add_row = [&](uint4 rk, uint4 rv) __attribute__((always_inline)) {
               float fk[8], fv[8];
-              unpack8(*reinterpret_cast<const uint4 *>(&stage_k[(e - c0) * D + part * 8]), fk);
-              unpack8(*reinterpret_cast<const uint4 *>(&stage_v[(e - c0) * D + part * 8]), fv);
+              unpack8(rk, fk);
+              unpack8(rv, fv);
 #pragma unroll
               for (int x = 0; x < 8; ++x) {
                 sk[sp][x] += fk[x];
                 sv[sp][x] += fv[x];
               }
+            };
+            auto row_k = [&](int e) { return *reinterpret_cast<const uint4 *>(&stage_k[(e - c0) * D + part * 8]); };
+            auto row_v = [&](int e) { return *reinterpret_cast<const uint4 *>(&stage_v[(e - c0) * D + part * 8]); };
+            int e = e0;
+            if constexpr (OWN == 128) {
+              // Four rows' LDS reads in flight at once: at 1024 slots the
+              // routes are uneven enough that some slots sum tens of rows.
+              // Still added in token order.
+              for (; e + 4 <= e1; e += 4) {
+                uint4 rk[4], rv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  rk[u] = row_k(e + u);
+                  rv[u] = row_v(e + u);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) add_row(rk[u], rv[u]);
+              }
             }
+            for (; e < e1; ++e) add_row(row_k(e), row_v(e));
           }
         }
         __syncthreads();
