@@ -18,7 +18,8 @@
 //   k_merge_refresh       16 slots per workgroup: each slot sums the tokens
 //       routed to it in token order (fp32, deterministic, no global
 //       atomics), writes bf16(state + bf16(sum)) and its LayerNorm /
-//       normalized-value attention rows.
+//       normalized-value attention rows.  When the attention rows are
+//       updated in place, a slot no token merges into is left untouched.
 
 #include "kvm_device.hpp"
 #include "kvm_internal.hpp"
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(512) void k_rank_append(
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_merge_refresh(
     kvm_layer L, int n_tok, int s_after, kvm_state st, AttnRows attn_out,
-    UpdateScratch sc, int parity) {
+    UpdateScratch sc, int parity, int in_place) {
   constexpr int G = D / 8;
   constexpr int SPW = 64 / G;   // slots per wave
   constexpr int SPB = 4 * SPW;  // slots per workgroup
@@ -438,11 +439,19 @@ __global__ __launch_bounds__(kThreads) void k_merge_refresh(
   const bool valid = j < s_after;
   const int jj = valid ? j : 0;
 
-  // The slot's current sums and vlen (in flight during the listing).
+  // The slot's current sums and vlen, in flight during the listing (in
+  // place: loaded after it, for the slots that change).
   const int64_t so = (int64_t(row) * st.capacity + jj) * D + part * 8;
-  const uint4 k_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_k) + so);
-  const uint4 v_raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_v) + so);
-  const float vlen = static_cast<const float *>(st.s_vlen)[int64_t(row) * st.capacity + jj];
+  auto load_k = [&]() { return *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_k) + so); };
+  auto load_v = [&]() { return *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(st.s_v) + so); };
+  auto load_vlen = [&]() { return static_cast<const float *>(st.s_vlen)[int64_t(row) * st.capacity + jj]; };
+  uint4 k_raw = make_uint4(0, 0, 0, 0), v_raw = make_uint4(0, 0, 0, 0);
+  float vlen = 0.f;
+  if (!in_place) {
+    k_raw = load_k();
+    v_raw = load_v();
+    vlen = load_vlen();
+  }
 
   if (tid < SPB) {
     cnt[tid] = 0;
@@ -482,6 +491,14 @@ __global__ __launch_bounds__(kThreads) void k_merge_refresh(
     sorted[o + r] = x;
   }
   __syncthreads();
+  if (in_place) {
+    // Unchanged slots keep their state and attention rows (appended slots
+    // got theirs from k_rank_append); no barrier follows.
+    if (n == 0) return;
+    k_raw = load_k();
+    v_raw = load_v();
+    vlen = load_vlen();
+  }
 
   float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -719,8 +736,9 @@ static hipError_t launch_update_d(const kvm_layer &L, const kvm_seq &src,
   }
   constexpr int spb = 4 * (64 / (D / 8));
   const dim3 mgrid{rows, unsigned((s_after + spb - 1) / spb), 1u};
+  const int in_place = attn_out.k == attn_in.k && attn_out.v == attn_in.v && attn_out.cap == attn_in.cap;
   hipLaunchKernelGGL(k_merge_refresh<D>, mgrid, dim3(kThreads), size_t(n_tok) * 12, stream, L,
-                     int(n_tok), s_after, st, attn_out, sc, parity);
+                     int(n_tok), s_after, st, attn_out, sc, parity, in_place);
   return hipGetLastError();
 }
 
