@@ -228,15 +228,38 @@ __global__ __launch_bounds__(D) void k_decode_combine(
   const int pid = blockIdx.x;
   const int b = pid / Hq, h = pid % Hq;
   const int d = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < nseg; ++s)
-    M = fmaxf(M, part_ml[(int64_t(pid) * nseg + s) * 2]);
-  float a = 0.f, l = 0.f;
-  for (int s = 0; s < nseg; ++s) {
-    const float ms = part_ml[(int64_t(pid) * nseg + s) * 2];
-    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    a += part_acc[(int64_t(pid) * nseg + s) * D + d] * f;
-    l += part_ml[(int64_t(pid) * nseg + s) * 2 + 1] * f;
+  const float *ml = part_ml + int64_t(pid) * nseg * 2;
+  const float *acc = part_acc + int64_t(pid) * nseg * D + d;
+  float M = -INFINITY, a = 0.f, l = 0.f;
+  constexpr int kMaxSeg = 16;
+  if (nseg <= kMaxSeg) {
+    // Every partial loaded at once (one memory round trip), then the same
+    // arithmetic in the same segment order as the loop below.
+    float m[kMaxSeg], sl[kMaxSeg], x[kMaxSeg];
+#pragma unroll
+    for (int s = 0; s < kMaxSeg; ++s) {
+      m[s] = s < nseg ? ml[2 * s] : -INFINITY;
+      sl[s] = s < nseg ? ml[2 * s + 1] : 0.f;
+      x[s] = s < nseg ? acc[s * D] : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < kMaxSeg; ++s) M = fmaxf(M, m[s]);
+#pragma unroll
+    for (int s = 0; s < kMaxSeg; ++s) {
+      if (s < nseg) {
+        const float f = (m[s] == -INFINITY) ? 0.f : exp2f(m[s] - M);
+        a += x[s] * f;
+        l += sl[s] * f;
+      }
+    }
+  } else {
+    for (int s = 0; s < nseg; ++s) M = fmaxf(M, ml[2 * s]);
+    for (int s = 0; s < nseg; ++s) {
+      const float ms = ml[2 * s];
+      const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+      a += acc[s * D] * f;
+      l += ml[2 * s + 1] * f;
+    }
   }
   out[b * o_sb + h * o_sh + d] = uint16_t(f2bf(a / l));
 }
