@@ -143,3 +143,35 @@ def test_mlp_kernels_match_torch_ops(lib, with_prev):
         assert torch.equal(got, ref), float((got.float() - ref.float()).abs().max())
         h = torch.randn(B, Tn, 4 * d, device=DEV, generator=gen).bfloat16()
         assert torch.equal(_relu_square(h), torch.nn.functional.relu(h).square())
+        # in place (out is the input): the same values
+        h2 = h.clone()
+        assert torch.equal(_relu_square(h2, out=h2), torch.nn.functional.relu(h).square())
+
+
+def test_mlp_row_chunks_match_whole_input(lib):
+    """MLP.ffn runs inputs of more than _FFN_CHUNK rows in row chunks (each
+    chunk's hidden activations stay in the last-level cache); rows are
+    independent, so the chunked result is compared with the same ops on the
+    whole input, here with a ragged last chunk."""
+    from kvm_amd.backbone import MLP
+    from kvm_amd.linear import linear
+    from types import SimpleNamespace
+
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    d = 256
+    cfg = SimpleNamespace(ffn_expansion=4.0, hidden_size=d, use_tokenshift_ffn=0, num_hidden_layers=2)
+    mlp = MLP(cfg, 0).to(DEV, torch.bfloat16).eval()
+    with torch.no_grad():
+        mlp.c_proj.weight.copy_((torch.randn(d, 4 * d, device=DEV, generator=gen) / 32).bfloat16())
+        rows = 2 * MLP._FFN_CHUNK + 1234
+        x = torch.randn(1, rows, d, device=DEV, generator=gen).bfloat16()
+        got = mlp.ffn(x)
+        ref = torch.nn.functional.linear(linear(x, mlp.c_fc.weight, relu_square=True), mlp.c_proj.weight)
+    assert got.shape == ref.shape
+    diff = (got.float() - ref.float()).abs()
+    eq = float((diff == 0).float().mean())
+    T.log(f"[mlp-chunks] rows {rows}: equal {eq * 100:.3f}%, max |diff| {float(diff.max()):.3e}")
+    # The same GEMMs per row; only a different kernel choice for the chunk
+    # shape could reorder the K sums (one bf16 rounding of the output).
+    assert torch.allclose(got.float(), ref.float(), rtol=2 ** -7, atol=1e-3)
+    assert eq >= 0.99
