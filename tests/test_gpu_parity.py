@@ -716,6 +716,65 @@ def test_chain_matches_per_update_kernels(lib, monkeypatch, B, Hq, Hkv, Tn, D, C
     T.log(f"[chain] {plan.n_updates} updates, S={S}, {n_app} appended tokens: identical")
 
 
+@pytest.mark.parametrize("C,D,n_keys", [(128, 128, 12), (100, 64, 5)])
+def test_chain_append_ties_match_per_update_kernels(lib, monkeypatch, C, D, n_keys):
+    """Exact novelty ties: every key is one of n_keys vectors per head, so
+    many tokens of a chunk have the same novelty (and many slots the same
+    key).  The appending chain (a bitonic sort of novelty-and-index keys)
+    must select the same least-novel tokens as the per-update kernels, ties
+    to the lower index, and route to the same lowest slots among equal
+    scores: routes, appends, state and outputs bit for bit."""
+    B, Hq, Hkv = 1, 4, 2
+    Tn = C * 11 + C // 3
+    T.log(f"[chain-ties] C{C} D{D} {n_keys} distinct keys per head, T{Tn}")
+    cfg = T.mixer_config(Hq, Hkv, D, C, mode="power_law", sink=1, min_len=C, n_max=4, factor=6.0)
+    gen = torch.Generator().manual_seed(29)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    ln_b = (0.1 * torch.randn(D, generator=gen)).bfloat16()
+    m = T.make_mixer(cfg, ln_w, ln_b, torch.ones(Hq), torch.ones(Hq))
+    q, _, v, g = _random_inputs(B, Hq, Hkv, Tn, D, 31)
+    base = (torch.randn(B, Hkv, n_keys, D, generator=gen) / math.sqrt(D)).bfloat16()
+    pick = torch.randint(0, n_keys, (B, Hkv, Tn), generator=gen)
+    k = torch.gather(base, 2, pick.unsqueeze(-1).expand(B, Hkv, Tn, D))
+    q, k, v, g = (t.to(DEV) for t in (q, k, v, g))
+    plan = m.make_plan(Tn)
+    assert sum(plan.upd_n_append) > 0
+    res = {}
+    for name, chain in (("chain", "1"), ("per-update", "0")):
+        monkeypatch.setenv("KVM_AMD_CHAIN", chain)
+        with torch.no_grad():
+            res[name] = m.prefill_raw(q, k, v, g, route_log=True)
+        torch.cuda.synchronize()
+    a, b = res["chain"], res["per-update"]
+    S = plan.final_state_len
+    for key in ("route_log", "append_log", "out"):
+        assert torch.equal(a[key], b[key]), key
+    for key in ("state_k", "state_v", "state_vlen", "state_k_attn", "state_v_attn"):
+        assert torch.equal(a[key][:, :S], b[key][:, :S]), key
+    # The append sets against the oracle with the same lower-index tie rule.
+    ocfg = O.OracleConfig(
+        q_heads=Hq, kv_heads=Hkv, head_dim=D, value_dim=D, chunk_len=C, n_bswa_chunks=cfg.n_bswa_chunks,
+        n_max_d_chunks=cfg.n_max_d_chunks, sink_len=cfg.sink_len, rope_partial_dim=cfg.rope_partial_dim,
+        state_budget_mode="power_law", state_growth_factor=cfg.state_growth_factor,
+        state_growth_exponent=cfg.state_growth_exponent, state_round_down=1, state_min_len=C,
+        append_tie_break="lower_index")
+    p = O.OracleParams(ln_weight=ln_w, ln_bias=ln_b, front_temp=torch.ones(Hq).bfloat16(),
+                       state_temp=torch.ones(Hq).bfloat16())
+    rec = O.Recorder()
+    O.prefill(q.cpu(), k.cpu(), v.cpu(), g.cpu(), p, ocfg, rec)
+    alog = a["append_log"].cpu()
+    assert len(rec.updates) == plan.n_updates
+    checked = 0
+    for i, u in enumerate(rec.updates):
+        for r in range(B * Hkv):
+            want = sorted(u.append_idx[r // Hkv, r % Hkv].tolist()) if u.append_idx is not None else []
+            got = torch.nonzero(alog[i, r]).flatten().tolist()
+            assert got == want, f"update {i} row {r}: appended {got} against the oracle's {want}"
+            checked += len(want)
+    T.log(f"[chain-ties] {plan.n_updates} updates, S={S}, {checked} appended tokens: identical to the "
+          f"per-update kernels and to the oracle")
+
+
 @pytest.mark.parametrize("B,Hkv,Tn,D,min_len,skew", [
     (1, 32, 8192, 128, 768, False),   # 96 owned slots per member
     (1, 32, 8192, 128, 1024, False),  # 128 owned slots per member
