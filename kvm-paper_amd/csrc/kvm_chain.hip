@@ -858,7 +858,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
   __shared__ float own_vl[OWN];
   __shared__ int tok_lds[kChainMax];  // first token of each update (list.tok_begin)
   __shared__ int sorted[kFixedMaxTok];
-  __shared__ int wsc[kChainWaves][OWN];  // per-wave slot counts, then per-wave offsets
+  __shared__ int wsc[kChainWaves][OWN];  // per-wave slot counts
   __shared__ int cnt[OWN], off[OWN];
   __shared__ int ok_lds;
   __shared__ float ln_w[D], ln_b[D];  // ln_s_k parameters (LDS: no wait on global loads)
@@ -1136,18 +1136,23 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       __syncthreads();
       if (fail_lds) return;  // a partial never arrived: the launch is abandoned
       KVM_TS(15);
-      if (tid < 64) {  // per-wave offsets, then the exclusive prefix over slots (one wave)
+      // Every wave computes the exclusive prefix over slots (slot e's first
+      // list position, and its position after the tokens of lower waves)
+      // itself, so that each places its own tokens without another barrier;
+      // wave 0 also keeps off / cnt for the sums.
+      int ntot;  // tokens routed to my slots
+      {
         constexpr int PER = OWN / 64;  // consecutive slots per lane
-        int run[PER], tot = 0;
+        int run[PER], mine_pre[PER], tot = 0;
 #pragma unroll
         for (int x = 0; x < PER; ++x) {
-          const int e = tid * PER + x;
+          const int e = lane * PER + x;
           run[x] = 0;
+          mine_pre[x] = 0;
 #pragma unroll
           for (int w = 0; w < kChainWaves; ++w) {
-            const int c = wsc[w][e];
-            wsc[w][e] = run[x];
-            run[x] += c;
+            if (w == wave) mine_pre[x] = run[x];
+            run[x] += wsc[w][e];
           }
           tot += run[x];
         }
@@ -1155,19 +1160,28 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
           const int y = __shfl_up(incl, o);
-          if (tid >= o) incl += y;
+          if (lane >= o) incl += y;
         }
         int base = incl - tot;
+        int pos[PER];
 #pragma unroll
         for (int x = 0; x < PER; ++x) {
-          off[tid * PER + x] = base;
-          cnt[tid * PER + x] = run[x];
+          if (wave == 0) {
+            off[lane * PER + x] = base;
+            cnt[lane * PER + x] = run[x];
+          }
+          pos[x] = base + mine_pre[x];
           base += run[x];
         }
+        ntot = __shfl(incl, 63);
+        int at = 0;
+#pragma unroll
+        for (int x = 0; x < PER; ++x) {
+          const int v = __shfl(pos[x], (mine ? my_loc : 0) / PER);
+          if ((mine ? my_loc : 0) % PER == x) at = v;
+        }
+        if (mine) sorted[at + rank] = tid;
       }
-      __syncthreads();
-      if (mine) sorted[off[my_loc] + wsc[wave][my_loc] + rank] = tid;
-      const int ntot = off[OWN - 1] + cnt[OWN - 1];  // tokens routed to my slots
       __syncthreads();
       KVM_TS(2);
 
