@@ -1224,8 +1224,10 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
       };
       // Adds the staged rows c0 .. of the slots of half h to the sums, in
       // token order; `arrived`: wait for this wave's gathers, then for every
-      // wave's (not needed when the rows were staged for an earlier half).
-      auto stage_sum = [&](int c0, int h, bool arrived) __attribute__((always_inline)) {
+      // wave's (not needed when the rows were staged for an earlier half);
+      // `release`: a barrier after the reads, before another gather reuses
+      // the staging buffers (the merge's final barrier covers the last use).
+      auto stage_sum = [&](int c0, int h, bool arrived, bool release) __attribute__((always_inline)) {
         const int nrow = min(STAGE, ntot - c0);
         if (arrived) {
           wait_vm<0>();
@@ -1267,7 +1269,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
             for (; e < e1; ++e) add_row(row_k(e), row_v(e));
           }
         }
-        __syncthreads();
+        if (release) __syncthreads();
       };
       // Refreshed attention rows: keys into LDS (route operands), keys and
       // values into snapshot u0 + p straight from registers (non-temporal:
@@ -1342,7 +1344,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
 #pragma unroll 1
         for (int h = 0; h < NH; ++h) {
           zero_sums();
-          stage_sum(0, h, h == 0);
+          stage_sum(0, h, h == 0, false);
           if (h == 0) {
             KVM_TS(9);
             KVM_TS(10);
@@ -1358,7 +1360,7 @@ __global__ __launch_bounds__(kChainThreads) void k_chain_fixed(
           zero_sums();
           for (int c0 = 0; c0 < ntot; c0 += STAGE) {
             if (h > 0 || c0 > 0) gather(c0);
-            stage_sum(c0, h, true);
+            stage_sum(c0, h, true, true);
           }
           if (h == NH - 1 && do_route) load_bx(0, 4, KS / 2, KS * 3 / 4);
           refresh(h);
