@@ -523,21 +523,63 @@ __global__ __launch_bounds__(kChainThreads) void k_chain(
         if (t < n_tok) tok_a[t] = 0;
       }
       __syncthreads();
+      // Keys tid and tid + 512 in registers: a compare-exchange stage whose
+      // partner distance j is below 64 pairs keys of one wave (e ^ j is in
+      // e's 64-key block) and runs on lane shuffles; the others go through
+      // LDS, a barrier each.
+      constexpr int KPT = 2;  // keys per thread (n_tok <= 1024)
+      uint64_t rk[KPT];
+      auto load_keys = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int x = 0; x < KPT; ++x) {
+          const int e = tid + x * kChainThreads;
+          rk[x] = e < npow ? skey[e] : ~uint64_t(0);
+        }
+      };
+      auto store_keys = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int x = 0; x < KPT; ++x) {
+          const int e = tid + x * kChainThreads;
+          if (e < npow) skey[e] = rk[x];
+        }
+      };
+      load_keys();
       for (int k2 = 2; k2 <= npow; k2 <<= 1) {
-        for (int j = k2 >> 1; j > 0; j >>= 1) {
-          for (int e = tid; e < npow; e += kChainThreads) {
-            const int f = e ^ j;
-            if (f > e) {
-              const uint64_t a = skey[e], c = skey[f];
-              if ((a > c) == ((e & k2) == 0)) {
-                skey[e] = c;
-                skey[f] = a;
+        int j = k2 >> 1;
+        if (j >= 64) {
+          store_keys();
+          __syncthreads();
+          for (; j >= 64; j >>= 1) {
+            for (int e = tid; e < npow; e += kChainThreads) {
+              const int f = e ^ j;
+              if (f > e) {
+                const uint64_t a = skey[e], c = skey[f];
+                if ((a > c) == ((e & k2) == 0)) {
+                  skey[e] = c;
+                  skey[f] = a;
+                }
               }
             }
+            __syncthreads();
           }
-          __syncthreads();
+          load_keys();
+        }
+        for (; j > 0; j >>= 1) {
+#pragma unroll
+          for (int x = 0; x < KPT; ++x) {
+            const int e = tid + x * kChainThreads;
+            const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(rk[x])), j));
+            const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(rk[x] >> 32)), j));
+            const uint64_t o = (uint64_t(hi) << 32) | lo;
+            // The lower index of an ascending pair keeps the smaller key.
+            const bool take_min = ((e & k2) == 0) == ((e & j) == 0);
+            const uint64_t mn = rk[x] < o ? rk[x] : o, mx = rk[x] < o ? o : rk[x];
+            if (e < npow) rk[x] = take_min ? mn : mx;
+          }
         }
       }
+      store_keys();
+      __syncthreads();
       for (int r = tid; r < na; r += kChainThreads) tok_a[int(uint32_t(skey[r]))] = 1;
       __syncthreads();
       KVM_TS_A(3);
