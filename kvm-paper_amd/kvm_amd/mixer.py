@@ -626,6 +626,30 @@ class SequenceMixer(nn.Module):
             word.zero_()
         return bits
 
+    def _status_pending(self, device):
+        """Queue a copy of the status word into pinned host memory behind the
+        work already on the stream; returns a function that waits for that
+        copy only (not for work queued after it) and returns the word's bits,
+        clearing the word when any is set."""
+        word = self._status_word(device)
+        hosts = self.__dict__.setdefault("_status_host", {})
+        key = str(device)
+        if key not in hosts:
+            hosts[key] = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        host = hosts[key]
+        host.copy_(word, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+
+        def wait() -> int:
+            done.synchronize()
+            bits = int(host[0])
+            if bits:
+                word.zero_()
+            return bits
+
+        return wait
+
     @staticmethod
     def _raise_status(bits: int) -> None:
         if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT:
@@ -758,8 +782,22 @@ class SequenceMixer(nn.Module):
             cap = max(plan.final_state_len, min(self.chunk_len, self.max_state_len),
                       state_length_after_cycle(self.state_budget, self.chunk_len, self.n_bswa_chunks,
                                                int(T), plan.final_state_len, self.n_bswa_chunks * self.chunk_len))
-        res = self.prefill_raw(q, k, v, merge_gate, plan=plan, state_capacity=cap)
+        # The status word is read without stalling the GPU: the output
+        # projection is queued behind the prefill before the host waits for
+        # the word's copy.  A timed-out chain is repeated on the per-update
+        # kernels (bit-identical results), as prefill_raw does.
+        res = self.prefill_raw(q, k, v, merge_gate, plan=plan, state_capacity=cap, check_status=False)
+        status = self._status_pending(q.device)
         y = self.c_proj(res["out"].view(B, T, -1))
+        bits = status()
+        if bits & _lib.KVM_STATUS_CHAIN_TIMEOUT:
+            warnings.warn("kvm_prefill: the persistent update chain timed out waiting for its row group "
+                          "(another workload held compute units); repeating the prefill on the per-update "
+                          "kernels", RuntimeWarning, stacklevel=2)
+            res = self.prefill_raw(q, k, v, merge_gate, plan=plan, state_capacity=cap, chain=False)
+            y = self.c_proj(res["out"].view(B, T, -1))
+        else:
+            self._raise_status(bits)
         if past_key_values is not None:
             begin = self._bswa_begin_for_total_len(int(T))
             if plan.final_coverage != max(plan.initial_state_len, begin):

@@ -69,3 +69,29 @@ def test_chain_timeout_is_reported_or_repeated(monkeypatch, mode):
         torch.cuda.synchronize()
     assert torch.equal(again["out"], ref_out), "a prefill after a reported failure must be exact again"
     mixer.check_prefill_status()  # clear
+
+
+def test_forward_prefill_repeats_a_timed_out_chain(monkeypatch):
+    """The mixer's forward reads the status word after queueing its output
+    projection; a timed-out chain is still repeated on the per-update kernels
+    before the result is returned (same output as the normal forward)."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    import warnings
+
+    B, Hq, Hkv, D, C, Tn = 1, 4, 2, 128, 64, 64 * 10
+    cfg = T.mixer_config(Hq, Hkv, D, C, rope=32, mode="fixed", min_len=C, n_max=4, factor=4.0, expo=0.5)
+    mixer = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = _inputs(B, Hq, Hkv, D, Tn, seed=1)
+    T.log(f"[status] forward_prefill B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn}: normal, then a zero poll budget")
+    with torch.no_grad():
+        with warnings.catch_warnings():
+            warnings.simplefilter("error", RuntimeWarning)
+            good = mixer.forward_prefill(q, k, v, g, None, None, None).clone()
+        monkeypatch.setenv("KVM_AMD_CHAIN_POLLS", "0")
+        with pytest.warns(RuntimeWarning, match="per-update kernels"):
+            fallback = mixer.forward_prefill(q, k, v, g, None, None, None)
+        monkeypatch.delenv("KVM_AMD_CHAIN_POLLS")
+        torch.cuda.synchronize()
+    assert torch.equal(fallback, good)
+    mixer.check_prefill_status()  # the word was cleared by the forward's read
