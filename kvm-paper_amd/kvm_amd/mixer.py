@@ -632,11 +632,7 @@ class SequenceMixer(nn.Module):
         copy only (not for work queued after it) and returns the word's bits,
         clearing the word when any is set."""
         word = self._status_word(device)
-        hosts = self.__dict__.setdefault("_status_host", {})
-        key = str(device)
-        if key not in hosts:
-            hosts[key] = torch.empty(1, dtype=torch.int32, pin_memory=True)
-        host = hosts[key]
+        host = torch.empty(1, dtype=torch.int32, pin_memory=True)  # one per read: reads may overlap
         host.copy_(word, non_blocking=True)
         done = torch.cuda.Event()
         done.record()

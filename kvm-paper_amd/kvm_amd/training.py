@@ -96,10 +96,13 @@ class KVMPrefillFunction(torch.autograd.Function):
     def forward(ctx, mixer, q, k, v, gate, ln_w, ln_b, state_temp, front_temp):
         with torch.no_grad():
             # No status read here (a host synchronisation per layer and step):
-            # the word is sticky, and the backward reads it once before using
-            # anything the forward produced.
+            # a copy of the word into host memory is queued behind the
+            # prefill, and the backward waits for that copy (long complete by
+            # then, so without draining the stream) before using anything the
+            # forward produced.
             res = mixer.prefill_raw(q, k, v, gate, route_log=True, keep_snapshots=True, want_lse=True,
                                     check_status=False)
+            ctx.status = mixer._status_pending(q.device)
         ctx.mixer = mixer
         ctx.res = res
         ctx.save_for_backward(q, k, v, gate, ln_w, ln_b, state_temp, front_temp)
@@ -109,7 +112,7 @@ class KVMPrefillFunction(torch.autograd.Function):
     def backward(ctx, dout):
         q, k, v, gate, ln_w, ln_b, state_temp, front_temp = ctx.saved_tensors
         mixer, res = ctx.mixer, ctx.res
-        mixer.check_prefill_status()  # a timed-out update chain raises here, before its results are used
+        mixer._raise_status(ctx.status())  # a timed-out update chain raises here, before its results are used
         plan = res["plan"]
         dq, dk_w, dv_w, d_snap_k, d_snap_v, d_ts, d_tf = attention_backward(mixer, q, k, v, gate, res, dout)
         if plan.n_chunks > mixer.config.n_bswa_chunks:  # some query chunk read the memory state

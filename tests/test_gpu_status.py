@@ -95,3 +95,30 @@ def test_forward_prefill_repeats_a_timed_out_chain(monkeypatch):
         torch.cuda.synchronize()
     assert torch.equal(fallback, good)
     mixer.check_prefill_status()  # the word was cleared by the forward's read
+
+
+def test_training_backward_reports_a_timed_out_chain(monkeypatch):
+    """The differentiable prefill queues its status read behind the forward's
+    prefill; the backward waits for it and raises before using the forward's
+    results.  With the normal budget the same forward / backward runs clean."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from kvm_amd import training
+
+    B, Hq, Hkv, D, C, Tn = 1, 4, 2, 128, 64, 64 * 6
+    cfg = T.mixer_config(Hq, Hkv, D, C, rope=32, mode="fixed", min_len=C, n_max=4, factor=4.0, expo=0.5)
+    mixer = T.make_mixer(cfg, torch.ones(D), torch.zeros(D), torch.ones(Hq), torch.ones(Hq))
+    q, k, v, g = _inputs(B, Hq, Hkv, D, Tn, seed=2)
+    T.log(f"[status] training prefill B{B} Hq{Hq} Hkv{Hkv} D{D} C{C} T{Tn}: zero poll budget, then normal")
+    monkeypatch.setenv("KVM_AMD_CHAIN_POLLS", "0")
+    xs = [t.clone().requires_grad_(True) for t in (q, k, v, g)]
+    y = training.prefill_with_grad(mixer, *xs)
+    monkeypatch.delenv("KVM_AMD_CHAIN_POLLS")
+    with pytest.raises(RuntimeError, match="timed out"):
+        y.float().sum().backward()
+    xs = [t.clone().requires_grad_(True) for t in (q, k, v, g)]
+    y = training.prefill_with_grad(mixer, *xs)
+    y.float().sum().backward()
+    torch.cuda.synchronize()
+    assert all(x.grad is not None and torch.isfinite(x.grad.float()).all() for x in xs)
+    mixer.check_prefill_status()  # nothing left in the word
