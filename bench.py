@@ -37,6 +37,7 @@ sample of the prefill workload.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -336,6 +337,9 @@ def bench_e2e(args, torch, kvm_amd):
     more timed prefills: the reported prefill is the median of the three."""
     from kvm_amd.backbone import DecodeGraph, MixerConfig, RWKV7BackboneForCausalLM, StatesDictCache, init_random_
 
+    # The earlier workloads' cached allocator blocks are returned first, so
+    # that the decoder's buffers are laid out as in a process of its own.
+    torch.cuda.empty_cache()
     cfg = MixerConfig(vocab_size=65536, num_hidden_layers=24, num_attention_heads=16, hidden_size=2048,
                       mup_base_dim=2048, use_tokenshift_att=1, use_tokenshift_ffn=1, residual_scale=0.5,
                       rope_partial_dim=64, chunk_len=512, n_bswa_chunks=2, state_min_len=512,
@@ -348,6 +352,9 @@ def bench_e2e(args, torch, kvm_amd):
     ids = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=gen)
 
     def run(n, graph):
+        # The previous run's cache and HIP graph are released here, outside
+        # the timed region, not by a garbage collection inside it.
+        gc.collect()
         cache = StatesDictCache()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         torch.cuda.synchronize()
