@@ -372,6 +372,8 @@ def bench_e2e(args, torch, kvm_amd):
                            cache_position=torch.tensor([T + s]), logits_to_keep=1).logits[:, -1]
         e[2].record()
         torch.cuda.synchronize()
+        if runner is not None:
+            runner.close()
         return e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
 
     def breakdown():

@@ -634,6 +634,15 @@ class DecodeGraph:
     def _weights_signature(self):
         return tuple((p.data_ptr(), p._version) for p in self._params)
 
+    def close(self) -> None:
+        """Release the captured graph and its memory pool now.  Their teardown
+        waits for the device, so a caller chooses where it happens instead of
+        a garbage collection (possibly inside timed or latency-critical
+        work).  A later step captures the graph again."""
+        if self.graph is not None:
+            self.graph.reset()
+        self.graph = self.signature = None
+
     def _kvm_caches(self):
         from .decode_cache import KVMDecodeCache
         out = []
